@@ -1,0 +1,158 @@
+/*
+ * vnx — MI355X (gfx950) speculative-decoding verification kernels, C ABI.
+ *
+ * Drop-in boundary for VerseNext's speculative-decode path: the Python
+ * `SpeculativeDecoder` and the `DeviceBackend` "rocm" device call these entry
+ * points through ctypes.  Every reference citation below is relative to the
+ * CUI-hyg/VerseNext source tree.
+ *
+ * Conventions (all entry points):
+ *   - every pointer argument is a caller-owned DEVICE pointer unless noted;
+ *   - nothing here allocates device memory: entry points that need scratch
+ *     take `workspace` + `workspace_bytes` (query the size with the matching
+ *     *_workspace() function).  Its contents need no initialisation (each
+ *     call clears the counters it uses with a small kernel); calls that may
+ *     run concurrently (different streams) must not share a workspace;
+ *   - `stream` is a hipStream_t (NULL = the null stream); calls are
+ *     asynchronous on that stream;
+ *   - return value: VNX_OK (0) or a negative vnx_status; no exception or
+ *     longjmp crosses the ABI.  Argument checks happen on the host before
+ *     anything is launched;
+ *   - dtype codes: VNX_F32 (fp32), VNX_BF16 (bfloat16) for logits;
+ *   - token ids are int64, like the reference's int64 token arrays
+ *     (packages/verse_nex/verse_nex/speculative.py:161, :202-203);
+ *   - thread-compatible: the library keeps no mutable state after vnx_init()
+ *     except a host-side cache of checked temperatures (mutex-protected).
+ */
+#ifndef VNX_H_
+#define VNX_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum vnx_status {
+  VNX_OK = 0,
+  VNX_ERR_INVALID_ARG = -1,   /* shape / pointer / range error  -> ValueError   */
+  VNX_ERR_WORKSPACE = -2,     /* workspace missing or too small -> ValueError   */
+  VNX_ERR_UNSUPPORTED = -3,   /* dtype / size outside the kernels' range        */
+  VNX_ERR_HIP = -4,           /* a HIP runtime call failed      -> RuntimeError */
+  VNX_ERR_NO_DEVICE = -5      /* no gfx950 device / bad ordinal -> RuntimeError */
+};
+
+enum vnx_dtype { VNX_F32 = 0, VNX_BF16 = 1 };
+
+/* Flags written by vnx_spec_accept, one byte per (row, position). */
+enum vnx_accept_flag {
+  VNX_FLAG_NEAR_TIE = 1,      /* |u - p/q| < 1e-6 at this position                     */
+  VNX_FLAG_LSE_EDGE = 2,      /* a row LSE lies within 1e-7 of an fp32 rounding edge   */
+  VNX_FLAG_CDF_EDGE = 4,      /* the sampled CDF step lies within 1e-12*mass of u*mass */
+  VNX_FLAG_ZERO_RESIDUAL = 8, /* max(0,p-q) had zero mass; sampled from p instead      */
+  VNX_FLAG_BAD_ID = 16        /* draft id outside [0, V): treated as rejected          */
+};
+
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int vnx_version(void);
+
+/* Static text for a vnx_status code. */
+const char* vnx_status_string(int status);
+
+/* Text of the last HIP error seen by this thread ("" if none). */
+const char* vnx_last_hip_error(void);
+
+/* Selects `device` and checks it is a gfx950 GPU.  Safe to call repeatedly.
+ * Replaces: get_backend("rocm"/"rocm:N") device selection,
+ * packages/verse_torch/verse_torch/device.py:346-386 and
+ * packages/verse_torch/verse_torch/backend_torch.py:65-98. */
+int vnx_init(int device);
+
+/* ---------------------------------------------------------------------------
+ * Vocab-row reductions.
+ * logits: `rows` rows of `V` elements, row pitch `ld` elements (ld >= V).
+ * temperature: > 0; rows are scaled as RN(l / temperature) before the LSE
+ *   (sampler.py:95).  thresholds: NULL, or one float per row: scaled values
+ *   below it are masked to -inf (top-k keep rule `scaled >= kth`, sampler.py:98-102).
+ * ------------------------------------------------------------------------- */
+size_t vnx_row_lse_workspace(int64_t rows, int64_t V);
+
+/* lse[r] = log(sum_j exp(a_rj)) in fp64, rowmax[r] = max_j a_rj (fp32),
+ * argmax[r] = first index of the maximum of the RAW logits (numpy.argmax).
+ * rowmax / argmax may be NULL.
+ * Replaces the row reductions inside NumpyBackend.softmax (device.py:305-308),
+ * Tensor.softmax (packages/verse_torch/verse_torch/tensor.py:965-975) and
+ * Sampler.sample steps 1-3 (sampler.py:94-111). */
+int vnx_row_lse(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
+                float temperature, const float* thresholds,
+                double* lse, float* rowmax, int64_t* argmax,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* argmax[r] = numpy.argmax(logits[r, :V]) (first maximal index, NaN wins).
+ * Replaces np.argmax at speculative.py:158 and :220. */
+int vnx_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
+                   int64_t* argmax, void* workspace, size_t workspace_bytes, void* stream);
+
+/* out[r, j] = softmax(RN(l/temperature))[j] in fp32 (row pitch ldo).
+ * Replaces DeviceBackend.softmax (device.py:246-248, :305-308). */
+size_t vnx_softmax_workspace(int64_t rows, int64_t V);
+
+int vnx_softmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
+                float temperature, const float* thresholds, float* out, int64_t ldo,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Stochastic speculative acceptance (Leviathan et al. 2023, Alg. 1).
+ * target: B x (k+1) rows, row (b,i) at target + b*sb_t + i*ld_t,
+ * draft:  B x k rows,     row (b,i) at draft  + b*sb_d + i*ld_d
+ * (strides in elements; contiguous (B,k+1,V) is ld_t = V, sb_t = (k+1)*V),
+ * p_i = softmax(target_i / T), q_i = softmax(draft_i / T) (optional per-row
+ * thresholds thr_t (B*(k+1)) / thr_d (B*k), NULL = no top-k).
+ * draft_ids (B,k) int64, uniforms (B,k+1) fp32 in [0,1).
+ * Position i is accepted iff u_i < 1 and u_i*q_i(x_i) < p_i(x_i) (i.e.
+ * u_i < min(1, p/q)); n = first rejected position (k if none).  The emitted
+ * token at n is the inverse-CDF draw with u_k from norm(max(0, p_n - q_n))
+ * (n < k) or from p_k (n == k).
+ * Outputs: accept_len (B) int32 = n; out_ids (B, k+1) int64 = x_0..x_{n-1},
+ * the drawn token, then -1; flags (B, k+1) uint8 (vnx_accept_flag, may be
+ * NULL); lse_t (B*(k+1)) / lse_d (B*k) fp32 row LSEs as used (may be NULL).
+ * The reference verifier is the greedy special case of this rule:
+ * SpeculativeDecoder.verify / verify_then_commit, speculative.py:168-310.
+ * ------------------------------------------------------------------------- */
+size_t vnx_spec_accept_workspace(int64_t B, int k, int64_t V);
+
+int vnx_spec_accept(const void* target, const void* draft, int dtype,
+                    int64_t B, int k, int64_t V,
+                    int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
+                    const int64_t* draft_ids, const float* uniforms, float temperature,
+                    const float* thr_t, const float* thr_d,
+                    int32_t* accept_len, int64_t* out_ids, uint8_t* flags,
+                    float* lse_t, float* lse_d,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Greedy verify, the reference semantics batched:
+ * main_pred[b,i] = argmax(target row (b,i)) for i < rows_t (rows_t = k or k+1,
+ * row (b,i) at target + b*sb + i*ld), accepted[b,i] = draft_ids[b,i] ==
+ * main_pred[b,i] (i < k), accept_len[b] = length of the accepted prefix,
+ * out_ids[b,:] = accepted prefix, then main_pred at the first mismatch
+ * ("blessed" token), or main_pred[b,k] when all k match and rows_t == k+1
+ * (bonus), then -1.
+ * Replaces SpeculativeDecoder.verify (speculative.py:218-223) and the
+ * prefix loop of verify_then_commit (speculative.py:277-287), for all rows
+ * instead of batch row 0 only.  accepted / main_pred may be NULL.
+ * ------------------------------------------------------------------------- */
+size_t vnx_greedy_verify_workspace(int64_t B, int rows_t, int64_t V);
+
+int vnx_greedy_verify(const void* target, int dtype, int64_t B, int k, int rows_t,
+                      int64_t V, int64_t ld, int64_t sb, const int64_t* draft_ids,
+                      uint8_t* accepted, int64_t* main_pred,
+                      int32_t* accept_len, int64_t* out_ids,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VNX_H_ */

@@ -1,0 +1,163 @@
+"""GPU parity: vnx_spec_accept vs the canonical CPU oracle (oracle.speculative.spec_accept).
+
+Bar: accept_len and out_ids bit-exact; a row may differ only when a flag
+(near tie |u - p/q| < 1e-6, LSE within 1e-7 of an fp32 rounding edge, CDF
+edge) marks it on either side, and such rows are counted and reported.
+Row LSEs (fp32, as used) equal the oracle's except on LSE-edge rows."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.speculative import FLAG_BAD_ID, greedy_verify_batched, spec_accept
+from spec_inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+EXCUSE = 1 | 2 | 4  # near tie, LSE edge, CDF edge
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def run_gpu(hip, tgt, dft, ids, u, T, thr_t=None, thr_d=None, dtype=torch.float32):
+    tg = torch.from_numpy(tgt).to(hip.torch_device).to(dtype)
+    df = torch.from_numpy(dft).to(hip.torch_device).to(dtype)
+    res = hip.spec_accept(tg, df, torch.from_numpy(ids), torch.from_numpy(u), temperature=T,
+                          thr_t=None if thr_t is None else torch.from_numpy(thr_t),
+                          thr_d=None if thr_d is None else torch.from_numpy(thr_d))
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in res.items()}
+
+
+def compare(g, o, k):
+    B = g["accept_len"].shape[0]
+    explained, bad = [], []
+    for b in range(B):
+        same = g["accept_len"][b] == o["accept_len"][b] and np.array_equal(g["out_ids"][b], o["out_ids"][b])
+        if same:
+            continue
+        upto = max(int(g["accept_len"][b]), int(o["accept_len"][b]))
+        fl = (g["flags"][b, :upto + 1] | o["flags"][b, :upto + 1]) & EXCUSE
+        (explained if fl.any() else bad).append(b)
+    lse_ok_t = (g["lse_t"] == o["lse_t"]) | ((o["flags"] & 2) != 0)
+    return explained, bad, lse_ok_t
+
+
+def check(hip, tgt, dft, ids, u, T, thr_t=None, thr_d=None, max_explained=None):
+    k = ids.shape[1]
+    g = run_gpu(hip, tgt, dft, ids, u, T, thr_t, thr_d)
+    o = spec_accept(tgt, dft, ids, u, T, thr_t, thr_d)
+    explained, bad, lse_ok = compare(g, o, k)
+    B = ids.shape[0]
+    _say(f"  rows={B} explained={len(explained)} unexplained={len(bad)} "
+         f"mean_accept={g['accept_len'].mean():.3f} lse_t_equal={np.mean(g['lse_t'] == o['lse_t']):.4f} "
+         f"lse_d_equal={np.mean(g['lse_d'] == o['lse_d']):.4f}")
+    assert not bad, f"unexplained mismatches in rows {bad[:10]}"
+    assert len(explained) <= (max_explained if max_explained is not None else max(1, B // 100))
+    lse_d_ok = (g["lse_d"] == o["lse_d"]) | ((o["flags"][:, :k] & 2) != 0)
+    assert lse_ok.all() and lse_d_ok.all()
+    assert np.array_equal(g["flags"] & FLAG_BAD_ID, o["flags"] & FLAG_BAD_ID)
+    return g, o
+
+
+@pytest.mark.parametrize("B,k,V,T", [(8, 4, 1000, 1.0), (16, 8, 32000, 0.8), (5, 3, 4099, 1.7),
+                                     (3, 1, 7, 0.8), (4, 64, 2048, 0.9)])
+def test_accept_parity(hip, B, k, V, T):
+    _say(f"spec_accept B={B} k={k} V={V} T={T}")
+    tgt, dft, ids, u = make_inputs(B, k, V, T, seed_t=B + V, seed_d=k + 7, seed_x=V, seed_u=B * k)
+    check(hip, tgt, dft, ids, u, T)
+
+
+def test_accept_parity_config2_full_size(hip):
+    """B=64, k=8, V=248,320, T=0.8, no top-k."""
+    B, k, V, T = 64, 8, 248320, 0.8
+    _say(f"spec_accept config2 B={B} k={k} V={V}")
+    tgt, dft, ids, u = make_inputs(B, k, V, T)
+    g, o = check(hip, tgt, dft, ids, u, T, max_explained=2)
+    assert g["accept_len"].min() >= 0 and g["accept_len"].max() <= k
+
+
+def test_accept_bf16_logits(hip):
+    _say("spec_accept bf16")
+    B, k, V, T = 8, 6, 16000, 0.8
+    tgt, dft, ids, u = make_inputs(B, k, V, T, seed_t=11)
+    tb = torch.from_numpy(tgt).to(torch.bfloat16).float().numpy()  # bf16 values, exactly in fp32
+    db = torch.from_numpy(dft).to(torch.bfloat16).float().numpy()
+    g = run_gpu(hip, tb, db, ids, u, T, dtype=torch.bfloat16)
+    o = spec_accept(tb, db, ids, u, T)
+    explained, bad, _ = compare(g, o, k)
+    assert not bad and len(explained) <= 1
+
+
+def test_accept_with_topk_thresholds(hip):
+    from oracle import rows
+    _say("spec_accept top-k")
+    B, k, V, T, K = 6, 4, 20000, 0.8, 50
+    tgt, dft, ids, u = make_inputs(B, k, V, T, seed_t=21)
+    thr_t = np.array([[rows.topk_threshold(rows.scale(tgt[b, i], T), K) for i in range(k + 1)]
+                      for b in range(B)], np.float32)
+    thr_d = np.array([[rows.topk_threshold(rows.scale(dft[b, i], T), K) for i in range(k)]
+                      for b in range(B)], np.float32)
+    check(hip, tgt, dft, ids, u, T, thr_t, thr_d)
+
+
+def test_identical_draft_accepts_all_and_draws_bonus(hip):
+    _say("spec_accept p == q")
+    B, k, V = 8, 5, 3000
+    tgt, _, ids, u = make_inputs(B, k, V, 0.8, seed_t=31)
+    g, o = check(hip, tgt, tgt[:, :k].copy(), ids, u, 0.8)
+    assert np.all(g["accept_len"] == k)
+
+
+def test_low_temperature_equals_greedy(hip):
+    _say("spec_accept T=0.01 vs greedy")
+    rng = np.random.default_rng(0)
+    B, k, V = 16, 4, 512
+    tgt = rng.permuted(np.tile(np.arange(V, dtype=np.float32), (B, k + 1, 1)), axis=2)
+    dft = rng.permuted(np.tile(np.arange(V, dtype=np.float32), (B, k, 1)), axis=2)
+    pred = tgt.argmax(-1)
+    ids = np.where(rng.random((B, k)) < 0.6, pred[:, :k], dft.argmax(-1))
+    for i in range(k):
+        dft[np.arange(B), i, ids[:, i]] = V + 1
+    u = (rng.random((B, k + 1)) * 0.98).astype(np.float32)
+    g = run_gpu(hip, tgt, dft, ids, u, 0.01)
+    _, _, alen, out = greedy_verify_batched(tgt, ids)
+    assert np.array_equal(g["accept_len"], alen) and np.array_equal(g["out_ids"], out)
+
+
+def test_bad_ids_and_masked_entries(hip):
+    _say("spec_accept bad ids / -inf")
+    B, k, V = 4, 3, 1001
+    tgt, dft, ids, u = make_inputs(B, k, V, 1.0, seed_t=41)
+    ids[0, 1] = -3
+    ids[1, 0] = V + 5
+    tgt[2, :, ::3] = -np.inf
+    dft[3, :, 1::2] = -np.inf
+    g, o = check(hip, tgt, dft, ids, u, 1.0)
+    assert g["flags"][0, 1] & FLAG_BAD_ID and g["flags"][1, 0] & FLAG_BAD_ID
+    assert g["accept_len"][0] <= 1 and g["accept_len"][1] == 0
+
+
+def test_workspace_reuse_across_shapes(hip):
+    _say("spec_accept workspace reuse")
+    a = make_inputs(6, 5, 5000, 0.8, seed_t=51)
+    b = make_inputs(3, 2, 700, 0.8, seed_t=52)
+    g1 = run_gpu(hip, *a, 0.8)
+    run_gpu(hip, *b, 0.8)
+    g3 = run_gpu(hip, *a, 0.8)
+    for key in ("accept_len", "out_ids", "lse_t", "lse_d"):
+        assert np.array_equal(g1[key], g3[key])
+
+
+def test_strided_target_view(hip):
+    _say("spec_accept strided view")
+    B, k, V = 4, 3, 2048
+    tgt, dft, ids, u = make_inputs(B, k, V, 0.8, seed_t=61)
+    big = np.zeros((B, 10, V + 64), np.float32)
+    big[:, 2:2 + k + 1, :V] = tgt
+    view = torch.from_numpy(big).to(hip.torch_device)[:, 2:2 + k + 1, :V]
+    res = hip.spec_accept(view, torch.from_numpy(dft), torch.from_numpy(ids), torch.from_numpy(u), 0.8)
+    o = spec_accept(tgt, dft, ids, u, 0.8)
+    assert np.array_equal(res["accept_len"].cpu().numpy(), o["accept_len"])
+    assert np.array_equal(res["out_ids"].cpu().numpy(), o["out_ids"])

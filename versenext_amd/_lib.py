@@ -1,0 +1,97 @@
+"""ctypes binding of libvnx_hip.so (the C ABI declared in include/vnx.h).
+
+The library is loaded from this package directory only.  There is no
+fallback: if the library is missing or cannot be loaded, every GPU entry point
+raises RuntimeError naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "libvnx_hip.so")
+
+VNX_OK = 0
+VNX_ERR_INVALID_ARG = -1
+VNX_ERR_WORKSPACE = -2
+VNX_ERR_UNSUPPORTED = -3
+VNX_ERR_HIP = -4
+VNX_ERR_NO_DEVICE = -5
+
+VNX_F32 = 0
+VNX_BF16 = 1
+
+FLAG_NEAR_TIE = 1
+FLAG_LSE_EDGE = 2
+FLAG_CDF_EDGE = 4
+FLAG_ZERO_RESIDUAL = 8
+FLAG_BAD_ID = 16
+
+_c_i64 = ctypes.c_int64
+_c_sz = ctypes.c_size_t
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/vnx.h
+SIGNATURES = {
+    "vnx_version": (_int, []),
+    "vnx_status_string": (ctypes.c_char_p, [_int]),
+    "vnx_last_hip_error": (ctypes.c_char_p, []),
+    "vnx_init": (_int, [_int]),
+    "vnx_row_lse_workspace": (_c_sz, [_c_i64, _c_i64]),
+    "vnx_row_lse": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _f32, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "vnx_row_argmax": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_sz, _vp]),
+    "vnx_softmax_workspace": (_c_sz, [_c_i64, _c_i64]),
+    "vnx_softmax": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _f32, _vp, _vp, _c_i64, _vp, _c_sz, _vp]),
+    "vnx_spec_accept_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
+    "vnx_spec_accept": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                               _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "vnx_greedy_verify_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
+    "vnx_greedy_verify": (_int, [_vp, _int, _c_i64, _int, _int, _c_i64, _c_i64, _c_i64, _vp,
+                                 _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class VnxError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libvnx_hip.so (raises RuntimeError if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"vnx HIP library not found at {LIB_PATH}; build it with "
+                    "`python -m versenext_amd.build` (hipcc, gfx950)")
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = L
+    return _lib
+
+
+def check(status: int, what: str = "vnx call") -> None:
+    """Maps a vnx_status to the reference's error conventions
+    (ValueError for arguments, RuntimeError for the device; speculative.py:188-196,
+    device.py:371-378)."""
+    if status == VNX_OK:
+        return
+    L = lib()
+    text = L.vnx_status_string(status).decode()
+    if status in (VNX_ERR_INVALID_ARG, VNX_ERR_WORKSPACE, VNX_ERR_UNSUPPORTED):
+        raise ValueError(f"{what}: {text} (status {status})")
+    if status == VNX_ERR_HIP:
+        raise VnxError(f"{what}: {text}: {L.vnx_last_hip_error().decode()}")
+    raise VnxError(f"{what}: {text} (status {status})")

@@ -1,0 +1,128 @@
+// Library-level entry points: version, status text, device init, and the
+// host-side temperature check used by every kernel that scales logits.
+#include <math.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+
+#include "vnx_internal.h"
+
+namespace vnx {
+
+static thread_local char g_last_hip_error[256] = "";
+
+int hip_fail(hipError_t e) {
+  const char* s = hipGetErrorString(e);
+  strncpy(g_last_hip_error, s ? s : "unknown HIP error", sizeof(g_last_hip_error) - 1);
+  g_last_hip_error[sizeof(g_last_hip_error) - 1] = 0;
+  return VNX_ERR_HIP;
+}
+
+// True when q1 = RN(q0 + RN-exact(a - q0*T) * y), q0 = RN(a*y), y = RN(1/T),
+// equals RN(a/T) for every significand of a in [1, 2).  Scaling a by a power
+// of two scales every intermediate exactly (away from overflow/underflow), so
+// one binade covers all normal a; a = 0 and +-inf are exact by construction.
+static bool markstein_exact(float T) {
+  volatile float Tv = T;  // keep the host compiler from folding the loop
+  const float t = Tv;
+  const float y = 1.0f / t;
+  for (uint32_t m = 0; m < (1u << 23); ++m) {
+    uint32_t bits = (127u << 23) | m;
+    float a;
+    memcpy(&a, &bits, 4);
+    float q0 = a * y;
+    float r = fmaf(-q0, t, a);
+    float q1 = fmaf(r, y, q0);
+    float ref = a / t;
+    if (q1 != ref) return false;
+  }
+  return true;
+}
+
+Scale make_scale(float T) {
+  Scale s;
+  s.T = T;
+  s.y = 1.0f / T;
+  if (T == 1.0f) {
+    s.mode = 0;
+    return s;
+  }
+  static std::mutex mu;
+  static std::unordered_map<uint32_t, bool> cache;
+  uint32_t key;
+  memcpy(&key, &T, 4);
+  bool exact;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+      exact = it->second;
+    } else {
+      exact = markstein_exact(T);
+      cache.emplace(key, exact);
+    }
+  }
+  s.mode = exact ? 1 : 2;
+  return s;
+}
+
+__global__ void k_zero_u32(unsigned* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+int zero_counters(unsigned* p, int64_t n, hipStream_t st) {
+  if (n <= 0) return VNX_OK;
+  const int nt = 256;
+  hipLaunchKernelGGL(k_zero_u32, dim3((unsigned)((n + nt - 1) / nt)), dim3(nt), 0, st, p, n);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks) {
+  const int64_t target_wgs = 8192;
+  int64_t c = (target_wgs + rows - 1) / rows;
+  int64_t max_by_len = V / (256 * (int64_t)vec_elems);
+  if (max_by_len < 1) max_by_len = 1;
+  if (c > max_by_len) c = max_by_len;
+  if (c > max_chunks) c = max_chunks;
+  if (c < 1) c = 1;
+  return (int)c;
+}
+
+}  // namespace vnx
+
+extern "C" {
+
+int vnx_version(void) { return 100; }
+
+const char* vnx_status_string(int status) {
+  switch (status) {
+    case VNX_OK: return "ok";
+    case VNX_ERR_INVALID_ARG: return "invalid argument";
+    case VNX_ERR_WORKSPACE: return "workspace missing or too small";
+    case VNX_ERR_UNSUPPORTED: return "unsupported dtype or size";
+    case VNX_ERR_HIP: return "HIP runtime error";
+    case VNX_ERR_NO_DEVICE: return "no gfx950 device";
+    default: return "unknown status";
+  }
+}
+
+const char* vnx_last_hip_error(void) { return vnx::g_last_hip_error; }
+
+int vnx_init(int device) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return vnx::hip_fail(e);
+  if (device < 0 || device >= n) return VNX_ERR_NO_DEVICE;
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return vnx::hip_fail(e);
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return VNX_ERR_NO_DEVICE;
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return vnx::hip_fail(e);
+  return VNX_OK;
+}
+
+}  // extern "C"

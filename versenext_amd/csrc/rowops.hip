@@ -1,0 +1,242 @@
+// Vocab-row reductions: row LSE (+ max / argmax), row argmax, softmax.
+// Grid: one workgroup per (row, chunk); the last workgroup of a row merges
+// the chunk partials (fp64) and writes the row's outputs.
+#include "rowred.h"
+#include "vnx_internal.h"
+
+namespace vnx {
+
+constexpr int kNT = 256;
+constexpr int kNB = 8;
+
+struct RowParams {
+  const void* x;
+  int64_t rows, V, ld;
+  int chunks;
+  int64_t chunk_len;  // multiple of the vector width
+  Scale sc;
+  const float* thr;
+  double* lse;
+  float* rowmax;
+  int64_t* argmax;
+  float* part_m;
+  double* part_s;
+  float* part_v;
+  int64_t* part_i;
+  unsigned* counters;
+};
+
+template <typename Tin, bool LSE, bool ARGMAX>
+__global__ __launch_bounds__(kNT) void k_row_reduce(RowParams p) {
+  __shared__ ReduceLds lds;
+  __shared__ int last_flag;
+  const int64_t r = blockIdx.x / p.chunks;
+  const int c = blockIdx.x % p.chunks;
+  const Tin* row = static_cast<const Tin*>(p.x) + r * p.ld;
+  const int64_t c0 = (int64_t)c * p.chunk_len;
+  const int64_t c1 = c0 + p.chunk_len < p.V ? c0 + p.chunk_len : p.V;
+  const float thr = p.thr ? p.thr[r] : kNegInf;
+  ChunkResult cr = reduce_chunk<Tin, kNT, kNB, LSE, ARGMAX>(row, c0, c1, p.sc, thr, lds);
+  const int64_t slot = r * p.chunks + c;
+  if (threadIdx.x == 0) {
+    if constexpr (LSE) { st_agent(&p.part_m[slot], cr.m); st_agent(&p.part_s[slot], cr.s); }
+    if constexpr (ARGMAX) { st_agent(&p.part_v[slot], cr.av); st_agent(&p.part_i[slot], cr.ai); }
+  }
+  if (!arrive_last(&p.counters[r], (unsigned)p.chunks, &last_flag)) return;
+  if (threadIdx.x != 0) return;
+  if constexpr (LSE) {
+    float M = kNegInf;
+    double S = 0.0;
+    for (int j = 0; j < p.chunks; ++j)
+      merge_partial(M, S, ld_agent(&p.part_m[r * p.chunks + j]), ld_agent(&p.part_s[r * p.chunks + j]));
+    p.lse[r] = lse_of(M, S);
+    if (p.rowmax) p.rowmax[r] = M;
+  }
+  if constexpr (ARGMAX) {
+    float bv = kNegInf;
+    int64_t bi = INT64_MAX;
+    for (int j = 0; j < p.chunks; ++j) {
+      float v = ld_agent(&p.part_v[r * p.chunks + j]);
+      int64_t i = ld_agent(&p.part_i[r * p.chunks + j]);
+      if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    p.argmax[r] = bi;
+  }
+}
+
+// out = exp(a - M) / S with (M, S) of the row, fp32.
+template <typename Tin>
+__global__ __launch_bounds__(kNT) void k_softmax_write(const Tin* __restrict__ x, int64_t V, int64_t ld,
+                                                       Scale sc, const float* thr_p, const double* lse,
+                                                       float* __restrict__ out, int64_t ldo, int chunks,
+                                                       int64_t chunk_len) {
+  const int64_t r = blockIdx.x / chunks;
+  const int c = blockIdx.x % chunks;
+  const int64_t c0 = (int64_t)c * chunk_len;
+  const int64_t c1 = c0 + chunk_len < V ? c0 + chunk_len : V;
+  const float thr = thr_p ? thr_p[r] : kNegInf;
+  const double L = lse[r];
+  // exp(a - L) = exp(a - M) * exp(M - L): split L so the fp32 exponent is small.
+  const float M = (float)L;
+  const float corr = (float)exp((double)M - L);
+  const Tin* row = x + r * ld;
+  float* orow = out + r * ldo;
+  for (int64_t j = c0 + threadIdx.x; j < c1; j += kNT) {
+    float a = scale_logit(Vec<Tin>::load1(row + j), sc);
+    a = (a < thr) ? kNegInf : a;
+    orow[j] = (L == -__builtin_inf()) ? 0.0f : fast_exp(a - M) * corr;
+  }
+}
+
+static int row_common_check(const void* x, int dtype, int64_t rows, int64_t V, int64_t ld) {
+  if (!x || rows < 0 || V <= 0 || ld < V) return VNX_ERR_INVALID_ARG;
+  if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
+  const int ve = dtype == VNX_F32 ? 4 : 8;
+  if (!aligned16(x) || ld % ve != 0) return VNX_ERR_UNSUPPORTED;
+  return VNX_OK;
+}
+
+struct RowPlan {
+  int chunks;
+  int64_t chunk_len;
+};
+
+static RowPlan row_plan(int64_t rows, int64_t V, int dtype) {
+  const int ve = dtype == VNX_F32 ? 4 : 8;
+  RowPlan pl;
+  pl.chunks = pick_chunks(rows, V, ve, 64);
+  int64_t len = (V + pl.chunks - 1) / pl.chunks;
+  len = (len + ve - 1) / ve * ve;
+  pl.chunk_len = len;
+  pl.chunks = (int)((V + len - 1) / len);
+  return pl;
+}
+
+static size_t row_ws(int64_t rows, int64_t V, int dtype, RowParams*) {
+  RowPlan pl = row_plan(rows, V, dtype);
+  Carve cv(nullptr);
+  size_t n = (size_t)rows * pl.chunks;
+  cv.take<unsigned>(rows);
+  cv.take<float>(n);
+  cv.take<double>(n);
+  cv.take<float>(n);
+  cv.take<int64_t>(n);
+  return cv.bytes();
+}
+
+static void row_carve(void* ws, int64_t rows, const RowPlan& pl, RowParams& p) {
+  Carve cv(ws);
+  size_t n = (size_t)rows * pl.chunks;
+  p.counters = cv.take<unsigned>(rows);
+  p.part_m = cv.take<float>(n);
+  p.part_s = cv.take<double>(n);
+  p.part_v = cv.take<float>(n);
+  p.part_i = cv.take<int64_t>(n);
+}
+
+template <bool LSE, bool ARGMAX>
+static int launch_row_reduce(RowParams& p, int dtype, hipStream_t st) {
+  int zs = zero_counters(p.counters, p.rows, st);
+  if (zs) return zs;
+  dim3 grid((unsigned)(p.rows * p.chunks));
+  if (dtype == VNX_F32)
+    hipLaunchKernelGGL((k_row_reduce<float, LSE, ARGMAX>), grid, dim3(kNT), 0, st, p);
+  else
+    hipLaunchKernelGGL((k_row_reduce<__hip_bfloat16, LSE, ARGMAX>), grid, dim3(kNT), 0, st, p);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+}  // namespace vnx
+
+using namespace vnx;
+
+extern "C" {
+
+size_t vnx_row_lse_workspace(int64_t rows, int64_t V) {
+  if (rows <= 0 || V <= 0) return 256;
+  // Sized for the worse (fp32) plan; bf16 plans use fewer chunks.
+  return row_ws(rows, V, VNX_F32, nullptr);
+}
+
+int vnx_row_lse(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
+                float temperature, const float* thresholds, double* lse, float* rowmax,
+                int64_t* argmax, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = row_common_check(logits, dtype, rows, V, ld);
+  if (st) return st;
+  if (!lse || !(temperature > 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
+  if (rows == 0) return VNX_OK;
+  if (rows > (int64_t)1 << 24) return VNX_ERR_UNSUPPORTED;
+  RowPlan pl = row_plan(rows, V, dtype);
+  if (!workspace || workspace_bytes < row_ws(rows, V, dtype, nullptr)) return VNX_ERR_WORKSPACE;
+  RowParams p{};
+  p.x = logits; p.rows = rows; p.V = V; p.ld = ld;
+  p.chunks = pl.chunks; p.chunk_len = pl.chunk_len;
+  p.sc = make_scale(temperature);
+  p.thr = thresholds; p.lse = lse; p.rowmax = rowmax; p.argmax = argmax;
+  row_carve(workspace, rows, pl, p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (argmax) return launch_row_reduce<true, true>(p, dtype, s);
+  return launch_row_reduce<true, false>(p, dtype, s);
+}
+
+int vnx_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
+                   int64_t* argmax, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = row_common_check(logits, dtype, rows, V, ld);
+  if (st) return st;
+  if (!argmax) return VNX_ERR_INVALID_ARG;
+  if (rows == 0) return VNX_OK;
+  if (rows > (int64_t)1 << 24) return VNX_ERR_UNSUPPORTED;
+  RowPlan pl = row_plan(rows, V, dtype);
+  if (!workspace || workspace_bytes < row_ws(rows, V, dtype, nullptr)) return VNX_ERR_WORKSPACE;
+  RowParams p{};
+  p.x = logits; p.rows = rows; p.V = V; p.ld = ld;
+  p.chunks = pl.chunks; p.chunk_len = pl.chunk_len;
+  p.sc = make_scale(1.0f);
+  p.argmax = argmax;
+  row_carve(workspace, rows, pl, p);
+  return launch_row_reduce<false, true>(p, dtype, static_cast<hipStream_t>(stream));
+}
+
+int vnx_softmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
+                float temperature, const float* thresholds, float* out, int64_t ldo,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  int st = row_common_check(logits, dtype, rows, V, ld);
+  if (st) return st;
+  if (!out || ldo < V || !(temperature > 0.0f) || !__builtin_isfinite(temperature))
+    return VNX_ERR_INVALID_ARG;
+  if (rows == 0) return VNX_OK;
+  if (rows > (int64_t)1 << 24) return VNX_ERR_UNSUPPORTED;
+  RowPlan pl = row_plan(rows, V, dtype);
+  Carve cv(workspace);
+  double* lse = cv.take<double>(rows);
+  size_t need = cv.bytes() + row_ws(rows, V, dtype, nullptr);
+  if (!workspace || workspace_bytes < need) return VNX_ERR_WORKSPACE;
+  RowParams p{};
+  p.x = logits; p.rows = rows; p.V = V; p.ld = ld;
+  p.chunks = pl.chunks; p.chunk_len = pl.chunk_len;
+  p.sc = make_scale(temperature);
+  p.thr = thresholds; p.lse = lse;
+  row_carve(static_cast<char*>(workspace) + cv.bytes(), rows, pl, p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  st = launch_row_reduce<true, false>(p, dtype, s);
+  if (st) return st;
+  dim3 grid((unsigned)(rows * pl.chunks));
+  if (dtype == VNX_F32)
+    hipLaunchKernelGGL(k_softmax_write<float>, grid, dim3(kNT), 0, s, static_cast<const float*>(logits),
+                       V, ld, p.sc, thresholds, lse, out, ldo, pl.chunks, pl.chunk_len);
+  else
+    hipLaunchKernelGGL(k_softmax_write<__hip_bfloat16>, grid, dim3(kNT), 0, s,
+                       static_cast<const __hip_bfloat16*>(logits), V, ld, p.sc, thresholds, lse, out,
+                       ldo, pl.chunks, pl.chunk_len);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+size_t vnx_softmax_workspace(int64_t rows, int64_t V) {
+  Carve cv(nullptr);
+  cv.take<double>(rows > 0 ? rows : 1);
+  return cv.bytes() + vnx_row_lse_workspace(rows, V);
+}
+
+}  // extern "C"

@@ -1,0 +1,291 @@
+"""HipBackend: the "rocm" DeviceBackend, backed by libvnx_hip.so (gfx950 kernels).
+
+Interface parity with packages/verse_torch/verse_torch/backend_torch.py:246-379
+(`TorchBackend`): same constructor argument, `device_type` keeps the caller's
+prefix ("rocm" for "rocm:0"), `torch_device`, `from_numpy`, `to_numpy`, and
+the DeviceBackend operators.  Operators on the speculative-verification path
+(`softmax`, `row_lse`, `argmax`, `spec_accept`, `greedy_verify`) run the
+hand-written kernels; `matmul` / `linear` use PyTorch's rocBLAS GEMM and
+`layernorm` / `rmsnorm` / `rope` PyTorch elementwise ops (not on the hot path).
+
+Tensors: inputs may be torch tensors (any device; moved to this one) or
+numpy arrays; outputs are torch tensors on this device.  Kernels run on the
+current PyTorch stream of the device.  Each (device, stream) pair owns one
+zero-initialised workspace that the kernels leave zeroed after every call.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import numpy as np
+import torch
+
+from . import _lib
+from .device import DeviceBackend, _device_index, _parse_device, _to_torch_device_str
+
+
+def _to_tensor(x, device, dtype=None) -> torch.Tensor:
+    if isinstance(x, torch.Tensor):
+        t = x
+    elif isinstance(x, np.ndarray):
+        t = torch.from_numpy(np.ascontiguousarray(x))
+    elif hasattr(x, "data") and not isinstance(x, (list, tuple)):
+        return _to_tensor(x.data, device, dtype)  # verse_torch.Tensor-like objects
+    else:
+        t = torch.as_tensor(x)
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    if t.device != device:
+        t = t.to(device)
+    return t
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+_LOGIT_DTYPES = {torch.float32: _lib.VNX_F32, torch.bfloat16: _lib.VNX_BF16}
+
+
+class HipBackend(DeviceBackend):
+    def __init__(self, device: str = "rocm"):
+        self._device_str = str(device).lower()
+        if _parse_device(self._device_str) not in ("rocm", "cuda"):
+            raise RuntimeError(f"HipBackend serves rocm/cuda devices, got {device!r}")
+        if not torch.cuda.is_available():
+            raise RuntimeError(f"no ROCm GPU visible; device '{device}' is unavailable")
+        idx = _device_index(self._device_str)
+        self._torch_device = torch.device(_to_torch_device_str(self._device_str if ":" in self._device_str
+                                                               else self._device_str + f":{idx}"))
+        self._index = idx
+        L = _lib.lib()
+        with torch.cuda.device(idx):
+            _lib.check(L.vnx_init(idx), "vnx_init")
+        self._L = L
+        self._ws = {}
+        self._ws_lock = threading.Lock()
+
+    # ---- identity -------------------------------------------------------
+    @property
+    def device_type(self) -> str:
+        return self._device_str.split(":")[0]
+
+    @property
+    def torch_device(self):
+        return self._torch_device
+
+    @property
+    def torch_device_str(self) -> str:
+        return self._device_str
+
+    def from_numpy(self, x):
+        return _to_tensor(x, self._torch_device)
+
+    def to_numpy(self, t):
+        return t.detach().cpu().numpy() if isinstance(t, torch.Tensor) else np.asarray(t)
+
+    # ---- plumbing -------------------------------------------------------
+    def _stream(self):
+        return torch.cuda.current_stream(self._torch_device)
+
+    def _workspace(self, nbytes: int) -> torch.Tensor:
+        """Zeroed scratch for the current stream, grown on demand."""
+        st = self._stream().cuda_stream
+        with self._ws_lock:
+            buf = self._ws.get(st)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=self._torch_device)
+                self._ws[st] = buf
+            return buf
+
+    def _logits(self, x) -> torch.Tensor:
+        t = _to_tensor(x, self._torch_device)
+        if t.dtype not in _LOGIT_DTYPES:
+            t = t.to(torch.float32)
+        return t
+
+    @staticmethod
+    def _vec_ok(t: torch.Tensor) -> bool:
+        ve = 4 if t.dtype == torch.float32 else 8
+        if t.stride(-1) != 1 or t.data_ptr() % 16:
+            return False
+        return all(s % ve == 0 for s in t.stride()[:-1])
+
+    def _rows2d(self, x):
+        """(..., V) logits -> (rows, V) view with 16-byte aligned rows."""
+        t = self._logits(x)
+        V = t.shape[-1]
+        t2 = t.reshape(-1, V) if t.dim() != 2 else t
+        if not self._vec_ok(t2) or (t2.shape[0] > 1 and t2.stride(0) < V):
+            t2 = t2.contiguous()
+            if not self._vec_ok(t2):  # V not a multiple of the vector width: pad rows
+                ve = 4 if t2.dtype == torch.float32 else 8
+                ld = (V + ve - 1) // ve * ve
+                padded = torch.empty((t2.shape[0], ld), dtype=t2.dtype, device=t2.device)
+                padded[:, :V] = t2
+                t2 = padded[:, :V]
+        return t2
+
+    def _rows3d(self, x, nrows: int):
+        """(B, nrows, V) view usable with (ld, sb) strides."""
+        t = self._logits(x)
+        if t.dim() != 3 or t.shape[1] != nrows:
+            raise ValueError(f"expected logits of shape (B, {nrows}, V), got {tuple(t.shape)}")
+        V = t.shape[-1]
+        ok = self._vec_ok(t) and t.stride(1) >= V and t.stride(0) >= (nrows - 1) * t.stride(1) + V
+        if not ok:
+            t = t.contiguous()
+            if not self._vec_ok(t):
+                ve = 4 if t.dtype == torch.float32 else 8
+                ld = (V + ve - 1) // ve * ve
+                padded = torch.empty((t.shape[0], nrows, ld), dtype=t.dtype, device=t.device)
+                padded[..., :V] = t
+                t = padded[..., :V]
+        return t
+
+    # ---- DeviceBackend operators -------------------------------------------
+    def matmul(self, a, b):
+        return torch.matmul(_to_tensor(a, self._torch_device), _to_tensor(b, self._torch_device))
+
+    def linear(self, x, weight, bias=None):
+        x = _to_tensor(x, self._torch_device)
+        w = _to_tensor(weight, self._torch_device, x.dtype)
+        bb = None if bias is None else _to_tensor(bias, self._torch_device, x.dtype)
+        return torch.nn.functional.linear(x, w, bb)
+
+    def softmax(self, x, dim: int = -1, temperature: float = 1.0, thresholds=None):
+        t = self._logits(x)
+        moved = dim not in (-1, t.dim() - 1)
+        if moved:
+            t = t.movedim(dim, -1)
+        shape = t.shape
+        x2 = self._rows2d(t)
+        R, V = x2.shape
+        out = torch.empty((R, V), dtype=torch.float32, device=self._torch_device)
+        thr = None if thresholds is None else _to_tensor(thresholds, self._torch_device, torch.float32).contiguous()
+        ws = self._workspace(self._L.vnx_softmax_workspace(R, V))
+        _lib.check(self._L.vnx_softmax(_ptr(x2), _LOGIT_DTYPES[x2.dtype], R, V, x2.stride(0), float(temperature),
+                                       _ptr(thr), _ptr(out), V, _ptr(ws), ws.numel(),
+                                       ctypes.c_void_p(self._stream().cuda_stream)), "softmax")
+        out = out.reshape(shape)
+        return out.movedim(-1, dim) if moved else out
+
+    def layernorm(self, x, weight, bias, eps: float = 1e-5):
+        x = _to_tensor(x, self._torch_device)
+        w = _to_tensor(weight, self._torch_device, x.dtype)
+        bb = _to_tensor(bias, self._torch_device, x.dtype)
+        return torch.nn.functional.layer_norm(x, tuple(w.shape), w, bb, eps)
+
+    def rmsnorm(self, x, weight, eps: float = 1e-6):
+        x = _to_tensor(x, self._torch_device)
+        w = _to_tensor(weight, self._torch_device, x.dtype)
+        return x / torch.sqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * w
+
+    def rope(self, x, cos=None, sin=None):
+        if cos is None or sin is None:
+            return x
+        x = _to_tensor(x, self._torch_device)
+        cos = _to_tensor(cos, self._torch_device, x.dtype)
+        sin = _to_tensor(sin, self._torch_device, x.dtype)
+        d = x.shape[-1]
+        half = d // 2
+        x1, x2 = x[..., :half], x[..., half:]
+        cos_b = cos[..., :half] if cos.shape[-1] >= d else cos
+        sin_b = sin[..., :half] if sin.shape[-1] >= d else sin
+        return torch.cat([x1 * cos_b - x2 * sin_b, x1 * sin_b + x2 * cos_b], dim=-1)
+
+    # ---- verification operators -------------------------------------------
+    def row_lse(self, x, temperature: float = 1.0, thresholds=None, want_max: bool = False,
+                want_argmax: bool = False):
+        """Per-row log-sum-exp of RN(x / T) in fp64 (+ optional fp32 max, int64 raw argmax)."""
+        x2 = self._rows2d(x)
+        R, V = x2.shape
+        dev = self._torch_device
+        lse = torch.empty(R, dtype=torch.float64, device=dev)
+        mx = torch.empty(R, dtype=torch.float32, device=dev) if want_max else None
+        am = torch.empty(R, dtype=torch.int64, device=dev) if want_argmax else None
+        thr = None if thresholds is None else _to_tensor(thresholds, dev, torch.float32).contiguous()
+        ws = self._workspace(self._L.vnx_row_lse_workspace(R, V))
+        _lib.check(self._L.vnx_row_lse(_ptr(x2), _LOGIT_DTYPES[x2.dtype], R, V, x2.stride(0), float(temperature),
+                                       _ptr(thr), _ptr(lse), _ptr(mx), _ptr(am), _ptr(ws), ws.numel(),
+                                       ctypes.c_void_p(self._stream().cuda_stream)), "row_lse")
+        return lse, mx, am
+
+    def argmax(self, x) -> torch.Tensor:
+        """numpy.argmax over the last axis (first maximal index)."""
+        t = self._logits(x)
+        lead = t.shape[:-1]
+        x2 = self._rows2d(t)
+        R, V = x2.shape
+        am = torch.empty(R, dtype=torch.int64, device=self._torch_device)
+        ws = self._workspace(self._L.vnx_row_lse_workspace(R, V))
+        _lib.check(self._L.vnx_row_argmax(_ptr(x2), _LOGIT_DTYPES[x2.dtype], R, V, x2.stride(0), _ptr(am),
+                                          _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)),
+                   "argmax")
+        return am.reshape(lead)
+
+    def spec_accept(self, target, draft, draft_ids, uniforms, temperature: float = 1.0,
+                    thr_t=None, thr_d=None):
+        """Stochastic acceptance (see vnx_spec_accept in include/vnx.h).
+        target (B,k+1,V), draft (B,k,V) fp32/bf16; draft_ids (B,k); uniforms (B,k+1).
+        Returns dict of device tensors: accept_len (B,) int32, out_ids (B,k+1)
+        int64, flags (B,k+1) uint8, lse_t (B,k+1) f32, lse_d (B,k) f32."""
+        dev = self._torch_device
+        ids = _to_tensor(draft_ids, dev, torch.int64).contiguous()
+        if ids.dim() != 2:
+            raise ValueError("draft_ids must be (B, k)")
+        B, k = ids.shape
+        tg = self._rows3d(target, k + 1)
+        df = self._rows3d(draft, k)
+        if df.dtype != tg.dtype:
+            df = df.to(tg.dtype)
+        if tg.shape[0] != B or df.shape[0] != B or tg.shape[2] != df.shape[2]:
+            raise ValueError("target / draft / draft_ids shapes disagree")
+        V = tg.shape[2]
+        u = _to_tensor(uniforms, dev, torch.float32).contiguous()
+        if tuple(u.shape) != (B, k + 1):
+            raise ValueError(f"uniforms must be (B, k+1) = ({B}, {k + 1})")
+        tt = None if thr_t is None else _to_tensor(thr_t, dev, torch.float32).contiguous()
+        td = None if thr_d is None else _to_tensor(thr_d, dev, torch.float32).contiguous()
+        alen = torch.empty(B, dtype=torch.int32, device=dev)
+        out = torch.empty((B, k + 1), dtype=torch.int64, device=dev)
+        flags = torch.empty((B, k + 1), dtype=torch.uint8, device=dev)
+        lse_t = torch.empty((B, k + 1), dtype=torch.float32, device=dev)
+        lse_d = torch.empty((B, k), dtype=torch.float32, device=dev)
+        ws = self._workspace(self._L.vnx_spec_accept_workspace(B, k, V))
+        _lib.check(self._L.vnx_spec_accept(
+            _ptr(tg), _ptr(df), _LOGIT_DTYPES[tg.dtype], B, k, V,
+            tg.stride(1), tg.stride(0), df.stride(1), df.stride(0),
+            _ptr(ids), _ptr(u), float(temperature), _ptr(tt), _ptr(td),
+            _ptr(alen), _ptr(out), _ptr(flags), _ptr(lse_t), _ptr(lse_d),
+            _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "spec_accept")
+        return dict(accept_len=alen, out_ids=out, flags=flags, lse_t=lse_t, lse_d=lse_d)
+
+    def greedy_verify(self, target, draft_ids, rows_t: int | None = None):
+        """Greedy verify of every batch row (see vnx_greedy_verify).
+        target (B, rows_t, V) (may be a strided slice of (B, T, V) logits).
+        Returns (accepted (B,k) bool, main_pred (B,rows_t), accept_len (B,), out_ids (B,k+1))."""
+        dev = self._torch_device
+        ids = _to_tensor(draft_ids, dev, torch.int64).contiguous()
+        if ids.dim() != 2:
+            raise ValueError("draft_ids must be (B, k)")
+        B, k = ids.shape
+        rows_t = k if rows_t is None else int(rows_t)
+        tg = self._rows3d(target, rows_t)
+        if tg.shape[0] != B:
+            raise ValueError(f"batch mismatch: logits {tg.shape[0]} vs draft {B}")
+        V = tg.shape[2]
+        acc = torch.empty((B, k), dtype=torch.uint8, device=dev)
+        pred = torch.empty((B, rows_t), dtype=torch.int64, device=dev)
+        alen = torch.empty(B, dtype=torch.int32, device=dev)
+        out = torch.empty((B, k + 1), dtype=torch.int64, device=dev)
+        ws = self._workspace(self._L.vnx_greedy_verify_workspace(B, rows_t, V))
+        _lib.check(self._L.vnx_greedy_verify(
+            _ptr(tg), _LOGIT_DTYPES[tg.dtype], B, k, rows_t, V, tg.stride(1), tg.stride(0), _ptr(ids),
+            _ptr(acc), _ptr(pred), _ptr(alen), _ptr(out), _ptr(ws), ws.numel(),
+            ctypes.c_void_p(self._stream().cuda_stream)), "greedy_verify")
+        return acc.bool(), pred, alen, out
+
+
+__all__ = ["HipBackend"]
