@@ -138,7 +138,7 @@ def main():
                    "logits": "fp32 target N(0,2), draft = target + N(0,0.5)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_spec_pass1 + k_spec_pass2 (one vnx_spec_accept call)",
+                     "kernel": "k_spec_lse + k_spec_accept + k_spec_mass + k_spec_draw (one vnx_spec_accept call)",
                      "bytes_per_launch": nbytes, "event_ms_mean": round(mean_ms, 4),
                      "event_ms_min": round(float(np.min(ms)), 4), "event_ms_median": round(float(np.median(ms)), 4)},
         "emitted_tokens_per_s": round(emitted / (mean_ms * 1e-3), 1),

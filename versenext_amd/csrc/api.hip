@@ -1,6 +1,7 @@
 // Library-level entry points: version, status text, device init, and the
 // host-side temperature check used by every kernel that scales logits.
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -40,14 +41,10 @@ static bool markstein_exact(float T) {
   return true;
 }
 
-Scale make_scale(float T) {
-  Scale s;
-  s.T = T;
-  s.y = 1.0f / T;
-  if (T == 1.0f) {
-    s.mode = 0;
-    return s;
-  }
+int make_scale(float T, TScale* out) {
+  out->T = T;
+  out->y = 1.0f / T;
+  if (T == 1.0f) return SM_ID;
   static std::mutex mu;
   static std::unordered_map<uint32_t, bool> cache;
   uint32_t key;
@@ -63,8 +60,7 @@ Scale make_scale(float T) {
       cache.emplace(key, exact);
     }
   }
-  s.mode = exact ? 1 : 2;
-  return s;
+  return exact ? SM_MARK : SM_DIV;
 }
 
 __global__ void k_zero_u32(unsigned* p, int64_t n) {
@@ -80,8 +76,33 @@ int zero_counters(unsigned* p, int64_t n, hipStream_t st) {
   return VNX_OK;
 }
 
-int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks) {
-  const int64_t target_wgs = 8192;
+int device_cus() {
+  static std::mutex mu;
+  static std::unordered_map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> g(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cache.emplace(dev, n);
+  return n;
+}
+
+// VNX_WG_SCALE (a percentage, read once) scales every launch's workgroup
+// target for tuning sweeps; the default is 100.
+int64_t wg_scale_pct() {
+  static const int64_t t = [] {
+    const char* e = getenv("VNX_WG_SCALE");
+    const long long v = e ? atoll(e) : 0;
+    return (int64_t)(v >= 1 && v <= 10000 ? v : 100);
+  }();
+  return t;
+}
+
+int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks, int64_t target_wgs) {
+  target_wgs = target_wgs * wg_scale_pct() / 100;
   int64_t c = (target_wgs + rows - 1) / rows;
   int64_t max_by_len = V / (256 * (int64_t)vec_elems);
   if (max_by_len < 1) max_by_len = 1;

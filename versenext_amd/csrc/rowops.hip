@@ -14,7 +14,7 @@ struct RowParams {
   int64_t rows, V, ld;
   int chunks;
   int64_t chunk_len;  // multiple of the vector width
-  Scale sc;
+  TScale sc;
   const float* thr;
   double* lse;
   float* rowmax;
@@ -26,7 +26,7 @@ struct RowParams {
   unsigned* counters;
 };
 
-template <typename Tin, bool LSE, bool ARGMAX>
+template <typename Tin, int SM, bool THR, bool LSE, bool ARGMAX>
 __global__ __launch_bounds__(kNT) void k_row_reduce(RowParams p) {
   __shared__ ReduceLds lds;
   __shared__ int last_flag;
@@ -35,56 +35,66 @@ __global__ __launch_bounds__(kNT) void k_row_reduce(RowParams p) {
   const Tin* row = static_cast<const Tin*>(p.x) + r * p.ld;
   const int64_t c0 = (int64_t)c * p.chunk_len;
   const int64_t c1 = c0 + p.chunk_len < p.V ? c0 + p.chunk_len : p.V;
-  const float thr = p.thr ? p.thr[r] : kNegInf;
-  ChunkResult cr = reduce_chunk<Tin, kNT, kNB, LSE, ARGMAX>(row, c0, c1, p.sc, thr, lds);
+  const float thr = (THR && p.thr) ? p.thr[r] : kNegInf;
+  ChunkResult cr = reduce_chunk<Tin, SM, THR, LSE, ARGMAX, kNT, kNB>(row, c0, c1, p.sc, thr, lds);
   const int64_t slot = r * p.chunks + c;
   if (threadIdx.x == 0) {
     if constexpr (LSE) { st_agent(&p.part_m[slot], cr.m); st_agent(&p.part_s[slot], cr.s); }
     if constexpr (ARGMAX) { st_agent(&p.part_v[slot], cr.av); st_agent(&p.part_i[slot], cr.ai); }
   }
   if (!arrive_last(&p.counters[r], (unsigned)p.chunks, &last_flag)) return;
+  // Last workgroup of row r: the chunk partials go to LDS with one coherent
+  // load per thread (chunks <= kNT), then thread 0 merges them in order.
+  __shared__ float t_m[kNT], t_v[kNT];
+  __shared__ double t_s[kNT];
+  __shared__ int64_t t_i[kNT];
+  const int j = threadIdx.x;
+  if (j < p.chunks) {
+    if constexpr (LSE) { t_m[j] = ld_agent(&p.part_m[slot - c + j]); t_s[j] = ld_agent(&p.part_s[slot - c + j]); }
+    if constexpr (ARGMAX) { t_v[j] = ld_agent(&p.part_v[slot - c + j]); t_i[j] = ld_agent(&p.part_i[slot - c + j]); }
+  }
+  __syncthreads();
   if (threadIdx.x != 0) return;
   if constexpr (LSE) {
     float M = kNegInf;
     double S = 0.0;
-    for (int j = 0; j < p.chunks; ++j)
-      merge_partial(M, S, ld_agent(&p.part_m[r * p.chunks + j]), ld_agent(&p.part_s[r * p.chunks + j]));
+    for (int q = 0; q < p.chunks; ++q) merge_partial(M, S, t_m[q], t_s[q]);
     p.lse[r] = lse_of(M, S);
     if (p.rowmax) p.rowmax[r] = M;
   }
   if constexpr (ARGMAX) {
     float bv = kNegInf;
     int64_t bi = INT64_MAX;
-    for (int j = 0; j < p.chunks; ++j) {
-      float v = ld_agent(&p.part_v[r * p.chunks + j]);
-      int64_t i = ld_agent(&p.part_i[r * p.chunks + j]);
-      if (argmax_better(v, i, bv, bi)) { bv = v; bi = i; }
-    }
+    for (int q = 0; q < p.chunks; ++q)
+      if (argmax_better(t_v[q], t_i[q], bv, bi)) { bv = t_v[q]; bi = t_i[q]; }
     p.argmax[r] = bi;
   }
 }
 
-// out = exp(a - M) / S with (M, S) of the row, fp32.
-template <typename Tin>
+// out = exp(a - L) in fp32, L the row LSE: the exponent a*log2(e) - L*log2(e)
+// is formed with both products split into hi + lo parts.
+template <typename Tin, int SM, bool THR>
 __global__ __launch_bounds__(kNT) void k_softmax_write(const Tin* __restrict__ x, int64_t V, int64_t ld,
-                                                       Scale sc, const float* thr_p, const double* lse,
+                                                       TScale sc, const float* thr_p, const double* lse,
                                                        float* __restrict__ out, int64_t ldo, int chunks,
                                                        int64_t chunk_len) {
   const int64_t r = blockIdx.x / chunks;
   const int c = blockIdx.x % chunks;
   const int64_t c0 = (int64_t)c * chunk_len;
   const int64_t c1 = c0 + chunk_len < V ? c0 + chunk_len : V;
-  const float thr = thr_p ? thr_p[r] : kNegInf;
+  const float thr = (THR && thr_p) ? thr_p[r] : kNegInf;
   const double L = lse[r];
-  // exp(a - L) = exp(a - M) * exp(M - L): split L so the fp32 exponent is small.
-  const float M = (float)L;
-  const float corr = (float)exp((double)M - L);
+  const double Lt = L * 1.4426950408889634074;
+  const float hi = (float)Lt;
+  const float lo = (float)(Lt - (double)hi);
+  const bool finite = __builtin_isfinite(L);
   const Tin* row = x + r * ld;
   float* orow = out + r * ldo;
   for (int64_t j = c0 + threadIdx.x; j < c1; j += kNT) {
-    float a = scale_logit(Vec<Tin>::load1(row + j), sc);
-    a = (a < thr) ? kNegInf : a;
-    orow[j] = (L == -__builtin_inf()) ? 0.0f : fast_exp(a - M) * corr;
+    const float a = scaled<SM, THR>(Vec<Tin>::load1(row + j), sc, thr);
+    float t = __builtin_fmaf(a, kL2eHi, -hi);
+    t = __builtin_fmaf(a, kL2eLo, t) - lo;
+    orow[j] = finite ? __builtin_amdgcn_exp2f(t) : (L == -__builtin_inf() ? 0.0f : __builtin_nanf(""));
   }
 }
 
@@ -104,7 +114,7 @@ struct RowPlan {
 static RowPlan row_plan(int64_t rows, int64_t V, int dtype) {
   const int ve = dtype == VNX_F32 ? 4 : 8;
   RowPlan pl;
-  pl.chunks = pick_chunks(rows, V, ve, 64);
+  pl.chunks = pick_chunks(rows, V, ve, 64, 2048);
   int64_t len = (V + pl.chunks - 1) / pl.chunks;
   len = (len + ve - 1) / ve * ve;
   pl.chunk_len = len;
@@ -135,16 +145,17 @@ static void row_carve(void* ws, int64_t rows, const RowPlan& pl, RowParams& p) {
 }
 
 template <bool LSE, bool ARGMAX>
-static int launch_row_reduce(RowParams& p, int dtype, hipStream_t st) {
+static int launch_row_reduce(RowParams& p, int dtype, int sm, hipStream_t st) {
   int zs = zero_counters(p.counters, p.rows, st);
   if (zs) return zs;
   dim3 grid((unsigned)(p.rows * p.chunks));
-  if (dtype == VNX_F32)
-    hipLaunchKernelGGL((k_row_reduce<float, LSE, ARGMAX>), grid, dim3(kNT), 0, st, p);
-  else
-    hipLaunchKernelGGL((k_row_reduce<__hip_bfloat16, LSE, ARGMAX>), grid, dim3(kNT), 0, st, p);
-  VNX_LAUNCH_CHECK();
-  return VNX_OK;
+  return dispatch_tsm(dtype, sm, p.thr != nullptr, [&](auto tin, auto smc, auto thrc) {
+    using Tin = decltype(tin);
+    hipLaunchKernelGGL((k_row_reduce<Tin, decltype(smc)::value, decltype(thrc)::value, LSE, ARGMAX>), grid,
+                       dim3(kNT), 0, st, p);
+    VNX_LAUNCH_CHECK();
+    return (int)VNX_OK;
+  });
 }
 
 }  // namespace vnx
@@ -172,12 +183,12 @@ int vnx_row_lse(const void* logits, int dtype, int64_t rows, int64_t V, int64_t 
   RowParams p{};
   p.x = logits; p.rows = rows; p.V = V; p.ld = ld;
   p.chunks = pl.chunks; p.chunk_len = pl.chunk_len;
-  p.sc = make_scale(temperature);
+  const int sm = make_scale(temperature, &p.sc);
   p.thr = thresholds; p.lse = lse; p.rowmax = rowmax; p.argmax = argmax;
   row_carve(workspace, rows, pl, p);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (argmax) return launch_row_reduce<true, true>(p, dtype, s);
-  return launch_row_reduce<true, false>(p, dtype, s);
+  if (argmax) return launch_row_reduce<true, true>(p, dtype, sm, s);
+  return launch_row_reduce<true, false>(p, dtype, sm, s);
 }
 
 int vnx_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
@@ -192,10 +203,10 @@ int vnx_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64
   RowParams p{};
   p.x = logits; p.rows = rows; p.V = V; p.ld = ld;
   p.chunks = pl.chunks; p.chunk_len = pl.chunk_len;
-  p.sc = make_scale(1.0f);
+  const int sm = make_scale(1.0f, &p.sc);
   p.argmax = argmax;
   row_carve(workspace, rows, pl, p);
-  return launch_row_reduce<false, true>(p, dtype, static_cast<hipStream_t>(stream));
+  return launch_row_reduce<false, true>(p, dtype, sm, static_cast<hipStream_t>(stream));
 }
 
 int vnx_softmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld,
@@ -215,22 +226,21 @@ int vnx_softmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t 
   RowParams p{};
   p.x = logits; p.rows = rows; p.V = V; p.ld = ld;
   p.chunks = pl.chunks; p.chunk_len = pl.chunk_len;
-  p.sc = make_scale(temperature);
+  const int sm = make_scale(temperature, &p.sc);
   p.thr = thresholds; p.lse = lse;
   row_carve(static_cast<char*>(workspace) + cv.bytes(), rows, pl, p);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  st = launch_row_reduce<true, false>(p, dtype, s);
+  st = launch_row_reduce<true, false>(p, dtype, sm, s);
   if (st) return st;
   dim3 grid((unsigned)(rows * pl.chunks));
-  if (dtype == VNX_F32)
-    hipLaunchKernelGGL(k_softmax_write<float>, grid, dim3(kNT), 0, s, static_cast<const float*>(logits),
-                       V, ld, p.sc, thresholds, lse, out, ldo, pl.chunks, pl.chunk_len);
-  else
-    hipLaunchKernelGGL(k_softmax_write<__hip_bfloat16>, grid, dim3(kNT), 0, s,
-                       static_cast<const __hip_bfloat16*>(logits), V, ld, p.sc, thresholds, lse, out,
-                       ldo, pl.chunks, pl.chunk_len);
-  VNX_LAUNCH_CHECK();
-  return VNX_OK;
+  return dispatch_tsm(dtype, sm, thresholds != nullptr, [&](auto tin, auto smc, auto thrc) {
+    using Tin = decltype(tin);
+    hipLaunchKernelGGL((k_softmax_write<Tin, decltype(smc)::value, decltype(thrc)::value>), grid, dim3(kNT), 0,
+                       s, static_cast<const Tin*>(logits), V, ld, p.sc, thresholds, lse, out, ldo, pl.chunks,
+                       pl.chunk_len);
+    VNX_LAUNCH_CHECK();
+    return (int)VNX_OK;
+  });
 }
 
 size_t vnx_softmax_workspace(int64_t rows, int64_t V) {

@@ -28,29 +28,52 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr float kNegInf = -__builtin_inff();
 
 // ---------------------------------------------------------------------------
-// Temperature scaling: a = RN(l / T).
-// mode 0: T == 1 (identity); mode 1: Markstein correction step
-//   q0 = RN(l*y), r = l - q0*T (exact through fma), q1 = RN(q0 + r*y)
-// with y = RN(1/T); the host only selects mode 1 after checking every fp32
-// significand against true division for this T (vnx_host.cpp); mode 2: IEEE
-// division by the compiler's correctly rounded sequence.
+// Temperature scaling: a = RN(l / T), the value numpy gives for float32
+// `logits / temperature`.  The scaling mode is a template parameter so the
+// streaming loops carry no per-element branch:
+//   SM_ID   T == 1: a = l;
+//   SM_MARK Markstein correction step, y = RN(1/T):
+//             q0 = RN(l*y), r = l - q0*T (exact through fma), a = RN(q0 + r*y);
+//           the host selects it only after checking that it equals RN(l/T)
+//           for every fp32 significand with this T (api.hip).  r is NaN when
+//           l (or q0) is infinite; clamping r to +-FLT_MAX keeps a = q0 there,
+//           with one min and one max instead of a compare and select;
+//   SM_DIV  IEEE division (compiler's correctly rounded sequence).
 // ---------------------------------------------------------------------------
-struct Scale {
-  float T;
-  float y;
-  int mode;
+enum ScaleMode { SM_ID = 0, SM_MARK = 1, SM_DIV = 2 };
+
+struct TScale {
+  float T;  // temperature
+  float y;  // RN(1 / T)
 };
 
-__device__ __forceinline__ float scale_logit(float l, const Scale& s) {
-  if (s.mode == 0) return l;
-  if (s.mode == 1) {
-    float q0 = l * s.y;
+template <int SM>
+__device__ __forceinline__ float tscale(float l, const TScale& s) {
+  if constexpr (SM == SM_ID) {
+    return l;
+  } else if constexpr (SM == SM_MARK) {
+    const float q0 = l * s.y;
     float r = __builtin_fmaf(-q0, s.T, l);
-    float q1 = __builtin_fmaf(r, s.y, q0);
-    return __builtin_isfinite(q0) ? q1 : q0;
+    r = __builtin_fminf(__builtin_fmaxf(r, -3.40282347e38f), 3.40282347e38f);
+    return __builtin_fmaf(r, s.y, q0);
+  } else {
+    return l / s.T;
   }
-  return l / s.T;
 }
+
+// Scaled logit with the top-k mask (values below thr become -inf).
+template <int SM, bool THR>
+__device__ __forceinline__ float scaled(float l, const TScale& s, float thr) {
+  const float a = tscale<SM>(l, s);
+  if constexpr (THR) return (a < thr) ? -__builtin_inff() : a;
+  return a;
+}
+
+// log2(e) split for the compensated exponent of the LSE sums:
+// kL2eHi = RN32(log2 e), kL2eLo = RN32(log2 e - kL2eHi).
+constexpr float kL2eHi = 0x1.715476p+0f;
+constexpr float kL2eLo = 0x1.4ae0c0p-26f;
+constexpr double kLn2 = 0x1.62e42fefa39efp-1;
 
 // ---------------------------------------------------------------------------
 // Canonical exp (Cody-Waite reduction by ln2 + degree-7 Taylor polynomial).
@@ -70,10 +93,12 @@ __host__ __device__ __forceinline__ float vnx_exp_canon(float t) {
   const float c4 = 0x1.555556p-5f;        // 1/24,   0x3D2AAAAB
   const float c3 = 0x1.555556p-3f;        // 1/6,    0x3E2AAAAB
   const float c2 = 0x1p-1f;
-  if (!(t >= -86.5f)) return 0.0f;
-  if (t > 88.0f) t = 88.0f;
-  float kf = __builtin_rintf(t * kLog2e);
-  float r = __builtin_fmaf(-kf, kLn2Hi, t);
+  // Evaluated on t clamped into [-86.5, 88] and replaced by 0 for t < -86.5
+  // (and NaN) at the end: the same value as the early-return form, without a
+  // divergent branch per element.
+  const float tc = __builtin_fminf(__builtin_fmaxf(t, -86.5f), 88.0f);
+  float kf = __builtin_rintf(tc * kLog2e);
+  float r = __builtin_fmaf(-kf, kLn2Hi, tc);
   r = __builtin_fmaf(-kf, kLn2Lo, r);
   float p = c7;
   p = __builtin_fmaf(p, r, c6);
@@ -85,13 +110,8 @@ __host__ __device__ __forceinline__ float vnx_exp_canon(float t) {
   p = __builtin_fmaf(p, r, 1.0f);
   int k = (int)kf;
   float two_k = __uint_as_float((uint32_t)(k + 127) << 23);
-  return p * two_k;
-}
-
-// Fast exp for sums that are only accumulated (pass-1 log-sum-exp): one
-// v_exp_f32 on (x * log2 e).  Rounding noise averages out in the fp64 sum.
-__device__ __forceinline__ float fast_exp(float x) {
-  return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f);
+  const float e = p * two_k;
+  return (t >= -86.5f) ? e : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -168,6 +188,17 @@ __device__ __forceinline__ void block_argmax(float& v, int64_t& i, float* ldsv, 
 #pragma unroll
   for (int j = 1; j < NW; ++j)
     if (argmax_better(ldsv[j], ldsi[j], v, i)) { v = ldsv[j]; i = ldsi[j]; }
+}
+
+// Inclusive scan of one double per lane across the wave (lane order).
+__device__ __forceinline__ double wave_inclusive_scan(double v) {
+  const int l = threadIdx.x % VNX_WAVE;
+#pragma unroll
+  for (int o = 1; o < VNX_WAVE; o <<= 1) {
+    const double n = __shfl_up(v, o, VNX_WAVE);
+    if (l >= o) v += n;
+  }
+  return v;
 }
 
 // Inclusive scan of one double per thread across the block (NT threads).

@@ -22,10 +22,33 @@ int hip_fail(hipError_t e);
 // Checks the launch that was just enqueued.
 #define VNX_LAUNCH_CHECK() VNX_HIP_CHECK(hipGetLastError())
 
-// Builds the temperature-scaling descriptor for T > 0 (see scale_logit):
-// mode 0 for T == 1, mode 1 when the Markstein step is exact for every fp32
-// significand with this T (checked once per T on the host), else mode 2.
-Scale make_scale(float T);
+// Fills the temperature-scaling descriptor for T > 0 and returns the scaling
+// mode (tscale): SM_ID for T == 1, SM_MARK when the Markstein step equals
+// RN(l/T) for every fp32 significand with this T (checked once per T on the
+// host and cached), else SM_DIV.
+int make_scale(float T, TScale* out);
+
+template <int V>
+struct IntC { static constexpr int value = V; };
+template <bool V>
+struct BoolC { static constexpr bool value = V; };
+
+// Calls f(Tin{}, IntC<SM>{}, BoolC<THR>{}) for the runtime (dtype, mode, thr).
+template <typename F>
+int dispatch_tsm(int dtype, int sm, bool thr, F&& f) {
+  auto by_thr = [&](auto tin, auto smc) {
+    return thr ? f(tin, smc, BoolC<true>{}) : f(tin, smc, BoolC<false>{});
+  };
+  auto by_sm = [&](auto tin) {
+    switch (sm) {
+      case SM_ID: return by_thr(tin, IntC<SM_ID>{});
+      case SM_MARK: return by_thr(tin, IntC<SM_MARK>{});
+      default: return by_thr(tin, IntC<SM_DIV>{});
+    }
+  };
+  if (dtype == VNX_F32) return by_sm(float{});
+  return by_sm(__hip_bfloat16{});
+}
 
 // Bump allocator over a caller-provided workspace (256-byte aligned slices).
 struct Carve {
@@ -49,8 +72,27 @@ inline int elem_size(int dtype) { return dtype == VNX_F32 ? 4 : 2; }
 // stays valid inside captured HIP graphs).
 int zero_counters(unsigned* p, int64_t n, hipStream_t st);
 
-// Chunks per row for the streaming row kernels: enough workgroups to cover
-// every CU several times, chunks no shorter than one 256-thread x 16-byte pass.
-int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks);
+// Compute units of the current device (cached per device ordinal).
+int device_cus();
+
+// Percentage applied to every launch's workgroup target (VNX_WG_SCALE,
+// default 100; a tuning knob read once).
+int64_t wg_scale_pct();
+
+// Chunks per row for the streaming row kernels: about target_wgs workgroups
+// in the launch, chunks no shorter than one 256-thread x 16-byte pass, at most
+// max_chunks per row.
+int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks, int64_t target_wgs);
+
+// Rows (b, i), i < nrows, at x + b*sb + i*ld must not overlap inside a batch
+// row (ld >= V) and batch rows must not overlap (sb >= (nrows-1)*ld + V);
+// 16-byte vector loads need x, ld and sb aligned to the vector width.
+inline int check_rows(const void* x, int dtype, int64_t ld, int64_t sb, int nrows, int64_t V) {
+  if (!x) return VNX_ERR_INVALID_ARG;
+  if (ld < V || sb < (int64_t)(nrows - 1) * ld + V) return VNX_ERR_INVALID_ARG;
+  const int ve = dtype == VNX_F32 ? 4 : 8;
+  if (!aligned16(x) || ld % ve != 0 || sb % ve != 0) return VNX_ERR_UNSUPPORTED;
+  return VNX_OK;
+}
 
 }  // namespace vnx
