@@ -8,14 +8,21 @@ are resident in HBM before the timed region.
 value = algorithmic bytes per step / mean step time, with
   bytes = 4*V*[B*(2k+1) + sum_b r_b], r_b = 2 if row b rejects (p_n and q_n
   re-read by the residual draw) else 1 (p_k re-read by the bonus draw).
-The CPU baseline is the numpy/C checker (oracle/) on the same workload,
-timed on the host's cores (threads over batch rows).
+roofline = the dominant kernel, k_spec_lse (the one-pass row LSE over all
+  B*(2k+1) rows): algorithmic bytes 4*V*B*(2k+1) per launch / its mean launch
+  time, timed with HIP events the library records on the launch stream
+  (vnx_profile_begin / vnx_profile_end).  traffic = HBM bytes per launch from
+  the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, when present.
+The CPU baseline is the numpy/C checker (oracle/) on a bounded sample of the
+same workload, timed on the host's cores (threads over batch rows).
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -25,6 +32,8 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 B, K, V, T = 64, 8, 248320, 0.8
+PHASES = ("k_spec_lse", "k_spec_accept", "k_spec_mass", "k_spec_draw")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_spec_lse_config2_pmc.md")
 
 
 def make_inputs_gpu(device):
@@ -44,8 +53,23 @@ def algorithmic_bytes(accept_len):
     return 4 * V * (B * (2 * K + 1) + r)
 
 
-def cpu_baseline(tgt, dft, ids, u, budget_s: float = 20.0):
-    """Times the CPU checker on the same workload; threads over batch rows."""
+LSE_BYTES = 4 * V * B * (2 * K + 1)
+
+
+def traffic_from_profile():
+    """HBM bytes per k_spec_lse launch from the committed PMC summary (the line
+    `traffic_bytes_per_launch: N`), or None."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(tgt, dft, ids, u, budget_s: float = 12.0):
+    """Times the CPU checker on a bounded sample: whole config-2 batches, rows
+    split over the host's cores, repeated until about budget_s of CPU work."""
     import numpy as np
     from concurrent.futures import ThreadPoolExecutor
     from oracle.speculative import spec_accept
@@ -67,12 +91,12 @@ def cpu_baseline(tgt, dft, ids, u, budget_s: float = 20.0):
         total_t += dt
         total_bytes += algorithmic_bytes(alen)
         reps += 1
-        if total_t > budget_s or reps >= 3:
+        if total_t > budget_s or reps >= 200:
             break
     return dict(value=round(total_bytes / total_t / 1e9, 3), unit="GB/s", cores=cores, kind="port",
-                sample=f"full config-2 batch (B={B}, k={K}, V={V}) x{reps} through oracle.speculative."
+                sample=f"{reps} full config-2 batches (B={B}, k={K}, V={V}) through oracle.speculative."
                        f"spec_accept (numpy fp64 LSE + C canonical draw), {cores} threads over batch rows; "
-                       f"{total_t / reps:.2f} s per batch")
+                       f"{total_t / reps:.3f} s per batch")
 
 
 def main():
@@ -81,6 +105,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
@@ -90,6 +116,7 @@ def main():
     import numpy as np
     import torch
     from versenext_amd import get_backend
+    from versenext_amd import _lib
 
     hip = get_backend("rocm:0")
     dev = hip.torch_device
@@ -113,12 +140,34 @@ def main():
         e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # Per-kernel times from a second pass of the same steps with the library's
+    # phase events (kept out of the timed pass above).
+    L = _lib.lib()
+    _lib.check(L.vnx_profile_begin(args.steps), "vnx_profile_begin")
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    phase = (ctypes.c_double * len(PHASES))()
+    ncalls = ctypes.c_int(0)
+    _lib.check(L.vnx_profile_end(ctypes.cast(phase, ctypes.c_void_p), len(PHASES),
+                                 ctypes.cast(ctypes.pointer(ncalls), ctypes.c_void_p)), "vnx_profile_end")
+    phase_ms = {name: float(phase[i]) / max(1, ncalls.value) for i, name in enumerate(PHASES)}
     ms = [e0.elapsed_time(e1) for e0, e1 in evs]
     alen = res["accept_len"].cpu().numpy()
     nbytes = algorithmic_bytes(alen)
     mean_ms = float(np.mean(ms))
     gbs = nbytes / (mean_ms * 1e-3) / 1e9
+    lse_gbs = LSE_BYTES / (phase_ms["k_spec_lse"] * 1e-3) / 1e9
     emitted = int(alen.sum()) + B
+
+    if args.calib_copy:
+        n = 1 << 28  # 1 GiB of fp32
+        src = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     out = {
         "metric": "accept-kernel HBM GB/s",
@@ -135,15 +184,21 @@ def main():
         "data": "synthetic",
         "config": {"workload": "BASELINE config 2: fused stochastic acceptance (vnx_spec_accept)",
                    "batch": B, "k": K, "vocab": V, "temperature": T, "top_k": None,
-                   "logits": "fp32 target N(0,2), draft = target + N(0,0.5)"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_spec_lse + k_spec_accept + k_spec_mass + k_spec_draw (one vnx_spec_accept call)",
-                     "bytes_per_launch": nbytes, "event_ms_mean": round(mean_ms, 4),
-                     "event_ms_min": round(float(np.min(ms)), 4), "event_ms_median": round(float(np.median(ms)), 4)},
+                   "logits": "fp32 target N(0,2), draft = target + N(0,0.5)",
+                   "bytes_per_step": nbytes, "event_ms_mean": round(mean_ms, 4),
+                   "event_ms_min": round(float(np.min(ms)), 4),
+                   "event_ms_median": round(float(np.median(ms)), 4),
+                   "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(lse_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(lse_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "kernel": "k_spec_lse", "bytes_per_launch": LSE_BYTES,
+                     "launch_ms_mean": round(phase_ms["k_spec_lse"], 4),
+                     "timing": "HIP events recorded by the library around each launch on its stream "
+                               "(includes the gap before the next launch)",
+                     "phase_ms_mean": {k: round(v, 4) for k, v in phase_ms.items()},
+                     "profiled_calls": ncalls.value},
         "emitted_tokens_per_s": round(emitted / (mean_ms * 1e-3), 1),
         "mean_accept_len": round(float(alen.mean()), 3),
-        "verified_tokens_per_s": None,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(tgt, dft, ids, u)

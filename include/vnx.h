@@ -63,6 +63,17 @@ const char* vnx_status_string(int status);
 /* Text of the last HIP error seen by this thread ("" if none). */
 const char* vnx_last_hip_error(void);
 
+/* Phase profiling (a measurement aid with no counterpart in the reference).
+ * vnx_profile_begin(max_calls) creates events for up to max_calls entry-point
+ * calls; while active, each vnx_spec_accept call records an event before each
+ * of its four launches (lse, accept, mass, draw) and one after the last, on
+ * its own stream.  vnx_profile_end waits for the recorded events, writes the
+ * summed milliseconds of each phase into phase_ms[0..nphase) and the number of
+ * profiled calls into *ncalls, and releases the events.  Not for use while
+ * calls run concurrently on several streams. */
+int vnx_profile_begin(int max_calls);
+int vnx_profile_end(double* phase_ms, int nphase, int* ncalls);
+
 /* Selects `device` and checks it is a gfx950 GPU.  Safe to call repeatedly.
  * Replaces: get_backend("rocm"/"rocm:N") device selection,
  * packages/verse_torch/verse_torch/device.py:346-386 and

@@ -41,6 +41,8 @@ SIGNATURES = {
     "vnx_status_string": (ctypes.c_char_p, [_int]),
     "vnx_last_hip_error": (ctypes.c_char_p, []),
     "vnx_init": (_int, [_int]),
+    "vnx_profile_begin": (_int, [_int]),
+    "vnx_profile_end": (_int, [_vp, _int, _vp]),
     "vnx_row_lse_workspace": (_c_sz, [_c_i64, _c_i64]),
     "vnx_row_lse": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _f32, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "vnx_row_argmax": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_sz, _vp]),

@@ -6,6 +6,7 @@
 
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "vnx_internal.h"
 
@@ -112,9 +113,79 @@ int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks, int64_t 
   return (int)c;
 }
 
+// ---------------------------------------------------------------------------
+// Phase profiling: while active, entry points record hipEvents around each of
+// their launches into one slot per call (slots are handed out in call order).
+// ---------------------------------------------------------------------------
+namespace {
+struct Profile {
+  std::mutex mu;
+  bool active = false;
+  int max_calls = 0, next = 0, nphase = 0;
+  std::vector<hipEvent_t> ev;  // max_calls * (kMaxPhases + 1)
+};
+Profile g_prof;
+}  // namespace
+
+hipEvent_t* profile_slot(int nphase) {
+  std::lock_guard<std::mutex> g(g_prof.mu);
+  if (!g_prof.active || g_prof.next >= g_prof.max_calls || nphase > kMaxPhases) return nullptr;
+  if (g_prof.nphase == 0) g_prof.nphase = nphase;
+  if (g_prof.nphase != nphase) return nullptr;
+  return &g_prof.ev[(size_t)(g_prof.next++) * (kMaxPhases + 1)];
+}
+
 }  // namespace vnx
 
 extern "C" {
+
+int vnx_profile_begin(int max_calls) {
+  using namespace vnx;
+  if (max_calls < 1 || max_calls > (1 << 16)) return VNX_ERR_INVALID_ARG;
+  std::lock_guard<std::mutex> g(g_prof.mu);
+  if (g_prof.active) return VNX_ERR_INVALID_ARG;
+  g_prof.ev.assign((size_t)max_calls * (kMaxPhases + 1), nullptr);
+  for (auto& e : g_prof.ev) {
+    hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      for (auto& f : g_prof.ev)
+        if (f) (void)hipEventDestroy(f);
+      g_prof.ev.clear();
+      return hip_fail(err);
+    }
+  }
+  g_prof.active = true;
+  g_prof.max_calls = max_calls;
+  g_prof.next = 0;
+  g_prof.nphase = 0;
+  return VNX_OK;
+}
+
+int vnx_profile_end(double* phase_ms, int nphase, int* ncalls) {
+  using namespace vnx;
+  std::lock_guard<std::mutex> g(g_prof.mu);
+  if (!g_prof.active) return VNX_ERR_INVALID_ARG;
+  int st = VNX_OK;
+  const int np = g_prof.nphase;
+  if (phase_ms)
+    for (int j = 0; j < nphase; ++j) phase_ms[j] = 0.0;
+  for (int c = 0; c < g_prof.next && st == VNX_OK; ++c) {
+    hipEvent_t* e = &g_prof.ev[(size_t)c * (kMaxPhases + 1)];
+    hipError_t err = hipEventSynchronize(e[np]);
+    if (err != hipSuccess) { st = hip_fail(err); break; }
+    for (int j = 0; j < np && j < nphase; ++j) {
+      float ms = 0.0f;
+      err = hipEventElapsedTime(&ms, e[j], e[j + 1]);
+      if (err != hipSuccess) { st = hip_fail(err); break; }
+      if (phase_ms) phase_ms[j] += ms;
+    }
+  }
+  if (ncalls) *ncalls = g_prof.next;
+  for (auto& e : g_prof.ev) (void)hipEventDestroy(e);
+  g_prof.ev.clear();
+  g_prof.active = false;
+  return st;
+}
 
 int vnx_version(void) { return 100; }
 

@@ -604,19 +604,29 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype, int64_t B,
   spec_carve(workspace, B, k, pl, &p);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 g1((unsigned)(B * (2 * k + 1) * pl.chunks)), gb((unsigned)B), g2((unsigned)(B * pl.chunks2));
+  hipEvent_t* ev = profile_slot(4);
+  auto mark = [&](int j) -> int {
+    if (ev) VNX_HIP_CHECK(hipEventRecord(ev[j], s));
+    return VNX_OK;
+  };
   return dispatch_tsm(dtype, sm, thr_t || thr_d, [&](auto tin, auto smc, auto thrc) {
     using Tin = decltype(tin);
     constexpr int SM = decltype(smc)::value;
     constexpr bool THR = decltype(thrc)::value;
+    int e = mark(0);
+    if (e) return e;
     hipLaunchKernelGGL((k_spec_lse<Tin, SM, THR>), g1, dim3(kNT), 0, s, p);
     VNX_LAUNCH_CHECK();
+    if ((e = mark(1))) return e;
     hipLaunchKernelGGL((k_spec_accept<Tin, SM, THR>), gb, dim3(kNT), 0, s, p);
     VNX_LAUNCH_CHECK();
+    if ((e = mark(2))) return e;
     hipLaunchKernelGGL((k_spec_mass<Tin, SM, THR>), g2, dim3(kNT), 0, s, p);
     VNX_LAUNCH_CHECK();
+    if ((e = mark(3))) return e;
     hipLaunchKernelGGL((k_spec_draw<Tin, SM, THR>), gb, dim3(kNT), 0, s, p);
     VNX_LAUNCH_CHECK();
-    return (int)VNX_OK;
+    return mark(4);
   });
 }
 

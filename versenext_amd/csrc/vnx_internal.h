@@ -72,6 +72,13 @@ inline int elem_size(int dtype) { return dtype == VNX_F32 ? 4 : 2; }
 // stays valid inside captured HIP graphs).
 int zero_counters(unsigned* p, int64_t n, hipStream_t st);
 
+// Phase profiling (vnx_profile_begin / vnx_profile_end): returns this call's
+// kMaxPhases + 1 events while profiling is active and slots remain, else
+// nullptr.  The caller records event j before launch j and event nphase after
+// the last launch, on its stream.
+constexpr int kMaxPhases = 7;
+hipEvent_t* profile_slot(int nphase);
+
 // Compute units of the current device (cached per device ordinal).
 int device_cus();
 
