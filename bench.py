@@ -99,6 +99,65 @@ def cpu_baseline(tgt, dft, ids, u, budget_s: float = 12.0):
                        f"{total_t / reps:.3f} s per batch")
 
 
+GEMV_SHAPES = (("tied_head", 248320, 1024), ("w_gate_up", 4096, 1024), ("w_down", 1024, 4096))
+
+
+def bench_gemv(args):
+    """weight-only INT4 (group 128, fp16 scales) and INT8
+    (per-channel) GEMV, weights N(0, 0.02), fp16 activations N(0, 1), B in
+    {1, 8, 32}.  bytes per launch = weight + scales + 2*B*K (fp16 x) + 4*B*N
+    (fp32 y); time = HIP events around each launch on the current stream."""
+    import numpy as np
+    import torch
+    from versenext_amd import get_backend
+    from versenext_amd import quant as VQ
+
+    hip = get_backend("rocm:0")
+    dev = hip.torch_device
+    g = torch.Generator(device=dev)
+    g.manual_seed(20)
+    rows = []
+    for name, N, K in GEMV_SHAPES:
+        w = torch.randn((N, K), generator=g, device=dev) * 0.02
+        packed = {"int4_g128": VQ.quantize_int4_g(w, 128), "int8": VQ.quantize_int8(w)}
+        del w
+        for qtype in ("int4_g128", "int8"):
+            wq, sc = packed[qtype]
+            for B in (1, 8, 32):
+                x = (torch.randn((B, K), generator=g, device=dev)).to(torch.float16)
+                if qtype == "int8":
+                    fn = lambda: hip.gemv_w8(x, wq, sc)  # noqa: E731
+                else:
+                    fn = lambda: hip.gemv_w4(x, wq, sc, 128)  # noqa: E731
+                for _ in range(args.warmup):
+                    fn()
+                torch.cuda.synchronize()
+                evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                       for _ in range(args.steps)]
+                stream = torch.cuda.current_stream(dev)
+                for e0, e1 in evs:
+                    e0.record(stream)
+                    fn()
+                    e1.record(stream)
+                torch.cuda.synchronize()
+                us = float(np.mean([e0.elapsed_time(e1) for e0, e1 in evs])) * 1e3
+                nbytes = VQ.weight_bytes(qtype, N, K) + 2 * B * K + 4 * B * N
+                gbs = nbytes / (us * 1e-6) / 1e9
+                rows.append({"shape": name, "N": N, "K": K, "qtype": qtype, "B": B, "us": round(us, 2),
+                             "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "TFLOP/s": round(2 * B * N * K / (us * 1e-6) / 1e12, 2)})
+    head = [r for r in rows if r["shape"] == "tied_head" and r["qtype"] == "int4_g128"]
+    best = max(head, key=lambda r: r["GB/s"])
+    out = {"metric": "quantized GEMV HBM GB/s (config 4, INT4 g128 tied head, B=1)",
+           "value": [r for r in head if r["B"] == 1][0]["GB/s"], "unit": "GB/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "dtype": "int4/int8 x fp16",
+           "data": "synthetic", "config": {"workload": "BASELINE config 4: weight-only dequant-GEMV"},
+           "roofline": {"bound": "hbm", "achieved": best["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": best["frac"], "traffic": None, "kernel": "k_qgemv<4,*> (tied head)"},
+           "results": rows}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,11 +166,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
+    ap.add_argument("--workload", default="accept", choices=("accept", "gemv"),
+                    help="accept: BASELINE config 2 (the bench line); gemv: config 4")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
                                    "run with --gpus 1", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.workload == "gemv":
+        bench_gemv(args)
+        return
 
     import numpy as np
     import torch

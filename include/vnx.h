@@ -43,7 +43,7 @@ enum vnx_status {
   VNX_ERR_NO_DEVICE = -5      /* no gfx950 device / bad ordinal -> RuntimeError */
 };
 
-enum vnx_dtype { VNX_F32 = 0, VNX_BF16 = 1 };
+enum vnx_dtype { VNX_F32 = 0, VNX_BF16 = 1, VNX_F16 = 2 };
 
 /* Flags written by vnx_spec_accept, one byte per (row, position). */
 enum vnx_accept_flag {
@@ -161,6 +161,46 @@ int vnx_greedy_verify(const void* target, int dtype, int64_t B, int k, int rows_
                       uint8_t* accepted, int64_t* main_pred,
                       int32_t* accept_len, int64_t* out_ids,
                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Weight-only quantized GEMV / skinny GEMM (draft decode, tied LM head):
+ * y (B, N) fp32, row pitch ldy = x (B, K) fp16 (row pitch ldx) . W^T with W
+ * the dequantized (N, K) weight.  Matrix-core kernels (MFMA f16 -> f32); any
+ * B (processed 32 columns at a time).  K must be a multiple of 128; x and
+ * each weight row must start 16-byte aligned (ldx % 8 == 0, ldw % 16 == 0).
+ * Small N splits K over workgroups: the fp32 partials go to the workspace
+ * (vnx_gemv_workspace bytes; no initialisation needed) and are added in a
+ * fixed order, so results do not depend on scheduling.
+ * ------------------------------------------------------------------------- */
+
+size_t vnx_gemv_workspace(int64_t B, int64_t N, int64_t K);
+
+/* W4: wq (N, ceil(K/2)) bytes, row pitch ldw, two int4 per byte with the low
+ * nibble at the even column (the packing of quantize.py:36-68, _pack_int4);
+ * scales (N, K/group), row pitch lds, fp16 (VNX_F16) or fp32 (VNX_F32); the
+ * weight is q * s[n][k / group].  group = K with fp32 scales is the
+ * reference's per-channel INT4 (quantize_int4, quantize.py:231-258;
+ * matmul_int4, :277-309); group = 128 with fp16 scales is the group-128
+ * format.  Replaces matmul_int4 / QuantizedLinear.forward_fused
+ * (quantize.py:506-533). */
+int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+                float* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/* W8: wq (N, K) int8, row pitch ldw; scale (N) fp32 per output row (the
+ * per-channel INT8 of quantize_int8, quantize.py:187-214).  Replaces
+ * QuantizedLinear.forward for qtype="int8" (quantize.py:467-505). */
+int vnx_gemv_w8(const void* x, int64_t ldx, const int8_t* wq, int64_t ldw, const float* scale,
+                int64_t B, int64_t N, int64_t K, float* y, int64_t ldy, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* out[n][k] = q[n][k] * s (fp32, one rounded multiply): the weights the GEMV
+ * kernels use.  Replaces dequantize_int4 (quantize.py:261-274) and
+ * dequantize_int8 (quantize.py:216-224). */
+int vnx_dequant_w4(const uint8_t* wq, int64_t ldw, const void* scales, int scale_dtype, int64_t lds,
+                   int64_t N, int64_t K, int group, float* out, int64_t ldo, void* stream);
+int vnx_dequant_w8(const int8_t* wq, int64_t ldw, const float* scale, int64_t N, int64_t K,
+                   float* out, int64_t ldo, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,155 @@
+"""GPU parity of the weight-only quantized path against oracle/quant.py.
+
+Bar: the GPU quantizers and the dequantization kernels are bit-exact with the
+oracle; the GEMV (fp16 activations, fp32 accumulation on the matrix cores)
+agrees with the fp64 product of the same fp16 activations and dequantized
+weights within 1e-5 * sum_k |x_k w_k| per output (the fp32 tolerance of the
+north star, relative to the sum of magnitudes the rounding acts on)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as Q
+from versenext_amd import quant as VQ
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _weights(N, K, seed, std=0.02):
+    w = np.random.default_rng(seed).normal(0, std, (N, K)).astype(np.float32)
+    # exact ties for round-half-to-even in a few rows: multiples of scale/2
+    w[0, :8] = np.array([0.5, 1.5, 2.5, -0.5, -1.5, 3.5, -3.5, 7.0], np.float32) * std
+    return w
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4", "int4_g128"])
+def test_gpu_quantizers_match_oracle(hip, kind):
+    _say(f"quantizer {kind}")
+    w = _weights(300, 512, 1)
+    wt = torch.from_numpy(w).to(hip.torch_device)
+    if kind == "int8":
+        q, s = VQ.quantize_int8(wt)
+        qo, so = Q.quantize_int8(w)
+        assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy(), so)
+    elif kind == "int4":
+        q, s = VQ.quantize_int4(wt)
+        qo, so = Q.quantize_int4(w)
+        assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy(), so)
+    else:
+        q, s = VQ.quantize_int4_g(wt, 128)
+        qo, so = Q.quantize_int4_g(w, 128)
+        assert np.array_equal(q.cpu().numpy(), qo)
+        assert np.array_equal(s.cpu().numpy().view(np.uint16), so.view(np.uint16))
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4", "int4_g128"])
+def test_dequant_kernels_bit_exact(hip, kind):
+    _say(f"dequant {kind}")
+    N, K = 257, 1024
+    w = _weights(N, K, 2)
+    if kind == "int8":
+        q, s = Q.quantize_int8(w)
+        got = hip.dequant_w8(torch.from_numpy(q), torch.from_numpy(s.reshape(-1))).cpu().numpy()
+        ref = Q.dequantize_int8(q, s)
+    elif kind == "int4":
+        p, s = Q.quantize_int4(w)
+        got = hip.dequant_w4(torch.from_numpy(p), torch.from_numpy(s), K, K).cpu().numpy()
+        ref = Q.dequantize_int4(p, s, (N, K))
+    else:
+        p, s = Q.quantize_int4_g(w, 128)
+        got = hip.dequant_w4(torch.from_numpy(p), torch.from_numpy(s), K, 128).cpu().numpy()
+        ref = Q.dequantize_int4_g(p, s, (N, K), 128)
+    assert got.dtype == np.float32 and np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
+_QCACHE = {}
+
+
+def _quantized(kind, N, K, seed):
+    """Oracle-quantized weights, cached (the full-size head is 1 GB in fp32)."""
+    key = (kind, N, K, seed)
+    if key not in _QCACHE:
+        if len(_QCACHE) > 4:
+            _QCACHE.clear()
+        w = _weights(N, K, seed)
+        if kind == "int8":
+            _QCACHE[key] = Q.quantize_int8(w)
+        elif kind == "int4":
+            _QCACHE[key] = Q.quantize_int4(w)
+        else:
+            _QCACHE[key] = Q.quantize_int4_g(w, 128)
+        del w
+    return _QCACHE[key]
+
+
+def _gemv_check(hip, kind, N, K, B, seed, rows=None):
+    x16 = np.random.default_rng(seed + B).normal(0, 1, (B, K)).astype(np.float16)
+    xt = torch.from_numpy(x16)
+    if kind == "int8":
+        q, s = _quantized(kind, N, K, seed)
+        y = hip.gemv_w8(xt, torch.from_numpy(q), torch.from_numpy(s.reshape(-1)))
+        wd = lambda r: Q.dequantize_int8(q[r], s[r])  # noqa: E731
+    elif kind == "int4":
+        p, s = _quantized(kind, N, K, seed)
+        y = hip.gemv_w4(xt, torch.from_numpy(p), torch.from_numpy(s), K)
+        wd = lambda r: Q.dequantize_int4(p[r], s[r], (len(r), K))  # noqa: E731
+    else:
+        p, s = _quantized(kind, N, K, seed)
+        y = hip.gemv_w4(xt, torch.from_numpy(p), torch.from_numpy(s), 128)
+        wd = lambda r: Q.dequantize_int4_g(p[r], s[r], (len(r), K), 128)  # noqa: E731
+    y = y.cpu().numpy()
+    assert y.shape == (B, N) and y.dtype == np.float32
+    r = np.arange(N) if rows is None else rows
+    W = wd(r)
+    ref = Q.gemv_ref(x16, W)
+    mag = Q.gemv_abs(x16, W)
+    err = np.abs(y[:, r].astype(np.float64) - ref)
+    worst = float(np.max(err / (mag + 1e-30)))
+    _say(f"  {kind} N={N} K={K} B={B}: max err / sum|xw| = {worst:.2e}")
+    assert np.all(err <= RTOL * mag + 1e-30), worst
+
+
+@pytest.mark.parametrize("kind", ["int8", "int4", "int4_g128"])
+@pytest.mark.parametrize("N,K,B", [(4096, 1024, 1), (1000, 384, 3), (1024, 4096, 8), (333, 512, 17),
+                                   (512, 1024, 32), (256, 256, 40)])
+def test_gemv_parity(hip, kind, N, K, B):
+    _gemv_check(hip, kind, N, K, B, seed=N + K + B)
+
+
+@pytest.mark.parametrize("kind", ["int4_g128", "int8"])
+@pytest.mark.parametrize("B", [1, 8, 32])
+def test_gemv_tied_head_full_size(hip, kind, B):
+    """Config 4's tied LM head, 248,320 x 1024, checked on 4096 sampled rows
+    (including both ends and a partial last tile)."""
+    N, K = 248320, 1024
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(N - 40, N),
+                                     np.random.default_rng(B).choice(N, 4040, replace=False)]))
+    _gemv_check(hip, kind, N, K, B, seed=5, rows=rows)
+
+
+def test_quantized_linear_forward(hip):
+    _say("QuantizedLinear")
+    rng = np.random.default_rng(9)
+    w = rng.normal(0, 0.02, (640, 256)).astype(np.float32)
+    b = rng.normal(0, 1, 640).astype(np.float32)
+    x = rng.normal(0, 1, (2, 3, 256)).astype(np.float32)
+    for qtype in VQ.QuantizedLinear.QTYPES:
+        ql = VQ.QuantizedLinear(w, b, qtype=qtype)
+        y = ql(torch.from_numpy(x)).cpu().numpy()
+        wd = ql.dequantize().cpu().numpy().astype(np.float64)
+        x16 = x.astype(np.float16).astype(np.float64)
+        ref = x16 @ wd.T + b
+        assert y.shape == (2, 3, 640)
+        assert np.all(np.abs(y - ref) <= RTOL * (np.abs(x16) @ np.abs(wd).T) + 1e-6)
+
+
+def test_gemv_rejects_bad_shapes(hip):
+    x = torch.zeros((2, 100), dtype=torch.float16)
+    with pytest.raises(ValueError):
+        hip.gemv_w8(x, torch.zeros((8, 100), dtype=torch.int8), torch.ones(8))  # K % 128 != 0

@@ -22,6 +22,7 @@ VNX_ERR_NO_DEVICE = -5
 
 VNX_F32 = 0
 VNX_BF16 = 1
+VNX_F16 = 2
 
 FLAG_NEAR_TIE = 1
 FLAG_LSE_EDGE = 2
@@ -51,6 +52,13 @@ SIGNATURES = {
     "vnx_spec_accept_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
     "vnx_spec_accept": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "vnx_gemv_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "vnx_gemv_w4": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
+                           _vp, _c_i64, _vp, _c_sz, _vp]),
+    "vnx_gemv_w8": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64,
+                           _vp, _c_sz, _vp]),
+    "vnx_dequant_w4": (_int, [_vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _c_i64, _vp]),
+    "vnx_dequant_w8": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp]),
     "vnx_greedy_verify_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
     "vnx_greedy_verify": (_int, [_vp, _int, _c_i64, _int, _int, _c_i64, _c_i64, _c_i64, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),

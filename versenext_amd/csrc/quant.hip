@@ -1,0 +1,470 @@
+// Weight-only quantized GEMV / skinny GEMM for draft decode and the tied LM
+// head: y (B, N) fp32 = x (B, K) fp16 . dequant(W)^T.
+//   W4: int4 packed two per byte along K, low nibble = even k (the layout of
+//       quantize.py:36-68), one scale per (row, group of G columns), scales
+//       fp16 or fp32.  G = 128 with fp16 scales is the group-128 format;
+//       G = K with fp32 scales is the reference's per-channel INT4
+//       (quantize.py:231-258).
+//   W8: int8 (N, K), one fp32 scale per row (quantize.py:187-214).
+// The dequantized weight is q * s, so y = sum_g s_g * sum_{k in g} x_k q_k.
+//
+// Matrix cores: v_mfma_f32_16x16x32_f16 with A = 16 weight rows x 32 k (the
+// integers, converted exactly to fp16 in registers), B = 32 k x 16 batch
+// columns (x, staged in LDS) and a 16x16 fp32 accumulator per 128-k group.
+// The integers are read in offset form, u = q ^ 8 (0..15) or q ^ 0x80
+// (0..255); one v_perm_b32 per pair places two of them under 0x64 exponent
+// bytes (the fp16 values 1024 + u) and one packed fp16 subtract restores q
+// (exact: small integers).  A group's MFMA result is scaled by s_g and added
+// to the fp32 output.
+//
+// Work split: a workgroup (4 waves) owns 64*TPW consecutive rows (tiles of 16
+// rows; wave w takes tiles w, w+4, ...) and a K range; it streams its range in
+// slices, staging each slice of x (up to 32 batch columns) once in LDS for all
+// of its tiles.  Small N splits K over workgroups (grid.y); their fp32
+// partials go to the workspace and k_qreduce adds them in split order, so the
+// result does not depend on scheduling.  Within a 128-k group, lane (m = lane % 16, kq = lane / 16)
+// holds k = kq*32 + [0, 32) of row m (16 bytes of W4, 32 of W8), used as
+// four MFMA k-steps; the B operand takes x at the same k (the k order inside
+// a group is a permutation shared by A and B, so the dot product is unchanged).
+#include <stdlib.h>
+
+#include "vnx_internal.h"
+
+namespace vnx {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQNT = 256;        // threads per workgroup
+constexpr int kQTiles = 4;       // tiles per wave
+constexpr int kQRows = 16 * 4 * kQTiles;  // rows per workgroup (256)
+constexpr int kGK = 128;         // k per accumulation group
+constexpr int kXPad = 8;         // fp16 padding per LDS row of x (16 bytes)
+constexpr int kQMaxSplits = 8;   // K splits of small layers (k_qreduce adds them)
+
+struct QGemvParams {
+  const uint16_t* x;   // fp16 bits, (B, K), row pitch ldx
+  int64_t ldx;
+  const uint8_t* w;    // W4: (N, K/2) bytes; W8: (N, K) bytes; row pitch ldw bytes
+  int64_t ldw;
+  const void* sc;      // scales, row pitch lds elements
+  int64_t lds;
+  int sc_f16;          // 1: fp16 scales, 0: fp32
+  int64_t B, N, K;
+  int G;               // columns per scale (W4); W8 uses one scale per row
+  int gpg;             // 128-column groups per scale: G / 128
+  float* y;            // (B, N), row pitch ldy
+  int64_t ldy;
+  int64_t ksplit_len;  // K per grid.y split (multiple of kGK)
+  float* part;         // ksplit > 1: partials [split][B][N]
+};
+
+__device__ __forceinline__ float load_scale(const QGemvParams& p, int64_t row, unsigned g) {
+  if (p.sc_f16) {
+    const uint16_t h = static_cast<const uint16_t*>(p.sc)[row * p.lds + g];
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+  return static_cast<const float*>(p.sc)[row * p.lds + g];
+}
+
+// Integers -> fp16 with one v_perm_b32 per pair: the fp16 bits 0x64vv are
+// 1024 + vv for a byte vv, so selecting two offset-form bytes of u and two
+// 0x64 bytes of a constant gives the pair (1024 + u_a, 1024 + u_b); one packed
+// fp16 subtract then leaves the signed integers (exact: |q| <= 128).
+__device__ __forceinline__ fp16x2 pair_from(uint32_t u, uint32_t sel, fp16x2 off) {
+  const uint32_t bits = __builtin_amdgcn_perm(0x64646464u, u, sel);
+  return __builtin_bit_cast(fp16x2, bits) - off;
+}
+
+// Selectors: D = {u.b_lo, 0x64, u.b_hi, 0x64} (codes 0-3 pick u, 4 picks 0x64).
+constexpr uint32_t kSel01 = 0x04010400u;  // bytes 0, 1
+constexpr uint32_t kSel23 = 0x04030402u;  // bytes 2, 3
+
+__device__ __forceinline__ half8 pack_half8(fp16x2 p0, fp16x2 p1, fp16x2 p2, fp16x2 p3) {
+  half8 a;
+  a[0] = (_Float16)p0.x; a[1] = (_Float16)p0.y; a[2] = (_Float16)p1.x; a[3] = (_Float16)p1.y;
+  a[4] = (_Float16)p2.x; a[5] = (_Float16)p2.y; a[6] = (_Float16)p3.x; a[7] = (_Float16)p3.y;
+  return a;
+}
+
+// A operand of one MFMA k-step from one W4 dword (8 nibbles, nibble i = k i;
+// low nibble of byte j is k 2j).  Element order: k = 0, 2, 4, 6, 1, 3, 5, 7
+// (the low nibbles, then the high nibbles); x is staged in LDS in the same
+// order (stage_perm_w4).
+__device__ __forceinline__ half8 a_w4(uint32_t d) {
+  const uint32_t lo = (d ^ 0x88888888u) & 0x0F0F0F0Fu;         // q + 8 of k 0, 2, 4, 6
+  const uint32_t hi = ((d >> 4) ^ 0x08888888u) & 0x0F0F0F0Fu;  // q + 8 of k 1, 3, 5, 7
+  const fp16x2 off = {(__fp16)1032.0f, (__fp16)1032.0f};
+  return pack_half8(pair_from(lo, kSel01, off), pair_from(lo, kSel23, off), pair_from(hi, kSel01, off),
+                    pair_from(hi, kSel23, off));
+}
+
+// W8: two dwords = 8 int8 in k order (natural order, x staged unpermuted).
+__device__ __forceinline__ half8 a_w8(uint32_t d0, uint32_t d1) {
+  const uint32_t u0 = d0 ^ 0x80808080u, u1 = d1 ^ 0x80808080u;  // q + 128
+  const fp16x2 off = {(__fp16)1152.0f, (__fp16)1152.0f};
+  return pack_half8(pair_from(u0, kSel01, off), pair_from(u0, kSel23, off), pair_from(u1, kSel01, off),
+                    pair_from(u1, kSel23, off));
+}
+
+// W4 staging order of 8 consecutive fp16 (4 dwords w0..w3 = (h0,h1)..(h6,h7)):
+// h0, h2, h4, h6, h1, h3, h5, h7.
+__device__ __forceinline__ u32x4 stage_perm_w4(u32x4 v) {
+  u32x4 o;
+  o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);  // h0, h2
+  o.y = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);  // h4, h6
+  o.z = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);  // h1, h3
+  o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);  // h5, h7
+  return o;
+}
+
+template <int BITS, int NC, int TPW>
+__global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
+  constexpr int KS = 1024 / NC;                 // k per slice
+  constexpr int XS = KS + kXPad;                // LDS row pitch of x (fp16)
+  constexpr int NG = KS / kGK;                  // groups per slice
+  constexpr int WBYTES = BITS == 4 ? 16 : 32;   // weight bytes per lane per group
+  __shared__ __attribute__((aligned(16))) uint16_t xs[NC * 16 * XS];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
+  const int m = lane % 16, kq = lane / 16;
+  const int64_t row_base = (int64_t)blockIdx.x * (64 * TPW);
+  const int64_t kb = (int64_t)blockIdx.y * p.ksplit_len;
+  const int64_t ke = min(p.K, kb + p.ksplit_len);
+  // fp16 group scales can be read 16 bytes per row when a group is 128 wide.
+  const bool vec_sc = BITS == 4 && p.sc_f16 && p.G == kGK && (p.lds % 8) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.sc) & 15) == 0;
+
+  f32x4 yacc[TPW][NC];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) yacc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t k0 = kb; k0 < ke; k0 += KS) {
+    const int ks = (int)min((int64_t)KS, ke - k0);  // multiple of kGK
+    // ---- stage x[:, k0 : k0+ks) (zero rows past B, zero columns past ks) ----
+    __syncthreads();
+    // Batch rows past B are zero; they are written once (first slice) and
+    // never read from global memory.
+    const int brows = k0 == kb ? NC * 16 : (int)min((int64_t)NC * 16, p.B);
+    for (int idx = tid; idx < brows * (KS / 8); idx += kQNT) {
+      const int b = idx / (KS / 8), c8 = idx % (KS / 8);
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (b < p.B && c8 * 8 < ks) v = *reinterpret_cast<const u32x4*>(p.x + b * p.ldx + k0 + c8 * 8);
+      if constexpr (BITS == 4) v = stage_perm_w4(v);
+      *reinterpret_cast<u32x4*>(&xs[b * XS + c8 * 8]) = v;
+    }
+    __syncthreads();
+
+#pragma unroll 1
+    for (int t = 0; t < TPW; ++t) {
+      const int64_t row0 = row_base + (int64_t)(wave + 4 * t) * 16;
+      if (row0 >= p.N) break;
+      // A rows: m; D rows: 4*kq + j.  Rows past N read row N-1 (not stored).
+      const int64_t ra = min(row0 + m, p.N - 1);
+      const uint8_t* wr = p.w + ra * p.ldw + (BITS == 4 ? k0 / 2 : k0);
+      // All of the slice's weight loads first.
+      uint32_t wv[NG][WBYTES / 4];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g * kGK < ks) {
+          const uint8_t* src = wr + (BITS == 4 ? g * 64 + kq * 16 : g * 128 + kq * 32);
+          const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+          wv[g][0] = v0.x; wv[g][1] = v0.y; wv[g][2] = v0.z; wv[g][3] = v0.w;
+          if constexpr (BITS == 8) {
+            const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+            wv[g][4] = v1.x; wv[g][5] = v1.y; wv[g][6] = v1.z; wv[g][7] = v1.w;
+          }
+        }
+      }
+      // Scales of the lane's four D rows for the slice's groups (W4).
+      float sc[NG][4];
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t rd = min(row0 + 4 * kq + j, p.N - 1);
+          if (vec_sc && ks == KS && (k0 / kGK) % NG == 0) {
+            // The slice's NG scales of row rd: exactly NG halves (16 or 8
+            // bytes), aligned because lds % 8 == 0 and k0 / kGK % NG == 0.
+            const uint16_t* srow = static_cast<const uint16_t*>(p.sc) + rd * p.lds + k0 / kGK;
+            uint32_t wds[NG / 2];
+            if constexpr (NG == 8) {
+              const u32x4 v = *reinterpret_cast<const u32x4*>(srow);
+              wds[0] = v.x; wds[1] = v.y; wds[2] = v.z; wds[3] = v.w;
+            } else {
+              static_assert(NG == 4, "slices hold 4 or 8 groups");
+              const uint2 v = *reinterpret_cast<const uint2*>(srow);
+              wds[0] = v.x; wds[1] = v.y;
+            }
+#pragma unroll
+            for (int e = 0; e < NG; ++e)
+              sc[e][j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wds[e / 2] >> (16 * (e % 2))));
+          } else {
+            // Scale column of group g: (k0/128 + g) / gpg, in 32-bit
+            // arithmetic (gpg = 1 for group-128, K/128 for one scale per row).
+            const unsigned g0 = (unsigned)(k0 / kGK);
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+              if (g * kGK < ks) {
+                const unsigned col = p.gpg == 1 ? g0 + g : (g0 + (unsigned)g) / (unsigned)p.gpg;
+                sc[g][j] = load_scale(p, rd, col);
+              }
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g * kGK >= ks) break;
+        f32x4 acc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const half8 a = BITS == 4 ? a_w4(wv[g][s]) : a_w8(wv[g][2 * s], wv[g][2 * s + 1]);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int b = c * 16 + m;
+            const half8 bx = *reinterpret_cast<const half8*>(&xs[b * XS + g * kGK + kq * 32 + s * 8]);
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc[c], 0, 0, 0);
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if constexpr (BITS == 4) yacc[t][c][j] = __builtin_fmaf(sc[g][j], acc[c][j], yacc[t][c][j]);
+            else yacc[t][c][j] += acc[c][j];
+          }
+        }
+      }
+    }
+  }
+
+  // ---- store: lane holds D[row 4*kq + j][column m] ----
+  float* out = gridDim.y > 1 ? p.part + (int64_t)blockIdx.y * p.B * p.N : p.y;
+  const int64_t ldo = gridDim.y > 1 ? p.N : p.ldy;
+#pragma unroll 1
+  for (int t = 0; t < TPW; ++t) {
+    const int64_t row0 = row_base + (int64_t)(wave + 4 * t) * 16;
+    if (row0 >= p.N) break;
+    const int64_t n0 = row0 + 4 * kq;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t b = c * 16 + m;
+      if (b >= p.B) continue;
+      f32x4 v = yacc[t][c];
+      if constexpr (BITS == 8) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] *= load_scale(p, min(n0 + j, p.N - 1), 0);
+      }
+      float* dst = out + b * ldo + n0;
+      if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (n0 + j < p.N) dst[j] = v[j];
+      }
+    }
+  }
+}
+
+// y[b][n] = sum over splits, in split order (splits <= kQMaxSplits; the loads
+// are issued together, the adds run in order).
+
+__global__ void k_qreduce(const float* part, int splits, int64_t B, int64_t N, float* y, int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * N) return;
+  float v[kQMaxSplits];
+#pragma unroll
+  for (int k = 0; k < kQMaxSplits; ++k) v[k] = k < splits ? part[(int64_t)k * B * N + i] : 0.0f;
+  float s = v[0];
+#pragma unroll
+  for (int k = 1; k < kQMaxSplits; ++k)
+    if (k < splits) s += v[k];
+  y[(i / N) * ldy + (i % N)] = s;
+}
+
+// Dequantization (bit-exact reference for the kernels' weights):
+// out[n][k] = q[n][k] * s[n][k / G] in fp32 (one rounded multiply).
+__global__ void k_dequant(QGemvParams p, int bits, float* out, int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n = i / p.K, k = i % p.K;
+  if (n >= p.N) return;
+  int q;
+  if (bits == 4) {
+    const uint8_t byte = p.w[n * p.ldw + k / 2];
+    const int nib = (k & 1) ? (byte >> 4) : (byte & 0xF);
+    q = nib >= 8 ? nib - 16 : nib;
+  } else {
+    q = (int)static_cast<const int8_t*>(static_cast<const void*>(p.w))[n * p.ldw + k];
+  }
+  const float s = bits == 4 ? load_scale(p, n, k / p.G) : load_scale(p, n, 0);
+  out[n * ldo + k] = (float)q * s;
+}
+
+static int qgemv_check(const QGemvParams& p, int bits) {
+  if (!p.x || !p.w || !p.sc || !p.y) return VNX_ERR_INVALID_ARG;
+  if (p.B < 0 || p.N < 0 || p.K <= 0) return VNX_ERR_INVALID_ARG;
+  if (p.K % kGK) return VNX_ERR_UNSUPPORTED;
+  if (bits == 4 && (p.G <= 0 || p.G % kGK || p.K % p.G)) return VNX_ERR_UNSUPPORTED;
+  if (p.K > ((int64_t)1 << 30)) return VNX_ERR_UNSUPPORTED;
+  if (p.ldx < p.K || p.ldy < p.N) return VNX_ERR_INVALID_ARG;
+  if (p.ldw < (bits == 4 ? p.K / 2 : p.K)) return VNX_ERR_INVALID_ARG;
+  if (p.lds < (bits == 4 ? p.K / p.G : 1)) return VNX_ERR_INVALID_ARG;
+  // 16-byte vector loads of x and of every row's weights.
+  if (!aligned16(p.x) || p.ldx % 8 || !aligned16(p.w) || p.ldw % 16) return VNX_ERR_UNSUPPORTED;
+  return VNX_OK;
+}
+
+// Launch shape: rows per workgroup 64*TPW (TPW = 4 when N is large enough to
+// fill the GPU, else 1) and K splits so that small layers still spread over
+// about kQTargetWgs workgroups.
+constexpr int64_t kQTargetWgs = 512;
+
+// VNX_QTPW (1 or 4) overrides the tiles per wave for tuning sweeps.
+static int tpw_override() {
+  static const int t = [] {
+    const char* e = getenv("VNX_QTPW");
+    const int v = e ? atoi(e) : 0;
+    return (v == 1 || v == 4) ? v : 0;
+  }();
+  return t;
+}
+
+struct QPlan {
+  int tpw;
+  int64_t row_blocks;
+  int splits;
+  int64_t split_len;
+};
+
+// TPW = 4 amortises the x staging over more rows; it pays when the staged
+// slice is large (more than 16 batch columns) and N fills the GPU anyway.
+static QPlan qgemv_plan(int64_t B, int64_t N, int64_t K) {
+  QPlan q;
+  q.tpw = tpw_override() ? tpw_override() : (B > 16 && N >= 256 * kQTargetWgs ? 4 : 1);
+  q.row_blocks = (N + 64 * q.tpw - 1) / (64 * q.tpw);
+  const int64_t groups = K / kGK;
+  int64_t splits = (kQTargetWgs + q.row_blocks - 1) / q.row_blocks;
+  if (splits > groups) splits = groups;
+  if (splits > kQMaxSplits) splits = kQMaxSplits;
+  if (splits < 1) splits = 1;
+  const int64_t per = (groups + splits - 1) / splits;
+  q.split_len = per * kGK;
+  q.splits = (int)((K + q.split_len - 1) / q.split_len);
+  return q;
+}
+
+static size_t qgemv_ws(int64_t B, int64_t N, int64_t K) {
+  const QPlan q = qgemv_plan(B < 32 ? B : 32, N, K);
+  if (q.splits <= 1) return 0;
+  const int64_t b = B < 32 ? B : 32;
+  return (size_t)q.splits * b * N * sizeof(float);
+}
+
+static int qgemv_launch(QGemvParams p, int bits, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (p.B == 0 || p.N == 0) return VNX_OK;
+  if (!ws && qgemv_ws(p.B, p.N, p.K) > 0) return VNX_ERR_WORKSPACE;
+  if (ws_bytes < qgemv_ws(p.B, p.N, p.K)) return VNX_ERR_WORKSPACE;
+  p.part = static_cast<float*>(ws);
+  // Batch columns in chunks of 32 (two MFMA column blocks) or one of 16.
+  for (int64_t b0 = 0; b0 < p.B; b0 += 32) {
+    QGemvParams c = p;
+    c.x = p.x + b0 * p.ldx;
+    c.y = p.y + b0 * p.ldy;
+    c.B = min((int64_t)32, p.B - b0);
+    const bool two = c.B > 16;
+    const QPlan q = qgemv_plan(c.B, c.N, c.K);
+    c.ksplit_len = q.split_len;
+    const dim3 grid((unsigned)q.row_blocks, (unsigned)q.splits);
+#define VNX_QLAUNCH(BITS, NC, TPW) hipLaunchKernelGGL((k_qgemv<BITS, NC, TPW>), grid, dim3(kQNT), 0, s, c)
+    if (bits == 4) {
+      if (two) { if (q.tpw == 4) VNX_QLAUNCH(4, 2, 4); else VNX_QLAUNCH(4, 2, 1); }
+      else { if (q.tpw == 4) VNX_QLAUNCH(4, 1, 4); else VNX_QLAUNCH(4, 1, 1); }
+    } else {
+      if (two) { if (q.tpw == 4) VNX_QLAUNCH(8, 2, 4); else VNX_QLAUNCH(8, 2, 1); }
+      else { if (q.tpw == 4) VNX_QLAUNCH(8, 1, 4); else VNX_QLAUNCH(8, 1, 1); }
+    }
+#undef VNX_QLAUNCH
+    VNX_LAUNCH_CHECK();
+    if (q.splits > 1) {
+      const int64_t n = c.B * c.N;
+      hipLaunchKernelGGL(k_qreduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, c.part, q.splits, c.B,
+                         c.N, c.y, c.ldy);
+      VNX_LAUNCH_CHECK();
+    }
+  }
+  return VNX_OK;
+}
+
+}  // namespace vnx
+
+using namespace vnx;
+
+extern "C" {
+
+size_t vnx_gemv_workspace(int64_t B, int64_t N, int64_t K) {
+  if (B <= 0 || N <= 0 || K <= 0 || K % kGK) return 256;
+  const size_t w = qgemv_ws(B, N, K);
+  return w < 256 ? 256 : w;
+}
+
+int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, float* y,
+                int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+  if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
+  QGemvParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
+  p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.y = y; p.ldy = ldy;
+  p.gpg = group / kGK;
+  const int st = qgemv_check(p, 4);
+  if (st) return st;
+  return qgemv_launch(p, 4, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemv_w8(const void* x, int64_t ldx, const int8_t* wq, int64_t ldw, const float* scale,
+                int64_t B, int64_t N, int64_t K, float* y, int64_t ldy, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  QGemvParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = reinterpret_cast<const uint8_t*>(wq); p.ldw = ldw;
+  p.sc = scale; p.lds = 1; p.sc_f16 = 0; p.B = B; p.N = N; p.K = K; p.G = (int)K; p.y = y; p.ldy = ldy;
+  p.gpg = (int)(K / kGK);
+  const int st = qgemv_check(p, 8);
+  if (st) return st;
+  return qgemv_launch(p, 8, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int vnx_dequant_w4(const uint8_t* wq, int64_t ldw, const void* scales, int scale_dtype, int64_t lds,
+                   int64_t N, int64_t K, int group, float* out, int64_t ldo, void* stream) {
+  if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
+  if (!wq || !scales || !out || N < 0 || K <= 0 || group <= 0 || K % group) return VNX_ERR_INVALID_ARG;
+  if (ldw < (K + 1) / 2 || lds < K / group || ldo < K) return VNX_ERR_INVALID_ARG;
+  if (N == 0) return VNX_OK;
+  QGemvParams p{};
+  p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds; p.sc_f16 = scale_dtype == VNX_F16;
+  p.N = N; p.K = K; p.G = group;
+  const int64_t n = N * K;
+  hipLaunchKernelGGL(k_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p, 4, out, ldo);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_dequant_w8(const int8_t* wq, int64_t ldw, const float* scale, int64_t N, int64_t K, float* out,
+                   int64_t ldo, void* stream) {
+  if (!wq || !scale || !out || N < 0 || K <= 0 || ldw < K || ldo < K) return VNX_ERR_INVALID_ARG;
+  if (N == 0) return VNX_OK;
+  QGemvParams p{};
+  p.w = reinterpret_cast<const uint8_t*>(wq); p.ldw = ldw; p.sc = scale; p.lds = 1; p.sc_f16 = 0;
+  p.N = N; p.K = K; p.G = (int)K;
+  const int64_t n = N * K;
+  hipLaunchKernelGGL(k_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p, 8, out, ldo);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+}  // extern "C"

@@ -262,6 +262,87 @@ class HipBackend(DeviceBackend):
             _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "spec_accept")
         return dict(accept_len=alen, out_ids=out, flags=flags, lse_t=lse_t, lse_d=lse_d)
 
+    # ---- weight-only quantized GEMV -------------------------------------------
+    def _acts(self, x, K: int) -> torch.Tensor:
+        """(..., K) activations -> contiguous (B, K) fp16 on this device."""
+        t = _to_tensor(x, self._torch_device)
+        if t.shape[-1] != K:
+            raise ValueError(f"activations have {t.shape[-1]} features, the weight expects {K}")
+        return t.reshape(-1, K).to(torch.float16).contiguous()
+
+    @staticmethod
+    def _rows16(w: torch.Tensor) -> torch.Tensor:
+        """2-D byte weights whose rows start 16-byte aligned (pads the row pitch)."""
+        w = w.contiguous()
+        if w.stride(0) % 16 == 0 and w.data_ptr() % 16 == 0:
+            return w
+        ld = (w.shape[1] + 15) // 16 * 16
+        out = torch.zeros((w.shape[0], ld), dtype=w.dtype, device=w.device)
+        out[:, :w.shape[1]] = w
+        return out[:, :w.shape[1]]
+
+    def gemv_w4(self, x, wq, scales, group: int) -> torch.Tensor:
+        """y = x @ (q * s)^T for packed int4 wq (N, K/2) and scales (N, K/group)
+        (fp16 or fp32); returns (..., N) fp32 (vnx_gemv_w4)."""
+        dev = self._torch_device
+        w = self._rows16(_to_tensor(wq, dev, torch.uint8))
+        sc = _to_tensor(scales, dev)
+        if sc.dtype not in (torch.float16, torch.float32):
+            sc = sc.to(torch.float32)
+        sc = sc.reshape(w.shape[0], -1).contiguous()
+        N, K = w.shape[0], 2 * w.shape[1]
+        lead = _to_tensor(x, dev).shape[:-1]
+        x2 = self._acts(x, K)
+        B = x2.shape[0]
+        y = torch.empty((B, N), dtype=torch.float32, device=dev)
+        sdt = _lib.VNX_F16 if sc.dtype == torch.float16 else _lib.VNX_F32
+        ws = self._workspace(self._L.vnx_gemv_workspace(B, N, K))
+        _lib.check(self._L.vnx_gemv_w4(_ptr(x2), K, _ptr(w), w.stride(0), _ptr(sc), sdt, sc.stride(0), B, N, K,
+                                       int(group), _ptr(y), N, _ptr(ws), ws.numel(),
+                                       ctypes.c_void_p(self._stream().cuda_stream)), "gemv_w4")
+        return y.reshape(*lead, N)
+
+    def gemv_w8(self, x, wq, scale) -> torch.Tensor:
+        """y = x @ (q * s)^T for int8 wq (N, K) and per-row fp32 scale (N,)."""
+        dev = self._torch_device
+        w = self._rows16(_to_tensor(wq, dev, torch.int8))
+        sc = _to_tensor(scale, dev, torch.float32).reshape(-1).contiguous()
+        N, K = w.shape
+        lead = _to_tensor(x, dev).shape[:-1]
+        x2 = self._acts(x, K)
+        B = x2.shape[0]
+        y = torch.empty((B, N), dtype=torch.float32, device=dev)
+        ws = self._workspace(self._L.vnx_gemv_workspace(B, N, K))
+        _lib.check(self._L.vnx_gemv_w8(_ptr(x2), K, _ptr(w), w.stride(0), _ptr(sc), B, N, K, _ptr(y), N,
+                                       _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)),
+                   "gemv_w8")
+        return y.reshape(*lead, N)
+
+    def dequant_w4(self, wq, scales, K: int, group: int) -> torch.Tensor:
+        dev = self._torch_device
+        w = _to_tensor(wq, dev, torch.uint8).contiguous()
+        sc = _to_tensor(scales, dev)
+        if sc.dtype not in (torch.float16, torch.float32):
+            sc = sc.to(torch.float32)
+        sc = sc.reshape(w.shape[0], -1).contiguous()
+        N = w.shape[0]
+        out = torch.empty((N, K), dtype=torch.float32, device=dev)
+        sdt = _lib.VNX_F16 if sc.dtype == torch.float16 else _lib.VNX_F32
+        _lib.check(self._L.vnx_dequant_w4(_ptr(w), w.stride(0), _ptr(sc), sdt, sc.stride(0), N, K, int(group),
+                                          _ptr(out), K, ctypes.c_void_p(self._stream().cuda_stream)),
+                   "dequant_w4")
+        return out
+
+    def dequant_w8(self, wq, scale) -> torch.Tensor:
+        dev = self._torch_device
+        w = _to_tensor(wq, dev, torch.int8).contiguous()
+        sc = _to_tensor(scale, dev, torch.float32).reshape(-1).contiguous()
+        N, K = w.shape
+        out = torch.empty((N, K), dtype=torch.float32, device=dev)
+        _lib.check(self._L.vnx_dequant_w8(_ptr(w), w.stride(0), _ptr(sc), N, K, _ptr(out), K,
+                                          ctypes.c_void_p(self._stream().cuda_stream)), "dequant_w8")
+        return out
+
     def greedy_verify(self, target, draft_ids, rows_t: int | None = None):
         """Greedy verify of every batch row (see vnx_greedy_verify).
         target (B, rows_t, V) (may be a strided slice of (B, T, V) logits).
