@@ -106,13 +106,18 @@ def bench_gemv(args):
     """weight-only INT4 (group 128, fp16 scales) and INT8
     (per-channel) GEMV, weights N(0, 0.02), fp16 activations N(0, 1), B in
     {1, 8, 32}.  bytes per launch = weight + scales + 2*B*K (fp16 x) + 4*B*N
-    (fp32 y); time = HIP events around each launch on the current stream."""
+    (fp32 y).  Time: the C entry point is called `steps` times back to back on
+    preallocated buffers, between two HIP events on its stream, so the small
+    FFN layers are timed on the GPU rather than on the Python launch path."""
+    import ctypes
     import numpy as np
     import torch
     from versenext_amd import get_backend
     from versenext_amd import quant as VQ
+    from versenext_amd import _lib
 
     hip = get_backend("rocm:0")
+    L = _lib.lib()
     dev = hip.torch_device
     g = torch.Generator(device=dev)
     g.manual_seed(20)
@@ -125,22 +130,30 @@ def bench_gemv(args):
             wq, sc = packed[qtype]
             for B in (1, 8, 32):
                 x = (torch.randn((B, K), generator=g, device=dev)).to(torch.float16)
-                if qtype == "int8":
-                    fn = lambda: hip.gemv_w8(x, wq, sc)  # noqa: E731
-                else:
-                    fn = lambda: hip.gemv_w4(x, wq, sc, 128)  # noqa: E731
-                for _ in range(args.warmup):
-                    fn()
-                torch.cuda.synchronize()
-                evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                       for _ in range(args.steps)]
+                y = torch.empty((B, N), dtype=torch.float32, device=dev)
+                ws = torch.zeros(max(256, L.vnx_gemv_workspace(B, N, K)), dtype=torch.uint8, device=dev)
                 stream = torch.cuda.current_stream(dev)
-                for e0, e1 in evs:
-                    e0.record(stream)
-                    fn()
-                    e1.record(stream)
+                st = ctypes.c_void_p(stream.cuda_stream)
+                P = ctypes.c_void_p
+                if qtype == "int8":
+                    call, argv = L.vnx_gemv_w8, (P(x.data_ptr()), K, P(wq.data_ptr()), wq.stride(0),
+                                                 P(sc.data_ptr()), B, N, K, P(y.data_ptr()), N,
+                                                 P(ws.data_ptr()), ws.numel(), st)
+                else:
+                    call, argv = L.vnx_gemv_w4, (P(x.data_ptr()), K, P(wq.data_ptr()), wq.stride(0),
+                                                 P(sc.data_ptr()), _lib.VNX_F16, sc.stride(0), B, N, K, 128,
+                                                 P(y.data_ptr()), N, P(ws.data_ptr()), ws.numel(), st)
+                _lib.check(call(*argv), "gemv")
+                for _ in range(args.warmup):
+                    call(*argv)
                 torch.cuda.synchronize()
-                us = float(np.mean([e0.elapsed_time(e1) for e0, e1 in evs])) * 1e3
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(args.steps):
+                    call(*argv)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / args.steps
                 nbytes = VQ.weight_bytes(qtype, N, K) + 2 * B * K + 4 * B * N
                 gbs = nbytes / (us * 1e-6) / 1e9
                 rows.append({"shape": name, "N": N, "K": K, "qtype": qtype, "B": B, "us": round(us, 2),

@@ -202,6 +202,55 @@ int vnx_dequant_w4(const uint8_t* wq, int64_t ldw, const void* scales, int scale
 int vnx_dequant_w8(const int8_t* wq, int64_t ldw, const float* scale, int64_t N, int64_t K,
                    float* out, int64_t ldo, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Tree-verify attention over a KV cache.
+ * For batch row b, query head h and tree node i (i < N):
+ *   out[b,h,i,:] = sum_j softmax_j(scale * q[b,h,i,:] . k_j + mask_ij) v_j
+ * over the Tp prefix rows of the cache (all visible) followed by the N tree
+ * rows, tree row j visible to node i iff bit j of anc[b*anc_batch_stride + i]
+ * is set (ancestors-or-self; a chain tree gives causal attention).  Query head
+ * h reads kv head h / (H / Hkv).  This is DeviceBackend.attention
+ * (packages/verse_torch/verse_torch/device.py:260-270, scale 1/sqrt(d), an
+ * additive 0 / -inf mask) over the cache concatenated with the new rows as
+ * TriSparse does (packages/verse_nex/verse_nex/tri_sparse_attn.py:558-575),
+ * and the SDPA call of TorchBackend.attention (backend_torch.py:356-379).
+ * q (B,H,N,d), caches (B,Hkv,Tp,d), tree rows (B,Hkv,N,d): bf16 with the head
+ * dimension contiguous and strides {batch, head, row} in elements (multiples
+ * of 8, pointers 16-byte aligned).  The tree rows may live inside the cache
+ * (k_tree = k_cache + Tp*row stride).  out (B,H,N,d): fp32 or bf16 (round to
+ * nearest even), strides multiples of 4.  d in {64, 128}; 1 <= N <= 64.
+ * A node that sees no key (Tp == 0 and an empty mask word) gets zeros.
+ * The workspace (vnx_tree_attn_workspace bytes, no initialisation) holds the
+ * per-split partials when the keys are split over several workgroups.
+ * ------------------------------------------------------------------------- */
+typedef struct vnx_tree_attn_args {
+  const void* q;              /* bf16 (B, H, N, d)                              */
+  int64_t q_strides[3];       /* batch, head, row                               */
+  const void* k_cache;        /* bf16 (B, Hkv, Tp, d); may be NULL when Tp == 0 */
+  const void* v_cache;
+  int64_t cache_strides[3];   /* shared by k_cache and v_cache                  */
+  const void* k_tree;         /* bf16 (B, Hkv, N, d)                            */
+  const void* v_tree;
+  int64_t tree_strides[3];    /* shared by k_tree and v_tree                    */
+  const uint64_t* anc;        /* (B, N) ancestor-or-self words                  */
+  int64_t anc_batch_stride;   /* 0: one tree shared by all batch rows           */
+  void* out;
+  int out_dtype;              /* VNX_F32 or VNX_BF16                            */
+  int64_t out_strides[3];
+  int B, H, Hkv, Tp, N, d;
+  float scale;                /* > 0; 1/sqrt(d) in the reference               */
+} vnx_tree_attn_args;
+
+size_t vnx_tree_attn_workspace(int B, int H, int Hkv, int N, int Tp, int d);
+
+int vnx_tree_attn(const vnx_tree_attn_args* args, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* The launch shape vnx_tree_attn uses: key splits, query groups (of at most
+ * 64 rows for d = 64, 32 for d = 128) and keys per split. */
+int vnx_tree_attn_plan(int B, int H, int Hkv, int N, int Tp, int d, int* splits, int* groups,
+                       int* chunk);
+
 #ifdef __cplusplus
 }
 #endif

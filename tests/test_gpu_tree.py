@@ -1,0 +1,162 @@
+"""GPU parity of the tree-verify attention kernel (vnx_tree_attn) against
+oracle/tree.py.
+
+Bar: with fp32 output, |out - ref| <= RTOL * sum_j p_j |v_j| per element,
+where ref is the fp64 attention of the same bf16 inputs.  The kernel's error
+sources are the fp32 dot products (exact bf16 x bf16 products, fp32 sums),
+exp2 on the transcendental unit, and P carried as bf16 hi + lo parts
+(relative error <= 2^-17), each well under 1e-5 of the magnitude the
+rounding acts on, so RTOL = 2e-5 leaves a factor of ~4 over the worst case
+measured.  With bf16 output the result is additionally rounded once:
+|out - ref| <= 2^-8 |ref| + RTOL * mag.  (The north star's bf16 bar is 2e-2.)"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tree as OT
+from versenext_amd import _lib
+from versenext_amd import tree as T
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 2e-5
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _bf16(rng, shape, std=1.0):
+    return torch.from_numpy(rng.normal(0, std, shape).astype(np.float32)).to(torch.bfloat16)
+
+
+def _np(t):
+    return t.float().cpu().numpy() if t is not None else None
+
+
+def _check(out, ref, mag, bf16=False):
+    o = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(o - ref)
+    tol = RTOL * mag + (2.0 ** -8 * np.abs(ref) if bf16 else 0.0)
+    worst = float(np.max(err / (mag + 1e-300)))
+    assert np.all(err <= tol + 1e-30), f"worst err / mag = {worst:.3e}"
+    return worst
+
+
+def _run(hip, B, H, Hkv, N, Tp, d, parent=None, seed=0, out_dtype=torch.float32, per_batch=False,
+         cache_extra=0, inplace=False, std=1.0):
+    _say(f"tree_attn B={B} H={H} Hkv={Hkv} N={N} Tp={Tp} d={d} out={out_dtype} per_batch={per_batch} "
+         f"cache_extra={cache_extra} inplace={inplace}")
+    rng = np.random.default_rng(seed)
+    par = T.tree_from_branching((4, 3, 2)) if parent is None else np.asarray(parent, np.int32)
+    assert par.size == N
+    q = _bf16(rng, (B, H, N, d), std)
+    Tcap = Tp + N + cache_extra
+    kbuf = _bf16(rng, (B, Hkv, Tcap, d), std)
+    vbuf = _bf16(rng, (B, Hkv, Tcap, d))
+    dev = hip.torch_device
+    kbuf, vbuf, q = kbuf.to(dev), vbuf.to(dev), q.to(dev)
+    if inplace:  # tree rows written into the cache right after the prefix
+        kc, vc = kbuf[:, :, :Tp], vbuf[:, :, :Tp]
+        kt, vt = kbuf[:, :, Tp:Tp + N], vbuf[:, :, Tp:Tp + N]
+    else:
+        kc, vc = kbuf[:, :, :Tp], vbuf[:, :, :Tp]
+        kt = _bf16(rng, (B, Hkv, N, d), std).to(dev)
+        vt = _bf16(rng, (B, Hkv, N, d)).to(dev)
+    if per_batch:
+        words = np.stack([T.ancestor_words(par if b % 2 == 0 else T.chain(N)) for b in range(B)])
+    else:
+        words = T.ancestor_words(par)
+    out = hip.tree_attention(q, kc if Tp else None, vc if Tp else None, kt, vt, words, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref, mag = OT.tree_attention(_np(q), _np(kc) if Tp else None, _np(vc) if Tp else None, _np(kt), _np(vt),
+                                 words)
+    worst = _check(out, ref, mag, bf16=out_dtype == torch.bfloat16)
+    _say(f"  worst err / sum p|v| = {worst:.2e}")
+    return worst
+
+
+def _plan(B, H, Hkv, N, Tp, d):
+    import ctypes
+    s, g, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(_lib.lib().vnx_tree_attn_plan(B, H, Hkv, N, Tp, d, ctypes.byref(s), ctypes.byref(g),
+                                             ctypes.byref(c)), "plan")
+    return s.value, g.value, c.value
+
+
+def test_config3_shape_fp32(hip):
+    """B 16, 16 heads x 64, KV prefix 2048, tree (4,3,2)."""
+    _run(hip, 16, 16, 16, 40, 2048, 64, seed=10)
+
+
+def test_config3_shape_bf16_out(hip):
+    _run(hip, 4, 16, 16, 40, 2048, 64, seed=11, out_dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("H,Hkv,N,Tp", [(16, 8, 40, 512), (32, 4, 16, 200), (8, 1, 40, 96)])
+def test_gqa_query_groups(hip, H, Hkv, N, Tp):
+    par = T.tree_from_branching((4, 3, 2)) if N == 40 else T.tree_from_branching((4, 3))
+    _run(hip, 2, H, Hkv, N, Tp, 64, parent=par, seed=H + N)
+
+
+@pytest.mark.parametrize("H,Hkv,N,Tp", [(4, 2, 20, 300), (2, 2, 7, 33), (8, 2, 64, 0)])
+def test_head_dim_128(hip, H, Hkv, N, Tp):
+    rng = np.random.default_rng(N)
+    par = np.array([-1] + [int(rng.integers(-1, i)) for i in range(1, N)], np.int32)
+    _run(hip, 2, H, Hkv, N, Tp, 128, parent=par, seed=N + 1)
+
+
+@pytest.mark.parametrize("N,Tp", [(64, 0), (1, 77), (7, 1000), (33, 31), (64, 4096), (2, 1)])
+def test_edge_sizes(hip, N, Tp):
+    rng = np.random.default_rng(N * 7 + Tp)
+    par = np.array([-1] + [int(rng.integers(-1, i)) for i in range(1, N)], np.int32)
+    _run(hip, 3, 4, 2, N, Tp, 64, parent=par, seed=N + Tp)
+
+
+def test_chain_tree_per_batch_and_strided_cache(hip):
+    _run(hip, 4, 4, 4, 40, 700, 64, per_batch=True, cache_extra=100, seed=3)
+    _run(hip, 4, 4, 4, 40, 700, 64, inplace=True, cache_extra=64, seed=4)
+
+
+def test_splits_cover_one_and_many(hip):
+    assert _plan(64, 16, 16, 40, 2048, 64)[0] == 1
+    s, g, c = _plan(1, 1, 1, 40, 8192, 64)
+    assert s > 8 and g == 1
+    assert _plan(1, 2, 1, 40, 64, 64)[1] == 2  # 80 query rows: two groups
+    _run(hip, 64, 16, 16, 40, 2048, 64, seed=5)
+    _run(hip, 1, 1, 1, 40, 8192, 64, seed=6)
+
+
+def test_large_scores(hip):
+    """Scores of tens of units: the online max rescaling must hold."""
+    _run(hip, 2, 4, 4, 40, 1024, 64, seed=8, std=3.0)
+
+
+def test_attention_entry_point(hip):
+    """DeviceBackend.attention with a tree mask / no mask runs the kernel."""
+    rng = np.random.default_rng(12)
+    B, H, N, Tp, d = 2, 4, 12, 100, 64
+    par = T.tree_from_branching((3, 3))
+    dev = hip.torch_device
+    q = _bf16(rng, (B, H, N, d)).to(dev)
+    k = _bf16(rng, (B, H, Tp + N, d)).to(dev)
+    v = _bf16(rng, (B, H, Tp + N, d)).to(dev)
+    words = T.ancestor_words(par)
+    for mask, w in ((T.mask_from_words(words, Tp), words), (None, np.full(N, (1 << N) - 1, np.uint64))):
+        out = hip.attention(q, k, v, mask)
+        assert out.dtype == torch.bfloat16 and out.shape == (B, H, N, d)
+        ref, mag = OT.tree_attention(_np(q), _np(k[:, :, :Tp]), _np(v[:, :, :Tp]), _np(k[:, :, Tp:]),
+                                     _np(v[:, :, Tp:]), w)
+        _check(out, ref, mag, bf16=True)
+
+
+def test_rejects_bad_arguments(hip):
+    dev = hip.torch_device
+    z = lambda *s: torch.zeros(s, dtype=torch.bfloat16, device=dev)  # noqa: E731
+    with pytest.raises(ValueError):  # 65 nodes
+        hip.tree_attention(z(1, 1, 65, 64), None, None, z(1, 1, 65, 64), z(1, 1, 65, 64),
+                           np.ones(65, np.uint64))
+    with pytest.raises(ValueError):  # head dim 96
+        hip.tree_attention(z(1, 1, 4, 96), None, None, z(1, 1, 4, 96), z(1, 1, 4, 96), np.ones(4, np.uint64))
+    with pytest.raises(ValueError):  # 3 query heads over 2 kv heads
+        hip.tree_attention(z(1, 3, 4, 64), None, None, z(1, 2, 4, 64), z(1, 2, 4, 64), np.ones(4, np.uint64))

@@ -64,6 +64,27 @@ SIGNATURES = {
                                  _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
 }
 
+
+
+class TreeAttnArgs(ctypes.Structure):
+    """vnx_tree_attn_args (include/vnx.h)."""
+    _fields_ = [
+        ("q", _vp), ("q_strides", _c_i64 * 3),
+        ("k_cache", _vp), ("v_cache", _vp), ("cache_strides", _c_i64 * 3),
+        ("k_tree", _vp), ("v_tree", _vp), ("tree_strides", _c_i64 * 3),
+        ("anc", _vp), ("anc_batch_stride", _c_i64),
+        ("out", _vp), ("out_dtype", _int), ("out_strides", _c_i64 * 3),
+        ("B", _int), ("H", _int), ("Hkv", _int), ("Tp", _int), ("N", _int), ("d", _int),
+        ("scale", _f32),
+    ]
+
+
+SIGNATURES.update({
+    "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),
+    "vnx_tree_attn": (_int, [ctypes.POINTER(TreeAttnArgs), _vp, _c_sz, _vp]),
+    "vnx_tree_attn_plan": (_int, [_int, _int, _int, _int, _int, _int, _vp, _vp, _vp]),
+})
+
 _lib = None
 _lock = threading.Lock()
 

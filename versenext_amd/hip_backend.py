@@ -343,6 +343,111 @@ class HipBackend(DeviceBackend):
                                           ctypes.c_void_p(self._stream().cuda_stream)), "dequant_w8")
         return out
 
+    # ---- tree-verify attention ------------------------------------------------
+    def _heads_bf16(self, x, name: str) -> torch.Tensor:
+        """(B, heads, rows, d) bf16 view with the head dimension contiguous and
+        16-byte aligned strides (copied when it is not)."""
+        t = _to_tensor(x, self._torch_device, torch.bfloat16)
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be (B, heads, rows, d), got shape {tuple(t.shape)}")
+        if t.stride(-1) != 1 or t.data_ptr() % 16 or any(st % 8 for st in t.stride()[:3]):
+            t = t.contiguous()
+        return t
+
+    def tree_attention(self, q, k_cache, v_cache, k_tree, v_tree, anc, scale: float | None = None,
+                       out_dtype=torch.float32) -> torch.Tensor:
+        """Tree-verify attention (vnx_tree_attn).
+
+        q (B, H, N, d); k_cache / v_cache (B, Hkv, Tp, d) or None (Tp = 0);
+        k_tree / v_tree (B, Hkv, N, d); anc (N,) or (B, N) ancestor words
+        (tree.ancestor_words).  Inputs are read as bf16; returns (B, H, N, d)
+        in out_dtype (torch.float32 or torch.bfloat16)."""
+        dev = self._torch_device
+        qt = self._heads_bf16(q, "q")
+        kt = self._heads_bf16(k_tree, "k_tree")
+        vt = self._heads_bf16(v_tree, "v_tree")
+        B, H, N, d = qt.shape
+        if kt.shape != vt.shape or kt.shape[0] != B or kt.shape[2] != N or kt.shape[3] != d:
+            raise ValueError(f"tree rows {tuple(kt.shape)} / {tuple(vt.shape)} do not match q {tuple(qt.shape)}")
+        Hkv = kt.shape[1]
+        if kt.stride() != vt.stride():
+            kt, vt = kt.contiguous(), vt.contiguous()
+        if k_cache is None or v_cache is None:
+            if (k_cache is None) != (v_cache is None):
+                raise ValueError("pass both k_cache and v_cache, or neither")
+            kc = vc = None
+            Tp = 0
+            cstr = (0, 0, 0)
+        else:
+            kc = self._heads_bf16(k_cache, "k_cache")
+            vc = self._heads_bf16(v_cache, "v_cache")
+            if kc.shape != vc.shape or kc.shape[0] != B or kc.shape[1] != Hkv or kc.shape[3] != d:
+                raise ValueError(f"cache {tuple(kc.shape)} / {tuple(vc.shape)} does not match the tree rows")
+            if kc.stride() != vc.stride():
+                kc, vc = kc.contiguous(), vc.contiguous()
+            Tp = kc.shape[2]
+            cstr = kc.stride()[:3]
+            if Tp == 0:
+                kc = vc = None
+        a = anc.detach().cpu().numpy() if isinstance(anc, torch.Tensor) else np.asarray(anc)
+        a = np.ascontiguousarray(a.astype(np.uint64) if a.dtype != np.uint64 else a)
+        if a.shape not in ((N,), (B, N)):
+            raise ValueError(f"anc must be ({N},) or ({B}, {N}), got {a.shape}")
+        anc_t = torch.from_numpy(a.view(np.int64)).to(dev)
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("out_dtype must be torch.float32 or torch.bfloat16")
+        out = torch.empty((B, H, N, d), dtype=out_dtype, device=dev)
+        sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(d))
+        args = _lib.TreeAttnArgs()
+        args.q = qt.data_ptr()
+        args.q_strides[:] = list(qt.stride()[:3])
+        args.k_cache = kc.data_ptr() if kc is not None else None
+        args.v_cache = vc.data_ptr() if vc is not None else None
+        args.cache_strides[:] = list(cstr)
+        args.k_tree = kt.data_ptr()
+        args.v_tree = vt.data_ptr()
+        args.tree_strides[:] = list(kt.stride()[:3])
+        args.anc = anc_t.data_ptr()
+        args.anc_batch_stride = N if a.ndim == 2 else 0
+        args.out = out.data_ptr()
+        args.out_dtype = _lib.VNX_F32 if out_dtype == torch.float32 else _lib.VNX_BF16
+        args.out_strides[:] = list(out.stride()[:3])
+        args.B, args.H, args.Hkv, args.Tp, args.N, args.d = B, H, Hkv, Tp, N, d
+        args.scale = sc
+        ws = self._workspace(self._L.vnx_tree_attn_workspace(B, H, Hkv, N, Tp, d))
+        _lib.check(self._L.vnx_tree_attn(ctypes.byref(args), _ptr(ws), ws.numel(),
+                                         ctypes.c_void_p(self._stream().cuda_stream)), "tree_attn")
+        return out
+
+    def attention(self, q, k, v, mask=None):
+        """DeviceBackend.attention (device.py:260-270; TorchBackend's SDPA call,
+        backend_torch.py:356-379).  bf16 (B, H, Nq, d) queries over (B, Hkv, T, d)
+        keys with mask None, or an additive (Nq, T) token-tree mask (the first
+        T - Nq columns visible, the last Nq x Nq block 0 / -inf; see
+        tree.words_from_mask), run the tree-verify kernel and return bf16, as
+        SDPA does for bf16 inputs.  Anything else takes the generic composition
+        (matmul, vnx softmax, matmul)."""
+        from . import tree as _tree
+        words = None
+        if (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor) and isinstance(v, torch.Tensor)
+                and q.dtype == k.dtype == v.dtype == torch.bfloat16 and q.dim() == k.dim() == v.dim() == 4
+                and k.shape == v.shape and q.shape[-1] in (64, 128) and q.shape[-1] == k.shape[-1]
+                and q.shape[0] == k.shape[0] and q.shape[1] % k.shape[1] == 0):
+            nq, T = q.shape[2], k.shape[2]
+            if 1 <= nq <= _tree.MAX_NODES and T >= nq:
+                if mask is None:
+                    words = np.full(nq, (1 << nq) - 1, dtype=np.uint64)
+                else:
+                    m = mask.detach().float().cpu().numpy() if isinstance(mask, torch.Tensor) else np.asarray(mask)
+                    while m.ndim > 2 and m.shape[0] == 1:
+                        m = m[0]
+                    words = _tree.words_from_mask(m, T - nq)
+        if words is None:
+            return super().attention(q, k, v, mask)
+        Tp = k.shape[2] - q.shape[2]
+        kc, vc = (k[:, :, :Tp], v[:, :, :Tp]) if Tp else (None, None)
+        return self.tree_attention(q, kc, vc, k[:, :, Tp:], v[:, :, Tp:], words, out_dtype=torch.bfloat16)
+
     def greedy_verify(self, target, draft_ids, rows_t: int | None = None):
         """Greedy verify of every batch row (see vnx_greedy_verify).
         target (B, rows_t, V) (may be a strided slice of (B, T, V) logits).
