@@ -171,6 +171,120 @@ def bench_gemv(args):
     print(json.dumps(out), flush=True)
 
 
+def _timed(call, argv, steps, warmup, stream):
+    """Mean microseconds of `call(*argv)` issued back to back on `stream`
+    between two HIP events (torch's events on the library's launch stream)."""
+    import torch
+    from versenext_amd import _lib
+    _lib.check(call(*argv), call.__name__)
+    for _ in range(warmup):
+        call(*argv)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        call(*argv)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def bench_tree(args):
+    """tree verification.  B = 16, tree (4,3,2) = 40 nodes,
+    16 heads x 64 over a 2048-token bf16 KV prefix (N(0,1)); target logits
+    (16, 41, V) and draft logits (16, 17, V) fp32 N(0, 2).  Three kernels,
+    each timed alone with the C entry point called back to back on
+    preallocated buffers:
+      vnx_row_topk    expansion: node tokens = top-b of the parent's draft row,
+                      bytes 4*V*B*17;
+      vnx_tree_attn   ancestor-masked attention, bytes = K/V prefix 2*B*Hkv*Tp*d*2
+                      + q, out, tree K/V 4*B*H*N*d*2 (bf16 out);
+      vnx_tree_greedy argmax of the 41 target rows + longest accepted path,
+                      bytes 4*V*B*41."""
+    import numpy as np
+    import torch
+    from versenext_amd import get_backend, _lib
+    from versenext_amd import tree as TR
+
+    hip = get_backend("rocm:0")
+    L = _lib.lib()
+    dev = hip.torch_device
+    Bt, H, Hkv, d, Tp = 16, 16, 16, 64, 2048
+    par = TR.tree_from_branching((4, 3, 2))
+    N = par.size
+    g = torch.Generator(device=dev)
+    g.manual_seed(10)
+    q = torch.randn((Bt, H, N, d), generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.randn((Bt, Hkv, Tp, d), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((Bt, Hkv, Tp, d), generator=g, device=dev).to(torch.bfloat16)
+    kt = torch.randn((Bt, Hkv, N, d), generator=g, device=dev).to(torch.bfloat16)
+    vt = torch.randn((Bt, Hkv, N, d), generator=g, device=dev).to(torch.bfloat16)
+    tgt = torch.randn((Bt, N + 1, V), generator=g, device=dev) * 2.0
+    dft = torch.randn((Bt, 17, V), generator=g, device=dev) * 2.0
+    stream = torch.cuda.current_stream(dev)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    P = ctypes.c_void_p
+    rows = []
+
+    # expansion: top-b of the 17 parent draft rows (b = 4, the widest level)
+    tok = hip.expand_tree(dft, par).contiguous()
+    ids = torch.empty((Bt * 17, 4), dtype=torch.int64, device=dev)
+    ws_k = torch.zeros(L.vnx_row_topk_workspace(Bt * 17, V, 4), dtype=torch.uint8, device=dev)
+    us = _timed(L.vnx_row_topk, (P(dft.data_ptr()), _lib.VNX_F32, Bt * 17, V, V, 4, P(ids.data_ptr()), None, 4,
+                                 P(ws_k.data_ptr()), ws_k.numel(), st), args.steps, args.warmup, stream)
+    nb = 4 * V * Bt * 17
+    rows.append({"kernel": "vnx_row_topk (b=4)", "us": round(us, 2), "bytes": nb,
+                 "GB/s": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+
+    # attention
+    words = torch.from_numpy(TR.ancestor_words(par).view(np.int64)).to(dev)
+    out = torch.empty((Bt, H, N, d), dtype=torch.bfloat16, device=dev)
+    a = _lib.TreeAttnArgs()
+    a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
+    a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = list(kc.stride()[:3])
+    a.k_tree = kt.data_ptr(); a.v_tree = vt.data_ptr(); a.tree_strides[:] = list(kt.stride()[:3])
+    a.anc = words.data_ptr(); a.anc_batch_stride = 0
+    a.out = out.data_ptr(); a.out_dtype = _lib.VNX_BF16; a.out_strides[:] = list(out.stride()[:3])
+    a.B, a.H, a.Hkv, a.Tp, a.N, a.d = Bt, H, Hkv, Tp, N, d
+    a.scale = 1.0 / float(np.sqrt(d))
+    ws_a = torch.zeros(max(256, L.vnx_tree_attn_workspace(Bt, H, Hkv, N, Tp, d)), dtype=torch.uint8, device=dev)
+    us = _timed(L.vnx_tree_attn, (ctypes.byref(a), P(ws_a.data_ptr()), ws_a.numel(), st), args.steps,
+                args.warmup, stream)
+    nb = 2 * Bt * Hkv * Tp * d * 2 + 4 * Bt * H * N * d * 2
+    flop = 4 * Bt * H * N * (Tp + N) * d
+    attn = {"kernel": "vnx_tree_attn", "us": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
+            "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4), "TFLOP/s": round(flop / us / 1e6, 2)}
+    rows.append(attn)
+
+    # greedy path over the target rows
+    alen = torch.empty(Bt, dtype=torch.int32, device=dev)
+    best = torch.empty(Bt, dtype=torch.int32, device=dev)
+    oids = torch.empty((Bt, N + 1), dtype=torch.int64, device=dev)
+    ws_g = torch.zeros(L.vnx_tree_greedy_workspace(Bt, N, V), dtype=torch.uint8, device=dev)
+    parc = np.ascontiguousarray(par, dtype=np.int32)
+    us = _timed(L.vnx_tree_greedy, (P(tgt.data_ptr()), _lib.VNX_F32, Bt, N, V, V, (N + 1) * V, P(tok.data_ptr()), N,
+                                    parc.ctypes.data_as(P), P(alen.data_ptr()), P(best.data_ptr()),
+                                    P(oids.data_ptr()), None, P(ws_g.data_ptr()), ws_g.numel(), st),
+                args.steps, args.warmup, stream)
+    nb = 4 * V * Bt * (N + 1)
+    greedy = {"kernel": "vnx_tree_greedy", "us": round(us, 2), "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
+              "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    rows.append(greedy)
+    total_us = sum(r["us"] for r in rows)
+    total_b = sum(r["bytes"] for r in rows)
+    out_line = {"metric": "tree verification HBM GB/s (config 3: expansion + attention + greedy path)",
+                "value": round(total_b / total_us / 1e3, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "ms_per_step": round(total_us / 1e3, 4), "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": "bf16 attention / f32 logits",
+                "data": "synthetic",
+                "config": {"workload": "BASELINE config 3: tree verification", "batch": Bt, "tree": [4, 3, 2],
+                           "nodes": N, "heads": H, "kv_heads": Hkv, "head_dim": d, "kv_prefix": Tp, "vocab": V},
+                "roofline": {"bound": "hbm", "achieved": greedy["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": greedy["frac"], "traffic": None, "kernel": "vnx_tree_greedy"},
+                "accept_len": alen.cpu().tolist(), "results": rows}
+    print(json.dumps(out_line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,8 +293,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
-    ap.add_argument("--workload", default="accept", choices=("accept", "gemv"),
-                    help="accept: BASELINE config 2 (the bench line); gemv: config 4")
+    ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree"),
+                    help="accept: BASELINE config 2 (the bench line); gemv: config 4; tree: config 3")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
@@ -188,6 +302,9 @@ def main():
         sys.exit(2)
     if args.workload == "gemv":
         bench_gemv(args)
+        return
+    if args.workload == "tree":
+        bench_tree(args)
         return
 
     import numpy as np

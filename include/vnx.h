@@ -251,6 +251,44 @@ int vnx_tree_attn(const vnx_tree_attn_args* args, void* workspace, size_t worksp
 int vnx_tree_attn_plan(int B, int H, int Hkv, int N, int Tp, int d, int* splits, int* groups,
                        int* chunk);
 
+/* ---------------------------------------------------------------------------
+ * Greedy tree verification: the reference's greedy rule on a token tree.
+ * target: B x (N+1) rows at target + b*sb + i*ld (row 0: the prediction after
+ * the last committed token, row 1+n: after tree node n); tokens (B, N) int64,
+ * row pitch ld_tok; parent: a HOST array of N int32 (BFS order, parent[n] <
+ * n, -1 for the root's children) shared by all batch rows, 1 <= N <= 64.
+ * Node n is accepted iff tokens[b,n] == argmax(target row of its parent)
+ * (numpy.argmax order) and its parent is accepted.  accept_len[b] = depth of
+ * the deepest accepted node (lowest index among equally deep; 0 if none),
+ * best[b] = that node or -1 (may be NULL), out_ids (B, N+1) = its root path,
+ * the argmax of its own row (row 0 when none) as the bonus token, then -1;
+ * pred (B, N+1) = the row argmaxes (may be NULL).
+ * A chain tree (parent[n] = n-1) is the reference's verify + prefix rule
+ * (speculative.py:218-223, :277-287) with the bonus token of the full match.
+ * ------------------------------------------------------------------------- */
+size_t vnx_tree_greedy_workspace(int64_t B, int N, int64_t V);
+
+int vnx_tree_greedy(const void* target, int dtype, int64_t B, int N, int64_t V, int64_t ld, int64_t sb,
+                    const int64_t* tokens, int64_t ld_tok, const int32_t* parent, int32_t* accept_len,
+                    int32_t* best, int64_t* out_ids, int64_t* pred, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Row top-b (tree expansion): ids (rows, ldo) int64 = the b best ids of each
+ * row of raw logits (row pitch ld), value descending, ties to the lower id,
+ * NaN above every number (the numpy.argmax order, so b = 1 is argmax);
+ * vals (rows, ldo) fp32 their values (may be NULL).  1 <= b <= 16, b <= V.
+ * Replaces the top-k selection of Sampler.sample (np.partition,
+ * packages/verse_infra/verse_infra/verse_inference/sampler.py:98-102) and of
+ * _generate_with_logits (np.argpartition, cometspark.py:896-904) where a tree
+ * draft needs the ids themselves, in a fixed order.
+ * ------------------------------------------------------------------------- */
+size_t vnx_row_topk_workspace(int64_t rows, int64_t V, int b);
+
+int vnx_row_topk(const void* logits, int dtype, int64_t rows, int64_t V, int64_t ld, int b,
+                 int64_t* ids, float* vals, int64_t ldo, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

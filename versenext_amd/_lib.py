@@ -83,6 +83,11 @@ SIGNATURES.update({
     "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),
     "vnx_tree_attn": (_int, [ctypes.POINTER(TreeAttnArgs), _vp, _c_sz, _vp]),
     "vnx_tree_attn_plan": (_int, [_int, _int, _int, _int, _int, _int, _vp, _vp, _vp]),
+    "vnx_tree_greedy_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
+    "vnx_tree_greedy": (_int, [_vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp,
+                               _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "vnx_row_topk_workspace": (_c_sz, [_c_i64, _c_i64, _int]),
+    "vnx_row_topk": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _vp, _c_i64, _vp, _c_sz, _vp]),
 })
 
 _lib = None

@@ -473,5 +473,69 @@ class HipBackend(DeviceBackend):
             ctypes.c_void_p(self._stream().cuda_stream)), "greedy_verify")
         return acc.bool(), pred, alen, out
 
+    def tree_greedy(self, target, tokens, parent):
+        """Greedy tree verification (vnx_tree_greedy) of every batch row.
+
+        target (B, N+1, V) logits (row 0: after the last committed token,
+        row 1+n: after node n; may be a strided slice); tokens (B, N) node
+        tokens; parent (N,) BFS parent array (tree.tree_from_branching).
+        Returns (accept_len (B,) int32, best (B,) int32, out_ids (B, N+1) int64,
+        pred (B, N+1) int64); out_ids holds the accepted root path, the bonus
+        argmax, then -1."""
+        from . import tree as _tree
+        dev = self._torch_device
+        par = np.ascontiguousarray(_tree.check_parents(parent), dtype=np.int32)
+        N = par.size
+        tok = _to_tensor(tokens, dev, torch.int64)
+        if tok.dim() != 2 or tok.shape[1] != N:
+            raise ValueError(f"tokens must be (B, {N}), got {tuple(tok.shape)}")
+        if tok.stride(1) != 1:
+            tok = tok.contiguous()
+        B = tok.shape[0]
+        tg = self._rows3d(target, N + 1)
+        if tg.shape[0] != B:
+            raise ValueError(f"batch mismatch: logits {tg.shape[0]} vs tokens {B}")
+        V = tg.shape[2]
+        alen = torch.empty(B, dtype=torch.int32, device=dev)
+        best = torch.empty(B, dtype=torch.int32, device=dev)
+        out = torch.empty((B, N + 1), dtype=torch.int64, device=dev)
+        pred = torch.empty((B, N + 1), dtype=torch.int64, device=dev)
+        ws = self._workspace(self._L.vnx_tree_greedy_workspace(B, N, V))
+        _lib.check(self._L.vnx_tree_greedy(
+            _ptr(tg), _LOGIT_DTYPES[tg.dtype], B, N, V, tg.stride(1), tg.stride(0), _ptr(tok),
+            tok.stride(0), par.ctypes.data_as(ctypes.c_void_p), _ptr(alen), _ptr(best), _ptr(out),
+            _ptr(pred), _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "tree_greedy")
+        return alen, best, out, pred
+
+    def topk(self, x, b: int):
+        """(ids, vals): the b best ids of each row (vnx_row_topk; value
+        descending, ties to the lower id, NaN first), shapes (..., b)."""
+        t = self._rows2d(x)
+        rows, V = t.shape
+        lead = tuple(self._logits(x).shape[:-1])
+        ids = torch.empty((rows, b), dtype=torch.int64, device=self._torch_device)
+        vals = torch.empty((rows, b), dtype=torch.float32, device=self._torch_device)
+        ws = self._workspace(self._L.vnx_row_topk_workspace(rows, V, b))
+        _lib.check(self._L.vnx_row_topk(
+            _ptr(t), _LOGIT_DTYPES[t.dtype], rows, V, t.stride(0), int(b), _ptr(ids),
+            _ptr(vals), b, _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "row_topk")
+        return ids.reshape(*lead, b), vals.reshape(*lead, b)
+
+    def expand_tree(self, draft, parent):
+        """Node tokens (B, N) of a token tree: node n takes the r-th best id
+        of its parent's draft row (row 0 for the root, 1 + parent otherwise),
+        r = the number of earlier siblings of n.  draft (B, R, V)."""
+        from . import tree as _tree
+        par = _tree.check_parents(parent)
+        rows = np.where(par < 0, 0, par + 1)
+        rank = np.zeros(par.size, np.int64)
+        seen: dict = {}
+        for i, p in enumerate(par):
+            rank[i] = seen.get(int(p), 0)
+            seen[int(p)] = rank[i] + 1
+        ids, _ = self.topk(draft, int(rank.max()) + 1)
+        dev = self._torch_device
+        return ids[:, torch.from_numpy(rows).to(dev), torch.from_numpy(rank).to(dev)]
+
 
 __all__ = ["HipBackend"]
