@@ -285,6 +285,65 @@ def bench_tree(args):
     print(json.dumps(out_line), flush=True)
 
 
+def bench_lmhead(args):
+    """Verify-pass LM head (vnx_lm_head): logits (M, V) = x (M, 1024) . W^T with
+    M = B*(k+1) = 32*7 = 224 (config 5's verify batch), W the 248,320 x 1024
+    bf16 tied embedding (N(0, 0.02)), x bf16 N(0, 1).  bytes = 2*V*K (W) +
+    2*M*K (x) + out_bytes*M*V; flop = 2*M*V*K.  Timed back to back on
+    preallocated buffers; torch.matmul (hipBLASLt, bf16 out) on the same
+    operands is timed beside it."""
+    import torch
+    from versenext_amd import get_backend, _lib
+
+    hip = get_backend("rocm:0")
+    L = _lib.lib()
+    dev = hip.torch_device
+    M, Kd, Vh = 224, 1024, V
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    x = torch.randn((M, Kd), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((Vh, Kd), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    P = ctypes.c_void_p
+    rows = []
+    flop = 2 * M * Vh * Kd
+    for name, dt, esz in (("f32", _lib.VNX_F32, 4), ("bf16", _lib.VNX_BF16, 2)):
+        out = torch.empty((M, Vh), dtype=torch.float32 if esz == 4 else torch.bfloat16, device=dev)
+        us = _timed(L.vnx_lm_head, (P(x.data_ptr()), Kd, P(w.data_ptr()), Kd, M, Kd, Vh, P(out.data_ptr()), dt, Vh,
+                                    st), args.steps, args.warmup, stream)
+        nb = 2 * Vh * Kd + 2 * M * Kd + esz * M * Vh
+        rows.append({"kernel": f"vnx_lm_head ({name} out)", "us": round(us, 2), "bytes": nb,
+                     "GB/s": round(nb / us / 1e3, 1), "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "TFLOP/s": round(flop / us / 1e6, 1), "frac_mfma": round(flop / us / 1e6 / 2500.0, 4)})
+    # hipBLASLt reference point (bf16 out)
+    for _ in range(args.warmup):
+        torch.matmul(x, w.t())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        torch.matmul(x, w.t())
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    nb = 2 * Vh * Kd + 2 * M * Kd + 2 * M * Vh
+    rows.append({"kernel": "torch.matmul bf16 (hipBLASLt)", "us": round(us, 2), "bytes": nb,
+                 "GB/s": round(nb / us / 1e3, 1), "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+                 "TFLOP/s": round(flop / us / 1e6, 1), "frac_mfma": round(flop / us / 1e6 / 2500.0, 4)})
+    main_row = rows[0]
+    print(json.dumps({"metric": "verify LM head HBM GB/s (M=224, K=1024, V=248,320, fp32 logits)",
+                      "value": main_row["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+                      "warmup": args.warmup, "ms_per_step": round(main_row["us"] / 1e3, 4),
+                      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                      "data": "synthetic",
+                      "config": {"workload": "config 5 verify pass: tied LM head over B*(k+1) = 224 rows"},
+                      "roofline": {"bound": "hbm", "achieved": main_row["GB/s"], "peak": HBM_PEAK_GBS,
+                                   "unit": "GB/s", "frac": main_row["frac_hbm"], "traffic": None,
+                                   "kernel": "k_lm_head<14, false>"},
+                      "results": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,7 +352,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
-    ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree"),
+    ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree", "lmhead"),
                     help="accept: BASELINE config 2 (the bench line); gemv: config 4; tree: config 3")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -305,6 +364,9 @@ def main():
         return
     if args.workload == "tree":
         bench_tree(args)
+        return
+    if args.workload == "lmhead":
+        bench_lmhead(args)
         return
 
     import numpy as np

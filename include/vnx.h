@@ -289,6 +289,21 @@ int vnx_row_topk(const void* logits, int dtype, int64_t rows, int64_t V, int64_t
                  int64_t* ids, float* vals, int64_t ldo, void* workspace, size_t workspace_bytes,
                  void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Verify-pass LM head on the matrix cores: out (M, V) = x (M, K) . w (V, K)^T,
+ * x the final-norm hidden states of the verified positions (M = B*(k+1) <=
+ * 256), w the tied embedding table (one row per vocab id), both bf16 with K
+ * contiguous; fp32 accumulation; out fp32 (VNX_F32) or bf16 (VNX_BF16, round
+ * to nearest even), row pitch ldo.  K a multiple of 64; x, w 16-byte aligned
+ * with ldx, ldw multiples of 8; ldo a multiple of 4.  With out (B, k+1, V)
+ * contiguous the result feeds vnx_spec_accept / vnx_greedy_verify directly.
+ * Replaces the tied head CometSparkNexLM.head (cometspark.py:396-398, applied
+ * at :697 / :766; Linear.forward, packages/verse_torch/verse_torch/vnnn.py:
+ * 423-430) over the k+1 positions the verifier reads (speculative.py:218-220).
+ * ------------------------------------------------------------------------- */
+int vnx_lm_head(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t M, int64_t K, int64_t V,
+                void* out, int out_dtype, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -88,6 +88,7 @@ SIGNATURES.update({
                                _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "vnx_row_topk_workspace": (_c_sz, [_c_i64, _c_i64, _int]),
     "vnx_row_topk": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _vp, _c_i64, _vp, _c_sz, _vp]),
+    "vnx_lm_head": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
 })
 
 _lib = None

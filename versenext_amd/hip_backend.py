@@ -473,6 +473,38 @@ class HipBackend(DeviceBackend):
             ctypes.c_void_p(self._stream().cuda_stream)), "greedy_verify")
         return acc.bool(), pred, alen, out
 
+    def lm_head(self, x, weight, out=None, out_dtype=torch.float32) -> torch.Tensor:
+        """Verify-pass LM head (vnx_lm_head): x (..., K) . weight (V, K)^T on the
+        matrix cores, bf16 in, fp32 accumulate; returns (..., V) in out_dtype
+        (or writes `out`, a (rows, V) view with unit last stride)."""
+        dev = self._torch_device
+        xt = _to_tensor(x, dev, torch.bfloat16)
+        lead = tuple(xt.shape[:-1])
+        K = xt.shape[-1]
+        x2 = xt.reshape(-1, K)
+        if x2.stride(1) != 1 or x2.data_ptr() % 16 or x2.stride(0) % 8:
+            x2 = x2.contiguous()
+        wt = _to_tensor(weight, dev, torch.bfloat16)
+        if wt.dim() != 2 or wt.shape[1] != K:
+            raise ValueError(f"weight must be (V, {K}), got {tuple(wt.shape)}")
+        if wt.stride(1) != 1 or wt.data_ptr() % 16 or wt.stride(0) % 8:
+            wt = wt.contiguous()
+        M, V = x2.shape[0], wt.shape[0]
+        if out is None:
+            if out_dtype not in (torch.float32, torch.bfloat16):
+                raise ValueError("out_dtype must be torch.float32 or torch.bfloat16")
+            ldo = (V + 3) // 4 * 4
+            buf = torch.empty((M, ldo), dtype=out_dtype, device=dev)
+            o = buf[:, :V]
+        else:
+            o = out
+            if o.dim() != 2 or tuple(o.shape) != (M, V) or o.stride(1) != 1:
+                raise ValueError(f"out must be a ({M}, {V}) view with unit last stride")
+        _lib.check(self._L.vnx_lm_head(
+            _ptr(x2), x2.stride(0), _ptr(wt), wt.stride(0), M, K, V, _ptr(o),
+            _LOGIT_DTYPES[o.dtype], o.stride(0), ctypes.c_void_p(self._stream().cuda_stream)), "lm_head")
+        return o.reshape(*lead, V) if out is None else o
+
     def tree_greedy(self, target, tokens, parent):
         """Greedy tree verification (vnx_tree_greedy) of every batch row.
 
