@@ -344,15 +344,84 @@ def bench_lmhead(args):
                       "results": rows}), flush=True)
 
 
+E2E_B, E2E_K, E2E_T0, E2E_NEW, E2E_TEMP = 32, 6, 512, 256, 0.8
+
+
+def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, seed=0):
+    """BASELINE config 5 models on the GPU: the CometSparkV05 mate target
+    (random init, bf16) and a 2-layer mate-width draft with INT4 group-128
+    weights and head, caches for T0 + n_new + 2(k+1) positions."""
+    import torch
+    from versenext_amd import model as VM
+    dev = hip.torch_device
+    cap = T0 + n_new + 2 * (k + 1) + 16
+    tcfg, dcfg = VM.mate_target(), VM.mate_draft(draft_layers)
+    Wt = VM.init_weights(tcfg, seed=seed, device=dev)
+    target = VM.CometSparkGPU(tcfg, Wt, hip, batch=B, capacity=cap, dtype=torch.bfloat16)
+    del Wt
+    Wd = VM.init_weights(dcfg, seed=seed + 1, device=dev)
+    draft = VM.CometSparkGPU(dcfg, Wd, hip, batch=B, capacity=cap, dtype=torch.bfloat16, int4=True)
+    del Wd
+    torch.cuda.empty_cache()
+    return target, draft
+
+
+def bench_e2e(args):
+    """end-to-end speculative decode.  Target CometSparkV05
+    (D 1024, 20 layers = 5 MoD + 15 TriSparse, tied 248,320 head, random init,
+    bf16); draft: 2 mate-width TriSparse layers (D 1024, ffn 4096) with INT4
+    group-128 weights and tied head; k = 6, batch 32, 512-token uniform-random
+    prompts, 256 new tokens per sequence, temperature 0.8.
+    value = verified tokens / s = 32 * 256 committed tokens / wall time of the
+    decode rounds (prefill timed and reported separately)."""
+    import numpy as np
+    import torch
+    from versenext_amd import get_backend
+    from versenext_amd.e2e import SpecDecodeEngine
+
+    hip = get_backend("rocm:0")
+    dev = hip.torch_device
+    t_build = time.perf_counter()
+    target, draft = build_e2e(hip)
+    build_s = time.perf_counter() - t_build
+    g = torch.Generator(device=dev)
+    g.manual_seed(30)
+    prompts = torch.randint(0, V, (E2E_B, E2E_T0), generator=g, device=dev)
+    eng = SpecDecodeEngine(target, draft, hip, k=E2E_K, temperature=E2E_TEMP, seed=31)
+    runs = []
+    for r in range(max(1, args.e2e_runs)):
+        toks, st = eng.generate(prompts, E2E_NEW, phase_timing=(r == 0 and args.e2e_runs > 1))
+        runs.append(st)
+        print(json.dumps({"e2e_run": r, "rounds": st.rounds, "decode_s": round(st.decode_s, 4),
+                          "prefill_s": round(st.prefill_s, 4), "tokens_per_s": round(st.tokens_per_s, 1),
+                          "phase_s": {"draft": round(st.draft_s, 4), "verify": round(st.verify_s, 4),
+                                      "accept": round(st.accept_s, 4)}}), flush=True)
+    timed = runs[-1]
+    mean_tokens_round = float(np.mean(timed.per_round_tokens)) / E2E_B
+    out = {"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(timed.tokens_per_s, 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": timed.rounds, "warmup": len(runs) - 1,
+           "ms_per_step": round(timed.decode_s * 1e3 / timed.rounds, 3), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16 target / int4 draft / f32 logits",
+           "data": "synthetic (random-init weights, uniform-random prompts)",
+           "config": {"workload": "BASELINE config 5: end-to-end speculative decode", "batch": E2E_B, "k": E2E_K,
+                      "prompt": E2E_T0, "new_tokens": E2E_NEW, "temperature": E2E_TEMP,
+                      "target": target.cfg.name, "draft": draft.cfg.name + ", INT4 g128"},
+           "prefill_s": round(timed.prefill_s, 4), "build_s": round(build_s, 2),
+           "mean_tokens_per_round_per_seq": round(mean_tokens_round, 3),
+           "mean_accepted_per_round_per_seq": round(mean_tokens_round - 1.0, 3)}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--e2e-runs", type=int, default=2, help="e2e: decode runs (the last is reported)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
-    ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree", "lmhead"),
+    ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree", "lmhead", "e2e"),
                     help="accept: BASELINE config 2 (the bench line); gemv: config 4; tree: config 3")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -367,6 +436,9 @@ def main():
         return
     if args.workload == "lmhead":
         bench_lmhead(args)
+        return
+    if args.workload == "e2e":
+        bench_e2e(args)
         return
 
     import numpy as np

@@ -239,6 +239,16 @@ typedef struct vnx_tree_attn_args {
   int64_t out_strides[3];
   int B, H, Hkv, Tp, N, d;
   float scale;                /* > 0; 1/sqrt(d) in the reference               */
+  /* Ragged batches (per-sequence KV lengths, the commit / rollback of
+   * ParallelKVCache.batch_update / per_seq_lens, kv_cache_parallel.py:42-286):
+   * tp_batch, when not NULL, is a device array of B int32; batch row b then
+   * has min(max(tp_batch[b], 0), Tp) prefix rows (Tp is the maximum).  With
+   * tree_follows_prefix != 0 the tree rows of batch row b start right after
+   * its prefix: tree row j is read at k_tree + b*s0 + kvh*s1 + (tp_b + j)*s2
+   * (pass k_tree = k_cache and the cache strides to verify rows written into
+   * the cache in place). */
+  const int32_t* tp_batch;
+  int tree_follows_prefix;
 } vnx_tree_attn_args;
 
 size_t vnx_tree_attn_workspace(int B, int H, int Hkv, int N, int Tp, int d);

@@ -1,0 +1,216 @@
+"""CPU restatement of the CometSpark (VerseNex) language-model forward pass
+(test infrastructure only: the checker of versenext_amd/model.py, and the
+reference CPU path timed beside it).
+
+numpy float32, the whole sequence in parallel with no KV cache, the way the
+reference's verifier calls the model (speculative.py:202-213):
+- CometSparkV05LM.forward (spark/src/base_model.py:170-208): tok_emb(idx) x
+  sqrt(D), the blocks, the final RMSNorm, the tied head x @ tok_emb^T;
+- VerseNexBlock.forward (packages/verse_nex/verse_nex/cometspark.py:209-247);
+- RMSNorm (packages/verse_torch/verse_torch/vnnn.py:593-615 via
+  _normalize_kernel :468-508): x / sqrt(mean(x*x) + eps) * w;
+- TriSparseAttention.forward (packages/verse_nex/verse_nex/tri_sparse_attn.py
+  :536-613): projections, RoPE (:167-221), repeat_kv adjacent copies,
+  sliding-window path (:260-400; written here as one masked softmax over the
+  window, which the chunked form equals), global path (:469-495), ALiBi path
+  when use_alibi and T <= 1024 (:501-534), sigmoid gates (:585-608);
+- SwiGLUMLP (vnnn.py:779-807); MoDLayer / DensePart / Router / Expert
+  (packages/verse_nex/verse_nex/mod.py:142-213, :337-440, :466-803):
+  argsort(-logits)[:k] selection, softmax over the selected logits.
+
+Pinned by tests/test_oracle_model.py against golden vectors written by the
+reference itself (tests/golden/make_cometspark_small.py): the logits of the
+config-1 target for a 16-token prompt and its 128-token greedy stream.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F32 = np.float32
+
+
+def _rms(x, w, eps):
+    ms = (x * x).mean(axis=-1, keepdims=True)
+    return (x / np.sqrt(ms + F32(eps))) * w
+
+
+def _softmax(x, axis=-1):
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def _sigmoid(x):
+    return F32(1.0) / (F32(1.0) + np.exp(-x))
+
+
+def _silu(x):
+    return x * _sigmoid(x)
+
+
+def rope_tables(d, T, theta):
+    half = d // 2
+    i = np.arange(half, dtype=F32)
+    inv_freq = F32(1.0) / (F32(theta) ** (F32(2.0) * i / F32(d)))
+    ang = np.outer(np.arange(T, dtype=F32), inv_freq).astype(F32)
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], axis=-1).astype(F32)
+    sin = np.concatenate([np.sin(ang), np.sin(ang)], axis=-1).astype(F32)
+    return cos, sin
+
+
+def _rope(x, cos, sin):
+    """x (B, T, heads, d); rotate_half = concat(-x[half:], x[:half])."""
+    half = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    return x * cos[None, :, None, :] + rot * sin[None, :, None, :]
+
+
+def _attend(q, k, v, bias):
+    """softmax(q k^T / sqrt(d) + bias) v over (B, H, Tq, d) x (B|1, H, Tk, d)."""
+    scale = 1.0 / (q.shape[-1] ** 0.5)
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    if bias is not None:
+        s = s + bias
+    return _softmax(s) @ v
+
+
+def trisparse(W, p, cfg, x):
+    B, T, D = x.shape
+    H, Hkv = cfg.n_head, cfg.n_kv_head
+    d = D // H
+    rep = H // Hkv
+    q = (x @ W[p + "attn.wq.weight"].T).reshape(B, T, H, d)
+    k = (x @ W[p + "attn.wk.weight"].T).reshape(B, T, Hkv, d)
+    v = (x @ W[p + "attn.wv.weight"].T).reshape(B, T, Hkv, d)
+    if cfg.use_rope:
+        cos, sin = rope_tables(d, T, cfg.rope_theta)
+        q, k = _rope(q, cos, sin), _rope(k, cos, sin)
+    k = np.repeat(k, rep, axis=2).transpose(0, 2, 1, 3)
+    v = np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)
+    q = q.transpose(0, 2, 1, 3)
+    i = np.arange(T)[:, None]
+    j = np.arange(T)[None, :]
+    causal = j <= i
+    neg = F32(-1e9)
+    swa_mask = np.where(causal & ((i - j) < cfg.window_size), F32(0.0), neg).astype(F32)
+    swa = _attend(q, k, v, swa_mask[None, None])
+    g = W[p + "attn.global_tokens.weight"]
+    G = g.shape[0]
+    kg = np.repeat((g @ W[p + "attn.wk.weight"].T).reshape(1, G, Hkv, d), rep, axis=2).transpose(0, 2, 1, 3)
+    vg = np.repeat((g @ W[p + "attn.wv.weight"].T).reshape(1, G, Hkv, d), rep, axis=2).transpose(0, 2, 1, 3)
+    glob = _attend(q, kg, vg, None)
+    gate = _sigmoid(W[p + "attn.gate_logits"].astype(F32))
+    out = gate[0] * swa + gate[1] * glob
+    if cfg.use_alibi and T <= 1024:
+        slopes = (1.0 / (2.0 ** (np.arange(1, H + 1, dtype=F32) / H))).astype(F32)
+        dist = (i - j).astype(F32)
+        bias = np.where(causal[None], -slopes[:, None, None] * dist[None], neg).astype(F32)
+        out = out + gate[2] * _attend(q, k, v, bias[None])
+    out = out.transpose(0, 2, 1, 3).reshape(B, T, H * d)
+    return out @ W[p + "attn.proj.weight"].T
+
+
+def swiglu(x, wg, wu, wd):
+    return (_silu(x @ wg.T) * (x @ wu.T)) @ wd.T
+
+
+def _route(logits, k):
+    """argsort(-logits)[..., :k] and the softmax over the selected logits
+    (Router.forward, mod.py:337-440)."""
+    idx = np.argsort(-logits, axis=-1)[..., :k]
+    sel = np.take_along_axis(logits, idx, axis=-1)
+    return idx, _softmax(sel)
+
+
+def mod(W, p, cfg, x):
+    P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
+    pidx, pw = _route(x @ W[p + "ffn.part_router.gate.weight"].T, P)
+    out = np.zeros_like(x)
+    for q in range(P):
+        part_w = (pw * (pidx == q)).sum(axis=-1, keepdims=True)
+        rp = p + f"ffn.parts.{q}."
+        eidx, ew = _route(x @ W[rp + "router.gate.weight"].T, k)
+        comb = np.zeros_like(x)
+        for e in range(E):
+            we = (ew * (eidx == e)).sum(axis=-1)
+            mask = (eidx == e).any(axis=-1)
+            if not mask.any():
+                continue
+            ep = rp + f"experts.{e}."
+            ye = swiglu(x[mask], W[ep + "w_gate.weight"], W[ep + "w_up.weight"], W[ep + "w_down.weight"])
+            add = np.zeros_like(x)
+            add[mask] = ye * we[mask][:, None]
+            comb = comb + add
+        out = out + comb * part_w
+    return out
+
+
+def forward(W, cfg, idx, return_hidden=False):
+    """logits (B, T, V) float32 of the tokens idx (B, T)."""
+    idx = np.asarray(idx, dtype=np.int64)
+    if idx.ndim == 1:
+        idx = idx[None]
+    emb = W["tok_emb.weight"]
+    x = emb[idx].astype(F32)
+    if cfg.embedding_scale:
+        x = x * math.sqrt(cfg.dim)
+    x = x.astype(F32)
+    for i, kind in enumerate(cfg.layer_pattern):
+        p = f"blocks.{i}."
+        x = x + trisparse(W, p, cfg, _rms(x, W[p + "norm1.weight"], cfg.eps))
+        h = _rms(x, W[p + "norm2.weight"], cfg.eps)
+        if kind == "mod":
+            x = x + mod(W, p, cfg, h)
+        else:
+            x = x + swiglu(h, W[p + "ffn.w_gate.weight"], W[p + "ffn.w_up.weight"], W[p + "ffn.w_down.weight"])
+    x = _rms(x, W["norm.weight"], cfg.eps)
+    if return_hidden:
+        return x
+    return x @ emb.T
+
+
+def greedy_stream(W, cfg, prompt, n_new):
+    """The target's greedy continuation with a full re-forward per token (the
+    stream greedy speculative decoding reproduces, speculative.py:22)."""
+    seq = list(np.asarray(prompt, dtype=np.int64).reshape(-1))
+    out = []
+    for _ in range(n_new):
+        logits = forward(W, cfg, np.asarray(seq)[None])[0, -1]
+        t = int(np.argmax(logits))
+        out.append(t)
+        seq.append(t)
+    return np.asarray(out, dtype=np.int64)
+
+
+def spec_decode_greedy(Wt, cfg_t, Wd, cfg_d, prompt, n_new, k):
+    """The reference's greedy speculative decode, batch row 0
+    (SpeculativeDecoder.verify_then_commit, speculative.py:230-310): the draft
+    model proposes k tokens by greedy argmax (re-forwarding its context), the
+    target re-forwards [context, draft] and the longest prefix agreeing with
+    its argmax is committed plus the target's token at the first mismatch
+    (no bonus token when all k agree).  Returns (tokens, steps)."""
+    seq = list(np.asarray(prompt, dtype=np.int64).reshape(-1))
+    out = []
+    steps = 0
+    while len(out) < n_new:
+        ctx = list(seq)
+        draft = []
+        for _ in range(k):
+            t = int(np.argmax(forward(Wd, cfg_d, np.asarray(ctx)[None])[0, -1]))
+            draft.append(t)
+            ctx.append(t)
+        T = len(seq)
+        logits = forward(Wt, cfg_t, np.asarray(seq + draft)[None])[0]
+        pred = np.argmax(logits[T - 1:T - 1 + k], axis=-1)
+        n = 0
+        while n < k and draft[n] == int(pred[n]):
+            n += 1
+        acc = draft[:n] if n == k else draft[:n] + [int(pred[n])]
+        steps += 1
+        for t in acc:
+            if len(out) < n_new:
+                out.append(t)
+                seq.append(t)
+    return np.asarray(out, dtype=np.int64), steps

@@ -75,7 +75,7 @@ class TreeAttnArgs(ctypes.Structure):
         ("anc", _vp), ("anc_batch_stride", _c_i64),
         ("out", _vp), ("out_dtype", _int), ("out_strides", _c_i64 * 3),
         ("B", _int), ("H", _int), ("Hkv", _int), ("Tp", _int), ("N", _int), ("d", _int),
-        ("scale", _f32),
+        ("scale", _f32), ("tp_batch", _vp), ("tree_follows_prefix", _int),
     ]
 
 

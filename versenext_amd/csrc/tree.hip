@@ -54,6 +54,8 @@ struct TreeAttnParams {
   int64_t anc_sb;
   int B, H, Hkv, n_rep, Tp, N;
   int S, G, rows_per_group, chunk;  // key splits, query groups, keys per split
+  const int32_t* tp_batch;          // per-batch prefix rows (<= Tp), or NULL
+  int tree_follows_prefix;          // tree row j of batch b is tree row tp_b + j
   float c;                          // scale * log2(e)
 };
 
@@ -131,9 +133,13 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
   }
   __syncthreads();
 
+  // This batch row's prefix: Tp rows, or tp_batch[b] (clamped to [0, Tp])
+  // when the rows of a batch have different committed lengths.
+  int Tp = p.Tp;
+  if (p.tp_batch) Tp = min(max(p.tp_batch[b], 0), p.Tp);
   const int64_t cbase = b * p.c_sb + kvh * p.c_sh;
-  const int64_t tbase = b * p.t_sb + kvh * p.t_sh;
-  const int Tp = p.Tp, KT = p.Tp + p.N;
+  const int64_t tbase = b * p.t_sb + kvh * p.t_sh + (p.tree_follows_prefix ? (int64_t)Tp * p.t_sr : 0);
+  const int KT = Tp + p.N;
   // Row of key index `key` in K (or V): the prefix cache, then the tree rows;
   // keys past the end read tree row 0 (their scores are masked to -inf).
   auto krow = [&](int key, const uint16_t* cache, const uint16_t* tree) -> const uint16_t* {
@@ -447,6 +453,7 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   if (B == 0) return VNX_OK;
   if (!a->q || !a->k_tree || !a->v_tree || !a->anc || !a->out) return VNX_ERR_INVALID_ARG;
   if (Tp > 0 && (!a->k_cache || !a->v_cache)) return VNX_ERR_INVALID_ARG;
+  if (a->tp_batch && (reinterpret_cast<uintptr_t>(a->tp_batch) & 3u)) return VNX_ERR_INVALID_ARG;
   if (!(a->scale > 0.0f) || !__builtin_isfinite(a->scale)) return VNX_ERR_INVALID_ARG;
   if (a->anc_batch_stride < 0) return VNX_ERR_INVALID_ARG;
   // 16-byte loads of bf16 rows; 16-byte (fp32) / 8-byte (bf16) output stores.
@@ -479,6 +486,8 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   p.anc_sb = a->anc_batch_stride;
   p.B = B; p.H = H; p.Hkv = Hkv; p.n_rep = H / Hkv; p.Tp = Tp; p.N = N;
   p.S = pl.S; p.G = pl.G; p.rows_per_group = pl.rows_per_group; p.chunk = pl.chunk;
+  p.tp_batch = a->tp_batch;
+  p.tree_follows_prefix = a->tree_follows_prefix ? 1 : 0;
   p.c = (float)((double)a->scale * 1.4426950408889634);
   if (pl.S > 1) {
     Carve c(workspace);

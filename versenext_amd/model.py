@@ -1,0 +1,532 @@
+"""CometSpark (VerseNex) target and draft models on one MI355X, for end-to-end
+speculative decoding with an incremental (KV-cached) verify pass.
+
+Architecture (the reference's, restated for PyTorch-ROCm tensors):
+- CometSparkNexLM (packages/verse_nex/verse_nex/cometspark.py:294-449) with
+  the CometSparkV05LM embedding scale x sqrt(D) (spark/src/base_model.py:161,
+  :201-207): tok_emb -> blocks -> RMSNorm -> tied head;
+- VerseNexBlock (cometspark.py:209-247): x += attn(norm1(x)); x += ffn(norm2(x));
+  RMSNorm x / sqrt(mean(x^2) + 1e-6) * w (vnnn.py:593-615, :468-508);
+- TriSparseAttention (tri_sparse_attn.py:536-613): GQA projections, NeoX
+  rotate-half RoPE on q and k (:167-221), sigmoid(gate_logits) weighted sum of
+  a causal sliding-window path (window W), a path over the learnable global
+  sink tokens projected by wk / wv (:225-258, :469-495), and, when use_alibi
+  and the key count is at most 1024, a causal ALiBi path (:501-534);
+- FFN: SwiGLU w_down(silu(w_gate x) * w_up x) (vnnn.py:779-807) on
+  "trisparse" layers, MoD (mod.py:600-803) on "mod" layers: a soft part
+  router over all parts, inside each part a top-k expert router whose
+  softmax over the k selected logits weights SwiGLU experts.
+
+The incremental verify differs from the reference's only in what is
+recomputed: the reference re-runs the whole sequence without a KV cache
+(speculative.py:202-213) and reads logits at the k+1 verified positions; here
+every sequence keeps its own committed length in `lens` (the per-sequence
+lengths of ParallelKVCache, kv_cache_parallel.py:42-286), the k+1 new rows
+are written into the cache at lens[b] .. lens[b]+k, and a rejected suffix is
+rolled back by not advancing lens[b].  The rows the verifier reads see the
+same keys either way.
+
+Hot path on the gfx950 kernels of libvnx_hip.so: sliding-window and global
+attention of the new rows over the cache (vnx_tree_attn with per-row prefix
+lengths), the verify-pass LM head (vnx_lm_head), and the INT4 group-128
+draft GEMVs (vnx_gemv_w4).  Prefill, projections and FFN GEMMs run on
+PyTorch-ROCm (hipBLASLt / rocBLAS).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+from typing import Dict, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from . import quant as VQ
+
+
+# ---------------------------------------------------------------------------
+# Configurations
+# ---------------------------------------------------------------------------
+@dataclass
+class ModelConfig:
+    vocab_size: int
+    dim: int
+    n_layer: int
+    n_head: int
+    n_kv_head: int
+    layer_pattern: Sequence[str]
+    window_size: int
+    num_global_tokens: int
+    use_alibi: bool
+    use_rope: bool
+    rope_theta: float = 10000.0
+    num_dense_parts: int = 4
+    num_experts_per_part: int = 4
+    top_k: int = 2
+    expert_hidden: Optional[int] = None
+    mlp_hidden: Optional[int] = None
+    embedding_scale: bool = True
+    init_std: float = 0.02
+    eps: float = 1e-6
+    name: str = ""
+
+    def __post_init__(self):
+        self.layer_pattern = tuple(self.layer_pattern)
+        if len(self.layer_pattern) != self.n_layer:
+            raise ValueError("layer_pattern must have n_layer entries")
+        if any(k not in ("trisparse", "mod") for k in self.layer_pattern):
+            raise ValueError("layer kinds are 'trisparse' or 'mod'")
+        if self.dim % self.n_head or self.n_head % self.n_kv_head:
+            raise ValueError("dim % n_head and n_head % n_kv_head must be 0")
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.n_head
+
+    @property
+    def ffn_hidden(self) -> int:
+        """SwiGLUMLP hidden: 2/3 of 4*D rounded up to 64 (vnnn.py:794)."""
+        if self.mlp_hidden:
+            return int(self.mlp_hidden)
+        return int((4 * self.dim * 2 / 3 + 63) // 64) * 64
+
+    @property
+    def expert_hidden_eff(self) -> int:
+        """MoD expert hidden: floor(D*8/3/64)*64, at least 64 (mod.py:688)."""
+        if self.expert_hidden:
+            return int(self.expert_hidden)
+        return max(int(self.dim * 8 / 3 / 64) * 64, 64)
+
+
+def v02_pattern(n_layer: int, mod_every: int) -> list:
+    """_build_v02_pattern (cometspark.py:1347-1370): 'mod' at i % mod_every == 0."""
+    if mod_every < 1:
+        raise ValueError("mod_every must be >= 1")
+    return ["mod" if i % mod_every == 0 else "trisparse" for i in range(n_layer)]
+
+
+def mate_target() -> ModelConfig:
+    """CometSparkV05() (spark/src/base_model.py:760-838): the config-5 target."""
+    return ModelConfig(vocab_size=248320, dim=1024, n_layer=20, n_head=16, n_kv_head=8,
+                       layer_pattern=v02_pattern(20, 4), window_size=1024, num_global_tokens=128,
+                       use_alibi=False, use_rope=True, num_dense_parts=4, num_experts_per_part=4, top_k=2,
+                       name="CometSparkV05 (mate target)")
+
+
+def small_target() -> ModelConfig:
+    """CometSparkV05Small() (spark/src/base_model.py:842-918): the config-1 target."""
+    return ModelConfig(vocab_size=256, dim=64, n_layer=2, n_head=4, n_kv_head=2,
+                       layer_pattern=v02_pattern(2, 2), window_size=32, num_global_tokens=4,
+                       use_alibi=True, use_rope=False, num_dense_parts=2, num_experts_per_part=2, top_k=1,
+                       name="CometSparkV05Small (config-1 target)")
+
+
+def small_draft() -> ModelConfig:
+    """Config-1 draft: one 'trisparse' layer of the same family at D = 32."""
+    return ModelConfig(vocab_size=256, dim=32, n_layer=1, n_head=4, n_kv_head=2, layer_pattern=("trisparse",),
+                       window_size=32, num_global_tokens=4, use_alibi=True, use_rope=False,
+                       name="config-1 draft (1 x trisparse, D=32)")
+
+
+def mate_draft(n_layer: int = 2) -> ModelConfig:
+    """Config-5 draft: mate-width 'trisparse' layers (D = 1024, SwiGLU ffn 4096,
+    the config-4 GEMV shapes) with the tied 248,320-row head."""
+    return ModelConfig(vocab_size=248320, dim=1024, n_layer=n_layer, n_head=16, n_kv_head=8,
+                       layer_pattern=("trisparse",) * n_layer, window_size=1024, num_global_tokens=128,
+                       use_alibi=False, use_rope=True, mlp_hidden=4096,
+                       name=f"VerseNex draft ({n_layer} x trisparse, D=1024, ffn 4096)")
+
+
+# ---------------------------------------------------------------------------
+# Weights
+# ---------------------------------------------------------------------------
+def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
+    """Parameter names (the reference's module paths) and shapes."""
+    D, H, Hkv, d = cfg.dim, cfg.n_head, cfg.n_kv_head, cfg.head_dim
+    s = {"tok_emb.weight": (cfg.vocab_size, D), "norm.weight": (D,)}
+    for i, kind in enumerate(cfg.layer_pattern):
+        p = f"blocks.{i}."
+        s[p + "norm1.weight"] = (D,)
+        s[p + "norm2.weight"] = (D,)
+        s[p + "attn.wq.weight"] = (H * d, D)
+        s[p + "attn.wk.weight"] = (Hkv * d, D)
+        s[p + "attn.wv.weight"] = (Hkv * d, D)
+        s[p + "attn.proj.weight"] = (D, H * d)
+        s[p + "attn.global_tokens.weight"] = (cfg.num_global_tokens, D)
+        s[p + "attn.gate_logits"] = (3,)
+        if kind == "trisparse":
+            Hf = cfg.ffn_hidden
+            s[p + "ffn.w_gate.weight"] = (Hf, D)
+            s[p + "ffn.w_up.weight"] = (Hf, D)
+            s[p + "ffn.w_down.weight"] = (D, Hf)
+        else:
+            He, P, E = cfg.expert_hidden_eff, cfg.num_dense_parts, cfg.num_experts_per_part
+            s[p + "ffn.part_router.gate.weight"] = (P, D)
+            for q in range(P):
+                s[p + f"ffn.parts.{q}.router.gate.weight"] = (E, D)
+                for e in range(E):
+                    ep = p + f"ffn.parts.{q}.experts.{e}."
+                    s[ep + "w_gate.weight"] = (He, D)
+                    s[ep + "w_up.weight"] = (He, D)
+                    s[ep + "w_down.weight"] = (D, He)
+    return s
+
+
+def init_weights(cfg: ModelConfig, seed: int = 0, device="cpu") -> Dict[str, torch.Tensor]:
+    """Random-init fp32 weights with the reference's scheme
+    (CometSparkNexLM._init_weights, cometspark.py:455-481): every Linear /
+    Embedding ~ N(0, init_std), attn.proj and the trisparse w_down scaled by
+    1/sqrt(2*n_layer), RMSNorm weights 1, gate logits 0, global tokens
+    N(0, 0.02).  The values come from torch's generator (the reference draws
+    from numpy's legacy stream), so only the distribution is the reference's."""
+    g = torch.Generator(device=device)
+    g.manual_seed(int(seed))
+    res = 1.0 / math.sqrt(2 * cfg.n_layer)
+    out = {}
+    for name, shape in weight_shapes(cfg).items():
+        if name.endswith("norm1.weight") or name.endswith("norm2.weight") or name == "norm.weight":
+            t = torch.ones(shape, dtype=torch.float32, device=device)
+        elif name.endswith("gate_logits"):
+            t = torch.zeros(shape, dtype=torch.float32, device=device)
+        else:
+            t = torch.randn(shape, generator=g, dtype=torch.float32, device=device) * cfg.init_std
+            if name.endswith("attn.proj.weight") or (name.endswith("ffn.w_down.weight") and ".parts." not in name):
+                t = t * res
+        out[name] = t
+    return out
+
+
+def rope_tables(head_dim: int, max_len: int, theta: float):
+    """cos / sin tables of TriSparseAttention._build_rope_table
+    (tri_sparse_attn.py:167-180), computed in float32 as numpy does."""
+    half = head_dim // 2
+    i = np.arange(half, dtype=np.float32)
+    inv_freq = np.float32(1.0) / (np.float32(theta) ** (np.float32(2.0) * i / np.float32(head_dim)))
+    pos = np.arange(max_len, dtype=np.float32)
+    ang = np.outer(pos, inv_freq).astype(np.float32)
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], axis=-1).astype(np.float32)
+    sin = np.concatenate([np.sin(ang), np.sin(ang)], axis=-1).astype(np.float32)
+    return cos, sin
+
+
+def alibi_slopes(n_head: int) -> np.ndarray:
+    """m_h = 1 / 2^(h / n_head), h = 1..n_head (tri_sparse_attn.py:150-153)."""
+    return (1.0 / (2.0 ** (np.arange(1, n_head + 1, dtype=np.float32) / n_head))).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# The model
+# ---------------------------------------------------------------------------
+@dataclass
+class _Layer:
+    kind: str
+    norm1: torch.Tensor
+    norm2: torch.Tensor
+    wqkv: object
+    proj: object
+    gk: torch.Tensor          # (1, Hkv, G, d) global keys (compute dtype)
+    gv: torch.Tensor
+    gates: torch.Tensor       # sigmoid(gate_logits), fp32 (3,)
+    ffn: Dict[str, object] = field(default_factory=dict)
+    gk_pad: Optional[torch.Tensor] = None   # gk / gv zero-padded to >= 64 rows
+    gv_pad: Optional[torch.Tensor] = None
+
+
+class _Linear:
+    """y (M, N) fp32 = x (M, K) . W^T.  Dense weights run F.linear in the
+    compute dtype; INT4 group-128 weights (fp16 scales) run vnx_gemv_w4 for
+    M <= 64 rows and a dequantized copy (bit-exact q * s) for larger M
+    (prefill)."""
+
+    def __init__(self, w: torch.Tensor, dtype, hip, int4: bool):
+        self.N, self.K = w.shape
+        self.dtype = dtype
+        self.hip = hip
+        self.int4 = bool(int4) and self.K % 128 == 0
+        if self.int4:
+            wq, sc = VQ.quantize_int4_g(w.float(), 128)
+            self.wq, self.sc = wq.contiguous(), sc.contiguous()
+            self.wd = hip.dequant_w4(self.wq, self.sc, self.K, 128).to(dtype)
+            L = hip._L
+            self._ws = torch.zeros(max(256, L.vnx_gemv_workspace(64, self.N, self.K)), dtype=torch.uint8,
+                                   device=hip.torch_device)
+        else:
+            self.wd = w.to(dtype).contiguous()
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        M = x.shape[0]
+        if self.int4 and M <= 64:
+            x16 = x.to(torch.float16).contiguous()
+            y = torch.empty((M, self.N), dtype=torch.float32, device=x.device)
+            L = self.hip._L
+            _lib.check(L.vnx_gemv_w4(
+                ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq.data_ptr()), self.wq.stride(0),
+                ctypes.c_void_p(self.sc.data_ptr()), _lib.VNX_F16, self.sc.stride(0), M, self.N, self.K, 128,
+                ctypes.c_void_p(y.data_ptr()), self.N, ctypes.c_void_p(self._ws.data_ptr()), self._ws.numel(),
+                ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4")
+            return y
+        return torch.nn.functional.linear(x.to(self.dtype), self.wd).float()
+
+
+class CometSparkGPU:
+    """A CometSpark target or draft on one GPU with a per-sequence KV cache.
+
+    forward(tokens (B, n), lens (B,) int32) runs the n new tokens of every
+    sequence at positions lens[b] .. lens[b]+n-1, writes their keys / values
+    into the cache there and returns the final-norm hidden states (B, n, D)
+    fp32.  Committing a verify result is `lens += accepted + 1` (the rest of
+    the written rows is overwritten by the next call)."""
+
+    def __init__(self, cfg: ModelConfig, weights: Dict[str, torch.Tensor], hip, batch: int, capacity: int,
+                 dtype=torch.bfloat16, int4: bool = False):
+        self.cfg = cfg
+        self.hip = hip
+        self.dev = hip.torch_device
+        self.dtype = dtype
+        self.B = int(batch)
+        self.cap = int(capacity)
+        dev, D, d = self.dev, cfg.dim, cfg.head_dim
+        W = {k: (v if isinstance(v, torch.Tensor) else torch.from_numpy(np.asarray(v))).to(dev, torch.float32)
+             for k, v in weights.items()}
+        self.emb = W["tok_emb.weight"].to(dtype).contiguous()
+        self.emb_scale = math.sqrt(D) if cfg.embedding_scale else 1.0
+        self.norm = W["norm.weight"]
+        self.head = _Linear(W["tok_emb.weight"], dtype, hip, int4) if int4 else None
+        self.layers = []
+        for i, kind in enumerate(cfg.layer_pattern):
+            p = f"blocks.{i}."
+            wq, wk, wv = W[p + "attn.wq.weight"], W[p + "attn.wk.weight"], W[p + "attn.wv.weight"]
+            g = W[p + "attn.global_tokens.weight"]
+            G = g.shape[0]
+            gk = (g @ wk.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
+            gv = (g @ wv.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
+            L = _Layer(kind=kind, norm1=W[p + "norm1.weight"], norm2=W[p + "norm2.weight"],
+                       wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4),
+                       proj=_Linear(W[p + "attn.proj.weight"], dtype, hip, int4),
+                       gk=gk.to(dtype).contiguous(), gv=gv.to(dtype).contiguous(),
+                       gates=torch.sigmoid(W[p + "attn.gate_logits"]))
+            # The global rows double as the (never visible) tree rows of the
+            # kernel call, which reads up to 64 of them: pad with zeros.
+            gpad = max(G, 64)
+            L.gk_pad = torch.zeros((1, cfg.n_kv_head, gpad, d), dtype=dtype, device=dev)
+            L.gv_pad = torch.zeros((1, cfg.n_kv_head, gpad, d), dtype=dtype, device=dev)
+            L.gk_pad[:, :, :G] = L.gk
+            L.gv_pad[:, :, :G] = L.gv
+            if kind == "trisparse":
+                L.ffn["gu"] = _Linear(torch.cat([W[p + "ffn.w_gate.weight"], W[p + "ffn.w_up.weight"]], 0),
+                                      dtype, hip, int4)
+                L.ffn["down"] = _Linear(W[p + "ffn.w_down.weight"], dtype, hip, int4)
+            else:
+                P, E = cfg.num_dense_parts, cfg.num_experts_per_part
+                L.ffn["part_router"] = W[p + "ffn.part_router.gate.weight"]
+                L.ffn["routers"] = torch.stack([W[p + f"ffn.parts.{q}.router.gate.weight"] for q in range(P)])
+                w1, w2 = [], []
+                for q in range(P):
+                    for e in range(E):
+                        ep = p + f"ffn.parts.{q}.experts.{e}."
+                        w1.append(torch.cat([W[ep + "w_gate.weight"], W[ep + "w_up.weight"]], 0).t())
+                        w2.append(W[ep + "w_down.weight"].t())
+                # (P*E, D, 2He) and (P*E, He, D), contiguous: the batched
+                # products take them untransposed.
+                L.ffn["w1"] = torch.stack(w1).to(dtype).contiguous()
+                L.ffn["w2"] = torch.stack(w2).to(dtype).contiguous()
+            self.layers.append(L)
+        cos, sin = rope_tables(d, self.cap + 64, cfg.rope_theta)
+        self.cos = torch.from_numpy(cos).to(dev)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.slopes = torch.from_numpy(alibi_slopes(cfg.n_head)).to(dev)
+        Hkv = cfg.n_kv_head
+        self.kc = [torch.zeros((self.B, Hkv, self.cap, d), dtype=dtype, device=dev) for _ in self.layers]
+        self.vc = [torch.zeros((self.B, Hkv, self.cap, d), dtype=dtype, device=dev) for _ in self.layers]
+        self._words = {}
+        self.kernel_attention = (dtype == torch.bfloat16 and d in (64, 128) and not cfg.use_alibi)
+
+    # ---- pieces ---------------------------------------------------------
+    def _rms(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        ms = (x * x).mean(dim=-1, keepdim=True)
+        return x / torch.sqrt(ms + self.cfg.eps) * w
+
+    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """x (B, n, heads, d) fp32, pos (B, n) int64: x*cos + rotate_half(x)*sin."""
+        half = x.shape[-1] // 2
+        cos = self.cos[pos].unsqueeze(2)
+        sin = self.sin[pos].unsqueeze(2)
+        rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+        return x * cos + rot * sin
+
+    def _chain_words(self, n: int) -> torch.Tensor:
+        w = self._words.get(n)
+        if w is None:
+            a = np.array([(1 << (i + 1)) - 1 for i in range(n)], dtype=np.uint64)
+            w = torch.from_numpy(a.view(np.int64)).to(self.dev)
+            self._words[n] = w
+        return w
+
+    def _attn_kernel(self, q, li, lens, n, Tmax):
+        """Sliding-window + global paths on vnx_tree_attn.  q (B, H, n, d) bf16."""
+        cfg = self.cfg
+        B, H, _, d = q.shape
+        Hkv = cfg.n_kv_head
+        kc, vc = self.kc[li], self.vc[li]
+        out_s = torch.empty((B, H, n, d), dtype=torch.float32, device=self.dev)
+        a = _lib.TreeAttnArgs()
+        a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
+        a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = list(kc.stride()[:3])
+        a.k_tree = kc.data_ptr(); a.v_tree = vc.data_ptr(); a.tree_strides[:] = list(kc.stride()[:3])
+        a.anc = self._chain_words(n).data_ptr(); a.anc_batch_stride = 0
+        a.out = out_s.data_ptr(); a.out_dtype = _lib.VNX_F32; a.out_strides[:] = list(out_s.stride()[:3])
+        a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tmax, n, d
+        a.scale = 1.0 / math.sqrt(d)
+        a.tp_batch = lens.data_ptr(); a.tree_follows_prefix = 1
+        L = self.hip._L
+        st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        ws = self.hip._workspace(L.vnx_tree_attn_workspace(B, H, Hkv, n, Tmax, d))
+        _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "tree_attn")
+        # global sink tokens: every query sees the G global rows (the prefix),
+        # no tree row (empty ancestor words).
+        Ly = self.layers[li]
+        G = Ly.gk.shape[2]
+        out_g = torch.empty_like(out_s)
+        g = _lib.TreeAttnArgs()
+        g.q = q.data_ptr(); g.q_strides[:] = list(q.stride()[:3])
+        gs = [0, Ly.gk_pad.stride(1), Ly.gk_pad.stride(2)]
+        g.k_cache = Ly.gk_pad.data_ptr(); g.v_cache = Ly.gv_pad.data_ptr(); g.cache_strides[:] = gs
+        g.k_tree = Ly.gk_pad.data_ptr(); g.v_tree = Ly.gv_pad.data_ptr(); g.tree_strides[:] = gs
+        zero = self._words.get("zero")
+        if zero is None or zero.numel() < n:
+            zero = torch.zeros(64, dtype=torch.int64, device=self.dev)
+            self._words["zero"] = zero
+        g.anc = zero.data_ptr(); g.anc_batch_stride = 0
+        g.out = out_g.data_ptr(); g.out_dtype = _lib.VNX_F32; g.out_strides[:] = list(out_g.stride()[:3])
+        g.B, g.H, g.Hkv, g.Tp, g.N, g.d = B, H, Hkv, G, n, d
+        g.scale = 1.0 / math.sqrt(d)
+        g.tp_batch = None; g.tree_follows_prefix = 0
+        ws = self.hip._workspace(L.vnx_tree_attn_workspace(B, H, Hkv, n, G, d))
+        _lib.check(L.vnx_tree_attn(ctypes.byref(g), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "global attn")
+        return out_s, out_g
+
+    def _attn_torch(self, q, li, lens, n, Tmax):
+        """The same three paths with explicit fp32 masks (any head size,
+        ALiBi, windows shorter than the context, prefill).  q (B, H, n, d)."""
+        cfg = self.cfg
+        B, H, _, d = q.shape
+        rep = H // cfg.n_kv_head
+        Tk = Tmax + n
+        k = self.kc[li][:, :, :Tk].float().repeat_interleave(rep, dim=1)
+        v = self.vc[li][:, :, :Tk].float().repeat_interleave(rep, dim=1)
+        qf = q.float()
+        scale = 1.0 / math.sqrt(d)
+        scores = torch.matmul(qf, k.transpose(-1, -2).contiguous()) * scale        # (B, H, n, Tk)
+        qpos = lens.long().view(B, 1) + torch.arange(n, device=self.dev).view(1, n)  # (B, n)
+        kpos = torch.arange(Tk, device=self.dev).view(1, 1, Tk)
+        dist = qpos.unsqueeze(-1) - kpos                                            # (B, n, Tk)
+        causal = dist >= 0
+        swa_ok = causal & (dist < cfg.window_size)
+        neg = torch.tensor(-1e9, dtype=torch.float32, device=self.dev)
+        s_swa = torch.where(swa_ok.unsqueeze(1), scores, neg)
+        out = torch.matmul(torch.softmax(s_swa, dim=-1), v)
+        Ly = self.layers[li]
+        gk = Ly.gk.float().repeat_interleave(rep, dim=1)
+        gv = Ly.gv.float().repeat_interleave(rep, dim=1)
+        sg = torch.matmul(qf, gk.transpose(-1, -2).contiguous()) * scale
+        out_g = torch.matmul(torch.softmax(sg, dim=-1), gv)
+        res = Ly.gates[0] * out + Ly.gates[1] * out_g
+        if cfg.use_alibi:
+            # path C while the sequence holds at most 1024 keys (:600-607)
+            bias = -self.slopes.view(1, H, 1, 1) * dist.unsqueeze(1).float()
+            s_c = torch.where(causal.unsqueeze(1), scores + bias, neg)
+            out_c = torch.matmul(torch.softmax(s_c, dim=-1), v)
+            use_c = ((lens.long() + n) <= 1024).view(B, 1, 1, 1)
+            res = res + torch.where(use_c, Ly.gates[2] * out_c, torch.zeros_like(out_c))
+        return res
+
+    def _mod(self, L: _Layer, x: torch.Tensor) -> torch.Tensor:
+        """MoD FFN on (M, D) fp32: every expert runs on every row and the
+        router weights (zero for unselected experts) combine them."""
+        cfg = self.cfg
+        P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
+        pw = torch.softmax(x @ L.ffn["part_router"].t(), dim=-1)                   # (M, P)
+        rl = (x @ L.ffn["routers"].reshape(P * E, -1).t()).view(-1, P, E)          # (M, P, E) fp32
+        top_v, top_i = torch.topk(rl, k, dim=-1)
+        wsel = torch.softmax(top_v, dim=-1)                                        # (M, P, k)
+        comb = torch.zeros_like(rl).scatter_(-1, top_i, wsel) * pw.unsqueeze(-1)   # (M, P, E)
+        M = x.shape[0]
+        xb = x.to(self.dtype).unsqueeze(0).expand(P * E, M, cfg.dim).contiguous()
+        h = torch.matmul(xb, L.ffn["w1"])                                          # (PE, M, 2He)
+        He = cfg.expert_hidden_eff
+        a = torch.nn.functional.silu(h[..., :He].float()) * h[..., He:].float()
+        y = torch.matmul(a.to(self.dtype), L.ffn["w2"]).float()                    # (PE, M, D)
+        return (comb.reshape(M, P * E).t().unsqueeze(-1) * y).sum(0)
+
+    def _ffn(self, L: _Layer, x: torch.Tensor) -> torch.Tensor:
+        if L.kind == "mod":
+            return self._mod(L, x)
+        Hf = self.cfg.ffn_hidden
+        gu = L.ffn["gu"](x)
+        return L.ffn["down"](torch.nn.functional.silu(gu[:, :Hf]) * gu[:, Hf:])
+
+    # ---- forward --------------------------------------------------------
+    @torch.no_grad()
+    def forward(self, tokens: torch.Tensor, lens: torch.Tensor, Tmax: Optional[int] = None) -> torch.Tensor:
+        """tokens (B, n) int64, lens (B,) int32 on this device; Tmax >= max(lens)
+        (read back from the device when not given).  Returns (B, n, D) fp32."""
+        cfg = self.cfg
+        B, n = tokens.shape
+        if B != self.B:
+            raise ValueError(f"batch {B} != the cache's {self.B}")
+        if Tmax is None:
+            Tmax = int(lens.max())
+        if Tmax + n > self.cap:
+            raise ValueError(f"cache capacity {self.cap} exceeded ({Tmax} + {n})")
+        H, Hkv, d, D = cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.dim
+        pos = lens.long().view(B, 1) + torch.arange(n, device=self.dev).view(1, n)
+        x = self.emb[tokens].float() * self.emb_scale                                # (B, n, D)
+        bidx = torch.arange(B, device=self.dev).view(B, 1).expand(B, n)
+        use_kernel = self.kernel_attention and n <= 64 and Tmax + n <= cfg.window_size
+        for li, L in enumerate(self.layers):
+            h = self._rms(x, L.norm1).reshape(B * n, D)
+            qkv = L.wqkv(h).view(B, n, (H + 2 * Hkv), d)
+            q, k, v = qkv[:, :, :H], qkv[:, :, H:H + Hkv], qkv[:, :, H + Hkv:]
+            if cfg.use_rope:
+                q = self._rope(q, pos)
+                k = self._rope(k, pos)
+            # new rows into the cache at lens[b] + i
+            self.kc[li][bidx, :, pos] = k.to(self.dtype)
+            self.vc[li][bidx, :, pos] = v.to(self.dtype)
+            qh = q.permute(0, 2, 1, 3).to(self.dtype).contiguous()                  # (B, H, n, d)
+            if use_kernel:
+                o_s, o_g = self._attn_kernel(qh, li, lens, n, Tmax)
+                o = L.gates[0] * o_s + L.gates[1] * o_g
+            else:
+                o = self._attn_torch(qh, li, lens, n, Tmax)
+            o = o.permute(0, 2, 1, 3).reshape(B * n, H * d)
+            x = x + L.proj(o).view(B, n, D)
+            h2 = self._rms(x, L.norm2).reshape(B * n, D)
+            x = x + self._ffn(L, h2).view(B, n, D)
+        return self._rms(x, self.norm)
+
+    def logits(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """(B, n, V) fp32 logits of the tied head: vnx_lm_head (bf16, matrix
+        cores) for the verify pass, vnx_gemv_w4 for an INT4 draft, F.linear
+        for an fp32 model."""
+        B, n, D = hidden.shape
+        V = self.cfg.vocab_size
+        h2 = hidden.reshape(B * n, D)
+        if self.head is not None:
+            y = self.head(h2)
+            if out is not None:
+                out.view(B * n, V).copy_(y)
+                return out
+            return y.view(B, n, V)
+        if self.dtype == torch.bfloat16 and D % 64 == 0 and B * n <= 256:
+            if out is None:
+                out = torch.empty((B, n, V), dtype=torch.float32, device=self.dev)
+            self.hip.lm_head(h2.to(torch.bfloat16), self.emb, out=out.view(B * n, V))
+            return out
+        y = torch.nn.functional.linear(h2.to(self.dtype), self.emb).float()
+        if out is not None:
+            out.view(B * n, V).copy_(y)
+            return out
+        return y.view(B, n, V)
