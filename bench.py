@@ -387,15 +387,15 @@ def bench_e2e(args):
     g = torch.Generator(device=dev)
     g.manual_seed(30)
     prompts = torch.randint(0, V, (E2E_B, E2E_T0), generator=g, device=dev)
-    eng = SpecDecodeEngine(target, draft, hip, k=E2E_K, temperature=E2E_TEMP, seed=31)
+    eng = SpecDecodeEngine(target, draft, hip, k=E2E_K, temperature=E2E_TEMP, seed=31,
+                           use_graph=not args.e2e_eager)
     runs = []
     for r in range(max(1, args.e2e_runs)):
-        toks, st = eng.generate(prompts, E2E_NEW, phase_timing=(r == 0 and args.e2e_runs > 1))
+        toks, st = eng.generate(prompts, E2E_NEW)
         runs.append(st)
         print(json.dumps({"e2e_run": r, "rounds": st.rounds, "decode_s": round(st.decode_s, 4),
                           "prefill_s": round(st.prefill_s, 4), "tokens_per_s": round(st.tokens_per_s, 1),
-                          "phase_s": {"draft": round(st.draft_s, 4), "verify": round(st.verify_s, 4),
-                                      "accept": round(st.accept_s, 4)}}), flush=True)
+                          "graph": eng.graph is not None}), flush=True)
     timed = runs[-1]
     mean_tokens_round = float(np.mean(timed.per_round_tokens)) / E2E_B
     out = {"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(timed.tokens_per_s, 1),
@@ -404,6 +404,7 @@ def bench_e2e(args):
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16 target / int4 draft / f32 logits",
            "data": "synthetic (random-init weights, uniform-random prompts)",
            "config": {"workload": "BASELINE config 5: end-to-end speculative decode", "batch": E2E_B, "k": E2E_K,
+                      "rounds_as": "HIP graph replays" if eng.graph is not None else "eager launches",
                       "prompt": E2E_T0, "new_tokens": E2E_NEW, "temperature": E2E_TEMP,
                       "target": target.cfg.name, "draft": draft.cfg.name + ", INT4 g128"},
            "prefill_s": round(timed.prefill_s, 4), "build_s": round(build_s, 2),
@@ -419,6 +420,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--e2e-runs", type=int, default=2, help="e2e: decode runs (the last is reported)")
+    ap.add_argument("--e2e-eager", action="store_true", help="e2e: launch every round eagerly (no HIP graph)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
     ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree", "lmhead", "e2e"),

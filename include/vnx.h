@@ -142,6 +142,21 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
                     float* lse_t, float* lse_d,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Sampling (the draft's proposals, and any caller of Sampler.sample):
+ * out_ids[b] = the inverse-CDF draw with uniforms[b] from softmax(logits row
+ * b / T) (optional per-row top-k thresholds, NULL = none), the same draw the
+ * acceptance kernels make for the bonus token (the numpy Generator.choice
+ * rule, sampler.py:135-137, with the uniform given).  logits: B rows of V,
+ * row pitch ld.  flags (B) uint8 and lse (B) fp32 may be NULL.
+ * Replaces Sampler.sample steps 1-4 (sampler.py:94-138) and the draw of
+ * _generate_with_logits (cometspark.py:880, :903-911), with host uniforms
+ * in place of the RNG stream. */
+size_t vnx_sample_workspace(int64_t B, int64_t V);
+
+int vnx_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, const float* uniforms,
+               float temperature, const float* thresholds, int64_t* out_ids, uint8_t* flags, float* lse,
+               void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Greedy verify, the reference semantics batched:
  * main_pred[b,i] = argmax(target row (b,i)) for i < rows_t (rows_t = k or k+1,

@@ -234,3 +234,36 @@ def test_stochastic_spec_decode_runs_and_commits_consistently(hip):
     assert tk.shape == (B, 50) and tk.min() >= 0 and tk.max() < 1000
     assert st.rounds * B * 5 >= B * 50 and st.rounds <= 50
     _say(f"stochastic: {st.rounds} rounds, {st.accepted_drafts} drafts accepted")
+
+
+def test_graph_rounds_match_eager_rounds(hip, gold):
+    """The captured round (HIP graph, cache-bound prefix maxima) commits the
+    same streams as eager rounds: config 1 reproduces the reference's greedy
+    stream, and a bf16 toy batch agrees with its eager run."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    t = VM.CometSparkGPU(VM.small_target(), _w(gold, "t/"), hip, batch=1, capacity=256, dtype=torch.float32)
+    d = VM.CometSparkGPU(VM.small_draft(), _w(gold, "d/"), hip, batch=1, capacity=256, dtype=torch.float32)
+    eng = SpecDecodeEngine(t, d, hip, k=4, temperature=0.0, use_graph=True)
+    prompt = torch.from_numpy(gold["prompt"][None]).to(hip.torch_device)
+    toks, st = eng.generate(prompt, 128)
+    assert eng.graph is not None
+    assert np.array_equal(toks.cpu().numpy()[0], gold["greedy128"])
+    toks2, _ = eng.generate(prompt, 128)        # replays the same graph
+    assert np.array_equal(toks2.cpu().numpy()[0], gold["greedy128"])
+
+    cfg = _toy_cfg()
+    dcfg = VM.ModelConfig(vocab_size=1000, dim=128, n_layer=1, n_head=2, n_kv_head=1, layer_pattern=("trisparse",),
+                          window_size=1024, num_global_tokens=8, use_alibi=False, use_rope=True)
+    Wt, Wd = VM.init_weights(cfg, seed=21), VM.init_weights(dcfg, seed=22)
+    dev = hip.torch_device
+    B = 4
+    prompt = torch.from_numpy(np.random.default_rng(9).integers(0, 1000, (B, 24))).to(dev)
+    res = []
+    for g in (False, True):
+        tt = VM.CometSparkGPU(cfg, Wt, hip, batch=B, capacity=200, dtype=torch.bfloat16)
+        dd = VM.CometSparkGPU(dcfg, Wd, hip, batch=B, capacity=200, dtype=torch.bfloat16, int4=False)
+        e = SpecDecodeEngine(tt, dd, hip, k=5, temperature=0.0, use_graph=g)
+        res.append(e.generate(prompt, 60)[0])
+    agree = (res[0] == res[1]).float().mean().item()
+    _say(f"graph vs eager greedy agreement {agree:.3f}")
+    assert agree >= 0.9

@@ -161,3 +161,27 @@ def test_strided_target_view(hip):
     o = spec_accept(tgt, dft, ids, u, 0.8)
     assert np.array_equal(res["accept_len"].cpu().numpy(), o["accept_len"])
     assert np.array_equal(res["out_ids"].cpu().numpy(), o["out_ids"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sample_matches_oracle_bonus_draw(hip, dtype):
+    """vnx_sample = the k = 0 case of the acceptance rule: the draw from
+    softmax(row / T) with the row's uniform, bit-exact with the oracle
+    (CDF_EDGE / LSE_EDGE flagged rows excepted, at most one)."""
+    from oracle.speculative import spec_accept
+    rng = np.random.default_rng(77)
+    B, V, T = 48, 248320, 0.8
+    x = torch.from_numpy(rng.normal(0, 2, (B, V)).astype(np.float32)).to(dtype)
+    u = rng.random(B).astype(np.float32)
+    dev = hip.torch_device
+    res = hip.sample(x.to(dev), torch.from_numpy(u).to(dev), temperature=T, return_all=True)
+    torch.cuda.synchronize()
+    ref = spec_accept(x.float().numpy()[:, None], np.zeros((B, 0, V), np.float32), np.zeros((B, 0), np.int64),
+                      u[:, None], T)
+    got = res["ids"].cpu().numpy()
+    want = ref["out_ids"][:, 0]
+    fl = res["flags"].cpu().numpy() | ref["flags"][:, 0]
+    bad = np.flatnonzero(got != want)
+    assert all(fl[i] & (2 | 4) for i in bad), (bad, fl[bad])
+    assert len(bad) <= 1
+    np.testing.assert_array_equal(res["lse"].cpu().numpy()[fl & 2 == 0], ref["lse_t"][:, 0][fl & 2 == 0])

@@ -59,6 +59,8 @@ SIGNATURES = {
                            _vp, _c_sz, _vp]),
     "vnx_dequant_w4": (_int, [_vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _c_i64, _vp]),
     "vnx_dequant_w8": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp]),
+    "vnx_sample_workspace": (_c_sz, [_c_i64, _c_i64]),
+    "vnx_sample": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "vnx_greedy_verify_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
     "vnx_greedy_verify": (_int, [_vp, _int, _c_i64, _int, _int, _c_i64, _c_i64, _c_i64, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),

@@ -573,22 +573,27 @@ size_t vnx_spec_accept_workspace(int64_t B, int k, int64_t V) {
   return spec_ws_bytes(B, k, V);
 }
 
-int vnx_spec_accept(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
+// The four launches for k >= 0 draft positions (k = 0: the draw from p_0
+// alone, which is sampling from softmax(target / T)).
+static int spec_run(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
                     int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
                     const int64_t* draft_ids, const float* uniforms,
                     float temperature, const float* thr_t, const float* thr_d, int32_t* accept_len,
                     int64_t* out_ids, uint8_t* flags, float* lse_t, float* lse_d, void* workspace,
                     size_t workspace_bytes, void* stream) {
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
-  if (B < 0 || k < 1 || k > kMaxK || V <= 0) return VNX_ERR_INVALID_ARG;
+  if (B < 0 || k < 0 || k > kMaxK || V <= 0) return VNX_ERR_INVALID_ARG;
   if (!(temperature > 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
   if (B == 0) return VNX_OK;
   if (B > (1 << 20)) return VNX_ERR_UNSUPPORTED;
   int st = check_rows(target, dtype, ld_t, sb_t, k + 1, V);
   if (st) return st;
-  st = check_rows(draft, dtype, ld_d, sb_d, k, V);
-  if (st) return st;
-  if (!draft_ids || !uniforms || !accept_len || !out_ids) return VNX_ERR_INVALID_ARG;
+  if (k > 0) {
+    st = check_rows(draft, dtype, ld_d, sb_d, k, V);
+    if (st) return st;
+    if (!draft_ids) return VNX_ERR_INVALID_ARG;
+  }
+  if (!uniforms || !accept_len || !out_ids) return VNX_ERR_INVALID_ARG;
   const SpecPlan pl = spec_plan(B, k, V, dtype);
   if (B * (2 * k + 1) * (int64_t)pl.chunks >= INT32_MAX || B * (int64_t)pl.chunks2 >= INT32_MAX ||
       pl.nsb > kDrawLds || (2 * k + 1) * pl.chunks > kAccLds)
@@ -628,6 +633,36 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype, int64_t B,
     VNX_LAUNCH_CHECK();
     return mark(4);
   });
+}
+
+int vnx_spec_accept(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
+                    int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
+                    const int64_t* draft_ids, const float* uniforms,
+                    float temperature, const float* thr_t, const float* thr_d, int32_t* accept_len,
+                    int64_t* out_ids, uint8_t* flags, float* lse_t, float* lse_d, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (k < 1) return VNX_ERR_INVALID_ARG;
+  return spec_run(target, draft, dtype, B, k, V, ld_t, sb_t, ld_d, sb_d, draft_ids, uniforms, temperature,
+                  thr_t, thr_d, accept_len, out_ids, flags, lse_t, lse_d, workspace, workspace_bytes, stream);
+}
+
+size_t vnx_sample_workspace(int64_t B, int64_t V) {
+  if (B <= 0 || V <= 0) return 256;
+  return spec_ws_bytes(B, 0, V) + (((size_t)B * 4 + 255) & ~(size_t)255);
+}
+
+int vnx_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, const float* uniforms,
+               float temperature, const float* thresholds, int64_t* out_ids, uint8_t* flags, float* lse,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  if (B < 0 || V <= 0) return VNX_ERR_INVALID_ARG;
+  if (B == 0) return VNX_OK;
+  const size_t need = vnx_sample_workspace(B, V);
+  if (!workspace || workspace_bytes < need) return VNX_ERR_WORKSPACE;
+  // accept_len (always 0 here) lives at the end of the workspace.
+  const size_t head = need - (((size_t)B * 4 + 255) & ~(size_t)255);
+  int32_t* alen = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + head);
+  return spec_run(logits, logits, dtype, B, 0, V, ld, ld, ld, ld, nullptr, uniforms, temperature, thresholds,
+                  nullptr, alen, out_ids, flags, lse, nullptr, workspace, head, stream);
 }
 
 }  // extern "C"

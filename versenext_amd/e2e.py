@@ -50,8 +50,16 @@ class DecodeStats:
 
 
 class SpecDecodeEngine:
+    """One round = draft (k+1 one-token forwards + k draws), verify (one
+    (k+1)-token target forward + LM head), accept, commit; every round works
+    on the engine's static device buffers, so the whole round can be
+    captured once as a HIP graph (use_graph) and replayed: the uniforms of a
+    round are drawn into their buffers before each replay, and the attention
+    calls take the cache bound as their prefix maximum (each row reads only
+    its own lens[b] prefix rows)."""
+
     def __init__(self, target: CometSparkGPU, draft: CometSparkGPU, hip, k: int, temperature: float,
-                 seed: int = 31):
+                 seed: int = 31, use_graph: bool = False):
         if target.B != draft.B:
             raise ValueError("target and draft caches must have the same batch")
         if target.cfg.vocab_size != draft.cfg.vocab_size:
@@ -64,45 +72,70 @@ class SpecDecodeEngine:
         self.greedy = self.T <= 0.0
         self.B = target.B
         self.V = target.cfg.vocab_size
+        self.use_graph = bool(use_graph)
         dev = hip.torch_device
         self.dev = dev
         self.gen = torch.Generator(device=dev)
         self.gen.manual_seed(int(seed))
-        self.pbuf = torch.empty((self.B, self.k + 1, self.V), dtype=torch.float32, device=dev)
-        self.qbuf = torch.empty((self.B, self.k, self.V), dtype=torch.float32, device=dev)
-
-    # ---- phases ---------------------------------------------------------
-    def _sample(self, logits: torch.Tensor) -> torch.Tensor:
-        if self.greedy:
-            return self.hip.argmax(logits).view(-1)
-        probs = torch.softmax(logits / self.T, dim=-1)
-        return torch.multinomial(probs, 1, generator=self.gen).view(-1)
-
-    def _draft(self, c, lens_d, Tmax_d):
         B, k = self.B, self.k
-        xs = torch.empty((B, k), dtype=torch.int64, device=self.dev)
-        tok = c
+        self.pbuf = torch.empty((B, k + 1, self.V), dtype=torch.float32, device=dev)
+        self.qbuf = torch.empty((B, k, self.V), dtype=torch.float32, device=dev)
+        self.u_draft = torch.zeros((k, B), dtype=torch.float32, device=dev)
+        self.u_acc = torch.zeros((B, k + 1), dtype=torch.float32, device=dev)
+        self.xs = torch.zeros((B, k), dtype=torch.int64, device=dev)
+        self.c = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.lens_t = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.lens_d = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.count = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.info = torch.zeros(4, dtype=torch.int64, device=dev)
+        self.ar = torch.arange(k + 1, device=dev).view(1, k + 1)
+        self.out = None
+        self.n_new = 0
+        self.graph = None
+        # attention prefix bound used by captured rounds
+        self.bound_t = target.cap - (k + 2)
+        self.bound_d = draft.cap - (k + 2)
+
+    # ---- one round on the static buffers ---------------------------------
+    def _fill_uniforms(self):
+        if not self.greedy:
+            torch.rand(self.u_draft.shape, generator=self.gen, device=self.dev, out=self.u_draft)
+            torch.rand(self.u_acc.shape, generator=self.gen, device=self.dev, out=self.u_acc)
+
+    def _round(self, Tmax_t: int, Tmax_d: int):
+        B, k = self.B, self.k
+        tok = self.c
         for i in range(k + 1):
-            h = self.d.forward(tok.view(B, 1), lens_d + i, Tmax_d + i)
+            h = self.d.forward(tok.view(B, 1), self.lens_d + i, Tmax_d + i)
             if i == k:
                 break
-            self.qbuf[:, i] = self.d.logits(h).view(B, self.V)
-            tok = self._sample(self.qbuf[:, i])
-            xs[:, i] = tok
-        return xs
-
-    def _verify(self, c, xs, lens_t, Tmax_t):
-        toks = torch.cat([c.view(self.B, 1), xs], dim=1)
-        h = self.t.forward(toks, lens_t, Tmax_t)
+            self.d.logits(h, out=self.qbuf[:, i:i + 1])
+            if self.greedy:
+                tok = self.hip.argmax(self.qbuf[:, i]).view(B)
+            else:
+                tok = self.hip.sample(self.qbuf[:, i], self.u_draft[i], temperature=self.T)
+            self.xs[:, i] = tok
+        toks = torch.cat([self.c.view(B, 1), self.xs], dim=1)
+        h = self.t.forward(toks, self.lens_t, Tmax_t)
         self.t.logits(h, out=self.pbuf)
-
-    def _accept(self, xs):
         if self.greedy:
-            _, _, alen, out = self.hip.greedy_verify(self.pbuf, xs, rows_t=self.k + 1)
-            return alen, out
-        u = torch.rand((self.B, self.k + 1), generator=self.gen, device=self.dev)
-        res = self.hip.spec_accept(self.pbuf, self.qbuf, xs, u, temperature=self.T)
-        return res["accept_len"], res["out_ids"]
+            _, _, alen, ids = self.hip.greedy_verify(self.pbuf, self.xs, rows_t=k + 1)
+        else:
+            res = self.hip.spec_accept(self.pbuf, self.qbuf, self.xs, self.u_acc, temperature=self.T)
+            alen, ids = res["accept_len"], res["out_ids"]
+        # commit: ids[b, :n1] go to out[b, count_b ...]; other slots write the
+        # trash column (no data-dependent shapes, so the round can be captured)
+        n1 = alen.long() + 1
+        trash = self.out.shape[1] - 1
+        pos = self.count.view(B, 1) + self.ar
+        ok = (self.ar < n1.view(B, 1)) & (pos < trash)
+        self.out.scatter_(1, torch.where(ok, pos, torch.full_like(pos, trash)), ids)
+        self.count += n1
+        self.c.copy_(ids.gather(1, alen.long().view(B, 1)).view(B))
+        self.lens_t += n1.int()
+        self.lens_d += n1.int()
+        self.info.copy_(torch.stack([self.count.min(), self.lens_t.max().long(), self.lens_d.max().long(),
+                                     alen.long().sum()]))
 
     # ---- driver ---------------------------------------------------------
     @torch.no_grad()
@@ -117,57 +150,72 @@ class SpecDecodeEngine:
         dev = self.dev
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
-        lens_t = torch.zeros(B, dtype=torch.int32, device=dev)
-        lens_d = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.lens_t.zero_()
+        self.lens_d.zero_()
         if T0 > 1:
-            self.t.forward(prompts[:, :-1], lens_t, 0)
-            self.d.forward(prompts[:, :-1], lens_d, 0)
-        lens_t += T0 - 1
-        lens_d += T0 - 1
-        c = prompts[:, -1].clone()
+            self.t.forward(prompts[:, :-1], self.lens_t, 0)
+            self.d.forward(prompts[:, :-1], self.lens_d, 0)
+        self.lens_t += T0 - 1
+        self.lens_d += T0 - 1
+        self.c.copy_(prompts[:, -1])
+        self.count.zero_()
+        if self.out is None or self.n_new != n_new:
+            self.out = torch.full((B, n_new + k + 2), -1, dtype=torch.int64, device=dev)
+            self.n_new = n_new
+            self.graph = None
+        else:
+            self.out.fill_(-1)
         torch.cuda.synchronize(dev)
         st = DecodeStats(prefill_s=time.perf_counter() - t0)
-
-        out = torch.full((B, n_new + k + 1), -1, dtype=torch.int64, device=dev)
-        count = torch.zeros(B, dtype=torch.int64, device=dev)
-        ar = torch.arange(k + 1, device=dev).view(1, k + 1)
-        bidx = torch.arange(B, device=dev).view(B, 1).expand(B, k + 1)
-        Tmax_t = Tmax_d = T0 - 1
+        if T0 - 1 + n_new + 2 * (k + 1) > min(self.t.cap, self.d.cap):
+            raise ValueError("the caches cannot hold prompt + n_new tokens")
+        if self.use_graph and self.graph is None:
+            self._capture()
         t1 = time.perf_counter()
+        Tmax_t = Tmax_d = T0 - 1
         while True:
             ta = time.perf_counter()
-            xs = self._draft(c, lens_d, Tmax_d)
-            if phase_timing:
-                torch.cuda.synchronize(dev)
-            tb = time.perf_counter()
-            self._verify(c, xs, lens_t, Tmax_t)
-            if phase_timing:
-                torch.cuda.synchronize(dev)
-            tc = time.perf_counter()
-            alen, ids = self._accept(xs)
-            n1 = alen.long() + 1                                     # tokens committed this round
-            keep = ar < n1.view(B, 1)
-            pos = (count.view(B, 1) + ar).clamp(max=n_new + k)
-            out[bidx[keep], pos[keep]] = ids[keep]
-            count += n1
-            c = ids.gather(1, alen.long().view(B, 1)).view(B)
-            lens_t += n1.int()
-            lens_d += n1.int()
-            info = torch.stack([count.min(), lens_t.max().long(), lens_d.max().long(), alen.long().sum()]).cpu()
+            self._fill_uniforms()
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self._round(Tmax_t, Tmax_d)
+            info = self.info.cpu()
             st.rounds += 1
             st.per_round_tokens.append(int(info[3]) + B)
             if phase_timing:
-                td = time.perf_counter()
-                st.draft_s += tb - ta
-                st.verify_s += tc - tb
-                st.accept_s += td - tc
+                st.draft_s += time.perf_counter() - ta
             if int(info[0]) >= n_new:
                 break
             Tmax_t, Tmax_d = int(info[1]), int(info[2])
-            if Tmax_t + k + 1 > self.t.cap or Tmax_d + k + 1 > self.d.cap:
+            if Tmax_t + k + 2 > self.t.cap or Tmax_d + k + 2 > self.d.cap:
                 raise RuntimeError("KV cache capacity exhausted")
         torch.cuda.synchronize(dev)
         st.decode_s = time.perf_counter() - t1
         st.emitted = B * n_new
         st.accepted_drafts = sum(st.per_round_tokens) - B * st.rounds
-        return out[:, :n_new], st
+        return self.out[:, :n_new].clone(), st
+
+    def _capture(self):
+        """Captures one round on a side stream.  Warm-up rounds on that stream
+        first allocate every workspace and cached tensor; the caches and
+        counters they touch are restored afterwards (the warm-up only writes
+        cache rows past every lens[b], which later rounds overwrite)."""
+        saved = [x.clone() for x in (self.c, self.lens_t, self.lens_d, self.count, self.out)]
+        s = torch.cuda.Stream(device=self.dev)
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._fill_uniforms()
+                self._round(self.bound_t, self.bound_d)
+                for x, v in zip((self.c, self.lens_t, self.lens_d, self.count, self.out), saved):
+                    x.copy_(v)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            self._round(self.bound_t, self.bound_d)
+        torch.cuda.synchronize(self.dev)
+        for x, v in zip((self.c, self.lens_t, self.lens_d, self.count, self.out), saved):
+            x.copy_(v)
+        self.graph = g

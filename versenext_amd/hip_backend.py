@@ -262,6 +262,31 @@ class HipBackend(DeviceBackend):
             _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "spec_accept")
         return dict(accept_len=alen, out_ids=out, flags=flags, lse_t=lse_t, lse_d=lse_d)
 
+    def sample(self, logits, uniforms, temperature: float = 1.0, thresholds=None, out=None,
+               return_all: bool = False):
+        """Inverse-CDF draw per row from softmax(logits / T) with the given
+        uniforms (vnx_sample).  logits (B, V) (strided rows allowed);
+        returns ids (B,) int64 (written into `out` when given), or with
+        return_all a dict with ids, flags and the fp32 row LSEs."""
+        dev = self._torch_device
+        lg = self._rows2d(logits)
+        B, V = lg.shape
+        u = _to_tensor(uniforms, dev, torch.float32).reshape(-1).contiguous()
+        if u.numel() != B:
+            raise ValueError(f"uniforms must have {B} entries")
+        thr = None if thresholds is None else _to_tensor(thresholds, dev, torch.float32).contiguous()
+        ids = out if out is not None else torch.empty(B, dtype=torch.int64, device=dev)
+        flags = torch.empty(B, dtype=torch.uint8, device=dev) if return_all else None
+        lse = torch.empty(B, dtype=torch.float32, device=dev) if return_all else None
+        ws = self._workspace(self._L.vnx_sample_workspace(B, V))
+        _lib.check(self._L.vnx_sample(
+            _ptr(lg), _LOGIT_DTYPES[lg.dtype], B, V, lg.stride(0), _ptr(u), float(temperature), _ptr(thr),
+            _ptr(ids), _ptr(flags), _ptr(lse), _ptr(ws), ws.numel(),
+            ctypes.c_void_p(self._stream().cuda_stream)), "sample")
+        if return_all:
+            return dict(ids=ids, flags=flags, lse=lse)
+        return ids
+
     # ---- weight-only quantized GEMV -------------------------------------------
     def _acts(self, x, K: int) -> torch.Tensor:
         """(..., K) activations -> contiguous (B, K) fp16 on this device."""

@@ -341,6 +341,7 @@ class CometSparkGPU:
         self.kc = [torch.zeros((self.B, Hkv, self.cap, d), dtype=dtype, device=dev) for _ in self.layers]
         self.vc = [torch.zeros((self.B, Hkv, self.cap, d), dtype=dtype, device=dev) for _ in self.layers]
         self._words = {}
+        self._neg = torch.full((), -1e9, dtype=torch.float32, device=dev)  # the reference's mask value
         self.kernel_attention = (dtype == torch.bfloat16 and d in (64, 128) and not cfg.use_alibi)
 
     # ---- pieces ---------------------------------------------------------
@@ -424,7 +425,7 @@ class CometSparkGPU:
         dist = qpos.unsqueeze(-1) - kpos                                            # (B, n, Tk)
         causal = dist >= 0
         swa_ok = causal & (dist < cfg.window_size)
-        neg = torch.tensor(-1e9, dtype=torch.float32, device=self.dev)
+        neg = self._neg
         s_swa = torch.where(swa_ok.unsqueeze(1), scores, neg)
         out = torch.matmul(torch.softmax(s_swa, dim=-1), v)
         Ly = self.layers[li]
