@@ -366,22 +366,64 @@ def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, s
     return target, draft
 
 
+def cpu_baseline_e2e(Wt, Wd, prompt, budget_s: float = 15.0):
+    """The reference's CPU verify path restated in numpy (oracle/model.py:
+    full re-forward of [context, drafts] per round with no KV cache, head read
+    at the k+1 verified positions; draft re-forwarded per token; canonical
+    acceptance), timed on one sequence of the config-5 workload for about
+    budget_s of host time, BLAS threads limited to the box's CPU share."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import model as OM
+    from versenext_amd import model as VM
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    ct, cd = VM.mate_target(), VM.mate_draft(2)
+    rng = np.random.default_rng(31)
+    seq = [int(t) for t in prompt]
+    rounds, toks, tsum = 0, 0, 0.0
+    with threadpool_limits(limits=cores):
+        while rounds < 1 or (tsum < budget_s and rounds < 8):
+            ud = rng.random(E2E_K).astype(np.float32)
+            ua = rng.random(E2E_K + 1).astype(np.float32)
+            t0 = time.perf_counter()
+            acc = OM.spec_round_cpu(Wt, ct, Wd, cd, seq, E2E_K, E2E_TEMP, ud, ua)
+            tsum += time.perf_counter() - t0
+            seq += acc
+            toks += len(acc)
+            rounds += 1
+    return dict(value=round(toks / tsum, 3), unit="tokens/s", cores=cores, kind="port",
+                sample=f"{rounds} speculative rounds (k={E2E_K}, T={E2E_TEMP}) of one config-5 sequence "
+                       f"(512-token prompt) through oracle.model.spec_round_cpu: numpy fp32 re-forward of the "
+                       f"CometSparkV05 target and the 2-layer draft (fp32 weights), {toks} tokens committed, "
+                       f"{tsum / rounds:.2f} s per round, {cores} BLAS threads")
+
+
 def bench_e2e(args):
     """end-to-end speculative decode.  Target CometSparkV05
     (D 1024, 20 layers = 5 MoD + 15 TriSparse, tied 248,320 head, random init,
     bf16); draft: 2 mate-width TriSparse layers (D 1024, ffn 4096) with INT4
     group-128 weights and tied head; k = 6, batch 32, 512-token uniform-random
-    prompts, 256 new tokens per sequence, temperature 0.8.
+    prompts, 256 new tokens per sequence, temperature 0.8.  Each decode round
+    is one HIP graph replay.
     value = verified tokens / s = 32 * 256 committed tokens / wall time of the
-    decode rounds (prefill timed and reported separately)."""
+    decode rounds (prefill timed and reported separately).
+    The accept-kernel half of the metric is measured in
+    the same run after the models are freed: its k_spec_lse launch is the
+    roofline object, and its CPU leg rides along as cpu_baseline_accept."""
     import numpy as np
     import torch
     from versenext_amd import get_backend
+    from versenext_amd import model as VM
     from versenext_amd.e2e import SpecDecodeEngine
 
     hip = get_backend("rocm:0")
     dev = hip.torch_device
     t_build = time.perf_counter()
+    Wt_host = Wd_host = None
+    if not args.no_cpu:
+        Wt_host = {k: v.cpu().numpy() for k, v in VM.init_weights(VM.mate_target(), seed=0, device=dev).items()}
+        Wd_host = {k: v.cpu().numpy() for k, v in VM.init_weights(VM.mate_draft(2), seed=1, device=dev).items()}
     target, draft = build_e2e(hip)
     build_s = time.perf_counter() - t_build
     g = torch.Generator(device=dev)
@@ -397,52 +439,40 @@ def bench_e2e(args):
                           "prefill_s": round(st.prefill_s, 4), "tokens_per_s": round(st.tokens_per_s, 1),
                           "graph": eng.graph is not None}), flush=True)
     timed = runs[-1]
+    graphed = eng.graph is not None
+    tcfg_name, dcfg_name = target.cfg.name, draft.cfg.name
+    prompt0 = prompts[0].cpu().numpy()
     mean_tokens_round = float(np.mean(timed.per_round_tokens)) / E2E_B
+    del eng, target, draft, toks
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    acc = bench_accept(args, emit=False)
     out = {"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(timed.tokens_per_s, 1),
            "unit": "tokens/s", "n_gpus": 1, "steps": timed.rounds, "warmup": len(runs) - 1,
            "ms_per_step": round(timed.decode_s * 1e3 / timed.rounds, 3), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16 target / int4 draft / f32 logits",
            "data": "synthetic (random-init weights, uniform-random prompts)",
            "config": {"workload": "BASELINE config 5: end-to-end speculative decode", "batch": E2E_B, "k": E2E_K,
-                      "rounds_as": "HIP graph replays" if eng.graph is not None else "eager launches",
+                      "rounds_as": "HIP graph replays" if graphed else "eager launches",
                       "prompt": E2E_T0, "new_tokens": E2E_NEW, "temperature": E2E_TEMP,
-                      "target": target.cfg.name, "draft": draft.cfg.name + ", INT4 g128"},
+                      "target": tcfg_name, "draft": dcfg_name + ", INT4 g128",
+                      "step": "one speculative round: 7 draft forwards + 6 draws, one 7-token target verify "
+                              "+ LM head, acceptance, commit"},
            "prefill_s": round(timed.prefill_s, 4), "build_s": round(build_s, 2),
            "mean_tokens_per_round_per_seq": round(mean_tokens_round, 3),
-           "mean_accepted_per_round_per_seq": round(mean_tokens_round - 1.0, 3)}
+           "roofline": acc["roofline"],
+           "accept_kernel": {"metric": acc["metric"], "value": acc["value"], "unit": acc["unit"],
+                             "workload": acc["config"]["workload"], "frac_of_hbm_peak":
+                             acc["config"]["frac_of_hbm_peak"], "ms_per_call": acc["config"]["event_ms_mean"]}}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_e2e(Wt_host, Wd_host, prompt0)
+        out["cpu_baseline_accept"] = acc.get("cpu_baseline")
     print(json.dumps(out), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--e2e-runs", type=int, default=2, help="e2e: decode runs (the last is reported)")
-    ap.add_argument("--e2e-eager", action="store_true", help="e2e: launch every round eagerly (no HIP graph)")
-    ap.add_argument("--calib-copy", action="store_true",
-                    help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
-    ap.add_argument("--workload", default="accept", choices=("accept", "gemv", "tree", "lmhead", "e2e"),
-                    help="accept: BASELINE config 2 (the bench line); gemv: config 4; tree: config 3")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
-                                   "run with --gpus 1", "n_gpus": args.gpus}))
-        sys.exit(2)
-    if args.workload == "gemv":
-        bench_gemv(args)
-        return
-    if args.workload == "tree":
-        bench_tree(args)
-        return
-    if args.workload == "lmhead":
-        bench_lmhead(args)
-        return
-    if args.workload == "e2e":
-        bench_e2e(args)
-        return
-
+def bench_accept(args, emit=True):
+    """one vnx_spec_accept call per step (module docstring)."""
     import numpy as np
     import torch
     from versenext_amd import get_backend
@@ -532,8 +562,45 @@ def main():
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(tgt, dft, ids, u)
-    print(json.dumps(out), flush=True)
+    if emit:
+        print(json.dumps(out), flush=True)
+    return out
 
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--e2e-runs", type=int, default=2, help="e2e: decode runs (the last is reported)")
+    ap.add_argument("--e2e-eager", action="store_true", help="e2e: launch every round eagerly (no HIP graph)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
+    ap.add_argument("--workload", default="e2e", choices=("e2e", "accept", "gemv", "tree", "lmhead"),
+                    help="e2e: BASELINE config 5 verified tokens/s with the config-2 accept-kernel roofline "
+                         "(the bench line); accept: config 2 alone; gemv: config 4; tree: config 3; "
+                         "lmhead: the verify-pass LM head")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
+                                   "run with --gpus 1", "n_gpus": args.gpus}))
+        sys.exit(2)
+    if args.workload == "gemv":
+        bench_gemv(args)
+        return
+    if args.workload == "tree":
+        bench_tree(args)
+        return
+    if args.workload == "lmhead":
+        bench_lmhead(args)
+        return
+    if args.workload == "e2e":
+        bench_e2e(args)
+        return
+
+    bench_accept(args)
 
 if __name__ == "__main__":
     main()

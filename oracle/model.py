@@ -147,8 +147,10 @@ def mod(W, p, cfg, x):
     return out
 
 
-def forward(W, cfg, idx, return_hidden=False):
-    """logits (B, T, V) float32 of the tokens idx (B, T)."""
+def forward(W, cfg, idx, return_hidden=False, last_n=None):
+    """logits (B, T, V) float32 of the tokens idx (B, T); with last_n, only
+    the last last_n positions go through the head (the verifier reads k+1
+    rows, speculative.py:218-220)."""
     idx = np.asarray(idx, dtype=np.int64)
     if idx.ndim == 1:
         idx = idx[None]
@@ -168,6 +170,8 @@ def forward(W, cfg, idx, return_hidden=False):
     x = _rms(x, W["norm.weight"], cfg.eps)
     if return_hidden:
         return x
+    if last_n is not None:
+        x = x[:, -last_n:]
     return x @ emb.T
 
 
@@ -214,3 +218,31 @@ def spec_decode_greedy(Wt, cfg_t, Wd, cfg_d, prompt, n_new, k):
                 out.append(t)
                 seq.append(t)
     return np.asarray(out, dtype=np.int64), steps
+
+
+def spec_round_cpu(Wt, cfg_t, Wd, cfg_d, seq, k, temperature, u_draft, u_acc):
+    """One stochastic speculative round for one sequence on the CPU, the
+    reference's way (full re-forward, no KV cache, speculative.py:202-213):
+    k draft tokens drawn from softmax(draft logits / T) with u_draft[i]
+    (inverse CDF, the acceptance kernels' draw), one target re-forward of
+    [seq, drafts] read at the k+1 verified positions, then the canonical
+    acceptance (oracle.speculative.spec_accept) with u_acc.  Returns the
+    committed tokens (accepted drafts + the drawn / bonus token)."""
+    from .speculative import spec_accept
+    ctx = list(np.asarray(seq, dtype=np.int64).reshape(-1))
+    V = cfg_t.vocab_size
+    q = np.empty((1, k, V), np.float32)
+    xs = []
+    empty_d = np.zeros((1, 0, V), np.float32)
+    empty_i = np.zeros((1, 0), np.int64)
+    for i in range(k):
+        q[0, i] = forward(Wd, cfg_d, np.asarray(ctx)[None], last_n=1)[0, -1]
+        r = spec_accept(q[:, i:i + 1], empty_d, empty_i, np.asarray([[u_draft[i]]], np.float32), temperature)
+        x = int(r["out_ids"][0, 0])
+        xs.append(x)
+        ctx.append(x)
+    p = forward(Wt, cfg_t, np.asarray(ctx)[None], last_n=k + 1)
+    res = spec_accept(p, q, np.asarray([xs], np.int64), np.asarray(u_acc, np.float32).reshape(1, k + 1),
+                      temperature)
+    n = int(res["accept_len"][0])
+    return [int(t) for t in res["out_ids"][0, :n + 1]]
