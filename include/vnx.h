@@ -329,6 +329,49 @@ int vnx_row_topk(const void* logits, int dtype, int64_t rows, int64_t V, int64_t
 int vnx_lm_head(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t M, int64_t K, int64_t V,
                 void* out, int out_dtype, int64_t ldo, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Fused per-layer work of the CometSpark forward (verify and draft steps).
+ * Activation dtypes: VNX_F32, VNX_BF16 or VNX_F16; matrices row-major with
+ * the given row pitches (elements).
+ *
+ * vnx_rmsnorm: per row m < M of D <= 4096 values, s = x[m] + res[m] (res may
+ * be NULL), x_out[m] = s (x_out may be x, or NULL), y[m] = s / sqrt(mean(s^2)
+ * + eps) * w.  RMSNorm (packages/verse_torch/verse_torch/vnnn.py:593-615,
+ * :468-508) with the residual adds of VerseNexBlock.forward
+ * (packages/verse_nex/verse_nex/cometspark.py:236-247).
+ *
+ * vnx_rope_kv: qkv (B*n rows of (H + 2*Hkv) * d values, heads q | k | v);
+ * row (b, i) sits at position lens[b] + i.  q_out (B, H, n, d) contiguous =
+ * q with RoPE (rotate-half, x*cos + rotate_half(x)*sin with the cos / sin
+ * tables of table_rows x d fp32 values; rope = 0 copies), k with RoPE and v
+ * are written into the caches at (b, kv head, position) via the strides
+ * {c_sb, c_sh, c_sr}.  q_out and the caches are out_dtype (VNX_F32 or
+ * VNX_BF16).  Rows whose position is not below cap (nor, with RoPE, below
+ * table_rows) are skipped.  TriSparseAttention._apply_rope and its KV-cache
+ * concat (packages/verse_nex/verse_nex/tri_sparse_attn.py:182-221, :558-575).
+ *
+ * vnx_swiglu: out[m, c] = silu(gu[m, c]) * gu[m, Hf + c], c < Hf: the
+ * activation of SwiGLUMLP (vnnn.py:779-807) on a fused gate | up product.
+ *
+ * vnx_axpby: out[t] = coef[0] * a[t] + coef[1] * b[t], t < n, coef a device
+ * array: the sigmoid-gated sum of the TriSparse paths (tri_sparse_attn.py:
+ * 585-608).
+ * ------------------------------------------------------------------------- */
+int vnx_rmsnorm(const float* x, int64_t ldx, const void* res, int res_dtype, int64_t ldr, const float* w,
+                float eps, int64_t M, int64_t D, float* x_out, int64_t ldxo, void* y, int y_dtype, int64_t ldy,
+                void* stream);
+
+int vnx_rope_kv(const void* qkv, int dtype, int64_t ldq, int64_t B, int n, int H, int Hkv, int d,
+                const int32_t* lens, const float* cos_table, const float* sin_table, int64_t table_rows, int rope,
+                void* q_out, void* k_cache, void* v_cache, int out_dtype, int64_t c_sb, int64_t c_sh,
+                int64_t c_sr, int64_t cap, void* stream);
+
+int vnx_swiglu(const void* gu, int dtype, int64_t ldg, int64_t M, int64_t Hf, void* out, int out_dtype,
+               int64_t ldo, void* stream);
+
+int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void* out, int out_dtype,
+              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

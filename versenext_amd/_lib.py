@@ -24,6 +24,12 @@ VNX_F32 = 0
 VNX_BF16 = 1
 VNX_F16 = 2
 
+try:
+    import torch as _torch
+    DTYPE_CODES = {_torch.float32: VNX_F32, _torch.bfloat16: VNX_BF16, _torch.float16: VNX_F16}
+except Exception:  # the CPU-only ABI tests do not need torch dtypes
+    DTYPE_CODES = {}
+
 FLAG_NEAR_TIE = 1
 FLAG_LSE_EDGE = 2
 FLAG_CDF_EDGE = 4
@@ -91,6 +97,12 @@ SIGNATURES.update({
     "vnx_row_topk_workspace": (_c_sz, [_c_i64, _c_i64, _int]),
     "vnx_row_topk": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _vp, _c_i64, _vp, _c_sz, _vp]),
     "vnx_lm_head": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
+    "vnx_rmsnorm": (_int, [_vp, _c_i64, _vp, _int, _c_i64, _vp, _f32, _c_i64, _c_i64, _vp, _c_i64, _vp, _int,
+                           _c_i64, _vp]),
+    "vnx_rope_kv": (_int, [_vp, _int, _c_i64, _c_i64, _int, _int, _int, _int, _vp, _vp, _vp, _c_i64, _int,
+                           _vp, _vp, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),
+    "vnx_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
+    "vnx_axpby": (_int, [_vp, _vp, _vp, _c_i64, _vp, _int, _vp]),
 })
 
 _lib = None

@@ -1,0 +1,280 @@
+// Per-layer elementwise work of the CometSpark forward, fused so that a
+// verify or draft step launches a handful of kernels per layer instead of
+// dozens of small PyTorch ones:
+//   vnx_rmsnorm   x += r (optional residual), y = x / sqrt(mean(x^2) + eps) * w
+//                 (RMSNorm, packages/verse_torch/verse_torch/vnnn.py:593-615;
+//                 the residual adds of VerseNexBlock.forward, cometspark.py:236-247);
+//   vnx_rope_kv   RoPE of q and k at each sequence's positions lens[b] + i
+//                 (TriSparseAttention._apply_rope, tri_sparse_attn.py:182-221),
+//                 q to the attention layout, k / v written into the KV cache;
+//   vnx_swiglu    silu(g) * u of the fused gate|up product (SwiGLUMLP,
+//                 vnnn.py:779-807);
+//   vnx_axpby     c0 * a + c1 * b with device coefficients (the sigmoid-gated
+//                 sum of the TriSparse paths, tri_sparse_attn.py:585-608).
+// Activations are fp32, bf16 or fp16 (dtype codes of vnx.h); every kernel
+// reads its inputs once and writes its outputs once.
+#include "vnx_internal.h"
+
+namespace vnx {
+namespace {
+
+template <typename T>
+struct Elt;
+template <>
+struct Elt<float> {
+  __device__ __forceinline__ static float ld(const float* p) { return *p; }
+  __device__ __forceinline__ static void st(float* p, float v) { *p = v; }
+};
+template <>
+struct Elt<__hip_bfloat16> {
+  __device__ __forceinline__ static float ld(const __hip_bfloat16* p) {
+    return __uint_as_float((uint32_t)(*reinterpret_cast<const uint16_t*>(p)) << 16);
+  }
+  __device__ __forceinline__ static void st(__hip_bfloat16* p, float v) {
+    const uint32_t u = __float_as_uint(v);
+    uint16_t b;
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) b = (uint16_t)((u >> 16) | 0x40u);
+    else b = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);  // round to nearest even
+    *reinterpret_cast<uint16_t*>(p) = b;
+  }
+};
+template <>
+struct Elt<_Float16> {
+  __device__ __forceinline__ static float ld(const _Float16* p) { return (float)*p; }
+  __device__ __forceinline__ static void st(_Float16* p, float v) { *p = (_Float16)v; }
+};
+
+template <typename F>
+int by_dtype(int dt, F&& f) {
+  switch (dt) {
+    case VNX_F32: return f(float{});
+    case VNX_BF16: return f(__hip_bfloat16{});
+    case VNX_F16: return f(_Float16{});
+    default: return (int)VNX_ERR_UNSUPPORTED;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: one workgroup per row, the row held in registers (D <= 16 * 256).
+// ---------------------------------------------------------------------------
+constexpr int kRnThreads = 256;
+constexpr int kRnPer = 16;
+
+template <typename TR, typename TY>
+__global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t ldx, const TR* r, int64_t ldr,
+                                                        const float* w, float eps, int64_t D, float* xo,
+                                                        int64_t ldxo, TY* y, int64_t ldy) {
+  __shared__ float red[kRnThreads / VNX_WAVE];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  float v[kRnPer];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRnPer; ++j) {
+    const int64_t c = tid + (int64_t)j * kRnThreads;
+    float a = 0.0f;
+    if (c < D) {
+      a = x[row * ldx + c];
+      if (r) a += Elt<TR>::ld(r + row * ldr + c);
+    }
+    v[j] = a;
+    ss = __builtin_fmaf(a, a, ss);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, VNX_WAVE);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kRnThreads / VNX_WAVE; ++i) tot += red[i];
+  const float inv = 1.0f / __builtin_sqrtf(tot / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < kRnPer; ++j) {
+    const int64_t c = tid + (int64_t)j * kRnThreads;
+    if (c < D) {
+      if (xo) xo[row * ldxo + c] = v[j];
+      Elt<TY>::st(y + row * ldy + c, v[j] * inv * w[c]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE + KV-cache write.  qkv rows (b, i) hold [q heads | k heads | v heads]
+// of head_dim d; position p = lens[b] + i.  One thread per (row, head, pair
+// (j, j + d/2)) of the rotate-half form x*cos + rotate_half(x)*sin.
+// ---------------------------------------------------------------------------
+struct RopeParams {
+  const void* qkv;
+  int64_t ldq;
+  int64_t B;
+  int n, H, Hkv, d;
+  const int32_t* lens;
+  const float* cos;
+  const float* sin;
+  int rope;
+  void* q;                  // (B, H, n, d) contiguous, cache dtype
+  void* kc;
+  void* vc;
+  int64_t c_sb, c_sh, c_sr;  // cache strides (elements)
+  int64_t cap;               // rows of the cache (and at most the table length)
+};
+
+template <typename TQ, typename TO>
+__global__ __launch_bounds__(256) void k_rope_kv(RopeParams p) {
+  const int half = p.d / 2;
+  const int heads = p.H + 2 * p.Hkv;
+  const int64_t total = p.B * (int64_t)p.n * heads * half;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  const int j = (int)(t % half);
+  int64_t r = t / half;
+  const int hh = (int)(r % heads);
+  r /= heads;
+  const int i = (int)(r % p.n);
+  const int64_t b = r / p.n;
+  const int64_t pos = (int64_t)p.lens[b] + i;
+  if (pos < 0 || pos >= p.cap) return;  // never past the cache or the RoPE table
+  const TQ* src = static_cast<const TQ*>(p.qkv) + (b * p.n + i) * p.ldq + (int64_t)hh * p.d;
+  float x0 = Elt<TQ>::ld(src + j), x1 = Elt<TQ>::ld(src + j + half);
+  if (p.rope && hh < p.H + p.Hkv) {
+    const float c0 = p.cos[pos * p.d + j], c1 = p.cos[pos * p.d + j + half];
+    const float s0 = p.sin[pos * p.d + j], s1 = p.sin[pos * p.d + j + half];
+    const float y0 = x0 * c0 - x1 * s0;   // rotate_half(x)[j] = -x[j + half]
+    const float y1 = x1 * c1 + x0 * s1;   // rotate_half(x)[j + half] = x[j]
+    x0 = y0;
+    x1 = y1;
+  }
+  TO* dst;
+  if (hh < p.H) {
+    dst = static_cast<TO*>(p.q) + ((b * p.H + hh) * p.n + i) * (int64_t)p.d;
+  } else if (hh < p.H + p.Hkv) {
+    dst = static_cast<TO*>(p.kc) + b * p.c_sb + (int64_t)(hh - p.H) * p.c_sh + pos * p.c_sr;
+  } else {
+    dst = static_cast<TO*>(p.vc) + b * p.c_sb + (int64_t)(hh - p.H - p.Hkv) * p.c_sh + pos * p.c_sr;
+  }
+  Elt<TO>::st(dst + j, x0);
+  Elt<TO>::st(dst + j + half, x1);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU activation: out[m, c] = silu(gu[m, c]) * gu[m, Hf + c].
+// ---------------------------------------------------------------------------
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_swiglu(const TI* gu, int64_t ldg, int64_t M, int64_t Hf, TO* out,
+                                                int64_t ldo) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= M * Hf) return;
+  const int64_t m = t / Hf, c = t - m * Hf;
+  const float g = Elt<TI>::ld(gu + m * ldg + c);
+  const float u = Elt<TI>::ld(gu + m * ldg + Hf + c);
+  const float s = g / (1.0f + __expf(-g));
+  Elt<TO>::st(out + m * ldo + c, s * u);
+}
+
+// out = coef[0] * a + coef[1] * b (coef on the device, so captured graphs
+// keep reading the current gate values).
+template <typename TO>
+__global__ __launch_bounds__(256) void k_axpby(const float* a, const float* b, const float* coef, int64_t n,
+                                               TO* out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  Elt<TO>::st(out + t, coef[0] * a[t] + coef[1] * b[t]);
+}
+
+inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+}  // namespace vnx
+
+using namespace vnx;
+
+extern "C" {
+
+int vnx_rmsnorm(const float* x, int64_t ldx, const void* res, int res_dtype, int64_t ldr, const float* w,
+                float eps, int64_t M, int64_t D, float* x_out, int64_t ldxo, void* y, int y_dtype, int64_t ldy,
+                void* stream) {
+  if (!x || !w || !y || M < 0 || D <= 0 || ldx < D || ldy < D || (res && ldr < D) || (x_out && ldxo < D))
+    return VNX_ERR_INVALID_ARG;
+  if (D > (int64_t)kRnThreads * kRnPer || !(eps >= 0.0f)) return VNX_ERR_UNSUPPORTED;
+  if (M == 0) return VNX_OK;
+  if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rdt = res ? res_dtype : VNX_F32;
+  return by_dtype(rdt, [&](auto tr) {
+    using TR = decltype(tr);
+    return by_dtype(y_dtype, [&](auto ty) {
+      using TY = decltype(ty);
+      hipLaunchKernelGGL((k_rmsnorm<TR, TY>), dim3((unsigned)M), dim3(kRnThreads), 0, s, x, ldx,
+                         static_cast<const TR*>(res), ldr, w, eps, D, x_out, ldxo, static_cast<TY*>(y), ldy);
+      VNX_LAUNCH_CHECK();
+      return (int)VNX_OK;
+    });
+  });
+}
+
+int vnx_rope_kv(const void* qkv, int dtype, int64_t ldq, int64_t B, int n, int H, int Hkv, int d,
+                const int32_t* lens, const float* cos_table, const float* sin_table, int64_t table_rows, int rope,
+                void* q_out, void* k_cache, void* v_cache, int out_dtype, int64_t c_sb, int64_t c_sh,
+                int64_t c_sr, int64_t cap, void* stream) {
+  if (!qkv || !lens || !q_out || !k_cache || !v_cache || B < 0 || n < 1 || H < 1 || Hkv < 1 || d < 2 || d % 2)
+    return VNX_ERR_INVALID_ARG;
+  if (ldq < (int64_t)(H + 2 * Hkv) * d || c_sb < 0 || c_sh < 0 || c_sr < d) return VNX_ERR_INVALID_ARG;
+  if (rope && (!cos_table || !sin_table || table_rows < 1)) return VNX_ERR_INVALID_ARG;
+  if (cap < 1 || (out_dtype != VNX_F32 && out_dtype != VNX_BF16)) return VNX_ERR_INVALID_ARG;
+  if (B == 0) return VNX_OK;
+  // Positions lens[b] + i are read on the device; rows at or past the cache
+  // capacity (or the RoPE table) are skipped there, so a bad length cannot
+  // write out of bounds.
+  RopeParams p{};
+  p.qkv = qkv; p.ldq = ldq; p.B = B; p.n = n; p.H = H; p.Hkv = Hkv; p.d = d;
+  p.lens = lens; p.cos = cos_table; p.sin = sin_table; p.rope = rope ? 1 : 0;
+  p.q = q_out; p.kc = k_cache; p.vc = v_cache;
+  p.c_sb = c_sb; p.c_sh = c_sh; p.c_sr = c_sr;
+  p.cap = rope ? (cap < table_rows ? cap : table_rows) : cap;
+  const int64_t total = B * (int64_t)n * (H + 2 * Hkv) * (d / 2);
+  if (total >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return by_dtype(dtype, [&](auto tq) {
+    using TQ = decltype(tq);
+    if (out_dtype == VNX_F32)
+      hipLaunchKernelGGL((k_rope_kv<TQ, float>), dim3(blocks_for(total)), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((k_rope_kv<TQ, __hip_bfloat16>), dim3(blocks_for(total)), dim3(256), 0, s, p);
+    VNX_LAUNCH_CHECK();
+    return (int)VNX_OK;
+  });
+}
+
+int vnx_swiglu(const void* gu, int dtype, int64_t ldg, int64_t M, int64_t Hf, void* out, int out_dtype,
+               int64_t ldo, void* stream) {
+  if (!gu || !out || M < 0 || Hf <= 0 || ldg < 2 * Hf || ldo < Hf) return VNX_ERR_INVALID_ARG;
+  if (M == 0) return VNX_OK;
+  if (M * Hf >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return by_dtype(dtype, [&](auto ti) {
+    using TI = decltype(ti);
+    return by_dtype(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      hipLaunchKernelGGL((k_swiglu<TI, TO>), dim3(blocks_for(M * Hf)), dim3(256), 0, s,
+                         static_cast<const TI*>(gu), ldg, M, Hf, static_cast<TO*>(out), ldo);
+      VNX_LAUNCH_CHECK();
+      return (int)VNX_OK;
+    });
+  });
+}
+
+int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void* out, int out_dtype,
+              void* stream) {
+  if (!a || !b || !coef || !out || n < 0) return VNX_ERR_INVALID_ARG;
+  if (n == 0) return VNX_OK;
+  if (n >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return by_dtype(out_dtype, [&](auto to) {
+    using TO = decltype(to);
+    hipLaunchKernelGGL((k_axpby<TO>), dim3(blocks_for(n)), dim3(256), 0, s, a, b, coef, n, static_cast<TO*>(out));
+    VNX_LAUNCH_CHECK();
+    return (int)VNX_OK;
+  });
+}
+
+}  // extern "C"

@@ -255,19 +255,26 @@ class _Linear:
         else:
             self.wd = w.to(dtype).contiguous()
 
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+    def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x (M, K); returns (M, N) in the compute dtype (dense) or fp32
+        (INT4 GEMV, written into `out` when given: an (M, N) fp32 view with
+        unit column stride)."""
         M = x.shape[0]
         if self.int4 and M <= 64:
             x16 = x.to(torch.float16).contiguous()
-            y = torch.empty((M, self.N), dtype=torch.float32, device=x.device)
+            y = out if out is not None else torch.empty((M, self.N), dtype=torch.float32, device=x.device)
             L = self.hip._L
             _lib.check(L.vnx_gemv_w4(
                 ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq.data_ptr()), self.wq.stride(0),
                 ctypes.c_void_p(self.sc.data_ptr()), _lib.VNX_F16, self.sc.stride(0), M, self.N, self.K, 128,
-                ctypes.c_void_p(y.data_ptr()), self.N, ctypes.c_void_p(self._ws.data_ptr()), self._ws.numel(),
-                ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4")
+                ctypes.c_void_p(y.data_ptr()), y.stride(0), ctypes.c_void_p(self._ws.data_ptr()),
+                self._ws.numel(), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4")
             return y
-        return torch.nn.functional.linear(x.to(self.dtype), self.wd).float()
+        y = torch.nn.functional.linear(x.to(self.dtype), self.wd)
+        if out is not None:
+            out.copy_(y)
+            return out
+        return y
 
 
 class CometSparkGPU:
@@ -343,19 +350,23 @@ class CometSparkGPU:
         self._words = {}
         self._neg = torch.full((), -1e9, dtype=torch.float32, device=dev)  # the reference's mask value
         self.kernel_attention = (dtype == torch.bfloat16 and d in (64, 128) and not cfg.use_alibi)
+        # dtype of the activations fed to the projections: fp16 for the INT4
+        # GEMVs, else the compute dtype
+        self.act_dtype = torch.float16 if int4 else dtype
 
     # ---- pieces ---------------------------------------------------------
-    def _rms(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        ms = (x * x).mean(dim=-1, keepdim=True)
-        return x / torch.sqrt(ms + self.cfg.eps) * w
+    def _st(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
 
-    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        """x (B, n, heads, d) fp32, pos (B, n) int64: x*cos + rotate_half(x)*sin."""
-        half = x.shape[-1] // 2
-        cos = self.cos[pos].unsqueeze(2)
-        sin = self.sin[pos].unsqueeze(2)
-        rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
-        return x * cos + rot * sin
+    def _rms(self, x: torch.Tensor, res: Optional[torch.Tensor], w: torch.Tensor, y: torch.Tensor) -> None:
+        """x += res (in place, res may be None); y = RMSNorm(x) * w (vnx_rmsnorm)."""
+        M, D = x.shape
+        P = ctypes.c_void_p
+        _lib.check(self.hip._L.vnx_rmsnorm(
+            P(x.data_ptr()), x.stride(0), P(res.data_ptr()) if res is not None else None,
+            _lib.DTYPE_CODES[res.dtype] if res is not None else _lib.VNX_F32, res.stride(0) if res is not None else D,
+            P(w.data_ptr()), float(self.cfg.eps), M, D, P(x.data_ptr()), x.stride(0), P(y.data_ptr()),
+            _lib.DTYPE_CODES[y.dtype], y.stride(0), self._st()), "rmsnorm")
 
     def _chain_words(self, n: int) -> torch.Tensor:
         w = self._words.get(n)
@@ -365,48 +376,53 @@ class CometSparkGPU:
             self._words[n] = w
         return w
 
+    def _tree_call(self, q, kc, vc, cstr, tree_k, tree_v, tstr, anc, B, H, Hkv, Tp, n, d, tp, follows, out):
+        a = _lib.TreeAttnArgs()
+        a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
+        a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = cstr
+        a.k_tree = tree_k.data_ptr(); a.v_tree = tree_v.data_ptr(); a.tree_strides[:] = tstr
+        a.anc = anc.data_ptr(); a.anc_batch_stride = 0
+        # output rows in (B, n, H, d) order: the proj input layout
+        a.out = out.data_ptr(); a.out_dtype = _lib.VNX_F32; a.out_strides[:] = [n * H * d, d, H * d]
+        a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, n, d
+        a.scale = 1.0 / math.sqrt(d)
+        a.tp_batch = tp.data_ptr() if tp is not None else None
+        a.tree_follows_prefix = 1 if follows else 0
+        L = self.hip._L
+        ws = self.hip._workspace(L.vnx_tree_attn_workspace(B, H, Hkv, n, Tp, d))
+        _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), self._st()),
+                   "tree_attn")
+
     def _attn_kernel(self, q, li, lens, n, Tmax):
-        """Sliding-window + global paths on vnx_tree_attn.  q (B, H, n, d) bf16."""
+        """Sliding-window + global paths on vnx_tree_attn, combined with the
+        sigmoid gates into the proj input (B*n, H*d).  q (B, H, n, d) bf16."""
         cfg = self.cfg
         B, H, _, d = q.shape
         Hkv = cfg.n_kv_head
         kc, vc = self.kc[li], self.vc[li]
-        out_s = torch.empty((B, H, n, d), dtype=torch.float32, device=self.dev)
-        a = _lib.TreeAttnArgs()
-        a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
-        a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = list(kc.stride()[:3])
-        a.k_tree = kc.data_ptr(); a.v_tree = vc.data_ptr(); a.tree_strides[:] = list(kc.stride()[:3])
-        a.anc = self._chain_words(n).data_ptr(); a.anc_batch_stride = 0
-        a.out = out_s.data_ptr(); a.out_dtype = _lib.VNX_F32; a.out_strides[:] = list(out_s.stride()[:3])
-        a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tmax, n, d
-        a.scale = 1.0 / math.sqrt(d)
-        a.tp_batch = lens.data_ptr(); a.tree_follows_prefix = 1
-        L = self.hip._L
-        st = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
-        ws = self.hip._workspace(L.vnx_tree_attn_workspace(B, H, Hkv, n, Tmax, d))
-        _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "tree_attn")
-        # global sink tokens: every query sees the G global rows (the prefix),
-        # no tree row (empty ancestor words).
         Ly = self.layers[li]
-        G = Ly.gk.shape[2]
-        out_g = torch.empty_like(out_s)
-        g = _lib.TreeAttnArgs()
-        g.q = q.data_ptr(); g.q_strides[:] = list(q.stride()[:3])
-        gs = [0, Ly.gk_pad.stride(1), Ly.gk_pad.stride(2)]
-        g.k_cache = Ly.gk_pad.data_ptr(); g.v_cache = Ly.gv_pad.data_ptr(); g.cache_strides[:] = gs
-        g.k_tree = Ly.gk_pad.data_ptr(); g.v_tree = Ly.gv_pad.data_ptr(); g.tree_strides[:] = gs
+        o_s = torch.empty((B * n, H * d), dtype=torch.float32, device=self.dev)
+        o_g = torch.empty_like(o_s)
+        cstr = list(kc.stride()[:3])
+        # sliding window: each row's prefix of lens[b] rows, then its n new
+        # rows (written in place right after it) under the chain mask
+        self._tree_call(q, kc, vc, cstr, kc, vc, cstr, self._chain_words(n), B, H, Hkv, Tmax, n, d, lens, True,
+                        o_s)
+        # global sink tokens: all G rows visible as a batch-stride-0 prefix,
+        # no tree row visible (empty ancestor words)
         zero = self._words.get("zero")
-        if zero is None or zero.numel() < n:
+        if zero is None:
             zero = torch.zeros(64, dtype=torch.int64, device=self.dev)
             self._words["zero"] = zero
-        g.anc = zero.data_ptr(); g.anc_batch_stride = 0
-        g.out = out_g.data_ptr(); g.out_dtype = _lib.VNX_F32; g.out_strides[:] = list(out_g.stride()[:3])
-        g.B, g.H, g.Hkv, g.Tp, g.N, g.d = B, H, Hkv, G, n, d
-        g.scale = 1.0 / math.sqrt(d)
-        g.tp_batch = None; g.tree_follows_prefix = 0
-        ws = self.hip._workspace(L.vnx_tree_attn_workspace(B, H, Hkv, n, G, d))
-        _lib.check(L.vnx_tree_attn(ctypes.byref(g), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "global attn")
-        return out_s, out_g
+        gs = [0, Ly.gk_pad.stride(1), Ly.gk_pad.stride(2)]
+        self._tree_call(q, Ly.gk_pad, Ly.gv_pad, gs, Ly.gk_pad, Ly.gv_pad, gs, zero, B, H, Hkv, Ly.gk.shape[2], n,
+                        d, None, False, o_g)
+        o = torch.empty((B * n, H * d), dtype=self.act_dtype, device=self.dev)
+        _lib.check(self.hip._L.vnx_axpby(ctypes.c_void_p(o_s.data_ptr()), ctypes.c_void_p(o_g.data_ptr()),
+                                         ctypes.c_void_p(Ly.gates.data_ptr()), o.numel(),
+                                         ctypes.c_void_p(o.data_ptr()), _lib.DTYPE_CODES[o.dtype], self._st()),
+                   "axpby")
+        return o
 
     def _attn_torch(self, q, li, lens, n, Tmax):
         """The same three paths with explicit fp32 masks (any head size,
@@ -443,10 +459,12 @@ class CometSparkGPU:
             res = res + torch.where(use_c, Ly.gates[2] * out_c, torch.zeros_like(out_c))
         return res
 
-    def _mod(self, L: _Layer, x: torch.Tensor) -> torch.Tensor:
-        """MoD FFN on (M, D) fp32: every expert runs on every row and the
-        router weights (zero for unselected experts) combine them."""
+    def _mod(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
+        """MoD FFN on (M, D) activations: every expert runs on every row and
+        the router weights (zero for unselected experts) combine them.
+        Routing runs in fp32; returns (M, D) fp32."""
         cfg = self.cfg
+        x = h.float()
         P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
         pw = torch.softmax(x @ L.ffn["part_router"].t(), dim=-1)                   # (M, P)
         rl = (x @ L.ffn["routers"].reshape(P * E, -1).t()).view(-1, P, E)          # (M, P, E) fp32
@@ -454,19 +472,23 @@ class CometSparkGPU:
         wsel = torch.softmax(top_v, dim=-1)                                        # (M, P, k)
         comb = torch.zeros_like(rl).scatter_(-1, top_i, wsel) * pw.unsqueeze(-1)   # (M, P, E)
         M = x.shape[0]
-        xb = x.to(self.dtype).unsqueeze(0).expand(P * E, M, cfg.dim).contiguous()
+        xb = (h if h.dtype == self.dtype else h.to(self.dtype)).unsqueeze(0).expand(P * E, M, cfg.dim).contiguous()
         h = torch.matmul(xb, L.ffn["w1"])                                          # (PE, M, 2He)
         He = cfg.expert_hidden_eff
         a = torch.nn.functional.silu(h[..., :He].float()) * h[..., He:].float()
         y = torch.matmul(a.to(self.dtype), L.ffn["w2"]).float()                    # (PE, M, D)
         return (comb.reshape(M, P * E).t().unsqueeze(-1) * y).sum(0)
 
-    def _ffn(self, L: _Layer, x: torch.Tensor) -> torch.Tensor:
+    def _ffn(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
         if L.kind == "mod":
-            return self._mod(L, x)
+            return self._mod(L, h)
         Hf = self.cfg.ffn_hidden
-        gu = L.ffn["gu"](x)
-        return L.ffn["down"](torch.nn.functional.silu(gu[:, :Hf]) * gu[:, Hf:])
+        gu = L.ffn["gu"](h)
+        act = torch.empty((h.shape[0], Hf), dtype=self.act_dtype, device=self.dev)
+        _lib.check(self.hip._L.vnx_swiglu(ctypes.c_void_p(gu.data_ptr()), _lib.DTYPE_CODES[gu.dtype], gu.stride(0),
+                                          h.shape[0], Hf, ctypes.c_void_p(act.data_ptr()),
+                                          _lib.DTYPE_CODES[act.dtype], Hf, self._st()), "swiglu")
+        return L.ffn["down"](act)
 
     # ---- forward --------------------------------------------------------
     @torch.no_grad()
@@ -477,36 +499,42 @@ class CometSparkGPU:
         B, n = tokens.shape
         if B != self.B:
             raise ValueError(f"batch {B} != the cache's {self.B}")
+        if lens.dtype != torch.int32 or lens.numel() != B:
+            raise ValueError("lens must be (B,) int32")
         if Tmax is None:
             Tmax = int(lens.max())
         if Tmax + n > self.cap:
             raise ValueError(f"cache capacity {self.cap} exceeded ({Tmax} + {n})")
         H, Hkv, d, D = cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.dim
-        pos = lens.long().view(B, 1) + torch.arange(n, device=self.dev).view(1, n)
-        x = self.emb[tokens].float() * self.emb_scale                                # (B, n, D)
-        bidx = torch.arange(B, device=self.dev).view(B, 1).expand(B, n)
+        M = B * n
+        P = ctypes.c_void_p
+        L_ = self.hip._L
+        x = (self.emb[tokens.reshape(-1)].float() * self.emb_scale).contiguous()     # (M, D) fp32 residual
         use_kernel = self.kernel_attention and n <= 64 and Tmax + n <= cfg.window_size
+        pending = None
         for li, L in enumerate(self.layers):
-            h = self._rms(x, L.norm1).reshape(B * n, D)
-            qkv = L.wqkv(h).view(B, n, (H + 2 * Hkv), d)
-            q, k, v = qkv[:, :, :H], qkv[:, :, H:H + Hkv], qkv[:, :, H + Hkv:]
-            if cfg.use_rope:
-                q = self._rope(q, pos)
-                k = self._rope(k, pos)
-            # new rows into the cache at lens[b] + i
-            self.kc[li][bidx, :, pos] = k.to(self.dtype)
-            self.vc[li][bidx, :, pos] = v.to(self.dtype)
-            qh = q.permute(0, 2, 1, 3).to(self.dtype).contiguous()                  # (B, H, n, d)
+            h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
+            self._rms(x, pending, L.norm1, h)
+            qkv = L.wqkv(h)                                                          # (M, (H+2Hkv) d)
+            q = torch.empty((B, H, n, d), dtype=self.dtype, device=self.dev)
+            kc, vc = self.kc[li], self.vc[li]
+            _lib.check(L_.vnx_rope_kv(
+                P(qkv.data_ptr()), _lib.DTYPE_CODES[qkv.dtype], qkv.stride(0), B, n, H, Hkv, d, P(lens.data_ptr()),
+                P(self.cos.data_ptr()), P(self.sin.data_ptr()), self.cos.shape[0], int(cfg.use_rope),
+                P(q.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()), _lib.DTYPE_CODES[self.dtype],
+                kc.stride(0), kc.stride(1), kc.stride(2), self.cap, self._st()), "rope_kv")
             if use_kernel:
-                o_s, o_g = self._attn_kernel(qh, li, lens, n, Tmax)
-                o = L.gates[0] * o_s + L.gates[1] * o_g
+                o = self._attn_kernel(q, li, lens, n, Tmax)
             else:
-                o = self._attn_torch(qh, li, lens, n, Tmax)
-            o = o.permute(0, 2, 1, 3).reshape(B * n, H * d)
-            x = x + L.proj(o).view(B, n, D)
-            h2 = self._rms(x, L.norm2).reshape(B * n, D)
-            x = x + self._ffn(L, h2).view(B, n, D)
-        return self._rms(x, self.norm)
+                o = self._attn_torch(q, li, lens, n, Tmax).permute(0, 2, 1, 3).reshape(M, H * d)
+                o = o.to(self.act_dtype).contiguous()
+            a = L.proj(o)
+            h2 = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
+            self._rms(x, a, L.norm2, h2)
+            pending = self._ffn(L, h2)
+        out = torch.empty((M, D), dtype=torch.float32, device=self.dev)
+        self._rms(x, pending, self.norm, out)
+        return out.view(B, n, D)
 
     def logits(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """(B, n, V) fp32 logits of the tied head: vnx_lm_head (bf16, matrix
@@ -516,11 +544,10 @@ class CometSparkGPU:
         V = self.cfg.vocab_size
         h2 = hidden.reshape(B * n, D)
         if self.head is not None:
-            y = self.head(h2)
             if out is not None:
-                out.view(B * n, V).copy_(y)
+                self.head(h2, out=out.view(B * n, V))
                 return out
-            return y.view(B, n, V)
+            return self.head(h2).view(B, n, V)
         if self.dtype == torch.bfloat16 and D % 64 == 0 and B * n <= 256:
             if out is None:
                 out = torch.empty((B, n, V), dtype=torch.float32, device=self.dev)
