@@ -372,6 +372,22 @@ int vnx_swiglu(const void* gu, int dtype, int64_t ldg, int64_t M, int64_t Hf, vo
 int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void* out, int out_dtype,
               void* stream);
 
+/* MoD routing (Router.forward, packages/verse_nex/verse_nex/mod.py:337-440;
+ * MoDLayer.forward, :779-803): logits (M, P + P*E) fp32 = [part-router
+ * logits | the P expert routers' logits, part-major]; comb (M, P*E) fp32 =
+ * softmax(part logits)[p] x softmax over part p's top-k expert logits
+ * (larger first, ties to the lower index) for the selected experts, 0
+ * elsewhere.  P <= 8, E <= 16, 1 <= topk <= E. */
+int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int topk, float* comb, int64_t ldc,
+                  void* stream);
+
+/* out[m, x*He + j] = comb[m, x] * silu(gu[m, x*2He + j]) * gu[m, x*2He + He + j]
+ * for the PE experts x: the routed, weighted expert activations, so that one
+ * product with the experts' concatenated down projections is the MoD output
+ * (DensePart / Expert, mod.py:466-600). */
+int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, const float* comb, int64_t ldc, int64_t M, int PE,
+                   int64_t He, void* out, int out_dtype, int64_t ldo, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

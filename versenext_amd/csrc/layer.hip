@@ -10,7 +10,9 @@
 //   vnx_swiglu    silu(g) * u of the fused gate|up product (SwiGLUMLP,
 //                 vnnn.py:779-807);
 //   vnx_axpby     c0 * a + c1 * b with device coefficients (the sigmoid-gated
-//                 sum of the TriSparse paths, tri_sparse_attn.py:585-608).
+//                 sum of the TriSparse paths, tri_sparse_attn.py:585-608);
+//   vnx_mod_route / vnx_mod_swiglu  MoD routing weights and the weighted
+//                 expert activations (mod.py:142-213, :337-440, :779-803).
 // Activations are fp32, bf16 or fp16 (dtype codes of vnx.h); every kernel
 // reads its inputs once and writes its outputs once.
 #include "vnx_internal.h"
@@ -181,6 +183,71 @@ __global__ __launch_bounds__(256) void k_axpby(const float* a, const float* b, c
   Elt<TO>::st(out + t, coef[0] * a[t] + coef[1] * b[t]);
 }
 
+// ---------------------------------------------------------------------------
+// MoD routing (Router.forward, packages/verse_nex/verse_nex/mod.py:337-440,
+// MoDLayer.forward :779-803): per row, the part weights are the softmax of
+// the P part-router logits (top_k = P, all parts); inside part p the top-k
+// of its E expert logits (larger first, ties to the lower index) are weighted
+// by the softmax over the selected logits.  comb[m, p*E + e] = part weight x
+// expert weight, 0 for unselected experts.  One thread per row.
+// ---------------------------------------------------------------------------
+constexpr int kModMaxP = 8;
+constexpr int kModMaxE = 16;
+
+__global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E,
+                                                  int topk, float* comb, int64_t ldc) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  const float* l = logits + m * ld;
+  float* c = comb + m * ldc;
+  float mx = -__builtin_inff();
+  for (int p = 0; p < P; ++p) mx = fmaxf(mx, l[p]);
+  float sp = 0.0f;
+  for (int p = 0; p < P; ++p) sp += expf(l[p] - mx);
+  for (int p = 0; p < P; ++p) {
+    const float pw = expf(l[p] - mx) / sp;
+    const float* le = l + P + p * E;
+    uint32_t taken = 0;
+    int sel[kModMaxE];
+    for (int i = 0; i < topk; ++i) {
+      int best = -1;
+      for (int e = 0; e < E; ++e)
+        if (!((taken >> e) & 1u) && (best < 0 || le[e] > le[best])) best = e;
+      sel[i] = best;
+      taken |= 1u << best;
+    }
+    float ms = -__builtin_inff();
+    for (int i = 0; i < topk; ++i) ms = fmaxf(ms, le[sel[i]]);
+    float ss = 0.0f;
+    for (int i = 0; i < topk; ++i) ss += expf(le[sel[i]] - ms);
+    for (int e = 0; e < E; ++e) c[p * E + e] = 0.0f;
+    for (int i = 0; i < topk; ++i) c[p * E + sel[i]] = pw * (expf(le[sel[i]] - ms) / ss);
+  }
+}
+
+// Expert activations of all PE experts for every row, scaled by the routing
+// weights: out[m, x*He + j] = comb[m, x] * silu(gu[m, x*2He + j]) *
+// gu[m, x*2He + He + j] (gu = the fused gate|up product of every expert), so
+// one product with the concatenated down projections sums the experts.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_mod_swiglu(const TI* gu, int64_t ldg, const float* comb, int64_t ldc,
+                                                    int64_t M, int PE, int64_t He, TO* out, int64_t ldo) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = (int64_t)PE * He;
+  if (t >= M * per_row) return;
+  const int64_t m = t / per_row, r = t - m * per_row;
+  const int x = (int)(r / He);
+  const int64_t j = r - (int64_t)x * He;
+  const float w = comb[m * ldc + x];
+  float v = 0.0f;
+  if (w != 0.0f) {
+    const TI* g = gu + m * ldg + (int64_t)x * 2 * He;
+    const float a = Elt<TI>::ld(g + j), u = Elt<TI>::ld(g + He + j);
+    v = w * (a / (1.0f + __expf(-a))) * u;
+  }
+  Elt<TO>::st(out + m * ldo + r, v);
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -274,6 +341,39 @@ int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void
     hipLaunchKernelGGL((k_axpby<TO>), dim3(blocks_for(n)), dim3(256), 0, s, a, b, coef, n, static_cast<TO*>(out));
     VNX_LAUNCH_CHECK();
     return (int)VNX_OK;
+  });
+}
+
+int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int topk, float* comb, int64_t ldc,
+                  void* stream) {
+  if (!logits || !comb || M < 0 || P < 1 || E < 1 || topk < 1 || topk > E) return VNX_ERR_INVALID_ARG;
+  if (P > kModMaxP || E > kModMaxE) return VNX_ERR_UNSUPPORTED;
+  if (ld < P + (int64_t)P * E || ldc < (int64_t)P * E) return VNX_ERR_INVALID_ARG;
+  if (M == 0) return VNX_OK;
+  if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_mod_route, dim3((unsigned)((M + 63) / 64)), dim3(64), 0, s, logits, ld, M, P, E, topk,
+                     comb, ldc);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, const float* comb, int64_t ldc, int64_t M, int PE,
+                   int64_t He, void* out, int out_dtype, int64_t ldo, void* stream) {
+  if (!gu || !comb || !out || M < 0 || PE < 1 || He < 1) return VNX_ERR_INVALID_ARG;
+  if (ldg < 2 * He * PE || ldc < PE || ldo < He * PE) return VNX_ERR_INVALID_ARG;
+  if (M == 0) return VNX_OK;
+  if (M * PE * He >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return by_dtype(dtype, [&](auto ti) {
+    using TI = decltype(ti);
+    return by_dtype(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      hipLaunchKernelGGL((k_mod_swiglu<TI, TO>), dim3(blocks_for(M * PE * He)), dim3(256), 0, s,
+                         static_cast<const TI*>(gu), ldg, comb, ldc, M, PE, He, static_cast<TO*>(out), ldo);
+      VNX_LAUNCH_CHECK();
+      return (int)VNX_OK;
+    });
   });
 }
 

@@ -383,6 +383,11 @@ static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d) {
   const int64_t base = (int64_t)B * Hkv * pl.G;
   const int64_t target = (int64_t)device_cus() * 4 * wg_scale_pct() / 100;
   int S = (int)((target + base - 1) / base);
+  // A split must carry enough keys to pay for the merge launch: at least 24
+  // 32-key steps each (the config-3 sweep: 2 splits of 33 steps beat 4 of
+  // 17; a verify step over ~800 keys runs best unsplit).
+  const int sby_work = steps / 24 > 1 ? steps / 24 : 1;
+  S = S < sby_work ? S : sby_work;
   const int smax = (steps + 3) / 4;  // at least one 32-key step per wave
   if (ta_splits_override()) S = ta_splits_override();
   S = S < 1 ? 1 : (S > smax ? smax : S);

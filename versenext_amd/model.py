@@ -327,18 +327,21 @@ class CometSparkGPU:
                 L.ffn["down"] = _Linear(W[p + "ffn.w_down.weight"], dtype, hip, int4)
             else:
                 P, E = cfg.num_dense_parts, cfg.num_experts_per_part
-                L.ffn["part_router"] = W[p + "ffn.part_router.gate.weight"]
-                L.ffn["routers"] = torch.stack([W[p + f"ffn.parts.{q}.router.gate.weight"] for q in range(P)])
+                # routing logits [part router | expert routers, part-major] in
+                # one fp32 product
+                L.ffn["route"] = torch.cat([W[p + "ffn.part_router.gate.weight"]]
+                                           + [W[p + f"ffn.parts.{q}.router.gate.weight"] for q in range(P)],
+                                           0).contiguous()
                 w1, w2 = [], []
                 for q in range(P):
                     for e in range(E):
                         ep = p + f"ffn.parts.{q}.experts.{e}."
-                        w1.append(torch.cat([W[ep + "w_gate.weight"], W[ep + "w_up.weight"]], 0).t())
-                        w2.append(W[ep + "w_down.weight"].t())
-                # (P*E, D, 2He) and (P*E, He, D), contiguous: the batched
-                # products take them untransposed.
-                L.ffn["w1"] = torch.stack(w1).to(dtype).contiguous()
-                L.ffn["w2"] = torch.stack(w2).to(dtype).contiguous()
+                        w1.append(torch.cat([W[ep + "w_gate.weight"], W[ep + "w_up.weight"]], 0))
+                        w2.append(W[ep + "w_down.weight"])
+                # every expert's gate|up rows stacked: (P*E*2He, D); every
+                # expert's down projection side by side: (D, P*E*He)
+                L.ffn["w1"] = torch.cat(w1, 0).to(dtype).contiguous()
+                L.ffn["w2"] = torch.cat(w2, 1).to(dtype).contiguous()
             self.layers.append(L)
         cos, sin = rope_tables(d, self.cap + 64, cfg.rope_theta)
         self.cos = torch.from_numpy(cos).to(dev)
@@ -460,24 +463,26 @@ class CometSparkGPU:
         return res
 
     def _mod(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
-        """MoD FFN on (M, D) activations: every expert runs on every row and
-        the router weights (zero for unselected experts) combine them.
-        Routing runs in fp32; returns (M, D) fp32."""
+        """MoD FFN on (M, D) fp32 normalized rows: fp32 routing logits in one
+        product, the routing weights (vnx_mod_route), every expert's gate|up
+        in one product, the weighted activations (vnx_mod_swiglu; zero for
+        unselected experts) and one product with the concatenated down
+        projections, which sums the experts."""
         cfg = self.cfg
-        x = h.float()
         P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
-        pw = torch.softmax(x @ L.ffn["part_router"].t(), dim=-1)                   # (M, P)
-        rl = (x @ L.ffn["routers"].reshape(P * E, -1).t()).view(-1, P, E)          # (M, P, E) fp32
-        top_v, top_i = torch.topk(rl, k, dim=-1)
-        wsel = torch.softmax(top_v, dim=-1)                                        # (M, P, k)
-        comb = torch.zeros_like(rl).scatter_(-1, top_i, wsel) * pw.unsqueeze(-1)   # (M, P, E)
-        M = x.shape[0]
-        xb = (h if h.dtype == self.dtype else h.to(self.dtype)).unsqueeze(0).expand(P * E, M, cfg.dim).contiguous()
-        h = torch.matmul(xb, L.ffn["w1"])                                          # (PE, M, 2He)
-        He = cfg.expert_hidden_eff
-        a = torch.nn.functional.silu(h[..., :He].float()) * h[..., He:].float()
-        y = torch.matmul(a.to(self.dtype), L.ffn["w2"]).float()                    # (PE, M, D)
-        return (comb.reshape(M, P * E).t().unsqueeze(-1) * y).sum(0)
+        PE, He = P * E, cfg.expert_hidden_eff
+        M = h.shape[0]
+        P_ = ctypes.c_void_p
+        logits = torch.nn.functional.linear(h, L.ffn["route"])                    # (M, P + PE) fp32
+        comb = torch.empty((M, PE), dtype=torch.float32, device=self.dev)
+        _lib.check(self.hip._L.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k,
+                                             P_(comb.data_ptr()), PE, self._st()), "mod_route")
+        gu = torch.nn.functional.linear(h.to(self.dtype), L.ffn["w1"])            # (M, PE*2He)
+        act = torch.empty((M, PE * He), dtype=self.dtype, device=self.dev)
+        _lib.check(self.hip._L.vnx_mod_swiglu(P_(gu.data_ptr()), _lib.DTYPE_CODES[gu.dtype], gu.stride(0),
+                                              P_(comb.data_ptr()), PE, M, PE, He, P_(act.data_ptr()),
+                                              _lib.DTYPE_CODES[act.dtype], act.stride(0), self._st()), "mod_swiglu")
+        return torch.nn.functional.linear(act, L.ffn["w2"])                       # (M, D)
 
     def _ffn(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
         if L.kind == "mod":
@@ -529,7 +534,8 @@ class CometSparkGPU:
                 o = self._attn_torch(q, li, lens, n, Tmax).permute(0, 2, 1, 3).reshape(M, H * d)
                 o = o.to(self.act_dtype).contiguous()
             a = L.proj(o)
-            h2 = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
+            # MoD layers route on fp32 rows, as the reference does
+            h2 = torch.empty((M, D), dtype=torch.float32 if L.kind == "mod" else self.act_dtype, device=self.dev)
             self._rms(x, a, L.norm2, h2)
             pending = self._ffn(L, h2)
         out = torch.empty((M, D), dtype=torch.float32, device=self.dev)
