@@ -381,12 +381,18 @@ int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void
 int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int topk, float* comb, int64_t ldc,
                   void* stream);
 
-/* out[m, x*He + j] = comb[m, x] * silu(gu[m, x*2He + j]) * gu[m, x*2He + He + j]
- * for the PE experts x: the routed, weighted expert activations, so that one
- * product with the experts' concatenated down projections is the MoD output
- * (DensePart / Expert, mod.py:466-600). */
-int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, const float* comb, int64_t ldc, int64_t M, int PE,
-                   int64_t He, void* out, int out_dtype, int64_t ldo, void* stream);
+/* The routed, weighted expert activations (DensePart / Expert,
+ * mod.py:466-600): for row m and expert x < PE, with g = gu + m*ldg + x*sxg
+ * and o = out + m*ldo + x*sxo, o[j] = comb[m, x] * silu(g[j]) * g[He + j],
+ * j < He (0 for unselected experts).  Row-major (M, PE*2He) input is
+ * sxg = 2He, ldg = PE*2He; expert-major (PE, M, 2He) is ldg = 2He,
+ * sxg = M*2He (the same choices for out with He). */
+int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, int64_t sxg, const float* comb, int64_t ldc, int64_t M,
+                   int PE, int64_t He, void* out, int out_dtype, int64_t ldo, int64_t sxo, void* stream);
+
+/* out (M, D) fp32 = sum over x < PE of y[x] (y (PE, M, D) contiguous): the sum
+ * of the experts' (weighted) down projections (MoDLayer.forward, mod.py:779-803). */
+int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, float* out, void* stream);
 
 #ifdef __cplusplus
 }

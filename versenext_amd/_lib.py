@@ -104,7 +104,9 @@ SIGNATURES.update({
     "vnx_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
     "vnx_axpby": (_int, [_vp, _vp, _vp, _c_i64, _vp, _int, _vp]),
     "vnx_mod_route": (_int, [_vp, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64, _vp]),
-    "vnx_mod_swiglu": (_int, [_vp, _int, _c_i64, _vp, _c_i64, _c_i64, _int, _c_i64, _vp, _int, _c_i64, _vp]),
+    "vnx_mod_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _int, _c_i64, _vp, _int, _c_i64,
+                              _c_i64, _vp]),
+    "vnx_sum_experts": (_int, [_vp, _int, _c_i64, _int, _c_i64, _vp, _vp]),
 })
 
 _lib = None

@@ -229,9 +229,15 @@ __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t l
 // weights: out[m, x*He + j] = comb[m, x] * silu(gu[m, x*2He + j]) *
 // gu[m, x*2He + He + j] (gu = the fused gate|up product of every expert), so
 // one product with the concatenated down projections sums the experts.
+// gu row (m, x) at gu + m*ldg + x*sxg (gate in [0, He), up in [He, 2He));
+// out row (m, x) at out + m*ldo + x*sxo: the row-major (M, PE*2He) form of
+// one product over the concatenated experts (sxg = 2He, sxo = He) and the
+// expert-major (PE, M, 2He) form of a batched product (ldg = 2He,
+// sxg = M*2He) are both strides of this.
 template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void k_mod_swiglu(const TI* gu, int64_t ldg, const float* comb, int64_t ldc,
-                                                    int64_t M, int PE, int64_t He, TO* out, int64_t ldo) {
+__global__ __launch_bounds__(256) void k_mod_swiglu(const TI* gu, int64_t ldg, int64_t sxg, const float* comb,
+                                                    int64_t ldc, int64_t M, int PE, int64_t He, TO* out,
+                                                    int64_t ldo, int64_t sxo) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t per_row = (int64_t)PE * He;
   if (t >= M * per_row) return;
@@ -241,11 +247,22 @@ __global__ __launch_bounds__(256) void k_mod_swiglu(const TI* gu, int64_t ldg, c
   const float w = comb[m * ldc + x];
   float v = 0.0f;
   if (w != 0.0f) {
-    const TI* g = gu + m * ldg + (int64_t)x * 2 * He;
+    const TI* g = gu + m * ldg + (int64_t)x * sxg;
     const float a = Elt<TI>::ld(g + j), u = Elt<TI>::ld(g + He + j);
     v = w * (a / (1.0f + __expf(-a))) * u;
   }
-  Elt<TO>::st(out + m * ldo + r, v);
+  Elt<TO>::st(out + m * ldo + (int64_t)x * sxo + j, v);
+}
+
+// out[m, c] = sum over x < PE of y[x, m, c] (fp32 accumulation in x order):
+// the sum of the routed experts' down projections (already weighted).
+template <typename TY>
+__global__ __launch_bounds__(256) void k_sum_experts(const TY* y, int64_t M, int PE, int64_t D, float* out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= M * D) return;
+  float acc = 0.0f;
+  for (int x = 0; x < PE; ++x) acc += Elt<TY>::ld(y + (int64_t)x * M * D + t);
+  out[t] = acc;
 }
 
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -358,10 +375,16 @@ int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int 
   return VNX_OK;
 }
 
-int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, const float* comb, int64_t ldc, int64_t M, int PE,
-                   int64_t He, void* out, int out_dtype, int64_t ldo, void* stream) {
+int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, int64_t sxg, const float* comb, int64_t ldc, int64_t M,
+                   int PE, int64_t He, void* out, int out_dtype, int64_t ldo, int64_t sxo, void* stream) {
   if (!gu || !comb || !out || M < 0 || PE < 1 || He < 1) return VNX_ERR_INVALID_ARG;
-  if (ldg < 2 * He * PE || ldc < PE || ldo < He * PE) return VNX_ERR_INVALID_ARG;
+  if (ldg < 0 || sxg < 0 || ldo < 0 || sxo < 0 || ldc < PE) return VNX_ERR_INVALID_ARG;
+  // rows and experts must not overlap: either layout of the two products
+  const bool g_rowmajor = sxg >= 2 * He && ldg >= sxg * PE;
+  const bool g_expmajor = ldg >= 2 * He && sxg >= ldg * M;
+  const bool o_rowmajor = sxo >= He && ldo >= sxo * PE;
+  const bool o_expmajor = ldo >= He && sxo >= ldo * M;
+  if (!(g_rowmajor || g_expmajor) || !(o_rowmajor || o_expmajor)) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
   if (M * PE * He >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -370,10 +393,25 @@ int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, const float* comb, in
     return by_dtype(out_dtype, [&](auto to) {
       using TO = decltype(to);
       hipLaunchKernelGGL((k_mod_swiglu<TI, TO>), dim3(blocks_for(M * PE * He)), dim3(256), 0, s,
-                         static_cast<const TI*>(gu), ldg, comb, ldc, M, PE, He, static_cast<TO*>(out), ldo);
+                         static_cast<const TI*>(gu), ldg, sxg, comb, ldc, M, PE, He, static_cast<TO*>(out), ldo,
+                         sxo);
       VNX_LAUNCH_CHECK();
       return (int)VNX_OK;
     });
+  });
+}
+
+int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, float* out, void* stream) {
+  if (!y || !out || M < 0 || PE < 1 || D < 1) return VNX_ERR_INVALID_ARG;
+  if (M == 0) return VNX_OK;
+  if (M * D >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return by_dtype(dtype, [&](auto ty) {
+    using TY = decltype(ty);
+    hipLaunchKernelGGL((k_sum_experts<TY>), dim3(blocks_for(M * D)), dim3(256), 0, s, static_cast<const TY*>(y),
+                       M, PE, D, out);
+    VNX_LAUNCH_CHECK();
+    return (int)VNX_OK;
   });
 }
 

@@ -87,7 +87,10 @@ struct TaSmem {
   static constexpr size_t bytes = (q_bytes + v_bytes > merge_bytes) ? q_bytes + v_bytes : merge_bytes;
 };
 
-template <int D, int QT, bool OUT_BF16>
+// PF: issue the loads of a wave's next key step before the current step's
+// math (more registers: chosen when the grid is at most one workgroup per CU,
+// where latency, not occupancy, bounds the kernel).
+template <int D, int QT, bool OUT_BF16, bool PF>
 __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
   constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
   constexpr int DT = D / 16;          // 16-wide dimension tiles of O
@@ -163,23 +166,33 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
   const int k_hi = min(KT, k_lo + p.chunk);
   const int nsteps = (k_hi - k_lo + 31) >> 5;
 
-  for (int st = w; st < nsteps; st += 4) {
-    const int base = k_lo + st * 32;
-    // K fragments: A rows = keys base + kt*16 + col, k = dims ks*32 + grp*8 .. +8.
-    u32x4 kf[2][KS];
+  // One step's loads: K fragments (A rows = keys base + kt*16 + col, k = dims
+  // ks*32 + grp*8 .. +8) and V rows, coalesced (load v covers keys
+  // v*(64/LPR) + lane/LPR, chunk lane%LPR).  The loads of a wave's next step
+  // are issued before the current step's math, so HBM latency overlaps it.
+  auto load_step = [&](int base, u32x4 (&kf)[2][KS], u32x4 (&vv)[VLD]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       const uint16_t* r = krow(base + kt * 16 + col, p.kc, p.kt);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = ldg16(r + ks * 32 + grp * 8);
     }
-    // V rows, coalesced: load v covers keys v*(64/LPR) + lane/LPR, chunk lane%LPR.
-    u32x4 vv[VLD];
 #pragma unroll
     for (int v = 0; v < VLD; ++v) {
       const int key = base + v * (64 / LPR) + lane / LPR;
       vv[v] = ldg16(krow(key, p.vc, p.vt) + (lane % LPR) * 8);
       if (key >= k_hi) vv[v] = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  u32x4 kf[2][KS], vv[VLD], kfn[2][KS], vvn[VLD];
+  if (PF && w < nsteps) load_step(k_lo + w * 32, kf, vv);
+  for (int st = w; st < nsteps; st += 4) {
+    const int base = k_lo + st * 32;
+    const bool more = PF && st + 4 < nsteps;
+    if constexpr (PF) {
+      if (more) load_step(base + 4 * 32, kfn, vvn);
+    } else {
+      load_step(base, kf, vv);
     }
     wave_lds_sync();  // previous step's V^T reads are done
 #pragma unroll
@@ -245,6 +258,14 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], bh, o[qt][dt], 0, 0, 0);
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], bl, o[qt][dt], 0, 0, 0);
       }
+    }
+    if (more) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = kfn[kt][ks];
+#pragma unroll
+      for (int v = 0; v < VLD; ++v) vv[v] = vvn[v];
     }
   }
 
@@ -406,20 +427,29 @@ static size_t ta_ws_bytes(const TaPlan& pl, int B, int H, int N, int d) {
   return c.bytes();
 }
 
-template <int D, bool OB>
-static int ta_launch_d(const TreeAttnParams& p, int QT, hipStream_t st, hipEvent_t* ev) {
-  const dim3 grid((unsigned)((int64_t)p.B * p.Hkv * p.G * p.S));
-  if (ev) VNX_HIP_CHECK(hipEventRecord(ev[0], st));
+template <int D, bool OB, bool PF>
+static void ta_launch_qt(const TreeAttnParams& p, int QT, dim3 grid, hipStream_t st) {
   switch (QT) {
-    case 1: hipLaunchKernelGGL((k_tree_attn<D, 1, OB>), grid, dim3(kTaThreads), 0, st, p); break;
-    case 2: hipLaunchKernelGGL((k_tree_attn<D, 2, OB>), grid, dim3(kTaThreads), 0, st, p); break;
+    case 1: hipLaunchKernelGGL((k_tree_attn<D, 1, OB, PF>), grid, dim3(kTaThreads), 0, st, p); break;
+    case 2: hipLaunchKernelGGL((k_tree_attn<D, 2, OB, PF>), grid, dim3(kTaThreads), 0, st, p); break;
     case 3:
-      if constexpr (D == 64) hipLaunchKernelGGL((k_tree_attn<D, 3, OB>), grid, dim3(kTaThreads), 0, st, p);
+      if constexpr (D == 64) hipLaunchKernelGGL((k_tree_attn<D, 3, OB, PF>), grid, dim3(kTaThreads), 0, st, p);
       break;
     default:
-      if constexpr (D == 64) hipLaunchKernelGGL((k_tree_attn<D, 4, OB>), grid, dim3(kTaThreads), 0, st, p);
+      if constexpr (D == 64) hipLaunchKernelGGL((k_tree_attn<D, 4, OB, PF>), grid, dim3(kTaThreads), 0, st, p);
       break;
   }
+}
+
+template <int D, bool OB>
+static int ta_launch_d(const TreeAttnParams& p, int QT, hipStream_t st, hipEvent_t* ev) {
+  const int64_t nwg = (int64_t)p.B * p.Hkv * p.G * p.S;
+  const dim3 grid((unsigned)nwg);
+  if (ev) VNX_HIP_CHECK(hipEventRecord(ev[0], st));
+  if (nwg <= device_cus())
+    ta_launch_qt<D, OB, true>(p, QT, grid, st);
+  else
+    ta_launch_qt<D, OB, false>(p, QT, grid, st);
   VNX_LAUNCH_CHECK();
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[1], st));
   if (p.S > 1) {

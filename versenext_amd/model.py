@@ -338,10 +338,10 @@ class CometSparkGPU:
                         ep = p + f"ffn.parts.{q}.experts.{e}."
                         w1.append(torch.cat([W[ep + "w_gate.weight"], W[ep + "w_up.weight"]], 0))
                         w2.append(W[ep + "w_down.weight"])
-                # every expert's gate|up rows stacked: (P*E*2He, D); every
-                # expert's down projection side by side: (D, P*E*He)
-                L.ffn["w1"] = torch.cat(w1, 0).to(dtype).contiguous()
-                L.ffn["w2"] = torch.cat(w2, 1).to(dtype).contiguous()
+                # batched-product operands, untransposed and contiguous:
+                # (P*E, D, 2He) gate|up and (P*E, He, D) down
+                L.ffn["w1"] = torch.stack([w.t() for w in w1]).to(dtype).contiguous()
+                L.ffn["w2"] = torch.stack([w.t() for w in w2]).to(dtype).contiguous()
             self.layers.append(L)
         cos, sin = rope_tables(d, self.cap + 64, cfg.rope_theta)
         self.cos = torch.from_numpy(cos).to(dev)
@@ -464,25 +464,31 @@ class CometSparkGPU:
 
     def _mod(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
         """MoD FFN on (M, D) fp32 normalized rows: fp32 routing logits in one
-        product, the routing weights (vnx_mod_route), every expert's gate|up
-        in one product, the weighted activations (vnx_mod_swiglu; zero for
-        unselected experts) and one product with the concatenated down
-        projections, which sums the experts."""
+        product and the routing weights (vnx_mod_route); every expert's
+        gate|up and down as batched products over the P*E experts, with the
+        weighted activations in between (vnx_mod_swiglu; zero for unselected
+        experts) and the sum over experts after (vnx_sum_experts)."""
         cfg = self.cfg
         P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
-        PE, He = P * E, cfg.expert_hidden_eff
+        PE, He, D = P * E, cfg.expert_hidden_eff, cfg.dim
         M = h.shape[0]
         P_ = ctypes.c_void_p
+        L_ = self.hip._L
         logits = torch.nn.functional.linear(h, L.ffn["route"])                    # (M, P + PE) fp32
         comb = torch.empty((M, PE), dtype=torch.float32, device=self.dev)
-        _lib.check(self.hip._L.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k,
-                                             P_(comb.data_ptr()), PE, self._st()), "mod_route")
-        gu = torch.nn.functional.linear(h.to(self.dtype), L.ffn["w1"])            # (M, PE*2He)
-        act = torch.empty((M, PE * He), dtype=self.dtype, device=self.dev)
-        _lib.check(self.hip._L.vnx_mod_swiglu(P_(gu.data_ptr()), _lib.DTYPE_CODES[gu.dtype], gu.stride(0),
-                                              P_(comb.data_ptr()), PE, M, PE, He, P_(act.data_ptr()),
-                                              _lib.DTYPE_CODES[act.dtype], act.stride(0), self._st()), "mod_swiglu")
-        return torch.nn.functional.linear(act, L.ffn["w2"])                       # (M, D)
+        _lib.check(L_.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k, P_(comb.data_ptr()), PE,
+                                    self._st()), "mod_route")
+        xb = h.to(self.dtype).unsqueeze(0).expand(PE, M, D).contiguous()
+        gu = torch.matmul(xb, L.ffn["w1"])                                        # (PE, M, 2He)
+        act = torch.empty((PE, M, He), dtype=self.dtype, device=self.dev)
+        _lib.check(L_.vnx_mod_swiglu(P_(gu.data_ptr()), _lib.DTYPE_CODES[gu.dtype], 2 * He, M * 2 * He,
+                                     P_(comb.data_ptr()), PE, M, PE, He, P_(act.data_ptr()),
+                                     _lib.DTYPE_CODES[act.dtype], He, M * He, self._st()), "mod_swiglu")
+        y = torch.matmul(act, L.ffn["w2"])                                        # (PE, M, D)
+        out = torch.empty((M, D), dtype=torch.float32, device=self.dev)
+        _lib.check(L_.vnx_sum_experts(P_(y.data_ptr()), _lib.DTYPE_CODES[y.dtype], M, PE, D, P_(out.data_ptr()),
+                                      self._st()), "sum_experts")
+        return out
 
     def _ffn(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
         if L.kind == "mod":
