@@ -232,8 +232,8 @@ int vnx_dequant_w8(const int8_t* wq, int64_t ldw, const float* scale, int64_t N,
  * q (B,H,N,d), caches (B,Hkv,Tp,d), tree rows (B,Hkv,N,d): bf16 with the head
  * dimension contiguous and strides {batch, head, row} in elements (multiples
  * of 8, pointers 16-byte aligned).  The tree rows may live inside the cache
- * (k_tree = k_cache + Tp*row stride).  out (B,H,N,d): fp32 or bf16 (round to
- * nearest even), strides multiples of 4.  d in {64, 128}; 1 <= N <= 64.
+ * (k_tree = k_cache + Tp*row stride).  out (B,H,N,d): fp32, bf16 or fp16
+ * (round to nearest even), strides multiples of 4.  d in {64, 128}; 1 <= N <= 64.
  * A node that sees no key (Tp == 0 and an empty mask word) gets zeros.
  * The workspace (vnx_tree_attn_workspace bytes, no initialisation) holds the
  * per-split partials when the keys are split over several workgroups.
@@ -250,7 +250,7 @@ typedef struct vnx_tree_attn_args {
   const uint64_t* anc;        /* (B, N) ancestor-or-self words                  */
   int64_t anc_batch_stride;   /* 0: one tree shared by all batch rows           */
   void* out;
-  int out_dtype;              /* VNX_F32 or VNX_BF16                            */
+  int out_dtype;              /* VNX_F32, VNX_BF16 or VNX_F16                   */
   int64_t out_strides[3];
   int B, H, Hkv, Tp, N, d;
   float scale;                /* > 0; 1/sqrt(d) in the reference               */
@@ -264,6 +264,20 @@ typedef struct vnx_tree_attn_args {
    * the cache in place). */
   const int32_t* tp_batch;
   int tree_follows_prefix;
+  /* Gated second key segment (TriSparse's global-token path,
+   * tri_sparse_attn.py:469-495, mixed with the sigmoid gates, :585-608):
+   * when T2 > 0, every node also attends to the T2 rows of k_seg2 / v_seg2
+   * (all visible, softmax normalised on their own) and
+   *   out = gates[0] * (attention over prefix + tree) + gates[1] * (attention
+   *         over the T2 rows)
+   * with gates a device array of 2 fp32.  seg2_strides {batch, head, row} in
+   * elements (batch 0: one segment shared by all rows), multiples of 8.
+   * T2 == 0 (or zero-initialised trailing fields): no second segment. */
+  const void* k_seg2;
+  const void* v_seg2;
+  int64_t seg2_strides[3];
+  int T2;
+  const float* gates;
 } vnx_tree_attn_args;
 
 size_t vnx_tree_attn_workspace(int B, int H, int Hkv, int N, int Tp, int d);

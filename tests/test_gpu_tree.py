@@ -37,16 +37,17 @@ def _np(t):
 def _check(out, ref, mag, bf16=False):
     o = out.float().cpu().numpy().astype(np.float64)
     err = np.abs(o - ref)
-    tol = RTOL * mag + (2.0 ** -8 * np.abs(ref) if bf16 else 0.0)
+    rnd = 2.0 ** -8 if bf16 else (2.0 ** -11 if out.dtype == torch.float16 else 0.0)
+    tol = RTOL * mag + rnd * np.abs(ref)
     worst = float(np.max(err / (mag + 1e-300)))
     assert np.all(err <= tol + 1e-30), f"worst err / mag = {worst:.3e}"
     return worst
 
 
 def _run(hip, B, H, Hkv, N, Tp, d, parent=None, seed=0, out_dtype=torch.float32, per_batch=False,
-         cache_extra=0, inplace=False, std=1.0):
+         cache_extra=0, inplace=False, std=1.0, T2=0, gates=(0.3, 0.8)):
     _say(f"tree_attn B={B} H={H} Hkv={Hkv} N={N} Tp={Tp} d={d} out={out_dtype} per_batch={per_batch} "
-         f"cache_extra={cache_extra} inplace={inplace}")
+         f"cache_extra={cache_extra} inplace={inplace} T2={T2}")
     rng = np.random.default_rng(seed)
     par = T.tree_from_branching((4, 3, 2)) if parent is None else np.asarray(parent, np.int32)
     assert par.size == N
@@ -67,10 +68,21 @@ def _run(hip, B, H, Hkv, N, Tp, d, parent=None, seed=0, out_dtype=torch.float32,
         words = np.stack([T.ancestor_words(par if b % 2 == 0 else T.chain(N)) for b in range(B)])
     else:
         words = T.ancestor_words(par)
-    out = hip.tree_attention(q, kc if Tp else None, vc if Tp else None, kt, vt, words, out_dtype=out_dtype)
+    seg2 = None
+    if T2:
+        seg2 = (_bf16(rng, (1, Hkv, T2, d), std).to(dev), _bf16(rng, (1, Hkv, T2, d)).to(dev))
+    out = hip.tree_attention(q, kc if Tp else None, vc if Tp else None, kt, vt, words, out_dtype=out_dtype,
+                             seg2=seg2, gates=np.asarray(gates, np.float32) if T2 else None)
     torch.cuda.synchronize()
     ref, mag = OT.tree_attention(_np(q), _np(kc) if Tp else None, _np(vc) if Tp else None, _np(kt), _np(vt),
                                  words)
+    if T2:
+        # the second segment: its T2 rows as a prefix, every tree row masked
+        k2 = np.broadcast_to(_np(seg2[0]), (B, Hkv, T2, d))
+        v2 = np.broadcast_to(_np(seg2[1]), (B, Hkv, T2, d))
+        r2, m2 = OT.tree_attention(_np(q), k2, v2, _np(kt), _np(vt), np.zeros(N, np.uint64))
+        g1, g2 = float(np.float32(gates[0])), float(np.float32(gates[1]))
+        ref, mag = g1 * ref + g2 * r2, g1 * mag + g2 * m2
     worst = _check(out, ref, mag, bf16=out_dtype == torch.bfloat16)
     _say(f"  worst err / sum p|v| = {worst:.2e}")
     return worst
@@ -125,6 +137,37 @@ def test_splits_cover_one_and_many(hip):
     assert _plan(1, 2, 1, 40, 64, 64)[1] == 2  # 80 query rows: two groups
     _run(hip, 64, 16, 16, 40, 2048, 64, seed=5)
     _run(hip, 1, 1, 1, 40, 8192, 64, seed=6)
+
+
+@pytest.mark.parametrize("waves", ["4", "5", "8", "16"])
+@pytest.mark.parametrize("B,H,Hkv,N,Tp,d", [(8, 16, 8, 1, 640, 64), (8, 16, 8, 7, 301, 64),
+                                            (2, 16, 16, 40, 700, 64), (2, 4, 2, 20, 300, 128)])
+def test_workgroup_shapes(hip, monkeypatch, waves, B, H, Hkv, N, Tp, d):
+    """Every workgroup shape (4 waves, 4 with prefetch, 8, 16; a shape that
+    does not fit the query tile falls back to the default) on decode-like
+    (N 1, 7) and verify-like (N 40) calls."""
+    monkeypatch.setenv("VNX_TA_WAVES", waves)
+    par = T.chain(N) if N < 40 else None
+    if N == 20:
+        rng = np.random.default_rng(5)
+        par = np.array([-1] + [int(rng.integers(-1, i)) for i in range(1, N)], np.int32)
+    _run(hip, B, H, Hkv, N, Tp, d, parent=par, seed=N + Tp)
+
+
+@pytest.mark.parametrize("waves,splits,out_dtype,N,T2,d", [
+    ("16", None, torch.float32, 1, 128, 64), ("8", None, torch.bfloat16, 7, 128, 64),
+    ("5", None, torch.float16, 7, 100, 64), ("4", "3", torch.float32, 7, 128, 64),
+    ("16", "2", torch.float16, 1, 40, 64), ("8", None, torch.float32, 7, 128, 128),
+    ("4", "2", torch.bfloat16, 40, 64, 64)])
+def test_gated_second_segment(hip, monkeypatch, waves, splits, out_dtype, N, T2, d):
+    """TriSparse's fused sliding-window + global paths: out = g1 * tree
+    attention + g2 * attention over the T2 shared rows, with and without key
+    splits (the second segment then merges through its own slot)."""
+    monkeypatch.setenv("VNX_TA_WAVES", waves)
+    if splits:
+        monkeypatch.setenv("VNX_TA_SPLITS", splits)
+    par = T.chain(N) if N < 40 else None
+    _run(hip, 6, 16, 8, N, 500, d, parent=par, seed=N + T2, out_dtype=out_dtype, T2=T2)
 
 
 def test_large_scores(hip):

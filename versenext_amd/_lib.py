@@ -84,6 +84,7 @@ class TreeAttnArgs(ctypes.Structure):
         ("out", _vp), ("out_dtype", _int), ("out_strides", _c_i64 * 3),
         ("B", _int), ("H", _int), ("Hkv", _int), ("Tp", _int), ("N", _int), ("d", _int),
         ("scale", _f32), ("tp_batch", _vp), ("tree_follows_prefix", _int),
+        ("k_seg2", _vp), ("v_seg2", _vp), ("seg2_strides", _c_i64 * 3), ("T2", _int), ("gates", _vp),
     ]
 
 

@@ -34,8 +34,7 @@ namespace vnx {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kTaThreads = 256;  // 4 waves
-constexpr int kTaMaxN = 64;      // tree nodes per sequence (one 64-bit mask word)
+constexpr int kTaMaxN = 64;  // tree nodes per sequence (one 64-bit mask word)
 
 struct TreeAttnParams {
   const uint16_t* q;
@@ -45,8 +44,8 @@ struct TreeAttnParams {
   const uint16_t* vt;
   const uint64_t* anc;
   void* out;
-  float* part_o;   // [B*H*N][S][D] unnormalised partial outputs (S > 1)
-  float2* part_ml; // [B*H*N][S] (m, l) in the exp2 domain (S > 1)
+  float* part_o;   // [B*H*N][S+1][D] unnormalised partial outputs (S > 1)
+  float2* part_ml; // [B*H*N][S+1] (m, l) in the exp2 domain (S > 1)
   int64_t q_sb, q_sh, q_sr;
   int64_t c_sb, c_sh, c_sr;
   int64_t t_sb, t_sh, t_sr;
@@ -56,6 +55,13 @@ struct TreeAttnParams {
   int S, G, rows_per_group, chunk;  // key splits, query groups, keys per split
   const int32_t* tp_batch;          // per-batch prefix rows (<= Tp), or NULL
   int tree_follows_prefix;          // tree row j of batch b is tree row tp_b + j
+  // Second key segment: T2 rows visible to every node, normalised on its own
+  // and mixed as gates[0] * segment 1 + gates[1] * segment 2 (T2 == 0: none).
+  const uint16_t* k2;
+  const uint16_t* v2;
+  int64_t s2_sb, s2_sh, s2_sr;
+  int T2, W2;                       // rows; waves of split 0 that walk them
+  const float* gates;
   float c;                          // scale * log2(e)
 };
 
@@ -77,29 +83,56 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int D, int QT>
+// Four consecutive output elements: OT 0 fp32, 1 bf16, 2 fp16 (round to
+// nearest even).
+template <int OT>
+__device__ __forceinline__ void ta_store4(void* out, int64_t off, f32x4 v) {
+  if constexpr (OT == 0) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + off) = v;
+  } else if constexpr (OT == 1) {
+    __bf16 t4[4] = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]), static_cast<__bf16>(v[2]),
+                    static_cast<__bf16>(v[3])};
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + off) = __builtin_bit_cast(uint2, t4);
+  } else {
+    _Float16 t4[4] = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]),
+                      static_cast<_Float16>(v[3])};
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + off) = __builtin_bit_cast(uint2, t4);
+  }
+}
+
+template <int D, int QT, int NW>
 struct TaSmem {
   static constexpr int R = D + 8;  // row pitch (bf16) of the Q and V tiles, 16-byte multiple
   static constexpr int DT = D / 16;
   static constexpr size_t q_bytes = size_t(QT) * 16 * R * 2;
-  static constexpr size_t v_bytes = size_t(4) * 32 * R * 2;
-  static constexpr size_t merge_bytes = size_t(2) * QT * DT * 64 * 16 + size_t(2) * QT * 16 * 8;
+  static constexpr size_t v_bytes = size_t(NW) * 32 * R * 2;
+  static constexpr size_t o_bytes = size_t(NW) * QT * DT * 64 * 16;
+  static constexpr size_t merge_bytes = o_bytes + size_t(NW) * QT * 16 * 8;
   static constexpr size_t bytes = (q_bytes + v_bytes > merge_bytes) ? q_bytes + v_bytes : merge_bytes;
 };
 
-// PF: issue the loads of a wave's next key step before the current step's
-// math (more registers: chosen when the grid is at most one workgroup per CU,
-// where latency, not occupancy, bounds the kernel).
-template <int D, int QT, bool OUT_BF16, bool PF>
-__global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
+// The (D, QT, NW, PF) variants that fit: at most 64 KB of LDS, the VGPRs of
+// NW waves per CU (16 waves: 128 each), and the prefetch copy only at 4 waves.
+constexpr bool ta_variant_ok(int D, int QT, int NW, bool PF) {
+  if (PF && NW != 4) return false;
+  if (D == 64) return NW == 4 ? QT <= 4 : NW == 8 ? QT <= 2 : NW == 16 ? QT == 1 : false;
+  if (D == 128) return NW == 4 ? QT <= 2 : NW == 8 ? QT == 1 : false;
+  return false;
+}
+
+// One workgroup of NW waves per (b, kv head, query group, key split).  PF:
+// issue the loads of a wave's next key step before the current step's math
+// (more registers; for grids of at most one workgroup per CU).
+template <int D, int QT, int OT, int NW, bool PF>
+__global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
   constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
   constexpr int DT = D / 16;          // 16-wide dimension tiles of O
-  constexpr int R = TaSmem<D, QT>::R;
+  constexpr int R = TaSmem<D, QT, NW>::R;
   constexpr int LPR = D / 8;          // lanes per 16-byte-chunked row
   constexpr int VLD = D / 16;         // 16-byte V loads per lane per 32-key step
-  __shared__ __align__(16) char smem[TaSmem<D, QT>::bytes];
+  __shared__ __align__(16) char smem[TaSmem<D, QT, NW>::bytes];
   uint16_t* s_q = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* s_v = reinterpret_cast<uint16_t*>(smem + TaSmem<D, QT>::q_bytes);
+  uint16_t* s_v = reinterpret_cast<uint16_t*>(smem + TaSmem<D, QT, NW>::q_bytes);
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
   int bid = blockIdx.x;
@@ -113,7 +146,7 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
   const int nrows = min(p.rows_per_group, p.n_rep * p.N - row0);
 
   // Q rows of this group -> LDS (rows past nrows are zero).
-  for (int idx = tid; idx < QT * 16 * LPR; idx += kTaThreads) {
+  for (int idx = tid; idx < QT * 16 * LPR; idx += NW * 64) {
     const int r = idx / LPR, c8 = idx - r * LPR;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (r < nrows) {
@@ -136,18 +169,31 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
   }
   __syncthreads();
 
-  // This batch row's prefix: Tp rows, or tp_batch[b] (clamped to [0, Tp])
-  // when the rows of a batch have different committed lengths.
+  // The segment this wave walks: split 0 gives its last W2 waves the second
+  // segment (wave-uniform, so the selects below are scalar).
+  const bool has2 = p.T2 > 0 && s == 0;
+  const int nw1 = has2 ? NW - p.W2 : NW;
+  const bool seg2 = has2 && w >= nw1;
+  const int wi = seg2 ? w - nw1 : w;   // index among the segment's waves
+  const int nws = seg2 ? p.W2 : nw1;   // waves walking the segment
+  // Segment 1: this batch row's prefix of Tp rows, or tp_batch[b] (clamped
+  // to [0, Tp]) when the rows of a batch have different committed lengths,
+  // then the N tree rows.  Segment 2: T2 rows, no tree.
   int Tp = p.Tp;
   if (p.tp_batch) Tp = min(max(p.tp_batch[b], 0), p.Tp);
-  const int64_t cbase = b * p.c_sb + kvh * p.c_sh;
+  const uint16_t* kc = seg2 ? p.k2 : p.kc;
+  const uint16_t* vc = seg2 ? p.v2 : p.vc;
+  const int64_t cbase = seg2 ? b * p.s2_sb + kvh * p.s2_sh : b * p.c_sb + kvh * p.c_sh;
+  const int64_t csr = seg2 ? p.s2_sr : p.c_sr;
+  const int Tpe = seg2 ? p.T2 : Tp;
+  const int KT = seg2 ? p.T2 : Tp + p.N;
   const int64_t tbase = b * p.t_sb + kvh * p.t_sh + (p.tree_follows_prefix ? (int64_t)Tp * p.t_sr : 0);
-  const int KT = Tp + p.N;
-  // Row of key index `key` in K (or V): the prefix cache, then the tree rows;
-  // keys past the end read tree row 0 (their scores are masked to -inf).
+  // Row of key index `key` in K (or V): the prefix rows, then the tree rows;
+  // keys past the end read a valid row (their scores are masked to -inf).
   auto krow = [&](int key, const uint16_t* cache, const uint16_t* tree) -> const uint16_t* {
-    if (key < Tp) return cache + cbase + key * p.c_sr;
-    const int j = key - Tp < p.N ? key - Tp : 0;
+    if (key < Tpe) return cache + cbase + key * csr;
+    if (seg2) return cache + cbase;
+    const int j = key - Tpe < p.N ? key - Tpe : 0;
     return tree + tbase + j * p.t_sr;
   };
 
@@ -162,35 +208,34 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
   }
 
   uint16_t* vt_w = s_v + w * 32 * R;  // this wave's 32-key V tile
-  const int k_lo = s * p.chunk;
-  const int k_hi = min(KT, k_lo + p.chunk);
+  const int k_lo = seg2 ? 0 : s * p.chunk;
+  const int k_hi = seg2 ? p.T2 : min(KT, k_lo + p.chunk);
   const int nsteps = (k_hi - k_lo + 31) >> 5;
 
   // One step's loads: K fragments (A rows = keys base + kt*16 + col, k = dims
   // ks*32 + grp*8 .. +8) and V rows, coalesced (load v covers keys
-  // v*(64/LPR) + lane/LPR, chunk lane%LPR).  The loads of a wave's next step
-  // are issued before the current step's math, so HBM latency overlaps it.
+  // v*(64/LPR) + lane/LPR, chunk lane%LPR).
   auto load_step = [&](int base, u32x4 (&kf)[2][KS], u32x4 (&vv)[VLD]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const uint16_t* r = krow(base + kt * 16 + col, p.kc, p.kt);
+      const uint16_t* r = krow(base + kt * 16 + col, kc, p.kt);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = ldg16(r + ks * 32 + grp * 8);
     }
 #pragma unroll
     for (int v = 0; v < VLD; ++v) {
       const int key = base + v * (64 / LPR) + lane / LPR;
-      vv[v] = ldg16(krow(key, p.vc, p.vt) + (lane % LPR) * 8);
+      vv[v] = ldg16(krow(key, vc, p.vt) + (lane % LPR) * 8);
       if (key >= k_hi) vv[v] = u32x4{0u, 0u, 0u, 0u};
     }
   };
   u32x4 kf[2][KS], vv[VLD], kfn[2][KS], vvn[VLD];
-  if (PF && w < nsteps) load_step(k_lo + w * 32, kf, vv);
-  for (int st = w; st < nsteps; st += 4) {
+  if (PF && wi < nsteps) load_step(k_lo + wi * 32, kf, vv);
+  for (int st = wi; st < nsteps; st += nws) {
     const int base = k_lo + st * 32;
-    const bool more = PF && st + 4 < nsteps;
+    const bool more = PF && st + nws < nsteps;
     if constexpr (PF) {
-      if (more) load_step(base + 4 * 32, kfn, vvn);
+      if (more) load_step(base + nws * 32, kfn, vvn);
     } else {
       load_step(base, kf, vv);
     }
@@ -210,7 +255,7 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
       for (int e = 0; e < 8; ++e) e8[e] = vt_w[((e < 4 ? 0 : 16) + grp * 4 + (e & 3)) * R + dt * 16 + col];
       va[dt] = __builtin_bit_cast(bf16x8, e8);
     }
-    const bool edge = base + 32 > Tp;  // the step reaches tree keys or the end
+    const bool edge = base + 32 > Tpe;  // the step reaches tree keys or the end
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       f32x4 sa[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -228,7 +273,7 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
         for (int e = 0; e < 8; ++e) {
           const int key = base + (e < 4 ? 0 : 16) + grp * 4 + (e & 3);
           bool vis = key < k_hi;
-          if (key >= Tp) vis = vis && ((anc[qt] >> (key - Tp)) & 1ull);
+          if (key >= Tpe) vis = vis && ((anc[qt] >> (key - Tpe)) & 1ull);
           x[e] = vis ? x[e] : kNegInf;
         }
       }
@@ -276,80 +321,72 @@ __global__ __launch_bounds__(kTaThreads) void k_tree_attn(TreeAttnParams p) {
     l[qt] += __shfl_xor(l[qt], 32);
   }
 
-  // Merge the 4 waves (same lane layout in every wave): 2,3 -> 0,1, then 1 -> 0.
-  __syncthreads();  // Q / V tiles are dead; the merge slots alias them
+  // Merge: every wave parks (m, l, O) in LDS (the Q / V tiles are dead), then
+  // wave t combines dimension tile t of the segment-1 waves (and, apart, of
+  // the segment-2 waves) for all query columns.
+  __syncthreads();
   f32x4* s_o = reinterpret_cast<f32x4*>(smem);
-  float2* s_ml = reinterpret_cast<float2*>(smem + size_t(2) * QT * DT * 64 * 16);
-  auto put = [&](int slot) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) s_o[((slot * QT + qt) * DT + dt) * 64 + lane] = o[qt][dt];
-      if (grp == 0) s_ml[(slot * QT + qt) * 16 + col] = make_float2(m[qt], l[qt]);
-    }
-  };
-  auto take = [&](int slot) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const float2 ml = s_ml[(slot * QT + qt) * 16 + col];
-      const float mn = __builtin_fmaxf(m[qt], ml.x);
-      const float ms = mn == kNegInf ? 0.0f : mn;
-      const float fa = ex2(m[qt] - ms), fb = ex2(ml.x - ms);
-      m[qt] = mn;
-      l[qt] = l[qt] * fa + ml.y * fb;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[qt][dt] = o[qt][dt] * fa + s_o[((slot * QT + qt) * DT + dt) * 64 + lane] * fb;
-    }
-  };
-  if (w >= 2) put(w - 2);
-  __syncthreads();
-  if (w < 2) take(w);
-  __syncthreads();
-  if (w == 1) put(0);
-  __syncthreads();
-  if (w != 0) return;
-  take(0);
-
+  float2* s_ml = reinterpret_cast<float2*>(smem + TaSmem<D, QT, NW>::o_bytes);
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) s_o[((w * QT + qt) * DT + dt) * 64 + lane] = o[qt][dt];
+    if (grp == 0) s_ml[(w * QT + qt) * 16 + col] = make_float2(m[qt], l[qt]);
+  }
+  __syncthreads();
+  const float g1 = has2 && p.S == 1 ? p.gates[0] : 1.0f;
+  const float g2 = has2 && p.S == 1 ? p.gates[1] : 0.0f;
+  for (int t = w; t < QT * DT; t += NW) {
+    const int qt = t / DT, dt = t - qt * DT;
+    // (M, L, O) of waves [a, e) for this lane's column and 4 dimensions.
+    auto combine = [&](int a, int e, float& M, float& L, f32x4& O) {
+      M = kNegInf;
+      for (int i = a; i < e; ++i) M = __builtin_fmaxf(M, s_ml[(i * QT + qt) * 16 + col].x);
+      const float Ms = M == kNegInf ? 0.0f : M;
+      L = 0.0f;
+      O = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int i = a; i < e; ++i) {
+        const float2 ml = s_ml[(i * QT + qt) * 16 + col];
+        const float f = ex2(ml.x - Ms);
+        L += ml.y * f;
+        O += s_o[((i * QT + qt) * DT + dt) * 64 + lane] * f;
+      }
+    };
+    float M1, L1, M2 = kNegInf, L2 = 0.0f;
+    f32x4 O1, O2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    combine(0, nw1, M1, L1, O1);
+    if (has2) combine(nw1, NW, M2, L2, O2);
     const int r = qt * 16 + col;
     if (r >= nrows) continue;
     const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
     const int h = kvh * p.n_rep + rep;
     if (p.S == 1) {
-      const float inv = l[qt] > 0.0f ? 1.0f / l[qt] : 0.0f;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int64_t off = b * p.o_sb + h * p.o_sh + node * p.o_sr + dt * 16 + grp * 4;
-        const f32x4 v = o[qt][dt] * inv;
-        if constexpr (OUT_BF16) {
-          __bf16 t4[4] = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]), static_cast<__bf16>(v[2]),
-                          static_cast<__bf16>(v[3])};
-          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + off) = __builtin_bit_cast(uint2, t4);
-        } else {
-          *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + off) = v;
-        }
-      }
+      f32x4 v = O1 * (L1 > 0.0f ? g1 / L1 : 0.0f);
+      if (has2) v += O2 * (L2 > 0.0f ? g2 / L2 : 0.0f);
+      ta_store4<OT>(p.out, b * p.o_sb + h * p.o_sh + node * p.o_sr + dt * 16 + grp * 4, v);
     } else {
-      const int64_t prow = ((int64_t)(b * p.H + h) * p.N + node) * p.S + s;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<f32x4*>(p.part_o + prow * D + dt * 16 + grp * 4) = o[qt][dt];
-      if (grp == 0) p.part_ml[prow] = make_float2(m[qt], l[qt]);
+      const int64_t prow = ((int64_t)(b * p.H + h) * p.N + node) * (p.S + 1);
+      *reinterpret_cast<f32x4*>(p.part_o + (prow + s) * D + dt * 16 + grp * 4) = O1;
+      if (dt == 0 && grp == 0) p.part_ml[prow + s] = make_float2(M1, L1);
+      if (has2) {
+        *reinterpret_cast<f32x4*>(p.part_o + (prow + p.S) * D + dt * 16 + grp * 4) = O2;
+        if (dt == 0 && grp == 0) p.part_ml[prow + p.S] = make_float2(M2, L2);
+      }
     }
   }
 }
 
-// Combines the S key-split partials of every output row: one thread per
-// 4 consecutive dimensions.
-template <int D, bool OUT_BF16>
+// Combines the S key-split partials of every output row (and the gated
+// second segment, kept in slot S): one thread per 4 consecutive dimensions.
+template <int D, int OT>
 __global__ __launch_bounds__(256) void k_tree_merge(TreeAttnParams p) {
   constexpr int TPR = D / 4;  // threads per row
   const int64_t rows = (int64_t)p.B * p.H * p.N;
   const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
   if (row >= rows) return;
   const int c4 = threadIdx.x % TPR;
-  const float2* ml = p.part_ml + row * p.S;
+  const int SS = p.S + 1;
+  const float2* ml = p.part_ml + row * SS;
   float M = kNegInf;
   for (int s = 0; s < p.S; ++s) M = __builtin_fmaxf(M, ml[s].x);
   const float Ms = M == kNegInf ? 0.0f : M;
@@ -358,21 +395,20 @@ __global__ __launch_bounds__(256) void k_tree_merge(TreeAttnParams p) {
   for (int s = 0; s < p.S; ++s) {
     const float f = ex2(ml[s].x - Ms);
     L += ml[s].y * f;
-    acc += *reinterpret_cast<const f32x4*>(p.part_o + (row * p.S + s) * D + c4 * 4) * f;
+    acc += *reinterpret_cast<const f32x4*>(p.part_o + (row * SS + s) * D + c4 * 4) * f;
   }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  f32x4 v;
+  if (p.T2 > 0) {
+    const float L2 = ml[p.S].y;
+    const f32x4 o2 = *reinterpret_cast<const f32x4*>(p.part_o + (row * SS + p.S) * D + c4 * 4);
+    v = acc * (L > 0.0f ? p.gates[0] / L : 0.0f) + o2 * (L2 > 0.0f ? p.gates[1] / L2 : 0.0f);
+  } else {
+    v = acc * (L > 0.0f ? 1.0f / L : 0.0f);
+  }
   const int node = (int)(row % p.N);
   const int64_t bh = row / p.N;
   const int h = (int)(bh % p.H), b = (int)(bh / p.H);
-  const int64_t off = b * p.o_sb + h * p.o_sh + node * p.o_sr + c4 * 4;
-  const f32x4 v = acc * inv;
-  if constexpr (OUT_BF16) {
-    __bf16 t4[4] = {static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]), static_cast<__bf16>(v[2]),
-                    static_cast<__bf16>(v[3])};
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + off) = __builtin_bit_cast(uint2, t4);
-  } else {
-    *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + off) = v;
-  }
+  ta_store4<OT>(p.out, b * p.o_sb + h * p.o_sh + node * p.o_sr + c4 * 4, v);
 }
 
 // ---------------------------------------------------------------------------
@@ -382,15 +418,16 @@ struct TaPlan {
   int G, rows_per_group, QT, S, chunk;
 };
 
-// VNX_TA_SPLITS (>= 1) fixes the key splits for tuning sweeps.
-static int ta_splits_override() {
-  static const int v = [] {
-    const char* e = getenv("VNX_TA_SPLITS");
-    const int x = e ? atoi(e) : 0;
-    return x > 0 ? x : 0;
-  }();
-  return v;
+static int env_int(const char* name) {
+  const char* e = getenv(name);
+  const int x = e ? atoi(e) : 0;
+  return x > 0 ? x : 0;
 }
+
+// VNX_TA_SPLITS (>= 1) fixes the key splits and VNX_TA_WAVES (4, 8, 16; 5 =
+// 4 waves with prefetch) the workgroup shape, for tuning sweeps.
+static int ta_splits_override() { return env_int("VNX_TA_SPLITS"); }
+static int ta_waves_override() { return env_int("VNX_TA_WAVES"); }
 
 static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d) {
   TaPlan pl{};
@@ -421,41 +458,76 @@ static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d) {
 static size_t ta_ws_bytes(const TaPlan& pl, int B, int H, int N, int d) {
   if (pl.S <= 1) return 0;
   Carve c(nullptr);
-  const int64_t prow = (int64_t)B * H * N * pl.S;
+  const int64_t prow = (int64_t)B * H * N * (pl.S + 1);  // + the second segment's slot
   c.take<float>(prow * d);
   c.take<float2>(prow);
   return c.bytes();
 }
 
-template <int D, bool OB, bool PF>
+// Waves per workgroup (5: 4 with prefetch).  A grid of at most one workgroup
+// per CU gets the widest variant that fits, so each wave walks few key steps
+// and more loads are in flight per CU; larger grids keep 4 waves.
+static int ta_waves(int D, int QT, int64_t nwg) {
+  auto ok = [&](int nw) {
+    return nw == 5 ? ta_variant_ok(D, QT, 4, true) : ta_variant_ok(D, QT, nw, false);
+  };
+  const int o = ta_waves_override();
+  if (o && ok(o)) return o;
+  const int64_t cus = device_cus();
+  if (nwg <= cus) {
+    if (ok(16)) return 16;
+    if (ok(8)) return 8;
+    return 5;
+  }
+  if (nwg <= 2 * cus && ok(8)) return 8;
+  return 4;
+}
+
+template <int D, int OT, int NW, bool PF>
 static void ta_launch_qt(const TreeAttnParams& p, int QT, dim3 grid, hipStream_t st) {
+  const dim3 block(NW * 64);
   switch (QT) {
-    case 1: hipLaunchKernelGGL((k_tree_attn<D, 1, OB, PF>), grid, dim3(kTaThreads), 0, st, p); break;
-    case 2: hipLaunchKernelGGL((k_tree_attn<D, 2, OB, PF>), grid, dim3(kTaThreads), 0, st, p); break;
+    case 1:
+      if constexpr (ta_variant_ok(D, 1, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 1, OT, NW, PF>), grid, block, 0, st, p);
+      break;
+    case 2:
+      if constexpr (ta_variant_ok(D, 2, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 2, OT, NW, PF>), grid, block, 0, st, p);
+      break;
     case 3:
-      if constexpr (D == 64) hipLaunchKernelGGL((k_tree_attn<D, 3, OB, PF>), grid, dim3(kTaThreads), 0, st, p);
+      if constexpr (ta_variant_ok(D, 3, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 3, OT, NW, PF>), grid, block, 0, st, p);
       break;
     default:
-      if constexpr (D == 64) hipLaunchKernelGGL((k_tree_attn<D, 4, OB, PF>), grid, dim3(kTaThreads), 0, st, p);
+      if constexpr (ta_variant_ok(D, 4, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 4, OT, NW, PF>), grid, block, 0, st, p);
       break;
   }
 }
 
-template <int D, bool OB>
-static int ta_launch_d(const TreeAttnParams& p, int QT, hipStream_t st, hipEvent_t* ev) {
+template <int D, int OT>
+static int ta_launch_d(TreeAttnParams p, int QT, hipStream_t st, hipEvent_t* ev) {
   const int64_t nwg = (int64_t)p.B * p.Hkv * p.G * p.S;
   const dim3 grid((unsigned)nwg);
+  const int nw = ta_waves(D, QT, nwg);
+  const int waves = nw == 5 ? 4 : nw;
+  if (p.T2 > 0) {
+    // split 0's share of waves for the second segment: a quarter, at most
+    // one per 32-row step of it
+    const int steps2 = (p.T2 + 31) / 32;
+    p.W2 = waves / 4 < steps2 ? waves / 4 : steps2;
+    if (p.W2 < 1) p.W2 = 1;
+  }
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[0], st));
-  if (nwg <= device_cus())
-    ta_launch_qt<D, OB, true>(p, QT, grid, st);
-  else
-    ta_launch_qt<D, OB, false>(p, QT, grid, st);
+  switch (nw) {
+    case 16: ta_launch_qt<D, OT, 16, false>(p, QT, grid, st); break;
+    case 8: ta_launch_qt<D, OT, 8, false>(p, QT, grid, st); break;
+    case 5: ta_launch_qt<D, OT, 4, true>(p, QT, grid, st); break;
+    default: ta_launch_qt<D, OT, 4, false>(p, QT, grid, st); break;
+  }
   VNX_LAUNCH_CHECK();
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[1], st));
   if (p.S > 1) {
     const int64_t rows = (int64_t)p.B * p.H * p.N;
     const int rpb = 256 / (D / 4);
-    hipLaunchKernelGGL((k_tree_merge<D, OB>), dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((k_tree_merge<D, OT>), dim3((unsigned)((rows + rpb - 1) / rpb)), dim3(256), 0, st, p);
     VNX_LAUNCH_CHECK();
   }
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[2], st));
@@ -484,9 +556,17 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   const int B = a->B, H = a->H, Hkv = a->Hkv, N = a->N, Tp = a->Tp, d = a->d;
   if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || N < 1 || Tp < 0) return VNX_ERR_INVALID_ARG;
   if (N > kTaMaxN || (d != 64 && d != 128)) return VNX_ERR_UNSUPPORTED;
-  if (a->out_dtype != VNX_F32 && a->out_dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
+  if (a->out_dtype != VNX_F32 && a->out_dtype != VNX_BF16 && a->out_dtype != VNX_F16) return VNX_ERR_UNSUPPORTED;
+  if (a->T2 < 0) return VNX_ERR_INVALID_ARG;
   if (B == 0) return VNX_OK;
   if (!a->q || !a->k_tree || !a->v_tree || !a->anc || !a->out) return VNX_ERR_INVALID_ARG;
+  if (a->T2 > 0) {
+    if (!a->k_seg2 || !a->v_seg2 || !a->gates || (reinterpret_cast<uintptr_t>(a->gates) & 3u))
+      return VNX_ERR_INVALID_ARG;
+    if (!strides_ok(a->seg2_strides[0], a->seg2_strides[1], a->seg2_strides[2], 8) ||
+        !aligned16(a->k_seg2) || !aligned16(a->v_seg2))
+      return VNX_ERR_UNSUPPORTED;
+  }
   if (Tp > 0 && (!a->k_cache || !a->v_cache)) return VNX_ERR_INVALID_ARG;
   if (a->tp_batch && (reinterpret_cast<uintptr_t>(a->tp_batch) & 3u)) return VNX_ERR_INVALID_ARG;
   if (!(a->scale > 0.0f) || !__builtin_isfinite(a->scale)) return VNX_ERR_INVALID_ARG;
@@ -523,18 +603,28 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   p.S = pl.S; p.G = pl.G; p.rows_per_group = pl.rows_per_group; p.chunk = pl.chunk;
   p.tp_batch = a->tp_batch;
   p.tree_follows_prefix = a->tree_follows_prefix ? 1 : 0;
+  if (a->T2 > 0) {
+    p.k2 = static_cast<const uint16_t*>(a->k_seg2);
+    p.v2 = static_cast<const uint16_t*>(a->v_seg2);
+    p.s2_sb = a->seg2_strides[0]; p.s2_sh = a->seg2_strides[1]; p.s2_sr = a->seg2_strides[2];
+    p.T2 = a->T2;
+    p.gates = a->gates;
+  }
   p.c = (float)((double)a->scale * 1.4426950408889634);
   if (pl.S > 1) {
     Carve c(workspace);
-    const int64_t prow = (int64_t)B * H * N * pl.S;
+    const int64_t prow = (int64_t)B * H * N * (pl.S + 1);
     p.part_o = c.take<float>(prow * d);
     p.part_ml = c.take<float2>(prow);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipEvent_t* ev = profile_slot(2);
-  const bool ob = a->out_dtype == VNX_BF16;
-  if (d == 64) return ob ? ta_launch_d<64, true>(p, pl.QT, st, ev) : ta_launch_d<64, false>(p, pl.QT, st, ev);
-  return ob ? ta_launch_d<128, true>(p, pl.QT, st, ev) : ta_launch_d<128, false>(p, pl.QT, st, ev);
+  const int ot = a->out_dtype == VNX_F32 ? 0 : a->out_dtype == VNX_BF16 ? 1 : 2;
+  if (d == 64)
+    return ot == 0 ? ta_launch_d<64, 0>(p, pl.QT, st, ev)
+                   : ot == 1 ? ta_launch_d<64, 1>(p, pl.QT, st, ev) : ta_launch_d<64, 2>(p, pl.QT, st, ev);
+  return ot == 0 ? ta_launch_d<128, 0>(p, pl.QT, st, ev)
+                 : ot == 1 ? ta_launch_d<128, 1>(p, pl.QT, st, ev) : ta_launch_d<128, 2>(p, pl.QT, st, ev);
 }
 
 int vnx_tree_attn_plan(int B, int H, int Hkv, int N, int Tp, int d, int* splits, int* groups, int* chunk) {

@@ -380,13 +380,16 @@ class HipBackend(DeviceBackend):
         return t
 
     def tree_attention(self, q, k_cache, v_cache, k_tree, v_tree, anc, scale: float | None = None,
-                       out_dtype=torch.float32) -> torch.Tensor:
+                       out_dtype=torch.float32, seg2=None, gates=None) -> torch.Tensor:
         """Tree-verify attention (vnx_tree_attn).
 
         q (B, H, N, d); k_cache / v_cache (B, Hkv, Tp, d) or None (Tp = 0);
         k_tree / v_tree (B, Hkv, N, d); anc (N,) or (B, N) ancestor words
         (tree.ancestor_words).  Inputs are read as bf16; returns (B, H, N, d)
-        in out_dtype (torch.float32 or torch.bfloat16)."""
+        in out_dtype (torch.float32, torch.bfloat16 or torch.float16).
+        seg2 = (k2, v2), each (B or 1, Hkv, T2, d), with gates (2,) adds
+        TriSparse's gated global path: out = gates[0] * (the tree attention)
+        + gates[1] * (attention over the T2 rows, all visible)."""
         dev = self._torch_device
         qt = self._heads_bf16(q, "q")
         kt = self._heads_bf16(k_tree, "k_tree")
@@ -419,8 +422,8 @@ class HipBackend(DeviceBackend):
         if a.shape not in ((N,), (B, N)):
             raise ValueError(f"anc must be ({N},) or ({B}, {N}), got {a.shape}")
         anc_t = torch.from_numpy(a.view(np.int64)).to(dev)
-        if out_dtype not in (torch.float32, torch.bfloat16):
-            raise ValueError("out_dtype must be torch.float32 or torch.bfloat16")
+        if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise ValueError("out_dtype must be torch.float32, torch.bfloat16 or torch.float16")
         out = torch.empty((B, H, N, d), dtype=out_dtype, device=dev)
         sc = float(scale) if scale is not None else 1.0 / float(np.sqrt(d))
         args = _lib.TreeAttnArgs()
@@ -435,13 +438,32 @@ class HipBackend(DeviceBackend):
         args.anc = anc_t.data_ptr()
         args.anc_batch_stride = N if a.ndim == 2 else 0
         args.out = out.data_ptr()
-        args.out_dtype = _lib.VNX_F32 if out_dtype == torch.float32 else _lib.VNX_BF16
+        args.out_dtype = _lib.DTYPE_CODES[out_dtype]
         args.out_strides[:] = list(out.stride()[:3])
         args.B, args.H, args.Hkv, args.Tp, args.N, args.d = B, H, Hkv, Tp, N, d
         args.scale = sc
+        keep = []
+        if seg2 is not None:
+            k2 = self._heads_bf16(seg2[0], "k_seg2")
+            v2 = self._heads_bf16(seg2[1], "v_seg2")
+            if k2.shape != v2.shape or k2.shape[0] not in (1, B) or k2.shape[1] != Hkv or k2.shape[3] != d:
+                raise ValueError(f"second segment {tuple(k2.shape)} / {tuple(v2.shape)} does not match")
+            if k2.stride() != v2.stride():
+                k2, v2 = k2.contiguous(), v2.contiguous()
+            if gates is None:
+                raise ValueError("a second segment needs the two gates")
+            g = _to_tensor(gates, dev, torch.float32).reshape(-1).contiguous()
+            if g.numel() < 2:
+                raise ValueError("gates must hold two values")
+            keep = [k2, v2, g]
+            args.k_seg2, args.v_seg2 = k2.data_ptr(), v2.data_ptr()
+            args.seg2_strides[:] = [0 if k2.shape[0] == 1 else k2.stride(0), k2.stride(1), k2.stride(2)]
+            args.T2 = k2.shape[2]
+            args.gates = g.data_ptr()
         ws = self._workspace(self._L.vnx_tree_attn_workspace(B, H, Hkv, N, Tp, d))
         _lib.check(self._L.vnx_tree_attn(ctypes.byref(args), _ptr(ws), ws.numel(),
                                          ctypes.c_void_p(self._stream().cuda_stream)), "tree_attn")
+        del keep
         return out
 
     def attention(self, q, k, v, mask=None):

@@ -230,8 +230,6 @@ class _Layer:
     gv: torch.Tensor
     gates: torch.Tensor       # sigmoid(gate_logits), fp32 (3,)
     ffn: Dict[str, object] = field(default_factory=dict)
-    gk_pad: Optional[torch.Tensor] = None   # gk / gv zero-padded to >= 64 rows
-    gv_pad: Optional[torch.Tensor] = None
 
 
 class _Linear:
@@ -313,14 +311,7 @@ class CometSparkGPU:
                        wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4),
                        proj=_Linear(W[p + "attn.proj.weight"], dtype, hip, int4),
                        gk=gk.to(dtype).contiguous(), gv=gv.to(dtype).contiguous(),
-                       gates=torch.sigmoid(W[p + "attn.gate_logits"]))
-            # The global rows double as the (never visible) tree rows of the
-            # kernel call, which reads up to 64 of them: pad with zeros.
-            gpad = max(G, 64)
-            L.gk_pad = torch.zeros((1, cfg.n_kv_head, gpad, d), dtype=dtype, device=dev)
-            L.gv_pad = torch.zeros((1, cfg.n_kv_head, gpad, d), dtype=dtype, device=dev)
-            L.gk_pad[:, :, :G] = L.gk
-            L.gv_pad[:, :, :G] = L.gv
+                       gates=torch.sigmoid(W[p + "attn.gate_logits"].float()).contiguous())
             if kind == "trisparse":
                 L.ffn["gu"] = _Linear(torch.cat([W[p + "ffn.w_gate.weight"], W[p + "ffn.w_up.weight"]], 0),
                                       dtype, hip, int4)
@@ -379,52 +370,44 @@ class CometSparkGPU:
             self._words[n] = w
         return w
 
-    def _tree_call(self, q, kc, vc, cstr, tree_k, tree_v, tstr, anc, B, H, Hkv, Tp, n, d, tp, follows, out):
+    def _tree_call(self, q, kc, vc, cstr, tree_k, tree_v, tstr, anc, B, H, Hkv, Tp, n, d, tp, follows, out,
+                   seg2=None, gates=None):
         a = _lib.TreeAttnArgs()
         a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
         a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = cstr
         a.k_tree = tree_k.data_ptr(); a.v_tree = tree_v.data_ptr(); a.tree_strides[:] = tstr
         a.anc = anc.data_ptr(); a.anc_batch_stride = 0
         # output rows in (B, n, H, d) order: the proj input layout
-        a.out = out.data_ptr(); a.out_dtype = _lib.VNX_F32; a.out_strides[:] = [n * H * d, d, H * d]
+        a.out = out.data_ptr(); a.out_dtype = _lib.DTYPE_CODES[out.dtype]; a.out_strides[:] = [n * H * d, d, H * d]
         a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, n, d
         a.scale = 1.0 / math.sqrt(d)
         a.tp_batch = tp.data_ptr() if tp is not None else None
         a.tree_follows_prefix = 1 if follows else 0
+        if seg2 is not None:
+            k2, v2 = seg2
+            a.k_seg2 = k2.data_ptr(); a.v_seg2 = v2.data_ptr()
+            a.seg2_strides[:] = [0, k2.stride(1), k2.stride(2)]
+            a.T2 = k2.shape[2]
+            a.gates = gates.data_ptr()
         L = self.hip._L
         ws = self.hip._workspace(L.vnx_tree_attn_workspace(B, H, Hkv, n, Tp, d))
         _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), self._st()),
                    "tree_attn")
 
     def _attn_kernel(self, q, li, lens, n, Tmax):
-        """Sliding-window + global paths on vnx_tree_attn, combined with the
-        sigmoid gates into the proj input (B*n, H*d).  q (B, H, n, d) bf16."""
+        """Sliding-window and global paths in one vnx_tree_attn call: each
+        row's prefix of lens[b] cache rows, then its n new rows (written in
+        place right after it) under the chain mask, and the G global rows as
+        the gated second segment; writes the proj input (B*n, H*d) in the
+        activation dtype.  q (B, H, n, d) bf16."""
         cfg = self.cfg
         B, H, _, d = q.shape
-        Hkv = cfg.n_kv_head
         kc, vc = self.kc[li], self.vc[li]
         Ly = self.layers[li]
-        o_s = torch.empty((B * n, H * d), dtype=torch.float32, device=self.dev)
-        o_g = torch.empty_like(o_s)
-        cstr = list(kc.stride()[:3])
-        # sliding window: each row's prefix of lens[b] rows, then its n new
-        # rows (written in place right after it) under the chain mask
-        self._tree_call(q, kc, vc, cstr, kc, vc, cstr, self._chain_words(n), B, H, Hkv, Tmax, n, d, lens, True,
-                        o_s)
-        # global sink tokens: all G rows visible as a batch-stride-0 prefix,
-        # no tree row visible (empty ancestor words)
-        zero = self._words.get("zero")
-        if zero is None:
-            zero = torch.zeros(64, dtype=torch.int64, device=self.dev)
-            self._words["zero"] = zero
-        gs = [0, Ly.gk_pad.stride(1), Ly.gk_pad.stride(2)]
-        self._tree_call(q, Ly.gk_pad, Ly.gv_pad, gs, Ly.gk_pad, Ly.gv_pad, gs, zero, B, H, Hkv, Ly.gk.shape[2], n,
-                        d, None, False, o_g)
         o = torch.empty((B * n, H * d), dtype=self.act_dtype, device=self.dev)
-        _lib.check(self.hip._L.vnx_axpby(ctypes.c_void_p(o_s.data_ptr()), ctypes.c_void_p(o_g.data_ptr()),
-                                         ctypes.c_void_p(Ly.gates.data_ptr()), o.numel(),
-                                         ctypes.c_void_p(o.data_ptr()), _lib.DTYPE_CODES[o.dtype], self._st()),
-                   "axpby")
+        cstr = list(kc.stride()[:3])
+        self._tree_call(q, kc, vc, cstr, kc, vc, cstr, self._chain_words(n), B, H, cfg.n_kv_head, Tmax, n, d, lens,
+                        True, o, seg2=(Ly.gk, Ly.gv), gates=Ly.gates)
         return o
 
     def _attn_torch(self, q, li, lens, n, Tmax):
