@@ -46,6 +46,41 @@ struct Elt<_Float16> {
   __device__ __forceinline__ static void st(_Float16* p, float v) { *p = (_Float16)v; }
 };
 
+// Four consecutive elements as fp32 (16-byte loads for fp32, 8-byte for the
+// 16-bit types; the caller checks the alignment).
+template <typename T>
+__device__ __forceinline__ void ld4(const T* p, float (&v)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  } else {
+    const uint2 a = *reinterpret_cast<const uint2*>(p);
+    const T* e = reinterpret_cast<const T*>(&a);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = Elt<T>::ld(e + i);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st4(T* p, const float (&v)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint2 a;
+    T* e = reinterpret_cast<T*>(&a);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Elt<T>::st(e + i, v[i]);
+    *reinterpret_cast<uint2*>(p) = a;
+  }
+}
+
+// The 4-wide kernels need every row start at a multiple of 4 elements.
+inline bool vec4_ok(const void* p, int elt_bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % (4u * (unsigned)elt_bytes)) == 0;
+}
+inline int dtype_bytes(int dt) { return dt == VNX_F32 ? 4 : 2; }
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
 template <typename F>
 int by_dtype(int dt, F&& f) {
   switch (dt) {
@@ -69,15 +104,18 @@ __global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t 
   __shared__ float red[kRnThreads / VNX_WAVE];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
-  float v[kRnPer];
+  float v[kRnPer], wv[kRnPer];
   float ss = 0.0f;
+  // every load (x, residual, weight) issued before the reduction
 #pragma unroll
   for (int j = 0; j < kRnPer; ++j) {
-    const int64_t c = tid + (int64_t)j * kRnThreads;
+    const int c = tid + j * kRnThreads;
     float a = 0.0f;
+    wv[j] = 0.0f;
     if (c < D) {
       a = x[row * ldx + c];
       if (r) a += Elt<TR>::ld(r + row * ldr + c);
+      wv[j] = w[c];
     }
     v[j] = a;
     ss = __builtin_fmaf(a, a, ss);
@@ -92,10 +130,10 @@ __global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t 
   const float inv = 1.0f / __builtin_sqrtf(tot / (float)D + eps);
 #pragma unroll
   for (int j = 0; j < kRnPer; ++j) {
-    const int64_t c = tid + (int64_t)j * kRnThreads;
+    const int c = tid + j * kRnThreads;
     if (c < D) {
       if (xo) xo[row * ldxo + c] = v[j];
-      Elt<TY>::st(y + row * ldy + c, v[j] * inv * w[c]);
+      Elt<TY>::st(y + row * ldy + c, v[j] * inv * wv[j]);
     }
   }
 }
@@ -123,54 +161,62 @@ struct RopeParams {
 
 template <typename TQ, typename TO>
 __global__ __launch_bounds__(256) void k_rope_kv(RopeParams p) {
+  // one workgroup per token row (b, i); threads over (head, pair j)
   const int half = p.d / 2;
   const int heads = p.H + 2 * p.Hkv;
-  const int64_t total = p.B * (int64_t)p.n * heads * half;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= total) return;
-  const int j = (int)(t % half);
-  int64_t r = t / half;
-  const int hh = (int)(r % heads);
-  r /= heads;
-  const int i = (int)(r % p.n);
-  const int64_t b = r / p.n;
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / p.n;
+  const int i = (int)(row - b * p.n);
   const int64_t pos = (int64_t)p.lens[b] + i;
   if (pos < 0 || pos >= p.cap) return;  // never past the cache or the RoPE table
-  const TQ* src = static_cast<const TQ*>(p.qkv) + (b * p.n + i) * p.ldq + (int64_t)hh * p.d;
-  float x0 = Elt<TQ>::ld(src + j), x1 = Elt<TQ>::ld(src + j + half);
-  if (p.rope && hh < p.H + p.Hkv) {
-    const float c0 = p.cos[pos * p.d + j], c1 = p.cos[pos * p.d + j + half];
-    const float s0 = p.sin[pos * p.d + j], s1 = p.sin[pos * p.d + j + half];
-    const float y0 = x0 * c0 - x1 * s0;   // rotate_half(x)[j] = -x[j + half]
-    const float y1 = x1 * c1 + x0 * s1;   // rotate_half(x)[j + half] = x[j]
-    x0 = y0;
-    x1 = y1;
+  const TQ* src_row = static_cast<const TQ*>(p.qkv) + row * p.ldq;
+  for (int t = threadIdx.x; t < heads * half; t += blockDim.x) {
+    const int hh = t / half, j = t - hh * half;
+    const TQ* src = src_row + (int64_t)hh * p.d;
+    float x0 = Elt<TQ>::ld(src + j), x1 = Elt<TQ>::ld(src + j + half);
+    if (p.rope && hh < p.H + p.Hkv) {
+      const float c0 = p.cos[pos * p.d + j], c1 = p.cos[pos * p.d + j + half];
+      const float s0 = p.sin[pos * p.d + j], s1 = p.sin[pos * p.d + j + half];
+      const float y0 = x0 * c0 - x1 * s0;   // rotate_half(x)[j] = -x[j + half]
+      const float y1 = x1 * c1 + x0 * s1;   // rotate_half(x)[j + half] = x[j]
+      x0 = y0;
+      x1 = y1;
+    }
+    TO* dst;
+    if (hh < p.H) {
+      dst = static_cast<TO*>(p.q) + ((b * p.H + hh) * p.n + i) * (int64_t)p.d;
+    } else if (hh < p.H + p.Hkv) {
+      dst = static_cast<TO*>(p.kc) + b * p.c_sb + (int64_t)(hh - p.H) * p.c_sh + pos * p.c_sr;
+    } else {
+      dst = static_cast<TO*>(p.vc) + b * p.c_sb + (int64_t)(hh - p.H - p.Hkv) * p.c_sh + pos * p.c_sr;
+    }
+    Elt<TO>::st(dst + j, x0);
+    Elt<TO>::st(dst + j + half, x1);
   }
-  TO* dst;
-  if (hh < p.H) {
-    dst = static_cast<TO*>(p.q) + ((b * p.H + hh) * p.n + i) * (int64_t)p.d;
-  } else if (hh < p.H + p.Hkv) {
-    dst = static_cast<TO*>(p.kc) + b * p.c_sb + (int64_t)(hh - p.H) * p.c_sh + pos * p.c_sr;
-  } else {
-    dst = static_cast<TO*>(p.vc) + b * p.c_sb + (int64_t)(hh - p.H - p.Hkv) * p.c_sh + pos * p.c_sr;
-  }
-  Elt<TO>::st(dst + j, x0);
-  Elt<TO>::st(dst + j + half, x1);
 }
 
 // ---------------------------------------------------------------------------
 // SwiGLU activation: out[m, c] = silu(gu[m, c]) * gu[m, Hf + c].
 // ---------------------------------------------------------------------------
-template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void k_swiglu(const TI* gu, int64_t ldg, int64_t M, int64_t Hf, TO* out,
-                                                int64_t ldo) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= M * Hf) return;
-  const int64_t m = t / Hf, c = t - m * Hf;
-  const float g = Elt<TI>::ld(gu + m * ldg + c);
-  const float u = Elt<TI>::ld(gu + m * ldg + Hf + c);
-  const float s = g / (1.0f + __expf(-g));
-  Elt<TO>::st(out + m * ldo + c, s * u);
+// Grid: x = rows, y = column blocks of 256 * VW; VW = 4 reads and writes 4
+// consecutive columns per thread.
+template <typename TI, typename TO, int VW>
+__global__ __launch_bounds__(256) void k_swiglu(const TI* gu, int64_t ldg, int64_t Hf, TO* out, int64_t ldo) {
+  const int64_t m = blockIdx.x;
+  const int64_t c = ((int64_t)blockIdx.y * 256 + threadIdx.x) * VW;
+  if (c >= Hf) return;
+  const TI* g = gu + m * ldg + c;
+  TO* o = out + m * ldo + c;
+  if constexpr (VW == 4) {
+    float a[4], u[4], r[4];
+    ld4(g, a);
+    ld4(g + Hf, u);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = silu(a[e]) * u[e];
+    st4(o, r);
+  } else {
+    Elt<TO>::st(o, silu(Elt<TI>::ld(g)) * Elt<TI>::ld(g + Hf));
+  }
 }
 
 // out = coef[0] * a + coef[1] * b (coef on the device, so captured graphs
@@ -234,35 +280,56 @@ __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t l
 // one product over the concatenated experts (sxg = 2He, sxo = He) and the
 // expert-major (PE, M, 2He) form of a batched product (ldg = 2He,
 // sxg = M*2He) are both strides of this.
-template <typename TI, typename TO>
+// Grid: x = (row, expert) pairs m*PE + x, y = column blocks of 256 * VW.
+// The routing weight is uniform over a workgroup: an unselected expert's
+// block writes zeros without reading gu.
+template <typename TI, typename TO, int VW>
 __global__ __launch_bounds__(256) void k_mod_swiglu(const TI* gu, int64_t ldg, int64_t sxg, const float* comb,
-                                                    int64_t ldc, int64_t M, int PE, int64_t He, TO* out,
-                                                    int64_t ldo, int64_t sxo) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t per_row = (int64_t)PE * He;
-  if (t >= M * per_row) return;
-  const int64_t m = t / per_row, r = t - m * per_row;
-  const int x = (int)(r / He);
-  const int64_t j = r - (int64_t)x * He;
-  const float w = comb[m * ldc + x];
-  float v = 0.0f;
-  if (w != 0.0f) {
-    const TI* g = gu + m * ldg + (int64_t)x * sxg;
-    const float a = Elt<TI>::ld(g + j), u = Elt<TI>::ld(g + He + j);
-    v = w * (a / (1.0f + __expf(-a))) * u;
+                                                    int64_t ldc, int PE, int64_t He, TO* out, int64_t ldo,
+                                                    int64_t sxo) {
+  const int pair = blockIdx.x;
+  const int m = pair / PE, x = pair - m * PE;
+  const int64_t j = ((int64_t)blockIdx.y * 256 + threadIdx.x) * VW;
+  if (j >= He) return;
+  const float w = comb[(int64_t)m * ldc + x];
+  const TI* g = gu + m * ldg + (int64_t)x * sxg + j;
+  TO* o = out + m * ldo + (int64_t)x * sxo + j;
+  if constexpr (VW == 4) {
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f}, r[4];
+    if (w != 0.0f) {
+      ld4(g, a);
+      ld4(g + He, u);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = w != 0.0f ? w * silu(a[e]) * u[e] : 0.0f;
+    st4(o, r);
+  } else {
+    float v = 0.0f;
+    if (w != 0.0f) v = w * silu(Elt<TI>::ld(g)) * Elt<TI>::ld(g + He);
+    Elt<TO>::st(o, v);
   }
-  Elt<TO>::st(out + m * ldo + (int64_t)x * sxo + j, v);
 }
 
 // out[m, c] = sum over x < PE of y[x, m, c] (fp32 accumulation in x order):
 // the sum of the routed experts' down projections (already weighted).
-template <typename TY>
-__global__ __launch_bounds__(256) void k_sum_experts(const TY* y, int64_t M, int PE, int64_t D, float* out) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= M * D) return;
-  float acc = 0.0f;
-  for (int x = 0; x < PE; ++x) acc += Elt<TY>::ld(y + (int64_t)x * M * D + t);
-  out[t] = acc;
+// VW consecutive elements per thread.
+template <typename TY, int VW>
+__global__ __launch_bounds__(256) void k_sum_experts(const TY* y, int64_t MD, int PE, float* out) {
+  const int64_t t = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * VW;
+  if (t >= MD) return;
+  if constexpr (VW == 4) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, v[4];
+    for (int x = 0; x < PE; ++x) {
+      ld4(y + (int64_t)x * MD + t, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += v[e];
+    }
+    st4(out + t, acc);
+  } else {
+    float acc = 0.0f;
+    for (int x = 0; x < PE; ++x) acc += Elt<TY>::ld(y + (int64_t)x * MD + t);
+    out[t] = acc;
+  }
 }
 
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -315,15 +382,15 @@ int vnx_rope_kv(const void* qkv, int dtype, int64_t ldq, int64_t B, int n, int H
   p.q = q_out; p.kc = k_cache; p.vc = v_cache;
   p.c_sb = c_sb; p.c_sh = c_sh; p.c_sr = c_sr;
   p.cap = rope ? (cap < table_rows ? cap : table_rows) : cap;
-  const int64_t total = B * (int64_t)n * (H + 2 * Hkv) * (d / 2);
-  if (total >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  const int64_t rows = B * (int64_t)n;
+  if (rows >= INT32_MAX || (int64_t)(H + 2 * Hkv) * (d / 2) >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return by_dtype(dtype, [&](auto tq) {
     using TQ = decltype(tq);
     if (out_dtype == VNX_F32)
-      hipLaunchKernelGGL((k_rope_kv<TQ, float>), dim3(blocks_for(total)), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((k_rope_kv<TQ, float>), dim3((unsigned)rows), dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((k_rope_kv<TQ, __hip_bfloat16>), dim3(blocks_for(total)), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((k_rope_kv<TQ, __hip_bfloat16>), dim3((unsigned)rows), dim3(256), 0, s, p);
     VNX_LAUNCH_CHECK();
     return (int)VNX_OK;
   });
@@ -333,14 +400,20 @@ int vnx_swiglu(const void* gu, int dtype, int64_t ldg, int64_t M, int64_t Hf, vo
                int64_t ldo, void* stream) {
   if (!gu || !out || M < 0 || Hf <= 0 || ldg < 2 * Hf || ldo < Hf) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
-  if (M * Hf >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  if (M >= INT32_MAX || Hf > (int64_t)65535 * 256) return VNX_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool v4 = Hf % 4 == 0 && ldg % 4 == 0 && ldo % 4 == 0 && vec4_ok(gu, dtype_bytes(dtype)) &&
+                  vec4_ok(out, dtype_bytes(out_dtype));
   return by_dtype(dtype, [&](auto ti) {
     using TI = decltype(ti);
     return by_dtype(out_dtype, [&](auto to) {
       using TO = decltype(to);
-      hipLaunchKernelGGL((k_swiglu<TI, TO>), dim3(blocks_for(M * Hf)), dim3(256), 0, s,
-                         static_cast<const TI*>(gu), ldg, M, Hf, static_cast<TO*>(out), ldo);
+      if (v4)
+        hipLaunchKernelGGL((k_swiglu<TI, TO, 4>), dim3((unsigned)M, (unsigned)((Hf + 1023) / 1024)), dim3(256), 0,
+                           s, static_cast<const TI*>(gu), ldg, Hf, static_cast<TO*>(out), ldo);
+      else
+        hipLaunchKernelGGL((k_swiglu<TI, TO, 1>), dim3((unsigned)M, (unsigned)((Hf + 255) / 256)), dim3(256), 0,
+                           s, static_cast<const TI*>(gu), ldg, Hf, static_cast<TO*>(out), ldo);
       VNX_LAUNCH_CHECK();
       return (int)VNX_OK;
     });
@@ -386,15 +459,23 @@ int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, int64_t sxg, const fl
   const bool o_expmajor = ldo >= He && sxo >= ldo * M;
   if (!(g_rowmajor || g_expmajor) || !(o_rowmajor || o_expmajor)) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
-  if (M * PE * He >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
+  if (M * PE >= INT32_MAX || He > (int64_t)65535 * 256) return VNX_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool v4 = He % 4 == 0 && ldg % 4 == 0 && sxg % 4 == 0 && ldo % 4 == 0 && sxo % 4 == 0 &&
+                  vec4_ok(gu, dtype_bytes(dtype)) && vec4_ok(out, dtype_bytes(out_dtype));
+  const unsigned pairs = (unsigned)(M * PE);
   return by_dtype(dtype, [&](auto ti) {
     using TI = decltype(ti);
     return by_dtype(out_dtype, [&](auto to) {
       using TO = decltype(to);
-      hipLaunchKernelGGL((k_mod_swiglu<TI, TO>), dim3(blocks_for(M * PE * He)), dim3(256), 0, s,
-                         static_cast<const TI*>(gu), ldg, sxg, comb, ldc, M, PE, He, static_cast<TO*>(out), ldo,
-                         sxo);
+      if (v4)
+        hipLaunchKernelGGL((k_mod_swiglu<TI, TO, 4>), dim3(pairs, (unsigned)((He + 1023) / 1024)), dim3(256), 0, s,
+                           static_cast<const TI*>(gu), ldg, sxg, comb, ldc, PE, He, static_cast<TO*>(out), ldo,
+                           sxo);
+      else
+        hipLaunchKernelGGL((k_mod_swiglu<TI, TO, 1>), dim3(pairs, (unsigned)((He + 255) / 256)), dim3(256), 0, s,
+                           static_cast<const TI*>(gu), ldg, sxg, comb, ldc, PE, He, static_cast<TO*>(out), ldo,
+                           sxo);
       VNX_LAUNCH_CHECK();
       return (int)VNX_OK;
     });
@@ -406,10 +487,16 @@ int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, floa
   if (M == 0) return VNX_OK;
   if (M * D >= ((int64_t)1 << 40)) return VNX_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t MD = M * D;
+  const bool v4 = MD % 4 == 0 && vec4_ok(y, dtype_bytes(dtype)) && vec4_ok(out, 4);
   return by_dtype(dtype, [&](auto ty) {
     using TY = decltype(ty);
-    hipLaunchKernelGGL((k_sum_experts<TY>), dim3(blocks_for(M * D)), dim3(256), 0, s, static_cast<const TY*>(y),
-                       M, PE, D, out);
+    if (v4)
+      hipLaunchKernelGGL((k_sum_experts<TY, 4>), dim3(blocks_for(MD / 4)), dim3(256), 0, s,
+                         static_cast<const TY*>(y), MD, PE, out);
+    else
+      hipLaunchKernelGGL((k_sum_experts<TY, 1>), dim3(blocks_for(MD)), dim3(256), 0, s, static_cast<const TY*>(y),
+                         MD, PE, out);
     VNX_LAUNCH_CHECK();
     return (int)VNX_OK;
   });

@@ -17,12 +17,12 @@
 // (exact: small integers).  A group's MFMA result is scaled by s_g and added
 // to the fp32 output.
 //
-// Work split: a workgroup (4 waves) owns 64*TPW consecutive rows (tiles of 16
-// rows; wave w takes tiles w, w+4, ...) and a K range; it streams its range in
-// slices, staging each slice of x (up to 32 batch columns) once in LDS for all
-// of its tiles.  Small N splits K over workgroups (grid.y); their fp32
-// partials go to the workspace and k_qreduce adds them in split order, so the
-// result does not depend on scheduling.  Within a 128-k group, lane (m = lane % 16, kq = lane / 16)
+// Work split (large N): a workgroup (4 waves) owns 64*TPW consecutive rows
+// (tiles of 16 rows; wave w takes tiles w, w+4, ...) and all of K; it streams
+// K in slices, staging each slice of x (up to 32 batch columns) once in LDS
+// for all of its tiles.  Small N: k_qgemv_tile (one tile per workgroup, K
+// split over its waves and summed in wave order, so the result does not
+// depend on scheduling).  Within a 128-k group, lane (m = lane % 16, kq = lane / 16)
 // holds k = kq*32 + [0, 32) of row m (16 bytes of W4, 32 of W8), used as
 // four MFMA k-steps; the B operand takes x at the same k (the k order inside
 // a group is a permutation shared by A and B, so the dot product is unchanged).
@@ -40,7 +40,6 @@ constexpr int kQTiles = 4;       // tiles per wave
 constexpr int kQRows = 16 * 4 * kQTiles;  // rows per workgroup (256)
 constexpr int kGK = 128;         // k per accumulation group
 constexpr int kXPad = 8;         // fp16 padding per LDS row of x (16 bytes)
-constexpr int kQMaxSplits = 8;   // K splits of small layers (k_qreduce adds them)
 
 struct QGemvParams {
   const uint16_t* x;   // fp16 bits, (B, K), row pitch ldx
@@ -55,8 +54,7 @@ struct QGemvParams {
   int gpg;             // 128-column groups per scale: G / 128
   float* y;            // (B, N), row pitch ldy
   int64_t ldy;
-  int64_t ksplit_len;  // K per grid.y split (multiple of kGK)
-  float* part;         // ksplit > 1: partials [split][B][N]
+  int64_t ksplit_len;  // K per grid.y split (multiple of kGK; the launches use K)
 };
 
 __device__ __forceinline__ float load_scale(const QGemvParams& p, int64_t row, unsigned g) {
@@ -105,6 +103,15 @@ __device__ __forceinline__ half8 a_w8(uint32_t d0, uint32_t d1) {
   const fp16x2 off = {(__fp16)1152.0f, (__fp16)1152.0f};
   return pack_half8(pair_from(u0, kSel01, off), pair_from(u0, kSel23, off), pair_from(u1, kSel01, off),
                     pair_from(u1, kSel23, off));
+}
+
+// Orders one wave's LDS writes before its later LDS reads (and reads before
+// later writes): the LDS runs a wave's instructions in order, so only the
+// compiler's ordering needs pinning.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // W4 staging order of 8 consecutive fp16 (4 dwords w0..w3 = (h0,h1)..(h6,h7)):
@@ -243,8 +250,8 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
   }
 
   // ---- store: lane holds D[row 4*kq + j][column m] ----
-  float* out = gridDim.y > 1 ? p.part + (int64_t)blockIdx.y * p.B * p.N : p.y;
-  const int64_t ldo = gridDim.y > 1 ? p.N : p.ldy;
+  float* out = p.y;
+  const int64_t ldo = p.ldy;
 #pragma unroll 1
   for (int t = 0; t < TPW; ++t) {
     const int64_t row0 = row_base + (int64_t)(wave + 4 * t) * 16;
@@ -271,20 +278,129 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
   }
 }
 
-// y[b][n] = sum over splits, in split order (splits <= kQMaxSplits; the loads
-// are issued together, the adds run in order).
+// Small N (fewer than kQTileMaxN rows): one 16-row tile per workgroup and
+// the whole K inside it, split over its NW waves by 128-k group (wave w takes
+// groups w, w + NW, ..., two at a time so both groups' loads are in flight);
+// the waves' partial tiles are summed through LDS in wave order, so the
+// result does not depend on scheduling and no second launch is needed.  A
+// wave stages its group's x block (up to 32 batch rows x 128 k) through its
+// own LDS tile: coalesced 256-byte row reads in, the MFMA B-operand layout
+// out.
+template <int BITS, int NC, int NW>
+__global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
+  constexpr int WBYTES = BITS == 4 ? 16 : 32;
+  constexpr int XR = NC * 16;            // staged batch rows
+  constexpr int XP = kGK + kXPad;        // LDS row pitch (fp16)
+  constexpr int XL = XR * (kGK / 8) / 64;  // 16-byte x loads per lane per group
+  // the per-wave x tiles, reused for the partial tiles after the K loop
+  constexpr size_t kXBytes = size_t(NW) * XR * XP * 2, kRBytes = size_t(NW) * NC * 64 * 16;
+  __shared__ __attribute__((aligned(16))) char smem[kXBytes > kRBytes ? kXBytes : kRBytes];
+  auto xs_all = reinterpret_cast<uint16_t(*)[XR * XP]>(smem);
+  auto red = reinterpret_cast<f32x4(*)[NC][64]>(smem);
+  const int tid = threadIdx.x;
+  const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
+  const int m = lane % 16, kq = lane / 16;
+  uint16_t* xs = xs_all[wave];
+  const int64_t row0 = (int64_t)blockIdx.x * 16;
+  const int64_t ra = min(row0 + m, p.N - 1);     // A row (rows past N read row N-1, not stored)
+  const uint8_t* wr = p.w + ra * p.ldw;
+  const int ngroups = (int)(p.K / kGK);
 
-__global__ void k_qreduce(const float* part, int splits, int64_t B, int64_t N, float* y, int64_t ldy) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B * N) return;
-  float v[kQMaxSplits];
+  f32x4 yacc[NC];
 #pragma unroll
-  for (int k = 0; k < kQMaxSplits; ++k) v[k] = k < splits ? part[(int64_t)k * B * N + i] : 0.0f;
-  float s = v[0];
+  for (int c = 0; c < NC; ++c) yacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int g0 = wave; g0 < ngroups; g0 += 2 * NW) {
+    // two groups per pass: g0 and g0 + NW (the second weighted 0 when past K)
+    const int gg[2] = {g0, g0 + NW < ngroups ? g0 + NW : g0};
+    const bool second = g0 + NW < ngroups;
+    uint32_t wv[2][WBYTES / 4];
+    u32x4 xv[2][XL];
+    float sc[2][4];
 #pragma unroll
-  for (int k = 1; k < kQMaxSplits; ++k)
-    if (k < splits) s += v[k];
-  y[(i / N) * ldy + (i % N)] = s;
+    for (int u = 0; u < 2; ++u) {
+      const int64_t k0 = (int64_t)gg[u] * kGK;
+      const uint8_t* src = wr + (BITS == 4 ? k0 / 2 + kq * 16 : k0 + kq * 32);
+      const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+      wv[u][0] = v0.x; wv[u][1] = v0.y; wv[u][2] = v0.z; wv[u][3] = v0.w;
+      if constexpr (BITS == 8) {
+        const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+        wv[u][4] = v1.x; wv[u][5] = v1.y; wv[u][6] = v1.z; wv[u][7] = v1.w;
+      }
+      // x block: load i covers batch row (i*64 + lane) / 16, chunk lane % 16
+#pragma unroll
+      for (int i = 0; i < XL; ++i) {
+        const int b = (i * 64 + lane) / 16;
+        xv[u][i] = *reinterpret_cast<const u32x4*>(p.x + (int64_t)min(b, (int)p.B - 1) * p.ldx + k0 + m * 8);
+      }
+      if constexpr (BITS == 4) {
+        const unsigned col = p.gpg == 1 ? (unsigned)gg[u] : (unsigned)gg[u] / (unsigned)p.gpg;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[u][j] = load_scale(p, min(row0 + 4 * kq + j, p.N - 1), col);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      wave_lds_fence();  // the previous group's B-operand reads are done
+#pragma unroll
+      for (int i = 0; i < XL; ++i) {
+        const int b = (i * 64 + lane) / 16;
+        u32x4 v = b < p.B ? xv[u][i] : u32x4{0u, 0u, 0u, 0u};
+        if constexpr (BITS == 4) v = stage_perm_w4(v);
+        *reinterpret_cast<u32x4*>(&xs[b * XP + m * 8]) = v;
+      }
+      wave_lds_fence();
+      f32x4 acc[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const half8 a = BITS == 4 ? a_w4(wv[u][s4]) : a_w8(wv[u][2 * s4], wv[u][2 * s4 + 1]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const half8 bx = *reinterpret_cast<const half8*>(&xs[(c * 16 + m) * XP + kq * 32 + s4 * 8]);
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc[c], 0, 0, 0);
+        }
+      }
+      const bool use = u == 0 || second;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (BITS == 4) yacc[c][j] = __builtin_fmaf(use ? sc[u][j] : 0.0f, acc[c][j], yacc[c][j]);
+          else yacc[c][j] += use ? acc[c][j] : 0.0f;
+        }
+      }
+    }
+  }
+
+  __syncthreads();  // every wave is done with its x tile
+#pragma unroll
+  for (int c = 0; c < NC; ++c) red[wave][c][lane] = yacc[c];
+  __syncthreads();
+  // wave c sums column block c over the waves, in wave order, and stores it:
+  // lane holds D[row 4*kq + j][column m]
+  if (wave >= NC) return;
+  const int c = wave;
+  const int64_t b = c * 16 + m;
+  if (b >= p.B) return;
+  f32x4 v = red[0][c][lane];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) v += red[w][c][lane];
+  const int64_t n0 = row0 + 4 * kq;
+  if (n0 >= p.N) return;
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] *= load_scale(p, min(n0 + j, p.N - 1), 0);
+  }
+  float* dst = p.y + b * p.ldy + n0;
+  if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+    *reinterpret_cast<f32x4*>(dst) = v;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (n0 + j < p.N) dst[j] = v[j];
+  }
 }
 
 // Dequantization (bit-exact reference for the kernels' weights):
@@ -319,10 +435,12 @@ static int qgemv_check(const QGemvParams& p, int bits) {
   return VNX_OK;
 }
 
-// Launch shape: rows per workgroup 64*TPW (TPW = 4 when N is large enough to
-// fill the GPU, else 1) and K splits so that small layers still spread over
-// about kQTargetWgs workgroups.
+// Launch shape.  N >= kQTileMaxN: the LDS-staged kernel, 64*TPW rows per
+// workgroup (TPW = 4 when the staged x slice is large, more than 16 batch
+// columns, and N fills the GPU anyway, else 1), whole K.  Smaller N: the
+// tile kernel, one 16-row tile per workgroup with K split over its waves.
 constexpr int64_t kQTargetWgs = 512;
+constexpr int64_t kQTileMaxN = 64 * kQTargetWgs;
 
 // VNX_QTPW (1 or 4) overrides the tiles per wave for tuning sweeps.
 static int tpw_override() {
@@ -334,68 +452,45 @@ static int tpw_override() {
   return t;
 }
 
-struct QPlan {
-  int tpw;
-  int64_t row_blocks;
-  int splits;
-  int64_t split_len;
-};
-
-// TPW = 4 amortises the x staging over more rows; it pays when the staged
-// slice is large (more than 16 batch columns) and N fills the GPU anyway.
-static QPlan qgemv_plan(int64_t B, int64_t N, int64_t K) {
-  QPlan q;
-  q.tpw = tpw_override() ? tpw_override() : (B > 16 && N >= 256 * kQTargetWgs ? 4 : 1);
-  q.row_blocks = (N + 64 * q.tpw - 1) / (64 * q.tpw);
-  const int64_t groups = K / kGK;
-  int64_t splits = (kQTargetWgs + q.row_blocks - 1) / q.row_blocks;
-  if (splits > groups) splits = groups;
-  if (splits > kQMaxSplits) splits = kQMaxSplits;
-  if (splits < 1) splits = 1;
-  const int64_t per = (groups + splits - 1) / splits;
-  q.split_len = per * kGK;
-  q.splits = (int)((K + q.split_len - 1) / q.split_len);
-  return q;
-}
-
-static size_t qgemv_ws(int64_t B, int64_t N, int64_t K) {
-  const QPlan q = qgemv_plan(B < 32 ? B : 32, N, K);
-  if (q.splits <= 1) return 0;
-  const int64_t b = B < 32 ? B : 32;
-  return (size_t)q.splits * b * N * sizeof(float);
-}
-
-static int qgemv_launch(QGemvParams p, int bits, void* ws, size_t ws_bytes, hipStream_t s) {
+static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
   if (p.B == 0 || p.N == 0) return VNX_OK;
-  if (!ws && qgemv_ws(p.B, p.N, p.K) > 0) return VNX_ERR_WORKSPACE;
-  if (ws_bytes < qgemv_ws(p.B, p.N, p.K)) return VNX_ERR_WORKSPACE;
-  p.part = static_cast<float*>(ws);
   // Batch columns in chunks of 32 (two MFMA column blocks) or one of 16.
   for (int64_t b0 = 0; b0 < p.B; b0 += 32) {
     QGemvParams c = p;
     c.x = p.x + b0 * p.ldx;
     c.y = p.y + b0 * p.ldy;
     c.B = min((int64_t)32, p.B - b0);
+    c.ksplit_len = c.K;
     const bool two = c.B > 16;
-    const QPlan q = qgemv_plan(c.B, c.N, c.K);
-    c.ksplit_len = q.split_len;
-    const dim3 grid((unsigned)q.row_blocks, (unsigned)q.splits);
-#define VNX_QLAUNCH(BITS, NC, TPW) hipLaunchKernelGGL((k_qgemv<BITS, NC, TPW>), grid, dim3(kQNT), 0, s, c)
-    if (bits == 4) {
-      if (two) { if (q.tpw == 4) VNX_QLAUNCH(4, 2, 4); else VNX_QLAUNCH(4, 2, 1); }
-      else { if (q.tpw == 4) VNX_QLAUNCH(4, 1, 4); else VNX_QLAUNCH(4, 1, 1); }
+    if (c.N < kQTileMaxN) {
+      // 8 waves per tile while the tiles leave CUs idle, 4 beyond
+      const int64_t tiles = (c.N + 15) / 16;
+      const bool wide = tiles <= device_cus();
+      const dim3 grid((unsigned)tiles);
+#define VNX_QTILE(BITS, NC, NW) \
+  hipLaunchKernelGGL((k_qgemv_tile<BITS, NC, NW>), grid, dim3(NW * 64), 0, s, c)
+      if (bits == 4) {
+        if (two) { if (wide) VNX_QTILE(4, 2, 8); else VNX_QTILE(4, 2, 4); }
+        else { if (wide) VNX_QTILE(4, 1, 8); else VNX_QTILE(4, 1, 4); }
+      } else {
+        if (two) { if (wide) VNX_QTILE(8, 2, 8); else VNX_QTILE(8, 2, 4); }
+        else { if (wide) VNX_QTILE(8, 1, 8); else VNX_QTILE(8, 1, 4); }
+      }
+#undef VNX_QTILE
     } else {
-      if (two) { if (q.tpw == 4) VNX_QLAUNCH(8, 2, 4); else VNX_QLAUNCH(8, 2, 1); }
-      else { if (q.tpw == 4) VNX_QLAUNCH(8, 1, 4); else VNX_QLAUNCH(8, 1, 1); }
-    }
+      const int tpw = tpw_override() ? tpw_override() : (c.B > 16 && c.N >= 256 * kQTargetWgs ? 4 : 1);
+      const dim3 grid((unsigned)((c.N + 64 * tpw - 1) / (64 * tpw)));
+#define VNX_QLAUNCH(BITS, NC, TPW) hipLaunchKernelGGL((k_qgemv<BITS, NC, TPW>), grid, dim3(kQNT), 0, s, c)
+      if (bits == 4) {
+        if (two) { if (tpw == 4) VNX_QLAUNCH(4, 2, 4); else VNX_QLAUNCH(4, 2, 1); }
+        else { if (tpw == 4) VNX_QLAUNCH(4, 1, 4); else VNX_QLAUNCH(4, 1, 1); }
+      } else {
+        if (two) { if (tpw == 4) VNX_QLAUNCH(8, 2, 4); else VNX_QLAUNCH(8, 2, 1); }
+        else { if (tpw == 4) VNX_QLAUNCH(8, 1, 4); else VNX_QLAUNCH(8, 1, 1); }
+      }
 #undef VNX_QLAUNCH
-    VNX_LAUNCH_CHECK();
-    if (q.splits > 1) {
-      const int64_t n = c.B * c.N;
-      hipLaunchKernelGGL(k_qreduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, c.part, q.splits, c.B,
-                         c.N, c.y, c.ldy);
-      VNX_LAUNCH_CHECK();
     }
+    VNX_LAUNCH_CHECK();
   }
   return VNX_OK;
 }
@@ -407,9 +502,8 @@ using namespace vnx;
 extern "C" {
 
 size_t vnx_gemv_workspace(int64_t B, int64_t N, int64_t K) {
-  if (B <= 0 || N <= 0 || K <= 0 || K % kGK) return 256;
-  const size_t w = qgemv_ws(B, N, K);
-  return w < 256 ? 256 : w;
+  (void)B; (void)N; (void)K;
+  return 256;  // no kernel needs it: the small-N kernel sums its K split inside a workgroup
 }
 
 int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
@@ -422,7 +516,8 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
   p.gpg = group / kGK;
   const int st = qgemv_check(p, 4);
   if (st) return st;
-  return qgemv_launch(p, 4, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  (void)workspace; (void)workspace_bytes;
+  return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
 }
 
 int vnx_gemv_w8(const void* x, int64_t ldx, const int8_t* wq, int64_t ldw, const float* scale,
@@ -434,7 +529,8 @@ int vnx_gemv_w8(const void* x, int64_t ldx, const int8_t* wq, int64_t ldw, const
   p.gpg = (int)(K / kGK);
   const int st = qgemv_check(p, 8);
   if (st) return st;
-  return qgemv_launch(p, 8, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+  (void)workspace; (void)workspace_bytes;
+  return qgemv_launch(p, 8, static_cast<hipStream_t>(stream));
 }
 
 int vnx_dequant_w4(const uint8_t* wq, int64_t ldw, const void* scales, int scale_dtype, int64_t lds,
