@@ -408,6 +408,38 @@ int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, int64_t sxg, const fl
  * of the experts' (weighted) down projections (MoDLayer.forward, mod.py:779-803). */
 int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, float* out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Skinny bf16 GEMM of the verify forward: for batch z < batch,
+ *   acc[m, n] = sum_k x[z*sxb + m*ldx + k] * W_z[n, k]   (fp32 accumulation)
+ * x (M, K) bf16 activations; W_z (N, K) bf16 weights in the nn.Linear layout,
+ * given packed by vnx_pack_bf16 (batch z at w_packed + z*swb elements); y in
+ * y_dtype (VNX_F32, VNX_BF16 or VNX_F16, round to nearest even).  Replaces
+ * the Linear of the verifier's target forward (packages/verse_torch/
+ * verse_torch/vnnn.py Linear.forward, x @ W^T) for the M = batch x (k+1)
+ * rows of one round.  epilogue VNX_EPI_NONE: y[z*syb + m*ldy + n] = acc[m, n].
+ * VNX_EPI_SWIGLU: W rows come in blocks of 32 (16 gate rows, then the 16 up
+ * rows of the same hidden units) and
+ *   y[z*syb + m*ldy + blk*16 + c] = comb[m*ldc + z] * silu(acc[m, blk*32 + c])
+ *                                   * acc[m, blk*32 + 16 + c]
+ * (comb NULL: weight 1): SwiGLUMLP's activation (vnnn.py:779-807) and a MoD
+ * expert's routing weight (packages/verse_nex/verse_nex/mod.py:466-600).
+ * K multiple of 64; x 16-byte aligned, ldx and sxb multiples of 8 (sxb = 0
+ * shares x over the batch).  Deterministic (fixed summation order).
+ *
+ * vnx_pack_bf16: packs W (N, K) bf16, row pitch ldw, into the
+ * vnx_pack_bf16_size(N, K) bytes at out (16-byte aligned) that vnx_gemm_bf16
+ * reads: the matrix-core operand order, rows padded with zeros to a multiple
+ * of 32.  Done once per weight.
+ * ------------------------------------------------------------------------- */
+enum vnx_epilogue { VNX_EPI_NONE = 0, VNX_EPI_SWIGLU = 1 };
+
+size_t vnx_pack_bf16_size(int64_t N, int64_t K);
+int vnx_pack_bf16(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, void* stream);
+
+int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
+                  int64_t N, int64_t K, int batch, int epilogue, const float* comb, int64_t ldc, void* y,
+                  int y_dtype, int64_t ldy, int64_t syb, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,138 @@
+"""GPU parity of the verify-forward GEMM (vnx_gemm_bf16) against the fp64
+product of the same bf16 inputs.
+
+Bar: |y - ref| <= RTOL * sum_k |x_k w_k| per element (fp32 accumulation of
+exact bf16 products, so the error is a few ulps of the running sums, far
+below 1e-5 of that magnitude), plus one rounding of the output type (2^-8
+relative for bf16, 2^-11 for fp16).  The SwiGLU epilogue is held to the same
+bar propagated through silu(g) * u: RTOL * (1.1 * mag_g * |u| + |silu(g)| *
+mag_u) times the routing weight (silu' <= 1.1), plus the output rounding."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from versenext_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+P = ctypes.c_void_p
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _rnd(dtype):
+    return {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dtype]
+
+
+def _pack(w):
+    """(batch, N, K) bf16 -> packed (batch, elems) bf16 and the batch stride."""
+    L = _lib.lib()
+    batch, N, K = w.shape
+    elems = L.vnx_pack_bf16_size(N, K) // 2
+    out = torch.empty((batch, elems), dtype=torch.bfloat16, device=w.device)
+    st = P(torch.cuda.current_stream().cuda_stream)
+    for z in range(batch):
+        _lib.check(L.vnx_pack_bf16(P(w[z].data_ptr()), K, N, K, P(out[z].data_ptr()), st), "pack")
+    return out, elems
+
+
+def _gemm(x, w, M, N, K, batch, sxb, swb, y, ldy, syb, epi=0, comb=None):
+    st = P(torch.cuda.current_stream().cuda_stream)
+    wp, swb = _pack(w)
+    rc = _lib.lib().vnx_gemm_bf16(P(x.data_ptr()), K, sxb, P(wp.data_ptr()), swb, M, N, K, batch, epi,
+                                  P(comb.data_ptr()) if comb is not None else None, batch, P(y.data_ptr()),
+                                  _lib.DTYPE_CODES[y.dtype], ldy, syb, st)
+    torch.cuda.synchronize()
+    return rc
+
+
+def _inputs(hip, batch_x, batch_w, M, N, K, seed):
+    g = torch.Generator(device=hip.torch_device)
+    g.manual_seed(seed)
+    x = torch.randn((batch_x, M, K), generator=g, device=hip.torch_device).to(torch.bfloat16)
+    w = (torch.randn((batch_w, N, K), generator=g, device=hip.torch_device) * 0.05).to(torch.bfloat16)
+    return x, w
+
+
+@pytest.mark.parametrize("M,N,K,batch,shared_x,dtype", [
+    (224, 2048, 1024, 1, False, torch.float32), (224, 1024, 2752, 1, False, torch.bfloat16),
+    (37, 100, 192, 3, True, torch.float16), (224, 5504, 1024, 1, False, torch.bfloat16),
+    (1, 64, 64, 2, False, torch.float32), (257, 33, 128, 1, False, torch.float32)])
+def test_plain(hip, M, N, K, batch, shared_x, dtype):
+    _say(f"gemm M={M} N={N} K={K} batch={batch} shared_x={shared_x} out={dtype}")
+    x, w = _inputs(hip, 1 if shared_x else batch, batch, M, N, K, seed=M + N + K)
+    y = torch.empty((batch, M, N), dtype=dtype, device=hip.torch_device)
+    _lib.check(_gemm(x, w, M, N, K, batch, 0 if shared_x else M * K, N * K, y, N, M * N), "gemm")
+    torch.cuda.synchronize()
+    xd = x.double().cpu().expand(batch, M, K)
+    wd = w.double().cpu()
+    ref = torch.bmm(xd, wd.transpose(1, 2))
+    mag = torch.bmm(xd.abs(), wd.abs().transpose(1, 2))
+    err = (y.double().cpu() - ref).abs()
+    tol = RTOL * mag + _rnd(dtype) * ref.abs()
+    worst = float((err / (mag + 1e-300)).max())
+    assert bool((err <= tol + 1e-30).all()), f"worst err / mag = {worst:.3e}"
+    _say(f"  worst err / mag = {worst:.2e}")
+
+
+@pytest.mark.parametrize("M,H,K,batch,with_comb,dtype", [
+    (224, 2752, 1024, 1, False, torch.bfloat16), (224, 2688, 1024, 4, True, torch.bfloat16),
+    (30, 48, 128, 2, True, torch.float32), (5, 16, 64, 1, False, torch.float16)])
+def test_swiglu_epilogue(hip, M, H, K, batch, with_comb, dtype):
+    """W rows interleaved in blocks of 32 (16 gate rows, 16 up rows);
+    y[m, j] = comb[m, z] * silu(gate_j) * up_j."""
+    _say(f"gemm swiglu M={M} H={H} K={K} batch={batch} comb={with_comb} out={dtype}")
+    N = 2 * H
+    x, w = _inputs(hip, 1, batch, M, N, K, seed=H + K)
+    comb = None
+    if with_comb:
+        g = torch.Generator(device=hip.torch_device)
+        g.manual_seed(7)
+        comb = torch.rand((M, batch), generator=g, device=hip.torch_device)
+        comb[comb < 0.4] = 0.0
+    y = torch.empty((batch, M, H), dtype=dtype, device=hip.torch_device)
+    _lib.check(_gemm(x, w, M, N, K, batch, 0, N * K, y, H, M * H, epi=_lib.VNX_EPI_SWIGLU, comb=comb), "gemm")
+    torch.cuda.synchronize()
+    xd = x.double().cpu().expand(batch, M, K)
+    wd = w.double().cpu()
+    acc = torch.bmm(xd, wd.transpose(1, 2))                        # (batch, M, N)
+    mag = torch.bmm(xd.abs(), wd.abs().transpose(1, 2))
+    blk = torch.arange(N).view(-1, 32)
+    gi, ui = blk[:, :16].reshape(-1), blk[:, 16:].reshape(-1)      # hidden j -> gate / up rows
+    g_, u_ = acc[..., gi], acc[..., ui]
+    silu = g_ * torch.sigmoid(g_)
+    cw = comb.double().cpu().t().unsqueeze(-1) if comb is not None else torch.ones(batch, M, 1, dtype=torch.float64)
+    ref = cw * silu * u_
+    bound = cw * RTOL * (1.1 * mag[..., gi] * u_.abs() + silu.abs() * mag[..., ui]) + _rnd(dtype) * ref.abs()
+    err = (y.double().cpu() - ref).abs()
+    worst = float((err / (bound + 1e-300)).max())
+    assert bool((err <= bound + 1e-30).all()), f"worst err / bound = {worst:.3e}"
+    if comb is not None:
+        assert bool((y.cpu()[cw.expand_as(ref) == 0] == 0).all())
+
+
+def test_rejects_bad_shapes(hip):
+    x, w = _inputs(hip, 1, 1, 4, 64, 64, seed=1)
+    wp, _ = _pack(w)
+    y = torch.empty((4, 64), dtype=torch.float32, device=hip.torch_device)
+    st = P(torch.cuda.current_stream().cuda_stream)
+    L = _lib.lib()
+    # K not a multiple of 64
+    assert L.vnx_gemm_bf16(P(x.data_ptr()), 64, 0, P(wp.data_ptr()), 0, 4, 64, 32, 1, 0, None, 1,
+                           P(y.data_ptr()), _lib.VNX_F32, 64, 0, st) == _lib.VNX_ERR_UNSUPPORTED
+    # SwiGLU needs N a multiple of 32
+    assert L.vnx_gemm_bf16(P(x.data_ptr()), 64, 0, P(wp.data_ptr()), 0, 4, 48, 64, 1, 1, None, 1,
+                           P(y.data_ptr()), _lib.VNX_F32, 64, 0, st) == _lib.VNX_ERR_INVALID_ARG
+    # ldy shorter than a row
+    assert L.vnx_gemm_bf16(P(x.data_ptr()), 64, 0, P(wp.data_ptr()), 0, 4, 64, 64, 1, 0, None, 1,
+                           P(y.data_ptr()), _lib.VNX_F32, 32, 0, st) == _lib.VNX_ERR_INVALID_ARG
+    # a batch stride shorter than one packed weight
+    assert L.vnx_gemm_bf16(P(x.data_ptr()), 64, 0, P(wp.data_ptr()), 64, 4, 64, 64, 2, 0, None, 1,
+                           P(y.data_ptr()), _lib.VNX_F32, 64, 0, st) == _lib.VNX_ERR_INVALID_ARG
+    # packing needs K a multiple of 64
+    assert L.vnx_pack_bf16(P(w.data_ptr()), 64, 64, 32, P(wp.data_ptr()), st) == _lib.VNX_ERR_UNSUPPORTED

@@ -20,6 +20,7 @@ VNX_ERR_UNSUPPORTED = -3
 VNX_ERR_HIP = -4
 VNX_ERR_NO_DEVICE = -5
 
+VNX_EPI_NONE, VNX_EPI_SWIGLU = 0, 1
 VNX_F32 = 0
 VNX_BF16 = 1
 VNX_F16 = 2
@@ -104,6 +105,10 @@ SIGNATURES.update({
                            _vp, _vp, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),
     "vnx_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
     "vnx_axpby": (_int, [_vp, _vp, _vp, _c_i64, _vp, _int, _vp]),
+    "vnx_pack_bf16_size": (_c_sz, [_c_i64, _c_i64]),
+    "vnx_pack_bf16": (_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
+    "vnx_gemm_bf16": (_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _int, _int, _vp,
+                             _c_i64, _vp, _int, _c_i64, _c_i64, _vp]),
     "vnx_mod_route": (_int, [_vp, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64, _vp]),
     "vnx_mod_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _int, _c_i64, _vp, _int, _c_i64,
                               _c_i64, _vp]),

@@ -1,0 +1,296 @@
+// Skinny bf16 GEMM for the verify forward (vnx_gemm_bf16): Y = X . W^T for
+// the M <= a few hundred token rows of one speculative round (batch x (k+1)),
+// X (M, K) bf16 activations, W (N, K) bf16 (the nn.Linear layout, packed once
+// by vnx_pack_bf16), fp32 accumulation.  This is the Linear of the target's
+// verify forward (packages/verse_torch/verse_torch/vnnn.py Linear.forward:
+// x @ W^T), with the SwiGLU activation of SwiGLUMLP (vnnn.py:779-807) and the
+// routing weight of a MoD expert (packages/verse_nex/verse_nex/mod.py:
+// 466-600) optionally fused into the epilogue.
+//
+// At M ~ 224 the product sits near the machine balance (224 flops per weight
+// byte): the weights stream from HBM once, the activations are re-read from
+// L2 by every workgroup, and the per-CU L1 bandwidth decides the time.  So
+// every load is a full-line wave access:
+//  - W is packed into the v_mfma_f32_32x32x16_bf16 B-operand order: for row
+//    tile t (32 rows), K chunk c (64) and k-step s, lane (r = lane % 32,
+//    h = lane / 32) finds its 8 values W[t*32 + r][c*64 + h*32 + s*8 ..] at
+//    packed[((t*nch + c)*4 + s)*512 + lane*8]: one contiguous KB per wave
+//    load, four per chunk;
+//  - X goes through LDS: the workgroup loads 32 rows x 64 k per chunk with
+//    row-contiguous 16-byte lane loads, stores them with the 16-byte column
+//    index XOR-swizzled by (row / 2) % 8 (conflict-free both ways), and each
+//    wave reads its A operands (the same k permutation h*32 + s*8 as W, so
+//    the dot product is unchanged).
+// A workgroup owns a 32-row M tile and WN adjacent 32-column N tiles; its 4
+// waves are WN (N tiles) x WK (K splits, chunks kw, kw + WK, ...), the K
+// splits summed through LDS in split order (deterministic).  Workgroups are
+// ordered so that the M tiles of one N group land on one XCD (ids t, t + 8,
+// ...), whose L2 then serves that group's W rows to all of them.
+#include <stdlib.h>
+
+#include "vnx_internal.h"
+
+namespace vnx {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kVgChunk = 64;  // K per chunk
+constexpr int kVgXcds = 8;    // XCDs the dispatcher deals workgroups over
+constexpr int kVgRowB = 128;  // bytes of one staged X row (64 bf16)
+
+struct VgParams {
+  const uint16_t* x;
+  const uint16_t* w;       // packed
+  void* y;
+  const float* comb;       // SwiGLU weights comb[m * ldc + z], or NULL
+  int64_t ldx, sxb, swb, ldy, syb, ldc;
+  int M, N, K;             // N = rows of W
+  int mt, nt, ng;          // 32-row tiles of M and N; N groups of WN tiles
+  int order;               // 0: M tiles of an N group on one XCD; 1: M tiles adjacent
+};
+
+template <int OT>
+__device__ __forceinline__ void vg_store(char* y, int64_t off, float v) {
+  if constexpr (OT == 0) {
+    reinterpret_cast<float*>(y)[off] = v;
+  } else if constexpr (OT == 1) {
+    reinterpret_cast<__bf16*>(y)[off] = static_cast<__bf16>(v);
+  } else {
+    reinterpret_cast<_Float16*>(y)[off] = static_cast<_Float16>(v);
+  }
+}
+
+__device__ __forceinline__ bf16x8 as_b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// LDS byte offset of 16-byte column c16 (0..7) of staged row r (0..31).
+__device__ __forceinline__ int xs_off(int r, int c16) { return r * kVgRowB + ((c16 ^ ((r >> 1) & 7)) << 4); }
+
+// EPI 0: y[m, n] = acc.  EPI 1 (SwiGLU): W rows come in blocks of 32, the
+// first 16 the gate rows and the last 16 the up rows of hidden units
+// blk*16 .. +16; y[m, blk*16 + c] = comb * silu(gate) * up.
+template <int OT, int EPI, int WN>
+__global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
+  constexpr int WK = 4 / WN;
+  constexpr int SLAB = WK * 32 * kVgRowB;  // staged X bytes per pass (WK chunks)
+  constexpr int RED = 3 * 64 * 64;         // K-split partial tiles
+  __shared__ __attribute__((aligned(16))) char smem[2 * SLAB > RED ? 2 * SLAB : RED];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave % WN, wk = wave / WN;
+  const int z = blockIdx.y;
+  const int t = blockIdx.x;
+  int gi, mi;
+  if (p.order == 0) {
+    const int grp = t / (kVgXcds * p.mt), rem = t - grp * (kVgXcds * p.mt);
+    gi = grp * kVgXcds + rem % kVgXcds;
+    mi = rem / kVgXcds;
+  } else {
+    gi = t / p.mt;
+    mi = t - gi * p.mt;
+  }
+  if (gi >= p.ng) return;  // uniform over the workgroup
+  const int m0 = mi * 32;
+  const int ni = gi * WN + wn;             // this wave's N tile (past nt: computes, never stores)
+  const int nie = ni < p.nt ? ni : p.nt - 1;
+  const int r = lane & 31, h = lane >> 5;
+  const int nch = p.K / kVgChunk;
+  const int npass = (nch + WK - 1) / WK;
+
+  // X staging: thread tid loads, for j < WK, chunk (pass*WK + j), row
+  // tid / 8, 16-byte column tid % 8.
+  const int xr = tid >> 3, xc = tid & 7;
+  const uint16_t* xrow = p.x + z * p.sxb + (int64_t)min(m0 + xr, p.M - 1) * p.ldx + xc * 8;
+  const uint32_t xkeep = m0 + xr < p.M ? 0xFFFFFFFFu : 0u;
+  const uint16_t* wt = p.w + z * p.swb + (int64_t)nie * nch * 2048 + lane * 8;
+
+  f32x16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+
+  // Loads run PD passes ahead of the math: pass ps lives in ring slot
+  // ps % PD (the loop is unrolled by PD so the slots are registers).
+  constexpr int PD = WK > 2 ? 2 : 4;
+  u32x4 xv[PD][WK], wv[PD][4];
+  auto load_pass = [&](int ps, u32x4 (&xs)[WK], u32x4 (&ws)[4]) {
+#pragma unroll
+    for (int j = 0; j < WK; ++j) {
+      const int c = min(ps * WK + j, nch - 1);
+      xs[j] = *reinterpret_cast<const u32x4*>(xrow + c * kVgChunk);
+    }
+    const int c = min(ps * WK + wk, nch - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      ws[s] = *reinterpret_cast<const u32x4*>(wt + (c * 4 + s) * 512);  // re-read by the M tiles: keep in L2
+  };
+#pragma unroll
+  for (int j = 0; j < PD; ++j) load_pass(j, xv[j], wv[j]);
+  for (int ps0 = 0; ps0 < npass; ps0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; ++j) {
+      const int ps = ps0 + j;
+      char* buf = smem + (ps & 1) * SLAB;
+#pragma unroll
+      for (int q = 0; q < WK; ++q)
+        *reinterpret_cast<u32x4*>(buf + q * 32 * kVgRowB + xs_off(xr, xc)) = xv[j][q] & xkeep;
+      const u32x4 wq[4] = {wv[j][0], wv[j][1], wv[j][2], wv[j][3]};
+      __syncthreads();  // pass ps's X is staged; the other buffer was read before it
+      load_pass(ps + PD, xv[j], wv[j]);  // past the end: clamped re-reads, never used
+      if (ps * WK + wk < nch) {  // uniform per wave
+        const char* xb = buf + wk * 32 * kVgRowB;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(r, h * 4 + s));
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wq[s]), acc, 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  if constexpr (WK > 1) {
+    // K splits 1.. of each N tile -> LDS; split 0 adds them in split order
+    __syncthreads();  // the X buffers are dead
+    f32x16* red = reinterpret_cast<f32x16*>(smem);
+    if (wk > 0) red[((wk - 1) * WN + wn) * 64 + lane] = acc;
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int k = 1; k < WK; ++k) acc += red[((k - 1) * WN + wn) * 64 + lane];
+  }
+  if (ni >= p.nt) return;
+
+  // lane holds D[row 8i + 4h + e][col r] in acc[4i + e]
+  char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
+  if constexpr (EPI == 0) {
+    const int n = ni * 32 + r;
+    if (n >= p.N) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 8 * i + 4 * h + e;
+        if (m < p.M) vg_store<OT>(ybase, (int64_t)m * p.ldy + n, acc[4 * i + e]);
+      }
+  } else {
+    // lanes r < 16 hold the gate of hidden unit ni*16 + r; lane r + 16 its up
+    float up[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) up[i] = __shfl_xor(acc[i], 16);
+    if (r >= 16) return;
+    const int j = ni * 16 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 8 * i + 4 * h + e;
+        if (m >= p.M) continue;
+        const float g = acc[4 * i + e];
+        float v = g / (1.0f + __expf(-g)) * up[4 * i + e];
+        if (p.comb) v *= p.comb[(int64_t)m * p.ldc + z];
+        vg_store<OT>(ybase, (int64_t)m * p.ldy + j, v);
+      }
+  }
+}
+
+// Packing: one thread per 16 bytes of the packed layout (rows past N zero).
+__global__ __launch_bounds__(256) void k_vpack(const uint16_t* w, int64_t ldw, int N, int K, uint16_t* out,
+                                               int64_t total16) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total16) return;
+  const int nch = K / kVgChunk;
+  const int lane = (int)(i & 63);
+  const int64_t q = i >> 6;               // (tile*nch + c)*4 + s
+  const int s = (int)(q & 3);
+  const int64_t tc = q >> 2;
+  const int c = (int)(tc % nch);
+  const int64_t tile = tc / nch;
+  const int64_t row = tile * 32 + (lane & 31);
+  const int k = c * kVgChunk + (lane >> 5) * 32 + s * 8;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (row < N) v = *reinterpret_cast<const u32x4*>(w + row * ldw + k);
+  *reinterpret_cast<u32x4*>(out + i * 8) = v;
+}
+
+}  // namespace
+}  // namespace vnx
+
+using namespace vnx;
+
+extern "C" {
+
+size_t vnx_pack_bf16_size(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 0;
+  return (size_t)((N + 31) / 32) * 32 * (size_t)K * 2;
+}
+
+int vnx_pack_bf16(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, void* stream) {
+  if (!w || !out || N <= 0 || K <= 0 || ldw < K) return VNX_ERR_INVALID_ARG;
+  if (K % kVgChunk || ldw % 8 || !aligned16(w) || !aligned16(out)) return VNX_ERR_UNSUPPORTED;
+  if (N >= INT32_MAX || K >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  const int64_t total16 = (N + 31) / 32 * 32 * K / 8;
+  hipLaunchKernelGGL(k_vpack, dim3((unsigned)((total16 + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), ldw, (int)N, (int)K,
+                     static_cast<uint16_t*>(out), total16);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
+                  int64_t N, int64_t K, int batch, int epilogue, const float* comb, int64_t ldc, void* y,
+                  int y_dtype, int64_t ldy, int64_t syb, void* stream) {
+  if (!x || !w_packed || !y || M < 0 || N < 0 || K <= 0 || batch < 0) return VNX_ERR_INVALID_ARG;
+  if (epilogue != VNX_EPI_NONE && epilogue != VNX_EPI_SWIGLU) return VNX_ERR_INVALID_ARG;
+  if (y_dtype != VNX_F32 && y_dtype != VNX_BF16 && y_dtype != VNX_F16) return VNX_ERR_UNSUPPORTED;
+  const int64_t ncols = epilogue == VNX_EPI_SWIGLU ? N / 2 : N;
+  if (ldx < K || ldy < ncols || sxb < 0 || swb < 0 || syb < 0) return VNX_ERR_INVALID_ARG;
+  if (batch > 1 && swb < (N + 31) / 32 * 32 * K) return VNX_ERR_INVALID_ARG;
+  if (epilogue == VNX_EPI_SWIGLU && N % 32) return VNX_ERR_INVALID_ARG;
+  if (comb && (epilogue != VNX_EPI_SWIGLU || ldc < batch)) return VNX_ERR_INVALID_ARG;
+  if (M == 0 || N == 0 || batch == 0) return VNX_OK;
+  // 16-byte operand loads along K in 64-wide chunks
+  if (K % kVgChunk || ldx % 8 || sxb % 8 || swb % 8 || !aligned16(x) || !aligned16(w_packed))
+    return VNX_ERR_UNSUPPORTED;
+  if (M >= INT32_MAX || N >= INT32_MAX || K >= INT32_MAX || batch > 65535) return VNX_ERR_UNSUPPORTED;
+  VgParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.w = static_cast<const uint16_t*>(w_packed); p.y = y; p.comb = comb;
+  p.ldx = ldx; p.sxb = sxb; p.swb = swb; p.ldy = ldy; p.syb = syb; p.ldc = ldc;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.mt = (int)((M + 31) / 32);
+  p.nt = (int)((N + 31) / 32);
+  // N tiles per workgroup: the most that still keep about three quarters of
+  // the CUs busy (fewer tiles per workgroup split K over its waves instead)
+  const int64_t cus = device_cus();
+  int wn = 4;
+  while (wn > 1 && (int64_t)p.mt * ((p.nt + wn - 1) / wn) * batch < cus * 3 / 4) wn /= 2;
+  p.ng = (p.nt + wn - 1) / wn;
+  static const int order_env = [] {
+    const char* e = getenv("VNX_VG_ORDER");
+    return e ? atoi(e) : 0;
+  }();
+  p.order = order_env == 1 ? 1 : 0;
+  const int64_t groups = (p.ng + kVgXcds - 1) / kVgXcds;
+  const int64_t wgs = p.order == 0 ? groups * kVgXcds * p.mt : (int64_t)p.ng * p.mt;
+  if (wgs >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)wgs, (unsigned)batch);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool sw = epilogue == VNX_EPI_SWIGLU;
+  auto go = [&](auto ot) {
+    constexpr int OT = decltype(ot)::value;
+    if (sw) {
+      if (wn == 4) hipLaunchKernelGGL((k_vgemm<OT, 1, 4>), grid, dim3(256), 0, s, p);
+      else if (wn == 2) hipLaunchKernelGGL((k_vgemm<OT, 1, 2>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((k_vgemm<OT, 1, 1>), grid, dim3(256), 0, s, p);
+    } else {
+      if (wn == 4) hipLaunchKernelGGL((k_vgemm<OT, 0, 4>), grid, dim3(256), 0, s, p);
+      else if (wn == 2) hipLaunchKernelGGL((k_vgemm<OT, 0, 2>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((k_vgemm<OT, 0, 1>), grid, dim3(256), 0, s, p);
+    }
+  };
+  if (y_dtype == VNX_F32) go(IntC<0>{});
+  else if (y_dtype == VNX_BF16) go(IntC<1>{});
+  else go(IntC<2>{});
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+}  // extern "C"

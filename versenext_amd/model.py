@@ -238,11 +238,12 @@ class _Linear:
     M <= 64 rows and a dequantized copy (bit-exact q * s) for larger M
     (prefill)."""
 
-    def __init__(self, w: torch.Tensor, dtype, hip, int4: bool):
+    def __init__(self, w: torch.Tensor, dtype, hip, int4: bool, swiglu: bool = False):
         self.N, self.K = w.shape
         self.dtype = dtype
         self.hip = hip
         self.int4 = bool(int4) and self.K % 128 == 0
+        self.wp = None
         if self.int4:
             wq, sc = VQ.quantize_int4_g(w.float(), 128)
             self.wq, self.sc = wq.contiguous(), sc.contiguous()
@@ -252,6 +253,42 @@ class _Linear:
                                    device=hip.torch_device)
         else:
             self.wd = w.to(dtype).contiguous()
+            # verify-size products (M <= GEMM_MAX_M) run vnx_gemm_bf16 on a
+            # packed copy; for a fused [gate; up] weight its rows are
+            # interleaved in blocks of 16 gate + 16 up rows first (the
+            # SwiGLU epilogue's order)
+            self.swiglu = bool(swiglu) and self.N % 32 == 0
+            if dtype == torch.bfloat16 and self.K % 64 == 0:
+                src = self.wd
+                if self.swiglu:
+                    H = self.N // 2
+                    src = self.wd.view(2, H // 16, 16, self.K).transpose(0, 1).reshape(self.N, self.K).contiguous()
+                L = hip._L
+                self.wp = torch.empty(L.vnx_pack_bf16_size(self.N, self.K) // 2, dtype=torch.bfloat16,
+                                      device=hip.torch_device)
+                _lib.check(L.vnx_pack_bf16(ctypes.c_void_p(src.data_ptr()), self.K, self.N, self.K,
+                                           ctypes.c_void_p(self.wp.data_ptr()),
+                                           ctypes.c_void_p(torch.cuda.current_stream(hip.torch_device).cuda_stream)),
+                           "pack_bf16")
+
+    GEMM_MAX_M = 256
+
+    def gemm(self, x: torch.Tensor, epilogue: int = 0, out_dtype=None) -> Optional[torch.Tensor]:
+        """vnx_gemm_bf16 of the packed weight for x (M <= GEMM_MAX_M, bf16
+        rows): (M, N), or (M, N/2) with the SwiGLU epilogue; None when this
+        weight or x does not qualify."""
+        M = x.shape[0]
+        if self.wp is None or M > self.GEMM_MAX_M or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+            return None
+        if epilogue and not self.swiglu:
+            return None
+        ncols = self.N // 2 if epilogue else self.N
+        y = torch.empty((M, ncols), dtype=out_dtype or self.dtype, device=x.device)
+        _lib.check(self.hip._L.vnx_gemm_bf16(
+            ctypes.c_void_p(x.data_ptr()), x.stride(0), 0, ctypes.c_void_p(self.wp.data_ptr()), 0, M, self.N, self.K,
+            1, int(epilogue), None, 1, ctypes.c_void_p(y.data_ptr()), _lib.DTYPE_CODES[y.dtype], ncols, 0,
+            ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16")
+        return y
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x (M, K); returns (M, N) in the compute dtype (dense) or fp32
@@ -267,6 +304,9 @@ class _Linear:
                 ctypes.c_void_p(self.sc.data_ptr()), _lib.VNX_F16, self.sc.stride(0), M, self.N, self.K, 128,
                 ctypes.c_void_p(y.data_ptr()), y.stride(0), ctypes.c_void_p(self._ws.data_ptr()),
                 self._ws.numel(), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4")
+            return y
+        y = self.gemm(x) if out is None else None
+        if y is not None:
             return y
         y = torch.nn.functional.linear(x.to(self.dtype), self.wd)
         if out is not None:
@@ -314,7 +354,7 @@ class CometSparkGPU:
                        gates=torch.sigmoid(W[p + "attn.gate_logits"].float()).contiguous())
             if kind == "trisparse":
                 L.ffn["gu"] = _Linear(torch.cat([W[p + "ffn.w_gate.weight"], W[p + "ffn.w_up.weight"]], 0),
-                                      dtype, hip, int4)
+                                      dtype, hip, int4, swiglu=True)
                 L.ffn["down"] = _Linear(W[p + "ffn.w_down.weight"], dtype, hip, int4)
             else:
                 P, E = cfg.num_dense_parts, cfg.num_experts_per_part
@@ -477,6 +517,9 @@ class CometSparkGPU:
         if L.kind == "mod":
             return self._mod(L, h)
         Hf = self.cfg.ffn_hidden
+        act = L.ffn["gu"].gemm(h, epilogue=_lib.VNX_EPI_SWIGLU, out_dtype=self.act_dtype)
+        if act is not None:                      # gate|up product with the SwiGLU epilogue
+            return L.ffn["down"](act)
         gu = L.ffn["gu"](h)
         act = torch.empty((h.shape[0], Hf), dtype=self.act_dtype, device=self.dev)
         _lib.check(self.hip._L.vnx_swiglu(ctypes.c_void_p(gu.data_ptr()), _lib.DTYPE_CODES[gu.dtype], gu.stride(0),
