@@ -403,6 +403,119 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   }
 }
 
+// Large N, W4 with group-128 fp16 scales (the tied LM head of a draft):
+// x (up to 32 batch rows x K) is staged in LDS once per workgroup, and each
+// wave streams 16-row tiles (tiles w, w + 4, ... of the workgroup's range)
+// with the next tile's weights and scales in flight while it computes the
+// current one.  KG = K / 128 groups.
+template <int NC, int KG>
+__global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_per_wg) {
+  constexpr int XS = KG * kGK + kXPad;  // LDS row pitch of x (fp16)
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs_dyn[];
+  uint16_t* xs = xs_dyn;
+  const int tid = threadIdx.x;
+  const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
+  const int m = lane % 16, kq = lane / 16;
+  for (int idx = tid; idx < NC * 16 * KG * 16; idx += kQNT) {
+    const int b = idx / (KG * 16), c8 = idx % (KG * 16);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (b < p.B) v = *reinterpret_cast<const u32x4*>(p.x + b * p.ldx + c8 * 8);
+    *reinterpret_cast<u32x4*>(&xs[b * XS + c8 * 8]) = stage_perm_w4(v);
+  }
+  __syncthreads();
+
+  const int64_t tiles = (p.N + 15) / 16;
+  const int64_t t_lo = (int64_t)blockIdx.x * tiles_per_wg;
+  const int64_t t_hi = min(tiles, t_lo + tiles_per_wg);
+  // one tile's loads: weights (KG x 16 bytes per lane) and the fp16 scales of
+  // the lane's four D rows (KG halves each)
+  auto load = [&](int64_t tile, u32x4 (&wv)[KG], u32x4 (&sv)[4][KG / 8 > 0 ? KG / 8 : 1],
+                  uint2 (&sv4)[4]) {
+    const int64_t t = min(tile, tiles - 1);
+    const int64_t ra = min(t * 16 + m, p.N - 1);
+    const uint8_t* wr = p.w + ra * p.ldw + kq * 16;
+#pragma unroll
+    for (int g = 0; g < KG; ++g) wv[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + g * 64));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t rd = min(t * 16 + 4 * kq + j, p.N - 1);
+      const uint16_t* srow = static_cast<const uint16_t*>(p.sc) + rd * p.lds;
+      if constexpr (KG >= 8) {
+#pragma unroll
+        for (int q = 0; q < KG / 8; ++q) sv[j][q] = *reinterpret_cast<const u32x4*>(srow + q * 8);
+      } else {
+        sv4[j] = *reinterpret_cast<const uint2*>(srow);
+      }
+    }
+  };
+  auto scale = [&](const u32x4 (&sv)[4][KG / 8 > 0 ? KG / 8 : 1], const uint2 (&sv4)[4], int g, int j) {
+    uint32_t wd;
+    if constexpr (KG >= 8) {
+      const u32x4 v = sv[j][g / 8];
+      const int e = (g % 8) / 2;
+      wd = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+    } else {
+      wd = (g / 2) == 0 ? sv4[j].x : sv4[j].y;
+    }
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(wd >> (16 * (g % 2))));
+  };
+  auto compute_store = [&](int64_t tile, const u32x4 (&wv)[KG], const u32x4 (&sv)[4][KG / 8 > 0 ? KG / 8 : 1],
+                           const uint2 (&sv4)[4]) {
+    f32x4 yacc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) yacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      f32x4 acc[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint32_t wd[4] = {wv[g].x, wv[g].y, wv[g].z, wv[g].w};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const half8 a = a_w4(wd[s4]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const half8 bx = *reinterpret_cast<const half8*>(&xs[(c * 16 + m) * XS + g * kGK + kq * 32 + s4 * 8]);
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc[c], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) yacc[c][j] = __builtin_fmaf(scale(sv, sv4, g, j), acc[c][j], yacc[c][j]);
+    }
+    if (tile >= t_hi) return;
+    const int64_t n0 = tile * 16 + 4 * kq;
+    if (n0 >= p.N) return;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t b = c * 16 + m;
+      if (b >= p.B) continue;
+      float* dst = p.y + b * p.ldy + n0;
+      if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = yacc[c];
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (n0 + j < p.N) dst[j] = yacc[c][j];
+      }
+    }
+  };
+  // two tiles per pass in a two-slot ring: slot A's loads were issued a
+  // pass earlier, slot B's before slot A's math
+  u32x4 wa[KG], wb[KG], sa[4][KG / 8 > 0 ? KG / 8 : 1], sb[4][KG / 8 > 0 ? KG / 8 : 1];
+  uint2 sa4[4], sb4[4];
+  int64_t ta = t_lo + wave;
+  load(ta, wa, sa, sa4);
+  for (; ta < t_hi; ta += 8) {
+    const int64_t tb = ta + 4;
+    load(tb, wb, sb, sb4);
+    compute_store(ta, wa, sa, sa4);
+    load(ta + 8, wa, sa, sa4);
+    compute_store(tb, wb, sb, sb4);
+  }
+}
+
 // Dequantization (bit-exact reference for the kernels' weights):
 // out[n][k] = q[n][k] * s[n][k / G] in fp32 (one rounded multiply).
 __global__ void k_dequant(QGemvParams p, int bits, float* out, int64_t ldo) {
@@ -477,6 +590,21 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
         else { if (wide) VNX_QTILE(8, 1, 8); else VNX_QTILE(8, 1, 4); }
       }
 #undef VNX_QTILE
+    } else if (bits == 4 && c.G == kGK && c.sc_f16 && c.lds % 8 == 0 && aligned16(c.sc) &&
+               (c.K == 512 || c.K == 1024) && !getenv("VNX_QSTREAM_OFF")) {
+      // two workgroups per CU (x staged once each), tiles split evenly
+      const int64_t tiles = (c.N + 15) / 16;
+      const int64_t wgs_target = 2 * device_cus();
+      int64_t tpw = (tiles + wgs_target - 1) / wgs_target;
+      tpw = (tpw + 7) / 8 * 8;
+      const dim3 grid((unsigned)((tiles + tpw - 1) / tpw));
+      const int nc = two ? 2 : 1;
+      const size_t lds = (size_t)nc * 16 * (c.K + kXPad) * 2;
+#define VNX_QSTREAM(NC, KG) \
+  hipLaunchKernelGGL((k_qgemv_stream<NC, KG>), grid, dim3(kQNT), lds, s, c, (int)tpw)
+      if (c.K == 512) { if (two) VNX_QSTREAM(2, 4); else VNX_QSTREAM(1, 4); }
+      else { if (two) VNX_QSTREAM(2, 8); else VNX_QSTREAM(1, 8); }
+#undef VNX_QSTREAM
     } else {
       const int tpw = tpw_override() ? tpw_override() : (c.B > 16 && c.N >= 256 * kQTargetWgs ? 4 : 1);
       const dim3 grid((unsigned)((c.N + 64 * tpw - 1) / (64 * tpw)));
