@@ -375,6 +375,15 @@ int vnx_rmsnorm(const float* x, int64_t ldx, const void* res, int res_dtype, int
                 float eps, int64_t M, int64_t D, float* x_out, int64_t ldxo, void* y, int y_dtype, int64_t ldy,
                 void* stream);
 
+/* vnx_embed_rmsnorm: the first block's norm with the token embedding folded
+ * in (CometSparkV05LM.forward, spark/src/base_model.py:170-208: tok_emb(idx)
+ * x sqrt(D), then norm1): x_out[m] = emb[tokens[m]] * scale (fp32, emb row
+ * pitch lde, emb_dtype VNX_F32 / VNX_BF16 / VNX_F16; token ids clamped to
+ * [0, vocab)), y[m] = RMSNorm(x_out[m]) * w as vnx_rmsnorm. */
+int vnx_embed_rmsnorm(const int64_t* tokens, const void* emb, int emb_dtype, int64_t lde, int64_t vocab,
+                      float scale, const float* w, float eps, int64_t M, int64_t D, float* x_out, int64_t ldxo,
+                      void* y, int y_dtype, int64_t ldy, void* stream);
+
 int vnx_rope_kv(const void* qkv, int dtype, int64_t ldq, int64_t B, int n, int H, int Hkv, int d,
                 const int32_t* lens, const float* cos_table, const float* sin_table, int64_t table_rows, int rope,
                 void* q_out, void* k_cache, void* v_cache, int out_dtype, int64_t c_sb, int64_t c_sh,

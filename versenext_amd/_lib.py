@@ -103,6 +103,8 @@ SIGNATURES.update({
                            _c_i64, _vp]),
     "vnx_rope_kv": (_int, [_vp, _int, _c_i64, _c_i64, _int, _int, _int, _int, _vp, _vp, _vp, _c_i64, _int,
                            _vp, _vp, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),
+    "vnx_embed_rmsnorm": (_int, [_vp, _vp, _int, _c_i64, _c_i64, _f32, _vp, _f32, _c_i64, _c_i64, _vp, _c_i64,
+                                 _vp, _int, _c_i64, _vp]),
     "vnx_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
     "vnx_axpby": (_int, [_vp, _vp, _vp, _c_i64, _vp, _int, _vp]),
     "vnx_pack_bf16_size": (_c_sz, [_c_i64, _c_i64]),

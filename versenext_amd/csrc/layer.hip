@@ -97,6 +97,11 @@ int by_dtype(int dt, F&& f) {
 constexpr int kRnThreads = 256;
 constexpr int kRnPer = 16;
 
+template <typename TY>
+__device__ __forceinline__ void rms_tail(const float (&v)[kRnPer], const float (&wv)[kRnPer], float ss,
+                                         float* red, float eps, int64_t D, int64_t row, float* xo, int64_t ldxo,
+                                         TY* y, int64_t ldy);
+
 template <typename TR, typename TY>
 __global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t ldx, const TR* r, int64_t ldr,
                                                         const float* w, float eps, int64_t D, float* xo,
@@ -120,6 +125,17 @@ __global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t 
     v[j] = a;
     ss = __builtin_fmaf(a, a, ss);
   }
+  rms_tail<TY>(v, wv, ss, red, eps, D, row, xo, ldxo, y, ldy);
+}
+
+// x_out[row] = x (the residual stream), y[row] = x / sqrt(mean(x^2) + eps) * w
+// from a workgroup's values v (kRnPer per thread, column tid + j*256) and
+// their per-thread sum of squares ss.
+template <typename TY>
+__device__ __forceinline__ void rms_tail(const float (&v)[kRnPer], const float (&wv)[kRnPer], float ss,
+                                         float* red, float eps, int64_t D, int64_t row, float* xo, int64_t ldxo,
+                                         TY* y, int64_t ldy) {
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, VNX_WAVE);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -136,6 +152,36 @@ __global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t 
       Elt<TY>::st(y + row * ldy + c, v[j] * inv * wv[j]);
     }
   }
+}
+
+// The first layer's norm with the embedding lookup folded in: x[row] =
+// emb[tokens[row]] * scale (fp32), written to x_out as the residual stream.
+template <typename TE, typename TY>
+__global__ __launch_bounds__(kRnThreads) void k_embed_rmsnorm(const int64_t* tokens, const TE* emb, int64_t lde,
+                                                              int64_t vocab, float scale, const float* w, float eps,
+                                                              int64_t D, float* xo, int64_t ldxo, TY* y,
+                                                              int64_t ldy) {
+  __shared__ float red[kRnThreads / VNX_WAVE];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  int64_t tok = tokens[row];
+  tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);  // never outside the table
+  const TE* e = emb + tok * lde;
+  float v[kRnPer], wv[kRnPer];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRnPer; ++j) {
+    const int c = tid + j * kRnThreads;
+    float a = 0.0f;
+    wv[j] = 0.0f;
+    if (c < D) {
+      a = Elt<TE>::ld(e + c) * scale;
+      wv[j] = w[c];
+    }
+    v[j] = a;
+    ss = __builtin_fmaf(a, a, ss);
+  }
+  rms_tail<TY>(v, wv, ss, red, eps, D, row, xo, ldxo, y, ldy);
 }
 
 // ---------------------------------------------------------------------------
@@ -357,6 +403,28 @@ int vnx_rmsnorm(const float* x, int64_t ldx, const void* res, int res_dtype, int
       using TY = decltype(ty);
       hipLaunchKernelGGL((k_rmsnorm<TR, TY>), dim3((unsigned)M), dim3(kRnThreads), 0, s, x, ldx,
                          static_cast<const TR*>(res), ldr, w, eps, D, x_out, ldxo, static_cast<TY*>(y), ldy);
+      VNX_LAUNCH_CHECK();
+      return (int)VNX_OK;
+    });
+  });
+}
+
+int vnx_embed_rmsnorm(const int64_t* tokens, const void* emb, int emb_dtype, int64_t lde, int64_t vocab,
+                      float scale, const float* w, float eps, int64_t M, int64_t D, float* x_out, int64_t ldxo,
+                      void* y, int y_dtype, int64_t ldy, void* stream) {
+  if (!tokens || !emb || !w || !x_out || !y || M < 0 || D <= 0 || vocab <= 0 || lde < D || ldxo < D || ldy < D)
+    return VNX_ERR_INVALID_ARG;
+  if (D > (int64_t)kRnThreads * kRnPer || !(eps >= 0.0f)) return VNX_ERR_UNSUPPORTED;
+  if (M == 0) return VNX_OK;
+  if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return by_dtype(emb_dtype, [&](auto te) {
+    using TE = decltype(te);
+    return by_dtype(y_dtype, [&](auto ty) {
+      using TY = decltype(ty);
+      hipLaunchKernelGGL((k_embed_rmsnorm<TE, TY>), dim3((unsigned)M), dim3(kRnThreads), 0, s, tokens,
+                         static_cast<const TE*>(emb), lde, vocab, scale, w, eps, D, x_out, ldxo, static_cast<TY*>(y),
+                         ldy);
       VNX_LAUNCH_CHECK();
       return (int)VNX_OK;
     });

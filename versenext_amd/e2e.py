@@ -89,6 +89,7 @@ class SpecDecodeEngine:
         self.count = torch.zeros(B, dtype=torch.int64, device=dev)
         self.info = torch.zeros(4, dtype=torch.int64, device=dev)
         self.ar = torch.arange(k + 1, device=dev).view(1, k + 1)
+        self.steps_i32 = torch.arange(k + 1, dtype=torch.int32, device=dev).view(k + 1, 1)
         self.out = None
         self.n_new = 0
         self.graph = None
@@ -105,8 +106,10 @@ class SpecDecodeEngine:
     def _round(self, Tmax_t: int, Tmax_d: int):
         B, k = self.B, self.k
         tok = self.c
+        # the draft's positions lens_d[b] + i of all k+1 steps in one kernel
+        lens_steps = self.lens_d.view(1, B) + self.steps_i32
         for i in range(k + 1):
-            h = self.d.forward(tok.view(B, 1), self.lens_d + i, Tmax_d + i)
+            h = self.d.forward(tok.view(B, 1), lens_steps[i], Tmax_d + i, out_dtype=self.d.act_dtype)
             if i == k:
                 break
             self.d.logits(h, out=self.qbuf[:, i:i + 1])
@@ -116,7 +119,7 @@ class SpecDecodeEngine:
                 tok = self.hip.sample(self.qbuf[:, i], self.u_draft[i], temperature=self.T)
             self.xs[:, i] = tok
         toks = torch.cat([self.c.view(B, 1), self.xs], dim=1)
-        h = self.t.forward(toks, self.lens_t, Tmax_t)
+        h = self.t.forward(toks, self.lens_t, Tmax_t, out_dtype=self.t.act_dtype)
         self.t.logits(h, out=self.pbuf)
         if self.greedy:
             _, _, alen, ids = self.hip.greedy_verify(self.pbuf, self.xs, rows_t=k + 1)

@@ -528,10 +528,21 @@ class CometSparkGPU:
         return L.ffn["down"](act)
 
     # ---- forward --------------------------------------------------------
+    def _embed_rms(self, tokens: torch.Tensor, w: torch.Tensor, x: torch.Tensor, y: torch.Tensor) -> None:
+        """x = emb[tokens] * emb_scale (fp32); y = RMSNorm(x) * w (vnx_embed_rmsnorm)."""
+        M, D = x.shape
+        P = ctypes.c_void_p
+        _lib.check(self.hip._L.vnx_embed_rmsnorm(
+            P(tokens.data_ptr()), P(self.emb.data_ptr()), _lib.DTYPE_CODES[self.emb.dtype], self.emb.stride(0),
+            self.emb.shape[0], float(self.emb_scale), P(w.data_ptr()), float(self.cfg.eps), M, D, P(x.data_ptr()),
+            x.stride(0), P(y.data_ptr()), _lib.DTYPE_CODES[y.dtype], y.stride(0), self._st()), "embed_rmsnorm")
+
     @torch.no_grad()
-    def forward(self, tokens: torch.Tensor, lens: torch.Tensor, Tmax: Optional[int] = None) -> torch.Tensor:
+    def forward(self, tokens: torch.Tensor, lens: torch.Tensor, Tmax: Optional[int] = None,
+                out_dtype=torch.float32) -> torch.Tensor:
         """tokens (B, n) int64, lens (B,) int32 on this device; Tmax >= max(lens)
-        (read back from the device when not given).  Returns (B, n, D) fp32."""
+        (read back from the device when not given).  Returns (B, n, D) final-norm
+        hidden states in out_dtype (fp32 by default)."""
         cfg = self.cfg
         B, n = tokens.shape
         if B != self.B:
@@ -546,12 +557,19 @@ class CometSparkGPU:
         M = B * n
         P = ctypes.c_void_p
         L_ = self.hip._L
-        x = (self.emb[tokens.reshape(-1)].float() * self.emb_scale).contiguous()     # (M, D) fp32 residual
+        tok = tokens.reshape(-1).contiguous()
+        if not self.layers:
+            x = (self.emb[tok].float() * self.emb_scale).contiguous()
+        else:
+            x = torch.empty((M, D), dtype=torch.float32, device=self.dev)                # fp32 residual stream
         use_kernel = self.kernel_attention and n <= 64 and Tmax + n <= cfg.window_size
         pending = None
         for li, L in enumerate(self.layers):
             h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
-            self._rms(x, pending, L.norm1, h)
+            if li == 0:
+                self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
+            else:
+                self._rms(x, pending, L.norm1, h)
             qkv = L.wqkv(h)                                                          # (M, (H+2Hkv) d)
             q = torch.empty((B, H, n, d), dtype=self.dtype, device=self.dev)
             kc, vc = self.kc[li], self.vc[li]
@@ -570,7 +588,7 @@ class CometSparkGPU:
             h2 = torch.empty((M, D), dtype=torch.float32 if L.kind == "mod" else self.act_dtype, device=self.dev)
             self._rms(x, a, L.norm2, h2)
             pending = self._ffn(L, h2)
-        out = torch.empty((M, D), dtype=torch.float32, device=self.dev)
+        out = torch.empty((M, D), dtype=out_dtype, device=self.dev)
         self._rms(x, pending, self.norm, out)
         return out.view(B, n, D)
 
