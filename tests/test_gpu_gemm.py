@@ -62,7 +62,10 @@ def _inputs(hip, batch_x, batch_w, M, N, K, seed):
 @pytest.mark.parametrize("M,N,K,batch,shared_x,dtype", [
     (224, 2048, 1024, 1, False, torch.float32), (224, 1024, 2752, 1, False, torch.bfloat16),
     (37, 100, 192, 3, True, torch.float16), (224, 5504, 1024, 1, False, torch.bfloat16),
-    (1, 64, 64, 2, False, torch.float32), (257, 33, 128, 1, False, torch.float32)])
+    (1, 64, 64, 2, False, torch.float32), (257, 33, 128, 1, False, torch.float32),
+    # weight-streaming shape (256 x 128 workgroup tiles): many 128-column groups
+    (224, 16384, 1024, 1, False, torch.float32), (300, 8192, 192, 1, False, torch.bfloat16),
+    (224, 1024, 2688, 16, True, torch.bfloat16), (61, 16400, 64, 1, False, torch.float16)])
 def test_plain(hip, M, N, K, batch, shared_x, dtype):
     _say(f"gemm M={M} N={N} K={K} batch={batch} shared_x={shared_x} out={dtype}")
     x, w = _inputs(hip, 1 if shared_x else batch, batch, M, N, K, seed=M + N + K)

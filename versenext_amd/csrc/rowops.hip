@@ -114,7 +114,8 @@ struct RowPlan {
 static RowPlan row_plan(int64_t rows, int64_t V, int dtype) {
   const int ve = dtype == VNX_F32 ? 4 : 8;
   RowPlan pl;
-  pl.chunks = pick_chunks(rows, V, ve, 64, 2048);
+  // at least 8 vectors per thread per chunk (few rows: fewer, longer chunks)
+  pl.chunks = pick_chunks(rows, V, ve * 8, 64, 2048);
   int64_t len = (V + pl.chunks - 1) / pl.chunks;
   len = (len + ve - 1) / ve * ve;
   pl.chunk_len = len;

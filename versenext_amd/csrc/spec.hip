@@ -527,7 +527,9 @@ static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype) {
   const int ve = dtype == VNX_F32 ? 4 : 8;
   SpecPlan pl;
   const int64_t rows = B * (2 * k + 1);
-  int c = pick_chunks(rows, V, ve, std::min(kMaxChunks, kAccLds / (2 * k + 1)), kLseWgs);
+  // chunks of at least kNB / 2 vectors per thread: few rows (a decode batch)
+  // get fewer, longer workgroups instead of thousands of one-load ones
+  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccLds / (2 * k + 1)), kLseWgs);
   const int64_t len = ((V + c - 1) / c + ve - 1) / ve * ve;
   pl.len = len;
   pl.chunks = (int)((V + len - 1) / len);
