@@ -399,6 +399,36 @@ def cpu_baseline_e2e(Wt, Wd, prompt, budget_s: float = 15.0):
                        f"{tsum / rounds:.2f} s per round, {cores} BLAS threads")
 
 
+def trace_summary(d: str, top: int = 40) -> None:
+    """Per-round GPU time by kernel between the two marker kernels of an
+    --e2e-mark run (rocprofv3 --kernel-trace --output-format csv): the decode
+    rounds of the last run only (no prefill, capture or warm-up)."""
+    import collections
+    import csv
+    import glob
+    path = sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True))[0]
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(rows) if "scan" in r["Kernel_Name"].lower()]
+    if len(marks) < 2:
+        raise SystemExit("no marker kernels in the trace (run bench.py --workload e2e --e2e-mark)")
+    win = rows[marks[-2] + 1:marks[-1]]
+    lm = sum(1 for r in win if "k_lm_head" in r["Kernel_Name"])  # one verify head per round
+    rounds = max(1, lm)
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    busy = 0.0
+    for r in win:
+        du = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        agg[r["Kernel_Name"][:110]][0] += 1
+        agg[r["Kernel_Name"][:110]][1] += du
+        busy += du
+    span = (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e3
+    print(f"rounds {rounds}; window {span / rounds:.1f} us/round, kernels {len(win) / rounds:.1f}/round, "
+          f"kernel time {busy / rounds:.1f} us/round")
+    for name, (c, t) in sorted(agg.items(), key=lambda x: -x[1][1])[:top]:
+        print(f"{t / rounds:9.1f} us/round {c / rounds:6.1f} calls {t / c:8.1f} us  {name}")
+
+
 def bench_e2e(args):
     """end-to-end speculative decode.  Target CometSparkV05
     (D 1024, 20 layers = 5 MoD + 15 TriSparse, tied 248,320 head, random init,
@@ -432,8 +462,28 @@ def bench_e2e(args):
     eng = SpecDecodeEngine(target, draft, hip, k=E2E_K, temperature=E2E_TEMP, seed=31,
                            use_graph=not args.e2e_eager)
     runs = []
-    for r in range(max(1, args.e2e_runs)):
+    nruns = max(1, args.e2e_runs)
+    mark = torch.ones(64, dtype=torch.int16, device=dev) if args.e2e_mark else None
+    if mark is not None:
+        # marker kernels (an int16 scan, used nowhere else) bracket the last
+        # run's decode rounds in a kernel trace: one after its prefill, one
+        # after its last round (see --trace-summary)
+        fill = eng._fill_uniforms
+        armed = {"on": False}
+
+        def fill_marked():
+            if armed["on"]:
+                torch.cumsum(mark, 0)
+                armed["on"] = False
+            fill()
+        eng._fill_uniforms = fill_marked
+    for r in range(nruns):
+        if mark is not None and r == nruns - 1:
+            armed["on"] = True
         toks, st = eng.generate(prompts, E2E_NEW)
+        if mark is not None and r == nruns - 1:
+            torch.cumsum(mark, 0)
+            torch.cuda.synchronize()
         runs.append(st)
         print(json.dumps({"e2e_run": r, "rounds": st.rounds, "decode_s": round(st.decode_s, 4),
                           "prefill_s": round(st.prefill_s, 4), "tokens_per_s": round(st.tokens_per_s, 1),
@@ -576,6 +626,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--e2e-runs", type=int, default=2, help="e2e: decode runs (the last is reported)")
     ap.add_argument("--e2e-eager", action="store_true", help="e2e: launch every round eagerly (no HIP graph)")
+    ap.add_argument("--e2e-mark", action="store_true",
+                    help="e2e: bracket the last run's decode rounds with marker kernels for a kernel trace")
+    ap.add_argument("--trace-summary", metavar="DIR",
+                    help="print the per-round kernel table of a rocprofv3 kernel trace of an --e2e-mark run "
+                         "(DIR holds *kernel_trace.csv) and exit")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
     ap.add_argument("--workload", default="e2e", choices=("e2e", "accept", "gemv", "tree", "lmhead"),
@@ -583,6 +638,9 @@ def main():
                          "(the bench line); accept: config 2 alone; gemv: config 4; tree: config 3; "
                          "lmhead: the verify-pass LM head")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (one MI355X per box); "
                                    "run with --gpus 1", "n_gpus": args.gpus}))
