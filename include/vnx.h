@@ -400,9 +400,17 @@ int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void
  * logits | the P expert routers' logits, part-major]; comb (M, P*E) fp32 =
  * softmax(part logits)[p] x softmax over part p's top-k expert logits
  * (larger first, ties to the lower index) for the selected experts, 0
- * elsewhere.  P <= 8, E <= 16, 1 <= topk <= E. */
+ * elsewhere.  P <= 8, E <= 16, P + P*E <= 64, 1 <= topk <= E. */
 int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int topk, float* comb, int64_t ldc,
                   void* stream);
+
+/* vnx_mod_route with the router products folded in: logits[m, r] =
+ * sum_c h[m*ldh + c] * wr[r*ldw + c] (fp32, r < P + P*E <= 32: the part
+ * router's rows, then each part's expert-router rows), then the same
+ * routing weights into comb.  The router Linear (mod.py:337-440,
+ * `self.gate(router_input)`) and the top-k rule in one launch. */
+int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, int64_t M, int64_t D, int P, int E,
+                    int topk, float* comb, int64_t ldc, void* stream);
 
 /* The routed, weighted expert activations (DensePart / Expert,
  * mod.py:466-600): for row m and expert x < PE, with g = gu + m*ldg + x*sxg

@@ -172,3 +172,32 @@ def test_mod_swiglu_and_sum(hip, M, PE, He, layout, odt):
         for x in range(PE):   # fp32 accumulation in expert order
             ref_s = ref_s + y.float().cpu()[x]
         _close(s, ref_s, torch.float32, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("M,D,NP,NE,topk", [(224, 1024, 4, 4, 2), (5, 100, 2, 3, 1), (33, 64, 1, 8, 3)])
+def test_mod_route_from_hidden(hip, M, D, NP, NE, topk):
+    """vnx_mod_route_x (router products + routing) against torch fp32
+    logits and the reference rule: softmax over all part logits, per part the
+    top-k expert logits (ties to the lower index) re-softmaxed."""
+    _say(f"mod_route_x M={M} D={D} P={NP} E={NE} topk={topk}")
+    dev = hip.torch_device
+    g = _gen(hip, M + D + NP * NE)
+    h = torch.randn((M, D), generator=g, device=dev)
+    R = NP + NP * NE
+    wr = torch.randn((R, D), generator=g, device=dev) * 0.02   # router init scale: logits of order 1
+    comb = torch.empty((M, NP * NE), dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().vnx_mod_route_x(P(h.data_ptr()), D, P(wr.data_ptr()), D, M, D, NP, NE, topk,
+                                          P(comb.data_ptr()), NP * NE, _st()), "mod_route_x")
+    torch.cuda.synchronize()
+    lg = (h.double().cpu() @ wr.double().cpu().t())                       # (M, R)
+    pw = torch.softmax(lg[:, :NP], dim=-1)
+    ref = torch.zeros((M, NP * NE), dtype=torch.float64)
+    for p_ in range(NP):
+        le = lg[:, NP + p_ * NE:NP + (p_ + 1) * NE]
+        idx = torch.argsort(-le, dim=-1, stable=True)[:, :topk]
+        sel = torch.gather(le, 1, idx)
+        w = torch.softmax(sel, dim=-1) * pw[:, p_:p_ + 1]
+        ref[:, p_ * NE:(p_ + 1) * NE].scatter_(1, idx, w)
+    got = comb.double().cpu()
+    assert bool(((got > 0) == (ref > 0)).all()), "selected experts differ"
+    assert float((got - ref).abs().max()) < 2e-5

@@ -281,40 +281,106 @@ __global__ __launch_bounds__(256) void k_axpby(const float* a, const float* b, c
 // the P part-router logits (top_k = P, all parts); inside part p the top-k
 // of its E expert logits (larger first, ties to the lower index) are weighted
 // by the softmax over the selected logits.  comb[m, p*E + e] = part weight x
-// expert weight, 0 for unselected experts.  One thread per row.
+// expert weight, 0 for unselected experts.  One wave per row.
 // ---------------------------------------------------------------------------
 constexpr int kModMaxP = 8;
 constexpr int kModMaxE = 16;
 
+// One row's routing weights, computed by one wave: lane j < P + P*E holds
+// logit j (the P part logits, then the E expert logits of each part).  Part
+// weights are the softmax of the part logits; inside part p, lane j's rank
+// is the number of its segment's logits that beat it (larger, or equal at a
+// lower index), it is selected when rank < topk, and the selected logits are
+// re-softmaxed with the sum taken in rank order (largest first).  Lane
+// P + p*E + e writes c[p*E + e].  All exchanges are wave shuffles.
+__device__ void route_wave(float lj, int P, int E, int topk, float* c) {
+  const int lane = threadIdx.x & 63;
+  const int R = P + P * E;
+  // part softmax
+  float mx = -__builtin_inff();
+  for (int q = 0; q < P; ++q) mx = fmaxf(mx, __shfl(lj, q));
+  float sp = 0.0f;
+  for (int q = 0; q < P; ++q) sp += expf(__shfl(lj, q) - mx);
+  // this lane's part (every lane shuffles here, before the part lanes leave)
+  const int pl = lane >= P && lane < R ? (lane - P) / E : 0;
+  const float pw = expf(__shfl(lj, pl) - mx) / sp;
+  if (lane < P || lane >= R) return;  // (no shuffle below reads these lanes)
+  const int p = pl, e = lane - P - p * E, base = P + p * E;
+  // rank inside the segment, and the segment's largest logit
+  int rank = 0;
+  float ms = -__builtin_inff();
+  for (int e2 = 0; e2 < E; ++e2) {
+    const float v = __shfl(lj, base + e2);
+    rank += (v > lj || (v == lj && e2 < e)) ? 1 : 0;
+    ms = fmaxf(ms, v);
+  }
+  // sum of the selected terms in rank order
+  float ss = 0.0f;
+  for (int i = 0; i < topk; ++i) {
+    float vi = 0.0f;
+    for (int e2 = 0; e2 < E; ++e2) {
+      const float v = __shfl(lj, base + e2);
+      int r2 = 0;
+      for (int e3 = 0; e3 < E; ++e3) {
+        const float w = __shfl(lj, base + e3);
+        r2 += (w > v || (w == v && e3 < e2)) ? 1 : 0;
+      }
+      if (r2 == i) vi = v;
+    }
+    ss += expf(vi - ms);
+  }
+  c[p * E + e] = rank < topk ? pw * (expf(lj - ms) / ss) : 0.0f;
+}
+
 __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E,
                                                   int topk, float* comb, int64_t ldc) {
-  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (m >= M) return;
-  const float* l = logits + m * ld;
-  float* c = comb + m * ldc;
-  float mx = -__builtin_inff();
-  for (int p = 0; p < P; ++p) mx = fmaxf(mx, l[p]);
-  float sp = 0.0f;
-  for (int p = 0; p < P; ++p) sp += expf(l[p] - mx);
-  for (int p = 0; p < P; ++p) {
-    const float pw = expf(l[p] - mx) / sp;
-    const float* le = l + P + p * E;
-    uint32_t taken = 0;
-    int sel[kModMaxE];
-    for (int i = 0; i < topk; ++i) {
-      int best = -1;
-      for (int e = 0; e < E; ++e)
-        if (!((taken >> e) & 1u) && (best < 0 || le[e] > le[best])) best = e;
-      sel[i] = best;
-      taken |= 1u << best;
-    }
-    float ms = -__builtin_inff();
-    for (int i = 0; i < topk; ++i) ms = fmaxf(ms, le[sel[i]]);
-    float ss = 0.0f;
-    for (int i = 0; i < topk; ++i) ss += expf(le[sel[i]] - ms);
-    for (int e = 0; e < E; ++e) c[p * E + e] = 0.0f;
-    for (int i = 0; i < topk; ++i) c[p * E + sel[i]] = pw * (expf(le[sel[i]] - ms) / ss);
+  // one wave per row
+  const int64_t m = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int R = P + P * E;
+  const float lj = lane < R ? logits[m * ld + lane] : 0.0f;
+  route_wave(lj, P, E, topk, comb + m * ldc);
+}
+
+// The router products folded in: one workgroup per row computes its
+// R = P + P*E logits (fp32 dot products: per-thread partial sums over
+// columns tid, tid + 256, ..., then the wave and workgroup sums in a fixed
+// order) and routes them.
+constexpr int kRouteMaxR = 32;
+
+__global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw,
+                                                     int64_t D, int P, int E, int topk, float* comb, int64_t ldc) {
+  __shared__ float red[4][kRouteMaxR];
+  __shared__ float lg[kRouteMaxR];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = P + P * E;
+  float acc[kRouteMaxR];
+#pragma unroll
+  for (int r = 0; r < kRouteMaxR; ++r) acc[r] = 0.0f;
+  for (int64_t c = tid; c < D; c += 256) {
+    // every row's load issued unconditionally (rows past R re-read row R-1
+    // and are not accumulated): no branches between the loads
+    const float x = h[m * ldh + c];
+    float wv[kRouteMaxR];
+#pragma unroll
+    for (int r = 0; r < kRouteMaxR; ++r) wv[r] = wr[(int64_t)(r < R ? r : R - 1) * ldw + c];
+#pragma unroll
+    for (int r = 0; r < kRouteMaxR; ++r) acc[r] = __builtin_fmaf(x, r < R ? wv[r] : 0.0f, acc[r]);
   }
+#pragma unroll
+  for (int r = 0; r < kRouteMaxR; ++r) {
+    if (r < R) {
+      float v = acc[r];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, VNX_WAVE);
+      if (lane == 0) red[wave][r] = v;
+    }
+  }
+  __syncthreads();
+  if (tid < R) lg[tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+  __syncthreads();
+  if (wave == 0) route_wave(lane < R ? lg[lane] : 0.0f, P, E, topk, comb + m * ldc);
 }
 
 // Expert activations of all PE experts for every row, scaled by the routing
@@ -505,13 +571,25 @@ int vnx_axpby(const float* a, const float* b, const float* coef, int64_t n, void
 int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int topk, float* comb, int64_t ldc,
                   void* stream) {
   if (!logits || !comb || M < 0 || P < 1 || E < 1 || topk < 1 || topk > E) return VNX_ERR_INVALID_ARG;
-  if (P > kModMaxP || E > kModMaxE) return VNX_ERR_UNSUPPORTED;
+  if (P > kModMaxP || E > kModMaxE || P + P * E > VNX_WAVE) return VNX_ERR_UNSUPPORTED;
   if (ld < P + (int64_t)P * E || ldc < (int64_t)P * E) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
   if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_mod_route, dim3((unsigned)((M + 63) / 64)), dim3(64), 0, s, logits, ld, M, P, E, topk,
-                     comb, ldc);
+  hipLaunchKernelGGL(k_mod_route, dim3((unsigned)M), dim3(64), 0, s, logits, ld, M, P, E, topk, comb, ldc);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, int64_t M, int64_t D, int P, int E,
+                    int topk, float* comb, int64_t ldc, void* stream) {
+  if (!h || !wr || !comb || M < 0 || D < 1 || P < 1 || E < 1 || topk < 1 || topk > E) return VNX_ERR_INVALID_ARG;
+  if (P > kModMaxP || E > kModMaxE || P + P * E > kRouteMaxR) return VNX_ERR_UNSUPPORTED;
+  if (ldh < D || ldw < D || ldc < (int64_t)P * E) return VNX_ERR_INVALID_ARG;
+  if (M == 0) return VNX_OK;
+  if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(k_mod_route_x, dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h, ldh, wr,
+                     ldw, D, P, E, topk, comb, ldc);
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }

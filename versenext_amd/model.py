@@ -497,10 +497,15 @@ class CometSparkGPU:
         M = h.shape[0]
         P_ = ctypes.c_void_p
         L_ = self.hip._L
-        logits = torch.nn.functional.linear(h, L.ffn["route"])                    # (M, P + PE) fp32
         comb = torch.empty((M, PE), dtype=torch.float32, device=self.dev)
-        _lib.check(L_.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k, P_(comb.data_ptr()), PE,
-                                    self._st()), "mod_route")
+        wr = L.ffn["route"]                                                        # (P + PE, D) fp32
+        if P + PE <= 32:      # router products and routing rule in one launch
+            _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), P_(wr.data_ptr()), wr.stride(0), M, D, P, E,
+                                          k, P_(comb.data_ptr()), PE, self._st()), "mod_route_x")
+        else:
+            logits = torch.nn.functional.linear(h, wr)                             # (M, P + PE) fp32
+            _lib.check(L_.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k, P_(comb.data_ptr()),
+                                        PE, self._st()), "mod_route")
         xb = h.to(self.dtype).unsqueeze(0).expand(PE, M, D).contiguous()
         gu = torch.matmul(xb, L.ffn["w1"])                                        # (PE, M, 2He)
         act = torch.empty((PE, M, He), dtype=self.dtype, device=self.dev)
