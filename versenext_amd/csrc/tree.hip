@@ -465,8 +465,9 @@ static size_t ta_ws_bytes(const TaPlan& pl, int B, int H, int N, int d) {
 }
 
 // Waves per workgroup (5: 4 with prefetch).  A grid of at most one workgroup
-// per CU gets the widest variant that fits, so each wave walks few key steps
-// and more loads are in flight per CU; larger grids keep 4 waves.
+// per CU gets 8 waves (16 when 8 does not fit the query tile), so each wave
+// walks few key steps and more loads are in flight per CU; larger grids keep
+// 4 waves.
 static int ta_waves(int D, int QT, int64_t nwg) {
   auto ok = [&](int nw) {
     return nw == 5 ? ta_variant_ok(D, QT, 4, true) : ta_variant_ok(D, QT, nw, false);
@@ -475,8 +476,8 @@ static int ta_waves(int D, int QT, int64_t nwg) {
   if (o && ok(o)) return o;
   const int64_t cus = device_cus();
   if (nwg <= cus) {
+    if (ok(8)) return 8;  // (measured at least as fast as 16 at decode shapes, with twice the registers)
     if (ok(16)) return 16;
-    if (ok(8)) return 8;
     return 5;
   }
   if (nwg <= 2 * cus && ok(8)) return 8;
