@@ -483,6 +483,9 @@ __global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_
       for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int j = 0; j < 4; ++j) yacc[c][j] = __builtin_fmaf(scale(sv, sv4, g, j), acc[c][j], yacc[c][j]);
+      // one group's conversions live at a time (the scheduler would otherwise
+      // hoist all of them, and the registers would cap the occupancy at one wave)
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (tile >= t_hi) return;
     const int64_t n0 = tile * 16 + 4 * kq;
