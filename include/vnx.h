@@ -408,9 +408,12 @@ int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int 
  * sum_c h[m*ldh + c] * wr[r*ldw + c] (fp32, r < P + P*E <= 32: the part
  * router's rows, then each part's expert-router rows), then the same
  * routing weights into comb.  The router Linear (mod.py:337-440,
- * `self.gate(router_input)`) and the top-k rule in one launch. */
+ * `self.gate(router_input)`) and the top-k rule in one launch.  With x_out
+ * (bf16, not NULL) it also writes `copies` bf16 copies of h, copy q at
+ * x_out + q*sxo (row pitch ldxo): the experts' input rows. */
 int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, int64_t M, int64_t D, int P, int E,
-                    int topk, float* comb, int64_t ldc, void* stream);
+                    int topk, float* comb, int64_t ldc, void* x_out, int64_t ldxo, int64_t sxo, int copies,
+                    void* stream);
 
 /* The routed, weighted expert activations (DensePart / Expert,
  * mod.py:466-600): for row m and expert x < PE, with g = gu + m*ldg + x*sxg

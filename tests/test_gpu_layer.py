@@ -186,9 +186,13 @@ def test_mod_route_from_hidden(hip, M, D, NP, NE, topk):
     R = NP + NP * NE
     wr = torch.randn((R, D), generator=g, device=dev) * 0.02   # router init scale: logits of order 1
     comb = torch.empty((M, NP * NE), dtype=torch.float32, device=dev)
+    copies = 3
+    xo = torch.empty((copies, M, D), dtype=torch.bfloat16, device=dev)
     _lib.check(_lib.lib().vnx_mod_route_x(P(h.data_ptr()), D, P(wr.data_ptr()), D, M, D, NP, NE, topk,
-                                          P(comb.data_ptr()), NP * NE, _st()), "mod_route_x")
+                                          P(comb.data_ptr()), NP * NE, P(xo.data_ptr()), D, M * D, copies, _st()),
+               "mod_route_x")
     torch.cuda.synchronize()
+    assert torch.equal(xo.cpu(), h.to(torch.bfloat16).cpu().unsqueeze(0).expand(copies, M, D))
     lg = (h.double().cpu() @ wr.double().cpu().t())                       # (M, R)
     pw = torch.softmax(lg[:, :NP], dim=-1)
     ref = torch.zeros((M, NP * NE), dtype=torch.float64)

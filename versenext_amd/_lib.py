@@ -111,7 +111,8 @@ SIGNATURES.update({
     "vnx_pack_bf16": (_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
     "vnx_gemm_bf16": (_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _int, _int, _vp,
                              _c_i64, _vp, _int, _c_i64, _c_i64, _vp]),
-    "vnx_mod_route_x": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64, _vp]),
+    "vnx_mod_route_x": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64, _vp,
+                               _c_i64, _c_i64, _int, _vp]),
     "vnx_mod_route": (_int, [_vp, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64, _vp]),
     "vnx_mod_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _int, _c_i64, _vp, _int, _c_i64,
                               _c_i64, _vp]),

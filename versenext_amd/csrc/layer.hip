@@ -349,7 +349,8 @@ __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t l
 constexpr int kRouteMaxR = 32;
 
 __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw,
-                                                     int64_t D, int P, int E, int topk, float* comb, int64_t ldc) {
+                                                     int64_t D, int P, int E, int topk, float* comb, int64_t ldc,
+                                                     __hip_bfloat16* xo, int64_t ldxo, int64_t sxo, int copies) {
   __shared__ float red[4][kRouteMaxR];
   __shared__ float lg[kRouteMaxR];
   const int64_t m = blockIdx.x;
@@ -362,6 +363,10 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
     // every row's load issued unconditionally (rows past R re-read row R-1
     // and are not accumulated): no branches between the loads
     const float x = h[m * ldh + c];
+    if (xo) {  // the experts' bf16 input rows, one copy per expert batch
+      __hip_bfloat16* dst = xo + m * ldxo + c;
+      for (int q = 0; q < copies; ++q) Elt<__hip_bfloat16>::st(dst + q * sxo, x);
+    }
     float wv[kRouteMaxR];
 #pragma unroll
     for (int r = 0; r < kRouteMaxR; ++r) wv[r] = wr[(int64_t)(r < R ? r : R - 1) * ldw + c];
@@ -582,14 +587,17 @@ int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int 
 }
 
 int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, int64_t M, int64_t D, int P, int E,
-                    int topk, float* comb, int64_t ldc, void* stream) {
+                    int topk, float* comb, int64_t ldc, void* x_out, int64_t ldxo, int64_t sxo, int copies,
+                    void* stream) {
   if (!h || !wr || !comb || M < 0 || D < 1 || P < 1 || E < 1 || topk < 1 || topk > E) return VNX_ERR_INVALID_ARG;
+  if (x_out && (ldxo < D || copies < 1 || (copies > 1 && sxo < M * ldxo))) return VNX_ERR_INVALID_ARG;
   if (P > kModMaxP || E > kModMaxE || P + P * E > kRouteMaxR) return VNX_ERR_UNSUPPORTED;
   if (ldh < D || ldw < D || ldc < (int64_t)P * E) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
   if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(k_mod_route_x, dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h, ldh, wr,
-                     ldw, D, P, E, topk, comb, ldc);
+                     ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo, sxo,
+                     x_out ? copies : 0);
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }

@@ -499,14 +499,18 @@ class CometSparkGPU:
         L_ = self.hip._L
         comb = torch.empty((M, PE), dtype=torch.float32, device=self.dev)
         wr = L.ffn["route"]                                                        # (P + PE, D) fp32
-        if P + PE <= 32:      # router products and routing rule in one launch
+        if P + PE <= 32 and self.dtype == torch.bfloat16:
+            # router products and routing rule in one launch, which also
+            # writes the experts' bf16 input rows (one copy per expert)
+            xb = torch.empty((PE, M, D), dtype=self.dtype, device=self.dev)
             _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), P_(wr.data_ptr()), wr.stride(0), M, D, P, E,
-                                          k, P_(comb.data_ptr()), PE, self._st()), "mod_route_x")
+                                          k, P_(comb.data_ptr()), PE, P_(xb.data_ptr()), D, M * D, PE, self._st()),
+                       "mod_route_x")
         else:
             logits = torch.nn.functional.linear(h, wr)                             # (M, P + PE) fp32
             _lib.check(L_.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k, P_(comb.data_ptr()),
                                         PE, self._st()), "mod_route")
-        xb = h.to(self.dtype).unsqueeze(0).expand(PE, M, D).contiguous()
+            xb = h.to(self.dtype).unsqueeze(0).expand(PE, M, D).contiguous()
         gu = torch.matmul(xb, L.ffn["w1"])                                        # (PE, M, 2He)
         act = torch.empty((PE, M, He), dtype=self.dtype, device=self.dev)
         _lib.check(L_.vnx_mod_swiglu(P_(gu.data_ptr()), _lib.DTYPE_CODES[gu.dtype], 2 * He, M * 2 * He,
