@@ -428,6 +428,19 @@ int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, int64_t sxg, const fl
  * of the experts' (weighted) down projections (MoDLayer.forward, mod.py:779-803). */
 int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, float* out, void* stream);
 
+/* Commit of one speculative round for all B sequences (the accept-and-advance
+ * step of SpeculativeDecoder.verify_then_commit, packages/verse_nex/
+ * verse_nex/speculative.py:277-310, with per-sequence KV lengths as in
+ * ParallelKVCache.batch_update, kv_cache_parallel.py:42-286): with n_b =
+ * clamp(accept_len[b], 0, k), ids[b*ld_ids + 0 .. n_b] (accepted drafts and
+ * the drawn / bonus token) are appended to out[b*ld_out + count[b] ...]
+ * (positions >= n_cap dropped), count[b], lens_t[b] and lens_d[b] advance by
+ * n_b + 1, c[b] = ids[b*ld_ids + n_b], and info = {min count, max lens_t,
+ * max lens_d, sum n_b} (int64).  B <= 1024; one launch. */
+int vnx_spec_commit(const int32_t* accept_len, const int64_t* out_ids, int64_t ld_ids, int B, int k, int64_t* out,
+                    int64_t ld_out, int64_t n_cap, int64_t* count, int64_t* c, int32_t* lens_t, int32_t* lens_d,
+                    int64_t* info, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Skinny bf16 GEMM of the verify forward: for batch z < batch,
  *   acc[m, n] = sum_k x[z*sxb + m*ldx + k] * W_z[n, k]   (fp32 accumulation)

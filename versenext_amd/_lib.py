@@ -107,6 +107,7 @@ SIGNATURES.update({
                                  _vp, _int, _c_i64, _vp]),
     "vnx_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
     "vnx_axpby": (_int, [_vp, _vp, _vp, _c_i64, _vp, _int, _vp]),
+    "vnx_spec_commit": (_int, [_vp, _vp, _c_i64, _int, _int, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vnx_pack_bf16_size": (_c_sz, [_c_i64, _c_i64]),
     "vnx_pack_bf16": (_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
     "vnx_gemm_bf16": (_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _int, _int, _vp,

@@ -564,6 +564,68 @@ static size_t spec_ws_bytes(int64_t B, int k, int64_t V) {
   return a > b ? a : b;
 }
 
+// Commit of one speculative round for every sequence (one workgroup, one
+// thread per sequence): the accepted drafts and the drawn / bonus token
+// ids[b, 0 .. n_b] go to out[b, count_b ...] (positions at or past n_cap are
+// dropped), count, lens_t and lens_d advance by n_b + 1 (the rejected suffix
+// of both caches is rolled back by not advancing), c[b] = ids[b, n_b], and
+// info = (min count, max lens_t, max lens_d, sum n_b) for the host's loop.
+constexpr int kCommitMaxB = 1024;
+
+__global__ __launch_bounds__(kCommitMaxB) void k_spec_commit(const int32_t* alen, const int64_t* ids, int64_t ldi,
+                                                             int B, int k, int64_t* out, int64_t ldo, int64_t n_cap,
+                                                             int64_t* count, int64_t* c, int32_t* lens_t,
+                                                             int32_t* lens_d, int64_t* info) {
+  __shared__ int64_t red[4][kCommitMaxB / VNX_WAVE];
+  const int b = threadIdx.x;
+  int64_t cnt = INT64_MAX, lt = INT64_MIN, ld_ = INT64_MIN, acc = 0;
+  if (b < B) {
+    const int n = min(max(alen[b], 0), k);  // accepted drafts
+    const int64_t c0 = count[b];
+    for (int j = 0; j <= n; ++j) {
+      const int64_t pos = c0 + j;
+      if (pos < n_cap) out[b * ldo + pos] = ids[b * ldi + j];
+    }
+    cnt = c0 + n + 1;
+    count[b] = cnt;
+    c[b] = ids[b * ldi + n];
+    lt = lens_t[b] + n + 1;
+    ld_ = lens_d[b] + n + 1;
+    lens_t[b] = (int32_t)lt;
+    lens_d[b] = (int32_t)ld_;
+    acc = n;
+  }
+  // workgroup min / max / max / sum (fixed order)
+  for (int o = 32; o > 0; o >>= 1) {
+    cnt = min(cnt, (int64_t)__shfl_xor(cnt, o));
+    lt = max(lt, (int64_t)__shfl_xor(lt, o));
+    ld_ = max(ld_, (int64_t)__shfl_xor(ld_, o));
+    acc += (int64_t)__shfl_xor(acc, o);
+  }
+  const int w = b / VNX_WAVE;
+  if ((b % VNX_WAVE) == 0) {
+    red[0][w] = cnt;
+    red[1][w] = lt;
+    red[2][w] = ld_;
+    red[3][w] = acc;
+  }
+  __syncthreads();
+  if (b == 0) {
+    const int nw = (int)((blockDim.x + VNX_WAVE - 1) / VNX_WAVE);
+    int64_t r0 = red[0][0], r1 = red[1][0], r2 = red[2][0], r3 = red[3][0];
+    for (int i = 1; i < nw; ++i) {
+      r0 = min(r0, red[0][i]);
+      r1 = max(r1, red[1][i]);
+      r2 = max(r2, red[2][i]);
+      r3 += red[3][i];
+    }
+    info[0] = r0;
+    info[1] = r1;
+    info[2] = r2;
+    info[3] = r3;
+  }
+}
+
 }  // namespace vnx
 
 using namespace vnx;
@@ -665,6 +727,20 @@ int vnx_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, 
   int32_t* alen = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + head);
   return spec_run(logits, logits, dtype, B, 0, V, ld, ld, ld, ld, nullptr, uniforms, temperature, thresholds,
                   nullptr, alen, out_ids, flags, lse, nullptr, workspace, head, stream);
+}
+
+int vnx_spec_commit(const int32_t* accept_len, const int64_t* out_ids, int64_t ld_ids, int B, int k, int64_t* out,
+                    int64_t ld_out, int64_t n_cap, int64_t* count, int64_t* c, int32_t* lens_t, int32_t* lens_d,
+                    int64_t* info, void* stream) {
+  if (!accept_len || !out_ids || !out || !count || !c || !lens_t || !lens_d || !info) return VNX_ERR_INVALID_ARG;
+  if (B < 0 || k < 0 || ld_ids < k + 1 || n_cap < 0 || ld_out < n_cap) return VNX_ERR_INVALID_ARG;
+  if (B > kCommitMaxB) return VNX_ERR_UNSUPPORTED;
+  if (B == 0) return VNX_OK;
+  const unsigned threads = (unsigned)((B + VNX_WAVE - 1) / VNX_WAVE * VNX_WAVE);
+  hipLaunchKernelGGL(k_spec_commit, dim3(1), dim3(threads), 0, static_cast<hipStream_t>(stream), accept_len,
+                     out_ids, ld_ids, B, k, out, ld_out, n_cap, count, c, lens_t, lens_d, info);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
 }
 
 }  // extern "C"

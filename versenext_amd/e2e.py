@@ -23,12 +23,14 @@ target's greedy stream.
 """
 from __future__ import annotations
 
+import ctypes
 import time
 from dataclasses import dataclass, field
 from typing import Optional
 
 import torch
 
+from . import _lib
 from .model import CometSparkGPU
 
 
@@ -82,13 +84,13 @@ class SpecDecodeEngine:
         self.qbuf = torch.empty((B, k, self.V), dtype=torch.float32, device=dev)
         self.u_draft = torch.zeros((k, B), dtype=torch.float32, device=dev)
         self.u_acc = torch.zeros((B, k + 1), dtype=torch.float32, device=dev)
-        self.xs = torch.zeros((B, k), dtype=torch.int64, device=dev)
+        self.xsT = torch.zeros((k, B), dtype=torch.int64, device=dev)   # draft token i of every row: xsT[i]
+        self.toks = torch.zeros((B, k + 1), dtype=torch.int64, device=dev)  # [c, x_1 .. x_k] per row
         self.c = torch.zeros(B, dtype=torch.int64, device=dev)
         self.lens_t = torch.zeros(B, dtype=torch.int32, device=dev)
         self.lens_d = torch.zeros(B, dtype=torch.int32, device=dev)
         self.count = torch.zeros(B, dtype=torch.int64, device=dev)
         self.info = torch.zeros(4, dtype=torch.int64, device=dev)
-        self.ar = torch.arange(k + 1, device=dev).view(1, k + 1)
         self.steps_i32 = torch.arange(k + 1, dtype=torch.int32, device=dev).view(k + 1, 1)
         self.out = None
         self.n_new = 0
@@ -114,31 +116,29 @@ class SpecDecodeEngine:
                 break
             self.d.logits(h, out=self.qbuf[:, i:i + 1])
             if self.greedy:
-                tok = self.hip.argmax(self.qbuf[:, i]).view(B)
+                self.xsT[i].copy_(self.hip.argmax(self.qbuf[:, i]).view(B))
             else:
-                tok = self.hip.sample(self.qbuf[:, i], self.u_draft[i], temperature=self.T)
-            self.xs[:, i] = tok
-        toks = torch.cat([self.c.view(B, 1), self.xs], dim=1)
-        h = self.t.forward(toks, self.lens_t, Tmax_t, out_dtype=self.t.act_dtype)
+                self.hip.sample(self.qbuf[:, i], self.u_draft[i], temperature=self.T, out=self.xsT[i])
+            tok = self.xsT[i]
+        torch.cat([self.c.view(B, 1), self.xsT.t()], dim=1, out=self.toks)
+        xs = self.toks[:, 1:]
+        h = self.t.forward(self.toks, self.lens_t, Tmax_t, out_dtype=self.t.act_dtype)
         self.t.logits(h, out=self.pbuf)
         if self.greedy:
-            _, _, alen, ids = self.hip.greedy_verify(self.pbuf, self.xs, rows_t=k + 1)
+            _, _, alen, ids = self.hip.greedy_verify(self.pbuf, xs, rows_t=k + 1)
         else:
-            res = self.hip.spec_accept(self.pbuf, self.qbuf, self.xs, self.u_acc, temperature=self.T)
+            res = self.hip.spec_accept(self.pbuf, self.qbuf, xs, self.u_acc, temperature=self.T)
             alen, ids = res["accept_len"], res["out_ids"]
-        # commit: ids[b, :n1] go to out[b, count_b ...]; other slots write the
-        # trash column (no data-dependent shapes, so the round can be captured)
-        n1 = alen.long() + 1
-        trash = self.out.shape[1] - 1
-        pos = self.count.view(B, 1) + self.ar
-        ok = (self.ar < n1.view(B, 1)) & (pos < trash)
-        self.out.scatter_(1, torch.where(ok, pos, torch.full_like(pos, trash)), ids)
-        self.count += n1
-        self.c.copy_(ids.gather(1, alen.long().view(B, 1)).view(B))
-        self.lens_t += n1.int()
-        self.lens_d += n1.int()
-        self.info.copy_(torch.stack([self.count.min(), self.lens_t.max().long(), self.lens_d.max().long(),
-                                     alen.long().sum()]))
+        # commit (one launch, no data-dependent shapes, so the round can be
+        # captured): ids[b, :n_b + 1] appended to out[b, count_b ...], counts,
+        # cache lengths and the next round's first token advanced, and the
+        # host's loop summary in info
+        P = ctypes.c_void_p
+        _lib.check(self.hip._L.vnx_spec_commit(
+            P(alen.data_ptr()), P(ids.data_ptr()), ids.stride(0), B, k, P(self.out.data_ptr()), self.out.stride(0),
+            self.out.shape[1] - 1, P(self.count.data_ptr()), P(self.c.data_ptr()), P(self.lens_t.data_ptr()),
+            P(self.lens_d.data_ptr()), P(self.info.data_ptr()),
+            ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)), "spec_commit")
 
     # ---- driver ---------------------------------------------------------
     @torch.no_grad()
