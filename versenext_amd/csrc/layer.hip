@@ -348,6 +348,7 @@ __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t l
 // order) and routes them.
 constexpr int kRouteMaxR = 32;
 
+template <int VW>
 __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw,
                                                      int64_t D, int P, int E, int topk, float* comb, int64_t ldc,
                                                      __hip_bfloat16* xo, int64_t ldxo, int64_t sxo, int copies) {
@@ -359,19 +360,34 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
   float acc[kRouteMaxR];
 #pragma unroll
   for (int r = 0; r < kRouteMaxR; ++r) acc[r] = 0.0f;
-  for (int64_t c = tid; c < D; c += 256) {
+  // thread tid takes columns tid*VW .. +VW of every 256*VW block
+  for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
     // every row's load issued unconditionally (rows past R re-read row R-1
     // and are not accumulated): no branches between the loads
-    const float x = h[m * ldh + c];
+    float x[VW];
+    if constexpr (VW == 4) {
+      ld4(h + m * ldh + c, x);
+    } else {
+      x[0] = h[m * ldh + c];
+    }
     if (xo) {  // the experts' bf16 input rows, one copy per expert batch
       __hip_bfloat16* dst = xo + m * ldxo + c;
-      for (int q = 0; q < copies; ++q) Elt<__hip_bfloat16>::st(dst + q * sxo, x);
+      for (int q = 0; q < copies; ++q) {
+        if constexpr (VW == 4) st4(dst + q * sxo, x);
+        else Elt<__hip_bfloat16>::st(dst + q * sxo, x[0]);
+      }
     }
-    float wv[kRouteMaxR];
+    float wv[kRouteMaxR][VW];
 #pragma unroll
-    for (int r = 0; r < kRouteMaxR; ++r) wv[r] = wr[(int64_t)(r < R ? r : R - 1) * ldw + c];
+    for (int r = 0; r < kRouteMaxR; ++r) {
+      const float* wrow = wr + (int64_t)(r < R ? r : R - 1) * ldw + c;
+      if constexpr (VW == 4) ld4(wrow, wv[r]);
+      else wv[r][0] = wrow[0];
+    }
 #pragma unroll
-    for (int r = 0; r < kRouteMaxR; ++r) acc[r] = __builtin_fmaf(x, r < R ? wv[r] : 0.0f, acc[r]);
+    for (int r = 0; r < kRouteMaxR; ++r)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) acc[r] = __builtin_fmaf(x[e], r < R ? wv[r][e] : 0.0f, acc[r]);
   }
 #pragma unroll
   for (int r = 0; r < kRouteMaxR; ++r) {
@@ -595,9 +611,16 @@ int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, i
   if (ldh < D || ldw < D || ldc < (int64_t)P * E) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
   if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(k_mod_route_x, dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h, ldh, wr,
-                     ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo, sxo,
-                     x_out ? copies : 0);
+  const bool v4 = D % 4 == 0 && ldh % 4 == 0 && ldw % 4 == 0 && vec4_ok(h, 4) && vec4_ok(wr, 4) &&
+                  (!x_out || (ldxo % 4 == 0 && sxo % 4 == 0 && vec4_ok(x_out, 2)));
+  if (v4)
+    hipLaunchKernelGGL((k_mod_route_x<4>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h,
+                       ldh, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo, sxo,
+                       x_out ? copies : 0);
+  else
+    hipLaunchKernelGGL((k_mod_route_x<1>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h,
+                       ldh, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo, sxo,
+                       x_out ? copies : 0);
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }
