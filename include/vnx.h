@@ -428,6 +428,14 @@ int vnx_mod_swiglu(const void* gu, int dtype, int64_t ldg, int64_t sxg, const fl
  * of the experts' (weighted) down projections (MoDLayer.forward, mod.py:779-803). */
 int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, float* out, void* stream);
 
+/* out[m*ldo + c] (fp32) = the sum, over experts z < E in ascending order
+ * with slots[m*E + z] >= 0, of y[z*syb + slots[m*E + z]*ldy + c], c < D: the
+ * expert sum of MoDLayer.forward (mod.py:779-803) over compact per-expert
+ * outputs (vnx_expert_gemm_bf16's row lists).  Equal to vnx_sum_experts of
+ * the dense outputs, whose unrouted rows are zero. */
+int vnx_sum_expert_rows(const void* y, int dtype, int64_t ldy, int64_t syb, const int32_t* slots, int64_t M,
+                        int E, int64_t D, float* out, int64_t ldo, void* stream);
+
 /* Commit of one speculative round for all B sequences (the accept-and-advance
  * step of SpeculativeDecoder.verify_then_commit, packages/verse_nex/
  * verse_nex/speculative.py:277-310, with per-sequence KV lengths as in
@@ -472,6 +480,27 @@ int vnx_pack_bf16(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, v
 int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
                   int64_t N, int64_t K, int batch, int epilogue, const float* comb, int64_t ldc, void* y,
                   int y_dtype, int64_t ldy, int64_t syb, void* stream);
+
+/* Routed MoD expert products (the expert FFNs of DensePart / Expert,
+ * packages/verse_nex/verse_nex/mod.py:466-600, evaluated only on the rows
+ * routed to each expert).  For expert z < experts, with its row list
+ * L_z = (l_0 < l_1 < ...) of n_z rows:
+ *   acc[j, n] = sum_k X_z[j, k] * W_z[n, k]  (fp32), j < n_z,
+ * written to y + z*syb + j*ldy (compact order) with the epilogue of
+ * vnx_gemm_bf16 (VNX_EPI_SWIGLU weights row j by comb[l_j*ldc + z]).
+ * route != 0: L_z = { m < M : comb[m*ldc + z] != 0 } (M <= 256; with
+ *   VNX_EPI_NONE comb only selects the rows), X_z[j] =
+ *   x[l_j] (x shared, sxb = 0); the call also writes rows[z*M + j] = l_j,
+ *   counts[z] = n_z and slots[m*experts + z] = j for m = l_j, else -1.
+ * route == 0: X_z[j] = x[z*sxb + j*ldx], n_z = counts[z] (counts NULL: M),
+ *   rows / slots unused.
+ * W_z packed by vnx_pack_bf16 at w_packed + z*swb elements; K multiple of
+ * 64.  Each element's summation order depends on the shapes only, not on
+ * the row lists (deterministic). */
+int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
+                         int64_t N, int64_t K, int experts, int epilogue, const float* comb, int64_t ldc, int route,
+                         int32_t* rows, int32_t* counts, int32_t* slots, void* y, int y_dtype, int64_t ldy,
+                         int64_t syb, void* stream);
 
 #ifdef __cplusplus
 }

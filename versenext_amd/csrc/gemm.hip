@@ -192,6 +192,232 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Routed MoD expert products (vnx_expert_gemm_bf16).  Expert z multiplies only
+// the rows routed to it (about top_k / E of them), and every expert's weight
+// should stream from HBM once, so a workgroup owns WN adjacent 32-row tiles
+// of W_z and a pass of up to 128 of the expert's rows (four MFMA row tiles
+// per wave, the W operand reused across them from registers): at the usual
+// <= 128 rows per expert one workgroup covers them all, and the workgroups of
+// further passes (grid.y) exit at once.  Its 4 waves are WN (N tiles) x WK
+// (K splits), as in k_vgemm.  X (128 rows x WK chunks per step) is staged
+// through LDS like k_vgemm's, the rows gathered through the row list.
+//
+// ROUTE: the row list of expert z is { m : comb[m*ldc + z] != 0 }, ascending;
+// each workgroup builds it in LDS from comb (M <= 256: one ballot per wave),
+// and the workgroup of N group 0, pass 0 publishes it (rows, counts, slots) for the
+// products and the sum that follow.  Otherwise the expert's rows are the
+// first counts[z] (all M when counts is NULL) rows of x + z*sxb.
+// Output row j of expert z: y + z*syb + j*ldy (the compact order).
+struct XgParams {
+  const uint16_t* x;
+  const uint16_t* w;       // packed; expert z at w + z*swb
+  void* y;
+  const float* comb;
+  int32_t* rows;           // (E, M): expert z's row list at rows[z*M ..]
+  int32_t* counts;         // (E)
+  int32_t* slots;          // (M, E): slot of row m in expert z's list, or -1
+  int64_t ldx, sxb, swb, ldy, syb, ldc;
+  int M, N, K, E;
+  int nt, ng;
+};
+
+constexpr int kXgRows = 128;  // rows per pass
+
+template <int OT, int EPI, int WN, bool ROUTE>
+__global__ __launch_bounds__(256) void k_xgemm(XgParams p) {
+  constexpr int WK = 4 / WN;
+  constexpr int SLAB = WK * kXgRows * kVgRowB;       // staged X bytes per step
+  constexpr int RED = (WK - 1) * WN * 4 * 64 * 64;   // K-split partial tiles
+  constexpr int SM = 2 * SLAB > RED ? 2 * SLAB : RED;
+  __shared__ __attribute__((aligned(16))) char smem[SM];
+  __shared__ int rl[256];
+  __shared__ float cwl[kXgRows];  // SwiGLU weights of the pass's rows
+  __shared__ unsigned long long wmask[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave % WN, wk = wave / WN;
+  // expert-major order: consecutive workgroups (dealt round-robin over the
+  // XCDs) are N groups of one expert, so every XCD gets an even share of the
+  // work however unevenly the rows are routed (giving each XCD whole experts
+  // measured up to 1.6x slower under skewed routing)
+  const int z = blockIdx.x / p.ng;
+  const int gi = blockIdx.x % p.ng;
+
+  int cnt;
+  if constexpr (ROUTE) {
+    const bool sel = tid < p.M && p.comb[(int64_t)tid * p.ldc + z] != 0.0f;
+    const unsigned long long b = __ballot(sel);
+    if (lane == 0) wmask[wave] = b;
+    __syncthreads();
+    int before = 0;
+    cnt = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int c = __popcll(wmask[w]);
+      before += w < wave ? c : 0;
+      cnt += c;
+    }
+    const int pos = before + __popcll(b & ((1ull << lane) - 1ull));
+    if (sel) rl[pos] = tid;
+    if (gi == 0 && blockIdx.y == 0) {
+      if (tid < p.M) p.slots[(int64_t)tid * p.E + z] = sel ? pos : -1;
+      if (sel) p.rows[(int64_t)z * p.M + pos] = tid;
+      if (tid == 0) p.counts[z] = cnt;
+    }
+    __syncthreads();
+  } else {
+    cnt = p.counts ? min(p.counts[z], p.M) : p.M;
+  }
+
+  const int ni = gi * WN + wn;             // this wave's N tile (past nt: computes, never stores)
+  const int nie = ni < p.nt ? ni : p.nt - 1;
+  const int r = lane & 31, h = lane >> 5;
+  const int nch = p.K / kVgChunk;
+  const int nstep = (nch + WK - 1) / WK;
+  const int xr = tid >> 3, xc = tid & 7;   // staging: rows xr + 32q, 16-byte column xc
+  const uint16_t* wt = p.w + z * p.swb + (int64_t)nie * nch * 2048 + lane * 8;
+  char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
+
+  // passes of 128 rows are dealt over grid.y, so an expert with more rows
+  // than one pass adds workgroups, not time to its workgroups' critical path
+  for (int m0 = blockIdx.y * kXgRows; m0 < cnt; m0 += gridDim.y * kXgRows) {
+    const int live = min(4, (cnt - m0 + 31) / 32);  // row tiles of this pass
+    const uint16_t* xrow[4];
+    uint32_t keep[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = m0 + xr + 32 * q;
+      const int jc = min(j, cnt - 1);
+      if constexpr (ROUTE) xrow[q] = p.x + (int64_t)rl[jc] * p.ldx + xc * 8;
+      else xrow[q] = p.x + z * p.sxb + (int64_t)jc * p.ldx + xc * 8;
+      keep[q] = j < cnt ? 0xFFFFFFFFu : 0u;
+    }
+    if (EPI == 1 && tid < kXgRows) {
+      // read before the epilogue: the K loop's barriers order it
+      const int j = m0 + tid;
+      cwl[tid] = p.comb && j < cnt ? p.comb[(int64_t)(ROUTE ? rl[j] : j) * p.ldc + z] : 1.0f;
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+
+    // The W loads run PDW steps ahead of the math (step st in W slot
+    // st % PDW), the X loads PDX steps (X slot st % PDX): W streams from HBM
+    // and needs the deeper ring, X is re-read from L2.  The X registers are
+    // free once staged, so the X loads of step st + PDX issue right after
+    // the barrier; a W slot is reloaded only after this step's MFMAs have
+    // read it (no register rotation, so nothing in flight has to be waited
+    // for at the loop edge).
+    // Both shapes keep two workgroups per CU (<= 256 registers a lane), so
+    // the workgroups of a second row pass run beside the first ones rather
+    // than after them; one workgroup per CU with deeper rings measured slower.
+    constexpr int PDW = WN == 4 ? 3 : 4, PDX = WN == 4 ? 3 : 2;
+    constexpr int UN = PDW > PDX ? PDW : PDX;  // loop unroll: a multiple of both
+    static_assert(UN % PDW == 0 && UN % PDX == 0, "ring depths must divide the unroll");
+    u32x4 xv[PDX][WK][4], wv[PDW][4];
+    auto load_x = [&](int st, u32x4 (&xs)[WK][4]) {
+#pragma unroll
+      for (int j = 0; j < WK; ++j) {
+        const int c = min(st * WK + j, nch - 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xs[j][q] = *reinterpret_cast<const u32x4*>(xrow[q] + c * kVgChunk);
+      }
+    };
+    auto load_w = [&](int st, u32x4 (&ws)[4]) {
+      const int c = min(st * WK + wk, nch - 1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ws[s] = *reinterpret_cast<const u32x4*>(wt + (c * 4 + s) * 512);
+    };
+#pragma unroll
+    for (int j = 0; j < PDW; ++j) load_w(j, wv[j]);
+#pragma unroll
+    for (int j = 0; j < PDX; ++j) load_x(j, xv[j]);
+    for (int st0 = 0; st0 < nstep; st0 += UN) {
+#pragma unroll
+      for (int j = 0; j < UN; ++j) {
+        const int st = st0 + j;
+        char* buf = smem + (st & 1) * SLAB;
+#pragma unroll
+        for (int c = 0; c < WK; ++c)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<u32x4*>(buf + c * kXgRows * kVgRowB + xs_off(xr + 32 * q, xc)) =
+                xv[j % PDX][c][q] & keep[q];
+        __syncthreads();  // step st's X is staged; the other buffer was read before it
+        load_x(st + PDX, xv[j % PDX]);  // past the end: clamped re-reads, never used
+        if (st * WK + wk < nch) {  // uniform per wave
+          const char* xb = buf + wk * kXgRows * kVgRowB;
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              // all four row tiles (rows past the count are zero and not stored)
+              const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s));
+              acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(st + PDW, wv[j % PDW]);
+      }
+    }
+    __syncthreads();  // the X buffers are dead
+    if constexpr (WK > 1) {
+      // K splits 1.. -> LDS; split 0 adds them in split order
+      f32x16* red = reinterpret_cast<f32x16*>(smem);
+      if (wk > 0)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i < live) red[(((wk - 1) * WN + wn) * 4 + i) * 64 + lane] = acc[i];
+      __syncthreads();
+      if (wk == 0)
+#pragma unroll
+        for (int k = 1; k < WK; ++k)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (i < live) acc[i] += red[(((k - 1) * WN + wn) * 4 + i) * 64 + lane];
+    }
+    if (wk == 0 && ni < p.nt) {
+      // lane holds D[row 8ii + 4h + e][col r] of row tile i in acc[i][4ii + e]
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i >= live) continue;
+        if constexpr (EPI == 0) {
+          const int n = ni * 32 + r;
+          if (n < p.N)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int j = m0 + i * 32 + 8 * ii + 4 * h + e;
+                if (j < cnt) vg_store<OT>(ybase, (int64_t)j * p.ldy + n, acc[i][4 * ii + e]);
+              }
+        } else {
+          float up[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) up[e] = __shfl_xor(acc[i][e], 16);
+          if (r < 16) {
+            const int col = ni * 16 + r;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int j = m0 + i * 32 + 8 * ii + 4 * h + e;
+                if (j >= cnt) continue;
+                const float g = acc[i][4 * ii + e];
+                float v = g / (1.0f + __expf(-g)) * up[4 * ii + e];
+                if (p.comb) v *= cwl[j - m0];
+                vg_store<OT>(ybase, (int64_t)j * p.ldy + col, v);
+              }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the reduction tiles are read before the next pass stages X
+  }
+}
+
 // Packing: one thread per 16 bytes of the packed layout (rows past N zero).
 __global__ __launch_bounds__(256) void k_vpack(const uint16_t* w, int64_t ldw, int N, int K, uint16_t* out,
                                                int64_t total16) {
@@ -289,6 +515,66 @@ int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed,
   if (y_dtype == VNX_F32) go(IntC<0>{});
   else if (y_dtype == VNX_BF16) go(IntC<1>{});
   else go(IntC<2>{});
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
+                         int64_t N, int64_t K, int experts, int epilogue, const float* comb, int64_t ldc, int route,
+                         int32_t* rows, int32_t* counts, int32_t* slots, void* y, int y_dtype, int64_t ldy,
+                         int64_t syb, void* stream) {
+  if (!x || !w_packed || !y || M < 0 || N < 0 || K <= 0 || experts < 0) return VNX_ERR_INVALID_ARG;
+  if (epilogue != VNX_EPI_NONE && epilogue != VNX_EPI_SWIGLU) return VNX_ERR_INVALID_ARG;
+  if (y_dtype != VNX_F32 && y_dtype != VNX_BF16 && y_dtype != VNX_F16) return VNX_ERR_UNSUPPORTED;
+  const int64_t ncols = epilogue == VNX_EPI_SWIGLU ? N / 2 : N;
+  if (ldx < K || ldy < ncols || sxb < 0 || swb < 0 || syb < 0) return VNX_ERR_INVALID_ARG;
+  if (experts > 1 && swb < (N + 31) / 32 * 32 * K) return VNX_ERR_INVALID_ARG;
+  if (epilogue == VNX_EPI_SWIGLU && N % 32) return VNX_ERR_INVALID_ARG;
+  if (comb && ((epilogue != VNX_EPI_SWIGLU && !route) || ldc < experts)) return VNX_ERR_INVALID_ARG;
+  if (route) {
+    // rows from the routing weights: comb, the three lists and a shared x
+    if (!comb || !rows || !counts || !slots || sxb != 0) return VNX_ERR_INVALID_ARG;
+    if (M > 256) return VNX_ERR_UNSUPPORTED;
+  }
+  if (M == 0 || N == 0 || experts == 0) return VNX_OK;
+  if (K % kVgChunk || ldx % 8 || sxb % 8 || swb % 8 || !aligned16(x) || !aligned16(w_packed))
+    return VNX_ERR_UNSUPPORTED;
+  if (M >= INT32_MAX || N >= INT32_MAX || K >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  XgParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.w = static_cast<const uint16_t*>(w_packed); p.y = y; p.comb = comb;
+  p.rows = rows; p.counts = counts; p.slots = slots;
+  p.ldx = ldx; p.sxb = sxb; p.swb = swb; p.ldy = ldy; p.syb = syb; p.ldc = ldc;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.E = experts;
+  p.nt = (int)((N + 31) / 32);
+  // 4 N tiles per workgroup unless that leaves the CUs short of workgroups;
+  // then 2 N tiles and K split over 2 waves each
+  const int64_t cus = device_cus();
+  const int wn = (int64_t)((p.nt + 3) / 4) * experts >= cus ? 4 : 2;
+  p.ng = (p.nt + wn - 1) / wn;
+  const int64_t wgs = (int64_t)experts * p.ng;
+  const int64_t passes = (M + kXgRows - 1) / kXgRows;
+  if (wgs >= INT32_MAX || passes > 65535) return VNX_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)wgs, (unsigned)passes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool sw = epilogue == VNX_EPI_SWIGLU;
+  auto go = [&](auto ot, auto rt) {
+    constexpr int OT = decltype(ot)::value;
+    constexpr bool RT = decltype(rt)::value != 0;
+    if (sw) {
+      if (wn == 4) hipLaunchKernelGGL((k_xgemm<OT, 1, 4, RT>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((k_xgemm<OT, 1, 2, RT>), grid, dim3(256), 0, s, p);
+    } else {
+      if (wn == 4) hipLaunchKernelGGL((k_xgemm<OT, 0, 4, RT>), grid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL((k_xgemm<OT, 0, 2, RT>), grid, dim3(256), 0, s, p);
+    }
+  };
+  auto go_r = [&](auto ot) {
+    if (route) go(ot, IntC<1>{});
+    else go(ot, IntC<0>{});
+  };
+  if (y_dtype == VNX_F32) go_r(IntC<0>{});
+  else if (y_dtype == VNX_BF16) go_r(IntC<1>{});
+  else go_r(IntC<2>{});
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }

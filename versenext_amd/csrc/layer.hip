@@ -465,6 +465,43 @@ __global__ __launch_bounds__(256) void k_sum_experts(const TY* y, int64_t MD, in
   }
 }
 
+// out[m] = the sum, in expert order, of the rows y[z][slots[m*E + z]] of the
+// experts that row m was routed to (slot >= 0): k_sum_experts over the
+// compact per-expert outputs.  Grid (column blocks, rows).
+template <typename TY, int VW>
+__global__ __launch_bounds__(256) void k_sum_expert_rows(const TY* y, int64_t ldy, int64_t syb,
+                                                         const int32_t* slots, int E, int64_t D, float* out,
+                                                         int64_t ldo) {
+  constexpr int ZB = 8;  // experts whose loads are in flight together
+  const int64_t m = blockIdx.y;
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VW;
+  if (c >= D) return;
+  float acc[VW];
+#pragma unroll
+  for (int e = 0; e < VW; ++e) acc[e] = 0.0f;
+  for (int z0 = 0; z0 < E; z0 += ZB) {
+    // every load of the batch issued before any is used: unrouted experts
+    // read row 0 and add +0.0, as their zero rows do in the dense sum
+    int sl[ZB];
+    float v[ZB][VW];
+#pragma unroll
+    for (int q = 0; q < ZB; ++q) sl[q] = z0 + q < E ? slots[m * E + z0 + q] : -1;
+#pragma unroll
+    for (int q = 0; q < ZB; ++q) {
+      const int zq = min(z0 + q, E - 1);
+      const TY* src = y + zq * syb + (int64_t)max(sl[q], 0) * ldy + c;
+      if constexpr (VW == 4) ld4(src, v[q]);
+      else v[q][0] = Elt<TY>::ld(src);
+    }
+#pragma unroll
+    for (int q = 0; q < ZB; ++q)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) acc[e] += sl[q] >= 0 ? v[q][e] : 0.0f;
+  }
+  if constexpr (VW == 4) st4(out + m * ldo + c, acc);
+  else out[m * ldo + c] = acc[0];
+}
+
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -674,6 +711,27 @@ int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, floa
     else
       hipLaunchKernelGGL((k_sum_experts<TY, 1>), dim3(blocks_for(MD)), dim3(256), 0, s, static_cast<const TY*>(y),
                          MD, PE, out);
+    VNX_LAUNCH_CHECK();
+    return (int)VNX_OK;
+  });
+}
+
+int vnx_sum_expert_rows(const void* y, int dtype, int64_t ldy, int64_t syb, const int32_t* slots, int64_t M,
+                        int E, int64_t D, float* out, int64_t ldo, void* stream) {
+  if (!y || !slots || !out || M < 0 || E < 1 || D < 1 || ldy < D || syb < 0 || ldo < D) return VNX_ERR_INVALID_ARG;
+  if (M == 0) return VNX_OK;
+  if (M > 65535) return VNX_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool v4 = D % 4 == 0 && ldy % 4 == 0 && syb % 4 == 0 && ldo % 4 == 0 && vec4_ok(y, dtype_bytes(dtype)) &&
+                  vec4_ok(out, 4);
+  return by_dtype(dtype, [&](auto ty) {
+    using TY = decltype(ty);
+    if (v4)
+      hipLaunchKernelGGL((k_sum_expert_rows<TY, 4>), dim3(blocks_for(D / 4), (unsigned)M), dim3(256), 0, s,
+                         static_cast<const TY*>(y), ldy, syb, slots, E, D, out, ldo);
+    else
+      hipLaunchKernelGGL((k_sum_expert_rows<TY, 1>), dim3(blocks_for(D), (unsigned)M), dim3(256), 0, s,
+                         static_cast<const TY*>(y), ldy, syb, slots, E, D, out, ldo);
     VNX_LAUNCH_CHECK();
     return (int)VNX_OK;
   });

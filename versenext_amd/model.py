@@ -232,6 +232,17 @@ class _Layer:
     ffn: Dict[str, object] = field(default_factory=dict)
 
 
+def _pack(w: torch.Tensor, hip) -> torch.Tensor:
+    """vnx_pack_bf16 of a contiguous (N, K) bf16 weight: the matrix-core
+    operand order read by vnx_gemm_bf16 / vnx_expert_gemm_bf16."""
+    N, K = w.shape
+    L = hip._L
+    out = torch.empty(L.vnx_pack_bf16_size(N, K) // 2, dtype=torch.bfloat16, device=hip.torch_device)
+    _lib.check(L.vnx_pack_bf16(ctypes.c_void_p(w.data_ptr()), K, N, K, ctypes.c_void_p(out.data_ptr()),
+                               ctypes.c_void_p(torch.cuda.current_stream(hip.torch_device).cuda_stream)), "pack_bf16")
+    return out
+
+
 class _Linear:
     """y (M, N) fp32 = x (M, K) . W^T.  Dense weights run F.linear in the
     compute dtype; INT4 group-128 weights (fp16 scales) run vnx_gemv_w4 for
@@ -373,6 +384,14 @@ class CometSparkGPU:
                 # (P*E, D, 2He) gate|up and (P*E, He, D) down
                 L.ffn["w1"] = torch.stack([w.t() for w in w1]).to(dtype).contiguous()
                 L.ffn["w2"] = torch.stack([w.t() for w in w2]).to(dtype).contiguous()
+                if dtype == torch.bfloat16 and D % 64 == 0 and cfg.expert_hidden_eff % 64 == 0:
+                    # packed per-expert copies for the routed products of
+                    # verify-size forwards (vnx_expert_gemm_bf16); gate|up
+                    # rows interleaved in blocks of 16 for the SwiGLU epilogue
+                    He = cfg.expert_hidden_eff
+                    L.ffn["w1p"] = torch.stack([_pack(w.to(dtype).view(2, He // 16, 16, D).transpose(0, 1)
+                                                      .reshape(2 * He, D).contiguous(), hip) for w in w1])
+                    L.ffn["w2p"] = torch.stack([_pack(w.to(dtype).contiguous(), hip) for w in w2])
             self.layers.append(L)
         cos, sin = rope_tables(d, self.cap + 64, cfg.rope_theta)
         self.cos = torch.from_numpy(cos).to(dev)
@@ -486,11 +505,14 @@ class CometSparkGPU:
         return res
 
     def _mod(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
-        """MoD FFN on (M, D) fp32 normalized rows: fp32 routing logits in one
-        product and the routing weights (vnx_mod_route); every expert's
-        gate|up and down as batched products over the P*E experts, with the
-        weighted activations in between (vnx_mod_swiglu; zero for unselected
-        experts) and the sum over experts after (vnx_sum_experts)."""
+        """MoD FFN on (M, D) fp32 normalized rows.  Verify-size forwards (bf16,
+        M <= 256): the routing weights (vnx_mod_route_x), each expert's
+        products on its routed rows only (vnx_expert_gemm_bf16) and the sum
+        over each row's experts (vnx_sum_expert_rows).  Otherwise fp32 routing
+        logits in one product and the routing weights (vnx_mod_route); every
+        expert's gate|up and down as batched products over the P*E experts,
+        with the weighted activations in between (vnx_mod_swiglu; zero for
+        unselected experts) and the sum over experts after (vnx_sum_experts)."""
         cfg = self.cfg
         P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
         PE, He, D = P * E, cfg.expert_hidden_eff, cfg.dim
@@ -499,6 +521,33 @@ class CometSparkGPU:
         L_ = self.hip._L
         comb = torch.empty((M, PE), dtype=torch.float32, device=self.dev)
         wr = L.ffn["route"]                                                        # (P + PE, D) fp32
+        if P + PE <= 32 and "w1p" in L.ffn and M <= 256:
+            # routed products: router + routing rule (one bf16 copy of h),
+            # then each expert's gate|up with the SwiGLU and routing weight
+            # fused and its down product on its own rows only, then the sum
+            # over each row's experts
+            xh = torch.empty((M, D), dtype=torch.bfloat16, device=self.dev)
+            _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), P_(wr.data_ptr()), wr.stride(0), M, D, P, E,
+                                          k, P_(comb.data_ptr()), PE, P_(xh.data_ptr()), D, 0, 1, self._st()),
+                       "mod_route_x")
+            rows = torch.empty((PE, M), dtype=torch.int32, device=self.dev)
+            counts = torch.empty((PE,), dtype=torch.int32, device=self.dev)
+            slots = torch.empty((M, PE), dtype=torch.int32, device=self.dev)
+            w1p, w2p = L.ffn["w1p"], L.ffn["w2p"]
+            act = torch.empty((PE, M, He), dtype=torch.bfloat16, device=self.dev)
+            _lib.check(L_.vnx_expert_gemm_bf16(
+                P_(xh.data_ptr()), D, 0, P_(w1p.data_ptr()), w1p.stride(0), M, 2 * He, D, PE, _lib.VNX_EPI_SWIGLU,
+                P_(comb.data_ptr()), PE, 1, P_(rows.data_ptr()), P_(counts.data_ptr()), P_(slots.data_ptr()),
+                P_(act.data_ptr()), _lib.VNX_BF16, He, M * He, self._st()), "expert_gemm w1")
+            y = torch.empty((PE, M, D), dtype=torch.bfloat16, device=self.dev)
+            _lib.check(L_.vnx_expert_gemm_bf16(
+                P_(act.data_ptr()), He, M * He, P_(w2p.data_ptr()), w2p.stride(0), M, D, He, PE, _lib.VNX_EPI_NONE,
+                None, 0, 0, None, P_(counts.data_ptr()), None, P_(y.data_ptr()), _lib.VNX_BF16, D, M * D,
+                self._st()), "expert_gemm w2")
+            out = torch.empty((M, D), dtype=torch.float32, device=self.dev)
+            _lib.check(L_.vnx_sum_expert_rows(P_(y.data_ptr()), _lib.VNX_BF16, D, M * D, P_(slots.data_ptr()), M, PE,
+                                              D, P_(out.data_ptr()), D, self._st()), "sum_expert_rows")
+            return out
         if P + PE <= 32 and self.dtype == torch.bfloat16:
             # router products and routing rule in one launch, which also
             # writes the experts' bf16 input rows (one copy per expert)
