@@ -202,6 +202,16 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
                 int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
                 float* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
 
+/* vnx_gemv_w4 of a fused [gate; up] weight with SwiGLU fused (SwiGLUMLP,
+ * packages/verse_torch/verse_torch/vnnn.py:779-807, on QuantizedLinear
+ * projections): W (N, K) has its rows interleaved in blocks of 16, the 8 gate
+ * rows of hidden units 8t .. 8t+7 then their 8 up rows (N % 16 == 0,
+ * N < 32768); y (B, N/2) fp16, row pitch ldy, y[b, j] = silu(acc[b, gate_j])
+ * * acc[b, up_j] in fp32, rounded once. */
+int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                       int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, void* y,
+                       int64_t ldy, void* stream);
+
 /* W8: wq (N, K) int8, row pitch ldw; scale (N) fp32 per output row (the
  * per-channel INT8 of quantize_int8, quantize.py:187-214).  Replaces
  * QuantizedLinear.forward for qtype="int8" (quantize.py:467-505). */

@@ -154,3 +154,44 @@ def test_gemv_rejects_bad_shapes(hip):
     x = torch.zeros((2, 100), dtype=torch.float16)
     with pytest.raises(ValueError):
         hip.gemv_w8(x, torch.zeros((8, 100), dtype=torch.int8), torch.ones(8))  # K % 128 != 0
+
+
+@pytest.mark.parametrize("H,K,B", [(4096, 1024, 32), (4096, 1024, 1), (64, 256, 17), (1000, 512, 40)])
+def test_gemv_swiglu_parity(hip, H, K, B):
+    """vnx_gemv_w4_swiglu: the group-128 GEMV of a [gate; up] weight whose rows
+    are interleaved in blocks of 8 gate + 8 up rows, with silu(gate) * up in
+    the epilogue (fp16 out).  Bar: the GEMV bar carried through silu(g) * u
+    (|silu'| <= 1.1) plus one fp16 rounding (and half an fp16 subnormal step)."""
+    import ctypes
+    from versenext_amd import _lib
+    _say(f"gemv swiglu H={H} K={K} B={B}")
+    N = 2 * H
+    p, s = _quantized("int4_g128", N, K, seed=H + K)
+    x16 = np.random.default_rng(B).normal(0, 1, (B, K)).astype(np.float16)
+    perm = np.arange(N).reshape(2, H // 8, 8).transpose(1, 0, 2).reshape(-1)   # packed row -> source row
+    dev = hip.torch_device
+    pq = torch.from_numpy(np.ascontiguousarray(p[perm])).to(dev)
+    sq = torch.from_numpy(np.ascontiguousarray(s[perm])).to(dev)
+    xt = torch.from_numpy(x16).to(dev)
+    y = torch.full((B, H), float("nan"), dtype=torch.float16, device=dev)
+    VP = ctypes.c_void_p
+    _lib.check(_lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0),
+                                             VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), B, N, K, 128,
+                                             VP(y.data_ptr()), H, VP(torch.cuda.current_stream().cuda_stream)),
+               "gemv_w4_swiglu")
+    torch.cuda.synchronize()
+    W = Q.dequantize_int4_g(p, s, (N, K), 128)
+    acc, mag = Q.gemv_ref(x16, W), Q.gemv_abs(x16, W)          # (B, N) fp64, source row order
+    g, u = acc[:, :H], acc[:, H:]
+    silu = g / (1.0 + np.exp(-g))
+    ref = silu * u
+    bound = RTOL * (1.1 * mag[:, :H] * np.abs(u) + np.abs(silu) * mag[:, H:]) + 2.0 ** -11 * np.abs(ref) + 2.0 ** -25
+    got = y.cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref)
+    worst = float(np.max(err / bound))
+    _say(f"  worst err / bound = {worst:.2e}")
+    assert np.all(err <= bound), worst
+    # rejects a weight whose rows are not whole 16-row blocks
+    assert _lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0), VP(sq.data_ptr()),
+                                         _lib.VNX_F16, sq.stride(0), B, N - 8, K, 128, VP(y.data_ptr()), H,
+                                         VP(torch.cuda.current_stream().cuda_stream)) == _lib.VNX_ERR_UNSUPPORTED

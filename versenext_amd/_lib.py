@@ -62,6 +62,8 @@ SIGNATURES = {
     "vnx_gemv_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
     "vnx_gemv_w4": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
                            _vp, _c_i64, _vp, _c_sz, _vp]),
+    "vnx_gemv_w4_swiglu": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
+                                  _vp, _c_i64, _vp]),
     "vnx_gemv_w8": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64,
                            _vp, _c_sz, _vp]),
     "vnx_dequant_w4": (_int, [_vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _c_i64, _vp]),

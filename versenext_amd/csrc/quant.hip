@@ -54,6 +54,7 @@ struct QGemvParams {
   int gpg;             // 128-column groups per scale: G / 128
   float* y;            // (B, N), row pitch ldy
   int64_t ldy;
+  uint16_t* yh;        // SwiGLU output: fp16 bits (B, N/2), row pitch ldy (then y is unused)
   int64_t ksplit_len;  // K per grid.y split (multiple of kGK; the launches use K)
 };
 
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
 // wave stages its group's x block (up to 32 batch rows x 128 k) through its
 // own LDS tile: coalesced 256-byte row reads in, the MFMA B-operand layout
 // out.
-template <int BITS, int NC, int NW>
+template <int BITS, int NC, int NW, bool SW = false>
 __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   constexpr int WBYTES = BITS == 4 ? 16 : 32;
   constexpr int XR = NC * 16;            // staged batch rows
@@ -392,6 +393,23 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   if constexpr (BITS == 8) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] *= load_scale(p, min(n0 + j, p.N - 1), 0);
+  }
+  if constexpr (SW) {
+    // rows 0-7 of the tile are the gate rows of hidden units tile*8 + 0..7,
+    // rows 8-15 their up rows: lane (m, kq) with kq < 2 holds gates 4kq + j,
+    // lane (m, kq + 2) the matching ups (same batch row m: N % 16 == 0, so
+    // both lanes are live or both returned above)
+    float u[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u[j] = __shfl_xor(v[j], 32);
+    if (kq >= 2) return;
+    uint16_t* dh = p.yh + b * p.ldy + (int64_t)blockIdx.x * 8 + 4 * kq;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g = v[j];
+      dh[j] = __builtin_bit_cast(uint16_t, (_Float16)(g / (1.0f + __expf(-g)) * u[j]));
+    }
+    return;
   }
   float* dst = p.y + b * p.ldy + n0;
   if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
@@ -537,13 +555,18 @@ __global__ void k_dequant(QGemvParams p, int bits, float* out, int64_t ldo) {
   out[n * ldo + k] = (float)q * s;
 }
 
+constexpr int64_t kQTargetWgs = 512;
+constexpr int64_t kQTileMaxN = 64 * kQTargetWgs;
+
 static int qgemv_check(const QGemvParams& p, int bits) {
-  if (!p.x || !p.w || !p.sc || !p.y) return VNX_ERR_INVALID_ARG;
+  if (!p.x || !p.w || !p.sc || (!p.y && !p.yh)) return VNX_ERR_INVALID_ARG;
   if (p.B < 0 || p.N < 0 || p.K <= 0) return VNX_ERR_INVALID_ARG;
   if (p.K % kGK) return VNX_ERR_UNSUPPORTED;
   if (bits == 4 && (p.G <= 0 || p.G % kGK || p.K % p.G)) return VNX_ERR_UNSUPPORTED;
   if (p.K > ((int64_t)1 << 30)) return VNX_ERR_UNSUPPORTED;
-  if (p.ldx < p.K || p.ldy < p.N) return VNX_ERR_INVALID_ARG;
+  if (p.ldx < p.K || p.ldy < (p.yh ? p.N / 2 : p.N)) return VNX_ERR_INVALID_ARG;
+  // SwiGLU: blocks of 8 gate + 8 up rows, one 16-row tile each (tile kernel)
+  if (p.yh && (p.N % 16 || p.N >= kQTileMaxN)) return VNX_ERR_UNSUPPORTED;
   if (p.ldw < (bits == 4 ? p.K / 2 : p.K)) return VNX_ERR_INVALID_ARG;
   if (p.lds < (bits == 4 ? p.K / p.G : 1)) return VNX_ERR_INVALID_ARG;
   // 16-byte vector loads of x and of every row's weights.
@@ -555,8 +578,6 @@ static int qgemv_check(const QGemvParams& p, int bits) {
 // workgroup (TPW = 4 when the staged x slice is large, more than 16 batch
 // columns, and N fills the GPU anyway, else 1), whole K.  Smaller N: the
 // tile kernel, one 16-row tile per workgroup with K split over its waves.
-constexpr int64_t kQTargetWgs = 512;
-constexpr int64_t kQTileMaxN = 64 * kQTargetWgs;
 
 // VNX_QTPW (1 or 4) overrides the tiles per wave for tuning sweeps.
 static int tpw_override() {
@@ -574,7 +595,8 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
   for (int64_t b0 = 0; b0 < p.B; b0 += 32) {
     QGemvParams c = p;
     c.x = p.x + b0 * p.ldx;
-    c.y = p.y + b0 * p.ldy;
+    if (p.y) c.y = p.y + b0 * p.ldy;
+    if (p.yh) c.yh = p.yh + b0 * p.ldy;
     c.B = min((int64_t)32, p.B - b0);
     c.ksplit_len = c.K;
     const bool two = c.B > 16;
@@ -585,7 +607,12 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       const dim3 grid((unsigned)tiles);
 #define VNX_QTILE(BITS, NC, NW) \
   hipLaunchKernelGGL((k_qgemv_tile<BITS, NC, NW>), grid, dim3(NW * 64), 0, s, c)
-      if (bits == 4) {
+#define VNX_QTILE_SW(NC, NW) \
+  hipLaunchKernelGGL((k_qgemv_tile<4, NC, NW, true>), grid, dim3(NW * 64), 0, s, c)
+      if (c.yh) {
+        if (two) { if (wide) VNX_QTILE_SW(2, 8); else VNX_QTILE_SW(2, 4); }
+        else { if (wide) VNX_QTILE_SW(1, 8); else VNX_QTILE_SW(1, 4); }
+      } else if (bits == 4) {
         if (two) { if (wide) VNX_QTILE(4, 2, 8); else VNX_QTILE(4, 2, 4); }
         else { if (wide) VNX_QTILE(4, 1, 8); else VNX_QTILE(4, 1, 4); }
       } else {
@@ -593,6 +620,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
         else { if (wide) VNX_QTILE(8, 1, 8); else VNX_QTILE(8, 1, 4); }
       }
 #undef VNX_QTILE
+#undef VNX_QTILE_SW
     } else if (bits == 4 && c.G == kGK && c.sc_f16 && c.lds % 8 == 0 && aligned16(c.sc) &&
                (c.K == 512 || c.K == 1024) && !getenv("VNX_QSTREAM_OFF")) {
       // two workgroups per CU (x staged once each), tiles split evenly
@@ -648,6 +676,20 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
   const int st = qgemv_check(p, 4);
   if (st) return st;
   (void)workspace; (void)workspace_bytes;
+  return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                       int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, void* y,
+                       int64_t ldy, void* stream) {
+  if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
+  if (!y) return VNX_ERR_INVALID_ARG;
+  QGemvParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
+  p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.yh = static_cast<uint16_t*>(y);
+  p.ldy = ldy; p.gpg = group / kGK;
+  const int st = qgemv_check(p, 4);
+  if (st) return st;
   return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
 }
 

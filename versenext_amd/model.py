@@ -255,9 +255,16 @@ class _Linear:
         self.hip = hip
         self.int4 = bool(int4) and self.K % 128 == 0
         self.wp = None
+        self.swiglu = bool(swiglu) and self.N % 32 == 0
         if self.int4:
             wq, sc = VQ.quantize_int4_g(w.float(), 128)
             self.wq, self.sc = wq.contiguous(), sc.contiguous()
+            if self.swiglu:
+                # rows reordered for vnx_gemv_w4_swiglu: blocks of 8 gate +
+                # 8 up rows (per-row quantization, so a pure permutation)
+                H = self.N // 2
+                self.wq_sw = wq.view(2, H // 8, 8, -1).transpose(0, 1).reshape(self.N, -1).contiguous()
+                self.sc_sw = sc.view(2, H // 8, 8, -1).transpose(0, 1).reshape(self.N, -1).contiguous()
             self.wd = hip.dequant_w4(self.wq, self.sc, self.K, 128).to(dtype)
             L = hip._L
             self._ws = torch.zeros(max(256, L.vnx_gemv_workspace(64, self.N, self.K)), dtype=torch.uint8,
@@ -268,7 +275,6 @@ class _Linear:
             # packed copy; for a fused [gate; up] weight its rows are
             # interleaved in blocks of 16 gate + 16 up rows first (the
             # SwiGLU epilogue's order)
-            self.swiglu = bool(swiglu) and self.N % 32 == 0
             if dtype == torch.bfloat16 and self.K % 64 == 0:
                 src = self.wd
                 if self.swiglu:
@@ -299,6 +305,22 @@ class _Linear:
             ctypes.c_void_p(x.data_ptr()), x.stride(0), 0, ctypes.c_void_p(self.wp.data_ptr()), 0, M, self.N, self.K,
             1, int(epilogue), None, 1, ctypes.c_void_p(y.data_ptr()), _lib.DTYPE_CODES[y.dtype], ncols, 0,
             ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16")
+        return y
+
+    def gemv_swiglu(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+        """silu(gate) * up (M, N/2) fp16 of a fused [gate; up] INT4 weight for
+        M <= 64 rows (vnx_gemv_w4_swiglu); None when it does not apply."""
+        M = x.shape[0]
+        if not (self.int4 and self.swiglu and M <= 64):
+            return None
+        x16 = x.to(torch.float16).contiguous()
+        H = self.N // 2
+        y = torch.empty((M, H), dtype=torch.float16, device=x.device)
+        _lib.check(self.hip._L.vnx_gemv_w4_swiglu(
+            ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq_sw.data_ptr()), self.wq_sw.stride(0),
+            ctypes.c_void_p(self.sc_sw.data_ptr()), _lib.VNX_F16, self.sc_sw.stride(0), M, self.N, self.K, 128,
+            ctypes.c_void_p(y.data_ptr()), H, ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)),
+            "gemv_w4_swiglu")
         return y
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -576,6 +598,8 @@ class CometSparkGPU:
             return self._mod(L, h)
         Hf = self.cfg.ffn_hidden
         act = L.ffn["gu"].gemm(h, epilogue=_lib.VNX_EPI_SWIGLU, out_dtype=self.act_dtype)
+        if act is None and self.act_dtype == torch.float16:
+            act = L.ffn["gu"].gemv_swiglu(h)     # INT4 draft decode
         if act is not None:                      # gate|up product with the SwiGLU epilogue
             return L.ffn["down"](act)
         gu = L.ffn["gu"](h)
