@@ -177,6 +177,29 @@ int vnx_greedy_verify(const void* target, int dtype, int64_t B, int k, int rows_
                       int32_t* accept_len, int64_t* out_ids,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* RoPE + KV-cache write of a q|k|v projection (vnx_rope_kv's work, done in
+ * the projection's epilogue).  Projection row m is token (m / n, m % n) at
+ * position lens[m / n] + m % n; heads are H query heads, then Hkv key heads,
+ * then Hkv value heads of d dims (d % 32 == 0).  Queries (rotated when rope)
+ * go to q_out (B, H, n, d) bf16; keys (rotated) and values to the bf16 caches
+ * at b*c_sb + head*c_sh + pos*c_sr; rows at or past cap (and table_rows when
+ * rope) are skipped.  NeoX rotate-half with the (table_rows, d) fp32 cos / sin
+ * tables.  The projection weight's rows must be permuted per head (see
+ * vnx_gemm_bf16_rope_kv / vnx_gemv_w4_rope_kv) so that each output tile holds
+ * rotate-half pairs. */
+typedef struct vnx_rope_kv_args {
+  const int32_t* lens;
+  int n, H, Hkv, d;
+  const float* cos_table;
+  const float* sin_table;
+  int64_t table_rows;
+  int rope;
+  void* q_out;
+  void* k_cache;
+  void* v_cache;
+  int64_t c_sb, c_sh, c_sr, cap;
+} vnx_rope_kv_args;
+
 /* ---------------------------------------------------------------------------
  * Weight-only quantized GEMV / skinny GEMM (draft decode, tied LM head):
  * y (B, N) fp32, row pitch ldy = x (B, K) fp16 (row pitch ldx) . W^T with W
@@ -211,6 +234,14 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
 int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
                        int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, void* y,
                        int64_t ldy, void* stream);
+
+/* vnx_gemv_w4 (group-128 fp16 scales) of a q|k|v projection with RoPE and
+ * the KV-cache write in the epilogue (rk; B rows = tokens): rows of W (and of
+ * its scales) permuted per head in 16-row tiles: tile t of head h holds dims
+ * t*8 .. t*8+7 then d/2 + t*8 .. d/2 + t*8+7.  N = (H + 2*Hkv)*d < 32768. */
+int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                        int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+                        const vnx_rope_kv_args* rk, void* stream);
 
 /* W8: wq (N, K) int8, row pitch ldw; scale (N) fp32 per output row (the
  * per-channel INT8 of quantize_int8, quantize.py:187-214).  Replaces
@@ -484,12 +515,24 @@ int vnx_spec_commit(const int32_t* accept_len, const int64_t* out_ids, int64_t l
  * ------------------------------------------------------------------------- */
 enum vnx_epilogue { VNX_EPI_NONE = 0, VNX_EPI_SWIGLU = 1 };
 
+
 size_t vnx_pack_bf16_size(int64_t N, int64_t K);
 int vnx_pack_bf16(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, void* stream);
 
 int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
                   int64_t N, int64_t K, int batch, int epilogue, const float* comb, int64_t ldc, void* y,
                   int y_dtype, int64_t ldy, int64_t syb, void* stream);
+
+/* vnx_gemm_bf16 (batch 1, shared x) of a q|k|v projection with RoPE and the
+ * KV-cache write in the epilogue (rk): the output goes to rk's q_out and
+ * caches instead of a y matrix.  N = (H + 2*Hkv)*d; W's rows, before
+ * vnx_pack_bf16, permuted per head in 32-row tiles: tile t of head h holds
+ * dims t*16 .. t*16+15 then d/2 + t*16 .. d/2 + t*16+15 (so packed row
+ * h*d + t*32 + r is source row h*d + (r < 16 ? t*16 + r : d/2 + t*16 + r - 16)).
+ * Replaces vnx_gemm_bf16 followed by vnx_rope_kv (TriSparseAttention's
+ * q/k/v projections and _apply_rope, tri_sparse_attn.py:182-221, :536-575). */
+int vnx_gemm_bf16_rope_kv(const void* x, int64_t ldx, const void* w_packed, int64_t M, int64_t N, int64_t K,
+                          const vnx_rope_kv_args* rk, void* stream);
 
 /* Routed MoD expert products (the expert FFNs of DensePart / Expert,
  * packages/verse_nex/verse_nex/mod.py:466-600, evaluated only on the rows

@@ -1,0 +1,163 @@
+"""GPU parity of the q|k|v projections with RoPE and the KV-cache write fused
+into their epilogues: vnx_gemm_bf16_rope_kv (bf16 weights) and
+vnx_gemv_w4_rope_kv (INT4 group-128 weights), against the fp64 projection of
+the same rounded inputs followed by NeoX rotate-half RoPE (the reference of
+vnx_rope_kv, TriSparseAttention._apply_rope).
+
+Bar per element: the GEMM bar carried through the rotation,
+RTOL * (mag_own * |cos| + mag_partner * |sin|), plus fp32 rounding of the
+rotation (1e-6 of |own cos| + |partner sin|) and one bf16 rounding of the
+result (2^-8 relative).  Rows whose position falls at or past the cache
+capacity are skipped: their q rows and cache rows keep a sentinel."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as Q
+from versenext_amd import _lib
+from versenext_amd import model as VM
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+VP = ctypes.c_void_p
+SENT = 7.0
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _st():
+    return VP(torch.cuda.current_stream().cuda_stream)
+
+
+def _setup(hip, B, n, H, Hkv, d, cap, T, seed):
+    dev = hip.torch_device
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    lens = torch.randint(0, cap - n + 2, (B,), generator=g, dtype=torch.int32)
+    lens[0] = cap - n + 1                    # its last row falls past the cache
+    ang = torch.rand((T, d), generator=g, dtype=torch.float64) * 6.0
+    cos, sin = torch.cos(ang).float(), torch.sin(ang).float()
+    q = torch.full((B, H, n, d), SENT, dtype=torch.bfloat16, device=dev)
+    kc = torch.full((B, Hkv, cap, d), SENT, dtype=torch.bfloat16, device=dev)
+    vc = torch.full_like(kc, SENT)
+    return lens, cos, sin, q, kc, vc
+
+
+def _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, rope, cap):
+    return _lib.RopeKvArgs(VP(lens_d.data_ptr()), n, H, Hkv, d, VP(cos_d.data_ptr()), VP(sin_d.data_ptr()),
+                           cos_d.shape[0], rope, VP(q.data_ptr()), VP(kc.data_ptr()), VP(vc.data_ptr()),
+                           kc.stride(0), kc.stride(1), kc.stride(2), cap)
+
+
+def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap):
+    heads = H + 2 * Hkv
+    acc = (x64 @ W64.t()).view(B, n, heads, d)
+    mag = (x64.abs() @ W64.abs().t()).view(B, n, heads, d)
+    half = d // 2
+    pos = lens.long().view(B, 1) + torch.arange(n).view(1, n)
+    ok = pos < cap
+    pc = pos.clamp(max=cos.shape[0] - 1)
+    c = cos.double()[pc].unsqueeze(2)
+    s = sin.double()[pc].unsqueeze(2)
+    rot = torch.cat([-acc[..., half:], acc[..., :half]], dim=-1)
+    mrot = torch.cat([mag[..., half:], mag[..., :half]], dim=-1)
+    rotated = torch.zeros(heads, dtype=torch.bool)
+    if rope:
+        rotated[:H + Hkv] = True
+    rs = rotated.view(1, 1, heads, 1)
+    ref = torch.where(rs, acc * c + rot * s, acc)
+    arot = torch.where(rs, (acc * c).abs() + (rot * s).abs(), acc.abs())
+    bound = torch.where(rs, RTOL * (mag * c.abs() + mrot * s.abs()), RTOL * mag) + 1e-6 * arot \
+        + 2.0 ** -8 * ref.abs() + 1e-30
+    qg, kg, vg = q.double().cpu(), kc.double().cpu(), vc.double().cpu()
+    worst = 0.0
+    for b in range(B):
+        for i in range(n):
+            if not ok[b, i]:
+                assert bool((qg[b, :, i] == SENT).all())
+                continue
+            p = int(pos[b, i])
+            for part, got in ((slice(0, H), qg[b, :, i]), (slice(H, H + Hkv), kg[b, :, p]),
+                              (slice(H + Hkv, heads), vg[b, :, p])):
+                err = (got - ref[b, i, part]).abs()
+                bd = bound[b, i, part]
+                worst = max(worst, float((err / bd).max()))
+                assert bool((err <= bd).all()), f"row ({b}, {i}) worst err / bound {worst:.3e}"
+    # cache rows that no token wrote keep the sentinel
+    written = torch.zeros((B, cap), dtype=torch.bool)
+    for b in range(B):
+        for i in range(n):
+            if ok[b, i]:
+                written[b, int(pos[b, i])] = True
+    assert bool((kg.permute(0, 2, 1, 3)[~written] == SENT).all())
+    _say(f"  worst err / bound = {worst:.2e}")
+
+
+@pytest.mark.parametrize("B,n,H,Hkv,d,K,rope", [(32, 7, 16, 8, 64, 1024, 1), (3, 5, 4, 2, 128, 128, 1),
+                                                 (2, 3, 2, 1, 32, 64, 0), (9, 1, 6, 3, 64, 192, 1)])
+def test_gemm_rope_kv(hip, B, n, H, Hkv, d, K, rope):
+    _say(f"gemm_bf16_rope_kv B={B} n={n} H={H} Hkv={Hkv} d={d} K={K} rope={rope}")
+    dev = hip.torch_device
+    heads = H + 2 * Hkv
+    N, M, cap, T = heads * d, B * n, 48, 64
+    g = torch.Generator(device="cpu")
+    g.manual_seed(B * n + d + K)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    W = (torch.randn((N, K), generator=g) * 0.05).to(torch.bfloat16)
+    lens, cos, sin, q, kc, vc = _setup(hip, B, n, H, Hkv, d, cap, T, seed=d + K)
+    wp = VM._pack(W[VM.rope_rows(heads, d, 16)].contiguous().to(dev), hip)
+    lens_d, cos_d, sin_d, xd = lens.to(dev), cos.to(dev), sin.to(dev), x.to(dev)
+    rk = _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, rope, cap)
+    _lib.check(_lib.lib().vnx_gemm_bf16_rope_kv(VP(xd.data_ptr()), K, VP(wp.data_ptr()), M, N, K, ctypes.byref(rk),
+                                                _st()), "gemm_bf16_rope_kv")
+    torch.cuda.synchronize()
+    _check(x.double(), W.double(), lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap)
+
+
+@pytest.mark.parametrize("B,n,H,Hkv,d,K", [(32, 1, 16, 8, 64, 1024), (20, 2, 4, 2, 64, 256), (3, 1, 2, 1, 128, 128)])
+def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K):
+    _say(f"gemv_w4_rope_kv B={B} n={n} H={H} Hkv={Hkv} d={d} K={K}")
+    dev = hip.torch_device
+    heads = H + 2 * Hkv
+    N, M, cap, T = heads * d, B * n, 40, 48
+    rng = np.random.default_rng(N + K)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    p, s = Q.quantize_int4_g(W, 128)
+    perm = VM.rope_rows(heads, d, 8).numpy()
+    pq = torch.from_numpy(np.ascontiguousarray(p[perm])).to(dev)
+    sq = torch.from_numpy(np.ascontiguousarray(s[perm])).to(dev)
+    x16 = rng.normal(0, 1, (M, K)).astype(np.float16)
+    xd = torch.from_numpy(x16).to(dev)
+    lens, cos, sin, q, kc, vc = _setup(hip, B, n, H, Hkv, d, cap, T, seed=M + d)
+    lens_d, cos_d, sin_d = lens.to(dev), cos.to(dev), sin.to(dev)
+    rk = _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, 1, cap)
+    _lib.check(_lib.lib().vnx_gemv_w4_rope_kv(VP(xd.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0),
+                                              VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), M, N, K, 128,
+                                              ctypes.byref(rk), _st()), "gemv_w4_rope_kv")
+    torch.cuda.synchronize()
+    Wd = torch.from_numpy(Q.dequantize_int4_g(p, s, (N, K), 128).astype(np.float64))
+    _check(torch.from_numpy(x16.astype(np.float64)), Wd, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, 1, cap)
+
+
+def test_rope_proj_rejects(hip):
+    dev = hip.torch_device
+    x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
+    wp = torch.zeros(64 * 64, dtype=torch.bfloat16, device=dev)
+    lens = torch.zeros(4, dtype=torch.int32, device=dev)
+    cs = torch.zeros((8, 16), dtype=torch.float32, device=dev)
+    q = torch.zeros(4096, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    rk = _lib.RopeKvArgs(VP(lens.data_ptr()), 1, 2, 1, 16, VP(cs.data_ptr()), VP(cs.data_ptr()), 8, 1,
+                         VP(q.data_ptr()), VP(q.data_ptr()), VP(q.data_ptr()), 64, 16, 16, 4)
+    # d = 16 is not a whole 32-row tile of rotate-half pairs
+    assert L.vnx_gemm_bf16_rope_kv(VP(x.data_ptr()), 64, VP(wp.data_ptr()), 4, 64, 64, ctypes.byref(rk),
+                                   _st()) == _lib.VNX_ERR_UNSUPPORTED
+    rk.d = 32
+    # N must be (H + 2 Hkv) d
+    assert L.vnx_gemm_bf16_rope_kv(VP(x.data_ptr()), 64, VP(wp.data_ptr()), 4, 96, 64, ctypes.byref(rk),
+                                   _st()) == _lib.VNX_ERR_INVALID_ARG

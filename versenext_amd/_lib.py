@@ -91,7 +91,20 @@ class TreeAttnArgs(ctypes.Structure):
     ]
 
 
+class RopeKvArgs(ctypes.Structure):
+    """vnx_rope_kv_args (include/vnx.h)."""
+    _fields_ = [
+        ("lens", _vp), ("n", _int), ("H", _int), ("Hkv", _int), ("d", _int),
+        ("cos_table", _vp), ("sin_table", _vp), ("table_rows", _c_i64), ("rope", _int),
+        ("q_out", _vp), ("k_cache", _vp), ("v_cache", _vp),
+        ("c_sb", _c_i64), ("c_sh", _c_i64), ("c_sr", _c_i64), ("cap", _c_i64),
+    ]
+
+
 SIGNATURES.update({
+    "vnx_gemm_bf16_rope_kv": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.POINTER(RopeKvArgs), _vp]),
+    "vnx_gemv_w4_rope_kv": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
+                                   ctypes.POINTER(RopeKvArgs), _vp]),
     "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),
     "vnx_tree_attn": (_int, [ctypes.POINTER(TreeAttnArgs), _vp, _c_sz, _vp]),
     "vnx_tree_attn_plan": (_int, [_int, _int, _int, _int, _int, _int, _vp, _vp, _vp]),

@@ -505,6 +505,24 @@ __global__ __launch_bounds__(256) void k_sum_expert_rows(const TY* y, int64_t ld
 inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
+
+int rope_out_from(const vnx_rope_kv_args* a, int64_t N, RopeOut* out) {
+  if (!a || !a->lens || !a->q_out || !a->k_cache || !a->v_cache) return VNX_ERR_INVALID_ARG;
+  if (a->n < 1 || a->H < 1 || a->Hkv < 1 || a->d < 2) return VNX_ERR_INVALID_ARG;
+  if (a->d % 32) return VNX_ERR_UNSUPPORTED;  // whole 32-row tiles of rotate-half pairs per head
+  if ((int64_t)(a->H + 2 * a->Hkv) * a->d != N) return VNX_ERR_INVALID_ARG;
+  if (a->c_sb < 0 || a->c_sh < 0 || a->c_sr < a->d || a->cap < 1) return VNX_ERR_INVALID_ARG;
+  if (a->rope && (!a->cos_table || !a->sin_table || a->table_rows < 1)) return VNX_ERR_INVALID_ARG;
+  RopeOut r{};
+  r.lens = a->lens; r.cos = a->cos_table; r.sin = a->sin_table;
+  r.q = static_cast<uint16_t*>(a->q_out); r.kc = static_cast<uint16_t*>(a->k_cache);
+  r.vc = static_cast<uint16_t*>(a->v_cache);
+  r.c_sb = a->c_sb; r.c_sh = a->c_sh; r.c_sr = a->c_sr;
+  r.cap = a->rope ? (a->cap < a->table_rows ? a->cap : a->table_rows) : a->cap;
+  r.n = a->n; r.H = a->H; r.Hkv = a->Hkv; r.d = a->d; r.rope = a->rope ? 1 : 0;
+  *out = r;
+  return VNX_OK;
+}
 }  // namespace vnx
 
 using namespace vnx;

@@ -55,6 +55,9 @@ struct QGemvParams {
   float* y;            // (B, N), row pitch ldy
   int64_t ldy;
   uint16_t* yh;        // SwiGLU output: fp16 bits (B, N/2), row pitch ldy (then y is unused)
+  int rope_on;         // RoPE + cache store epilogue (ro; y and yh unused)
+  int64_t row_off;     // batch row of x's first row (the launch's 32-row chunks)
+  RopeOut ro;
   int64_t ksplit_len;  // K per grid.y split (multiple of kGK; the launches use K)
 };
 
@@ -287,7 +290,8 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
 // wave stages its group's x block (up to 32 batch rows x 128 k) through its
 // own LDS tile: coalesced 256-byte row reads in, the MFMA B-operand layout
 // out.
-template <int BITS, int NC, int NW, bool SW = false>
+// QE: 0 plain fp32 output, 1 SwiGLU (fp16), 2 RoPE + KV-cache store.
+template <int BITS, int NC, int NW, int QE = 0>
 __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   constexpr int WBYTES = BITS == 4 ? 16 : 32;
   constexpr int XR = NC * 16;            // staged batch rows
@@ -394,7 +398,24 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] *= load_scale(p, min(n0 + j, p.N - 1), 0);
   }
-  if constexpr (SW) {
+  if constexpr (QE == 2) {
+    // tile t of head hh holds dims qb*8 + 0..7 (rows 0-7) and d/2 + qb*8 +
+    // 0..7 (rows 8-15): lane (m, kq) and lane (m, kq ^ 2) are partners
+    float part[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part[j] = __shfl_xor(v[j], 32);
+    const int t = blockIdx.x;
+    const int hh = t * 16 / p.ro.d;
+    const int qb = (t * 16 - hh * p.ro.d) / 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int rho = 4 * kq + j;
+      const int dim = rho < 8 ? qb * 8 + rho : p.ro.d / 2 + qb * 8 + (rho - 8);
+      rope_store(p.ro, p.row_off + b, hh, dim, v[j], part[j]);
+    }
+    return;
+  }
+  if constexpr (QE == 1) {
     // rows 0-7 of the tile are the gate rows of hidden units tile*8 + 0..7,
     // rows 8-15 their up rows: lane (m, kq) with kq < 2 holds gates 4kq + j,
     // lane (m, kq + 2) the matching ups (same batch row m: N % 16 == 0, so
@@ -559,12 +580,13 @@ constexpr int64_t kQTargetWgs = 512;
 constexpr int64_t kQTileMaxN = 64 * kQTargetWgs;
 
 static int qgemv_check(const QGemvParams& p, int bits) {
-  if (!p.x || !p.w || !p.sc || (!p.y && !p.yh)) return VNX_ERR_INVALID_ARG;
+  if (!p.x || !p.w || !p.sc || (!p.y && !p.yh && !p.rope_on)) return VNX_ERR_INVALID_ARG;
   if (p.B < 0 || p.N < 0 || p.K <= 0) return VNX_ERR_INVALID_ARG;
   if (p.K % kGK) return VNX_ERR_UNSUPPORTED;
   if (bits == 4 && (p.G <= 0 || p.G % kGK || p.K % p.G)) return VNX_ERR_UNSUPPORTED;
   if (p.K > ((int64_t)1 << 30)) return VNX_ERR_UNSUPPORTED;
-  if (p.ldx < p.K || p.ldy < (p.yh ? p.N / 2 : p.N)) return VNX_ERR_INVALID_ARG;
+  if (p.ldx < p.K || (!p.rope_on && p.ldy < (p.yh ? p.N / 2 : p.N))) return VNX_ERR_INVALID_ARG;
+  if (p.rope_on && (bits != 4 || p.N >= kQTileMaxN)) return VNX_ERR_UNSUPPORTED;
   // SwiGLU: blocks of 8 gate + 8 up rows, one 16-row tile each (tile kernel)
   if (p.yh && (p.N % 16 || p.N >= kQTileMaxN)) return VNX_ERR_UNSUPPORTED;
   if (p.ldw < (bits == 4 ? p.K / 2 : p.K)) return VNX_ERR_INVALID_ARG;
@@ -597,6 +619,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
     c.x = p.x + b0 * p.ldx;
     if (p.y) c.y = p.y + b0 * p.ldy;
     if (p.yh) c.yh = p.yh + b0 * p.ldy;
+    c.row_off = b0;
     c.B = min((int64_t)32, p.B - b0);
     c.ksplit_len = c.K;
     const bool two = c.B > 16;
@@ -607,11 +630,14 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       const dim3 grid((unsigned)tiles);
 #define VNX_QTILE(BITS, NC, NW) \
   hipLaunchKernelGGL((k_qgemv_tile<BITS, NC, NW>), grid, dim3(NW * 64), 0, s, c)
-#define VNX_QTILE_SW(NC, NW) \
-  hipLaunchKernelGGL((k_qgemv_tile<4, NC, NW, true>), grid, dim3(NW * 64), 0, s, c)
-      if (c.yh) {
-        if (two) { if (wide) VNX_QTILE_SW(2, 8); else VNX_QTILE_SW(2, 4); }
-        else { if (wide) VNX_QTILE_SW(1, 8); else VNX_QTILE_SW(1, 4); }
+#define VNX_QTILE_E(NC, NW, QE) \
+  hipLaunchKernelGGL((k_qgemv_tile<4, NC, NW, QE>), grid, dim3(NW * 64), 0, s, c)
+      if (c.rope_on) {
+        if (two) { if (wide) VNX_QTILE_E(2, 8, 2); else VNX_QTILE_E(2, 4, 2); }
+        else { if (wide) VNX_QTILE_E(1, 8, 2); else VNX_QTILE_E(1, 4, 2); }
+      } else if (c.yh) {
+        if (two) { if (wide) VNX_QTILE_E(2, 8, 1); else VNX_QTILE_E(2, 4, 1); }
+        else { if (wide) VNX_QTILE_E(1, 8, 1); else VNX_QTILE_E(1, 4, 1); }
       } else if (bits == 4) {
         if (two) { if (wide) VNX_QTILE(4, 2, 8); else VNX_QTILE(4, 2, 4); }
         else { if (wide) VNX_QTILE(4, 1, 8); else VNX_QTILE(4, 1, 4); }
@@ -620,7 +646,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
         else { if (wide) VNX_QTILE(8, 1, 8); else VNX_QTILE(8, 1, 4); }
       }
 #undef VNX_QTILE
-#undef VNX_QTILE_SW
+#undef VNX_QTILE_E
     } else if (bits == 4 && c.G == kGK && c.sc_f16 && c.lds % 8 == 0 && aligned16(c.sc) &&
                (c.K == 512 || c.K == 1024) && !getenv("VNX_QSTREAM_OFF")) {
       // two workgroups per CU (x staged once each), tiles split evenly
@@ -688,6 +714,22 @@ int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ld
   p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
   p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.yh = static_cast<uint16_t*>(y);
   p.ldy = ldy; p.gpg = group / kGK;
+  const int st = qgemv_check(p, 4);
+  if (st) return st;
+  return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                        int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+                        const vnx_rope_kv_args* rk, void* stream) {
+  if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
+  QGemvParams p{};
+  const int rs = rope_out_from(rk, N, &p.ro);
+  if (rs) return rs;
+  if (B % rk->n) return VNX_ERR_INVALID_ARG;  // rows are whole sequences of n tokens
+  p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
+  p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.rope_on = 1;
+  p.gpg = group / kGK;
   const int st = qgemv_check(p, 4);
   if (st) return st;
   return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));

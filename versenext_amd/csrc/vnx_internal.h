@@ -1,4 +1,5 @@
-// Host-side helpers shared by the vnx entry points.
+// Helpers shared by the vnx entry points (host side, plus the RoPE / KV-cache
+// store that the projection epilogues share).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -101,5 +102,45 @@ inline int check_rows(const void* x, int dtype, int64_t ld, int64_t sb, int nrow
   if (!aligned16(x) || ld % ve != 0 || sb % ve != 0) return VNX_ERR_UNSUPPORTED;
   return VNX_OK;
 }
+
+// RoPE + KV-cache store of a q|k|v projection epilogue (the per-row work of
+// vnx_rope_kv: TriSparseAttention._apply_rope, tri_sparse_attn.py:182-221,
+// and the cache write).  Row m is token (m / n, m % n) at position
+// lens[m / n] + m % n; rows at or past cap (the cache, and the RoPE table when
+// rope) are skipped.
+struct RopeOut {
+  const int32_t* lens;
+  const float* cos;
+  const float* sin;
+  uint16_t* q;               // (B, H, n, d) bf16 bits
+  uint16_t* kc;              // bf16 caches, strides c_sb, c_sh, c_sr
+  uint16_t* vc;
+  int64_t c_sb, c_sh, c_sr, cap;
+  int n, H, Hkv, d, rope;
+};
+
+// Stores element `dim` of head hh (q heads, then k, then v) for row m: own is
+// the projection's value at dim, partner its rotate-half partner (dim +- d/2).
+__device__ __forceinline__ void rope_store(const RopeOut& r, int64_t m, int hh, int dim, float own, float partner) {
+  const int64_t b = m / r.n;
+  const int ti = (int)(m - b * r.n);
+  const int64_t pos = (int64_t)r.lens[b] + ti;
+  if (pos < 0 || pos >= r.cap) return;
+  float y = own;
+  if (r.rope && hh < r.H + r.Hkv) {
+    // y[j] = x[j] cos[j] - x[j + d/2] sin[j];  y[j + d/2] = x[j + d/2] cos + x[j] sin
+    const float c = r.cos[pos * r.d + dim], s = r.sin[pos * r.d + dim];
+    const float sp = dim < r.d / 2 ? -partner : partner;
+    y = own * c + sp * s;
+  }
+  uint16_t* dst;
+  if (hh < r.H) dst = r.q + ((b * r.H + hh) * r.n + ti) * (int64_t)r.d;
+  else if (hh < r.H + r.Hkv) dst = r.kc + b * r.c_sb + (int64_t)(hh - r.H) * r.c_sh + pos * r.c_sr;
+  else dst = r.vc + b * r.c_sb + (int64_t)(hh - r.H - r.Hkv) * r.c_sh + pos * r.c_sr;
+  dst[dim] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y));
+}
+
+// Fills a RopeOut from the public argument block; VNX_OK or an error status.
+int rope_out_from(const vnx_rope_kv_args* a, int64_t N, RopeOut* out);
 
 }  // namespace vnx

@@ -232,6 +232,17 @@ class _Layer:
     ffn: Dict[str, object] = field(default_factory=dict)
 
 
+def rope_rows(heads: int, d: int, blk: int) -> torch.Tensor:
+    """Row order of a q|k|v weight for the RoPE epilogues: per head, blocks
+    of blk dims t*blk .. +blk followed by their rotate-half partners d/2 +
+    t*blk .. +blk (entry i = the source row of packed row i)."""
+    half = d // 2
+    t = torch.arange(half // blk).view(-1, 1, 1)
+    r = torch.arange(blk).view(1, 1, -1)
+    blocks = torch.cat([t * blk + r, half + t * blk + r], dim=1).reshape(-1)      # one head
+    return (torch.arange(heads).view(-1, 1) * d + blocks.view(1, -1)).reshape(-1)
+
+
 def _pack(w: torch.Tensor, hip) -> torch.Tensor:
     """vnx_pack_bf16 of a contiguous (N, K) bf16 weight: the matrix-core
     operand order read by vnx_gemm_bf16 / vnx_expert_gemm_bf16."""
@@ -249,8 +260,9 @@ class _Linear:
     M <= 64 rows and a dequantized copy (bit-exact q * s) for larger M
     (prefill)."""
 
-    def __init__(self, w: torch.Tensor, dtype, hip, int4: bool, swiglu: bool = False):
+    def __init__(self, w: torch.Tensor, dtype, hip, int4: bool, swiglu: bool = False, rope_head_dim: int = 0):
         self.N, self.K = w.shape
+        self.wp_rope = self.wq_rope = None
         self.dtype = dtype
         self.hip = hip
         self.int4 = bool(int4) and self.K % 128 == 0
@@ -265,6 +277,10 @@ class _Linear:
                 H = self.N // 2
                 self.wq_sw = wq.view(2, H // 8, 8, -1).transpose(0, 1).reshape(self.N, -1).contiguous()
                 self.sc_sw = sc.view(2, H // 8, 8, -1).transpose(0, 1).reshape(self.N, -1).contiguous()
+            if rope_head_dim and rope_head_dim % 32 == 0 and self.N % rope_head_dim == 0:
+                # rows in the order of vnx_gemv_w4_rope_kv's epilogue
+                perm = rope_rows(self.N // rope_head_dim, rope_head_dim, 8).to(wq.device)
+                self.wq_rope, self.sc_rope = wq[perm].contiguous(), sc[perm].contiguous()
             self.wd = hip.dequant_w4(self.wq, self.sc, self.K, 128).to(dtype)
             L = hip._L
             self._ws = torch.zeros(max(256, L.vnx_gemv_workspace(64, self.N, self.K)), dtype=torch.uint8,
@@ -287,6 +303,10 @@ class _Linear:
                                            ctypes.c_void_p(self.wp.data_ptr()),
                                            ctypes.c_void_p(torch.cuda.current_stream(hip.torch_device).cuda_stream)),
                            "pack_bf16")
+                if rope_head_dim and rope_head_dim % 32 == 0 and self.N % rope_head_dim == 0:
+                    # a second packed copy in the order of vnx_gemm_bf16_rope_kv's epilogue
+                    perm = rope_rows(self.N // rope_head_dim, rope_head_dim, 16).to(self.wd.device)
+                    self.wp_rope = _pack(self.wd[perm].contiguous(), hip)
 
     GEMM_MAX_M = 256
 
@@ -306,6 +326,28 @@ class _Linear:
             1, int(epilogue), None, 1, ctypes.c_void_p(y.data_ptr()), _lib.DTYPE_CODES[y.dtype], ncols, 0,
             ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16")
         return y
+
+    def rope_kv(self, x: torch.Tensor, rk) -> bool:
+        """The q|k|v projection of x with RoPE and the KV-cache write fused
+        (vnx_gemm_bf16_rope_kv for bf16 rows, M <= GEMM_MAX_M;
+        vnx_gemv_w4_rope_kv for INT4 weights, M <= 64); False (nothing done)
+        when neither applies."""
+        M = x.shape[0]
+        st = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        L = self.hip._L
+        if self.wp_rope is not None and M <= self.GEMM_MAX_M and x.dtype == torch.bfloat16 and x.stride(1) == 1:
+            _lib.check(L.vnx_gemm_bf16_rope_kv(ctypes.c_void_p(x.data_ptr()), x.stride(0),
+                                               ctypes.c_void_p(self.wp_rope.data_ptr()), M, self.N, self.K,
+                                               ctypes.byref(rk), st), "gemm_bf16_rope_kv")
+            return True
+        if self.wq_rope is not None and M <= 64:
+            x16 = x.to(torch.float16).contiguous()
+            _lib.check(L.vnx_gemv_w4_rope_kv(
+                ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq_rope.data_ptr()),
+                self.wq_rope.stride(0), ctypes.c_void_p(self.sc_rope.data_ptr()), _lib.VNX_F16,
+                self.sc_rope.stride(0), M, self.N, self.K, 128, ctypes.byref(rk), st), "gemv_w4_rope_kv")
+            return True
+        return False
 
     def gemv_swiglu(self, x: torch.Tensor) -> Optional[torch.Tensor]:
         """silu(gate) * up (M, N/2) fp16 of a fused [gate; up] INT4 weight for
@@ -381,7 +423,8 @@ class CometSparkGPU:
             gk = (g @ wk.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
             gv = (g @ wv.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
             L = _Layer(kind=kind, norm1=W[p + "norm1.weight"], norm2=W[p + "norm2.weight"],
-                       wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4),
+                       wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4,
+                                    rope_head_dim=d if dtype == torch.bfloat16 else 0),
                        proj=_Linear(W[p + "attn.proj.weight"], dtype, hip, int4),
                        gk=gk.to(dtype).contiguous(), gv=gv.to(dtype).contiguous(),
                        gates=torch.sigmoid(W[p + "attn.gate_logits"].float()).contiguous())
@@ -652,14 +695,19 @@ class CometSparkGPU:
                 self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
             else:
                 self._rms(x, pending, L.norm1, h)
-            qkv = L.wqkv(h)                                                          # (M, (H+2Hkv) d)
             q = torch.empty((B, H, n, d), dtype=self.dtype, device=self.dev)
             kc, vc = self.kc[li], self.vc[li]
-            _lib.check(L_.vnx_rope_kv(
-                P(qkv.data_ptr()), _lib.DTYPE_CODES[qkv.dtype], qkv.stride(0), B, n, H, Hkv, d, P(lens.data_ptr()),
-                P(self.cos.data_ptr()), P(self.sin.data_ptr()), self.cos.shape[0], int(cfg.use_rope),
-                P(q.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()), _lib.DTYPE_CODES[self.dtype],
-                kc.stride(0), kc.stride(1), kc.stride(2), self.cap, self._st()), "rope_kv")
+            rk = _lib.RopeKvArgs(P(lens.data_ptr()), n, H, Hkv, d, P(self.cos.data_ptr()), P(self.sin.data_ptr()),
+                                 self.cos.shape[0], int(cfg.use_rope), P(q.data_ptr()), P(kc.data_ptr()),
+                                 P(vc.data_ptr()), kc.stride(0), kc.stride(1), kc.stride(2), self.cap)
+            if not L.wqkv.rope_kv(h, rk):         # projection with RoPE + cache write fused
+                qkv = L.wqkv(h)                                                      # (M, (H+2Hkv) d)
+                _lib.check(L_.vnx_rope_kv(
+                    P(qkv.data_ptr()), _lib.DTYPE_CODES[qkv.dtype], qkv.stride(0), B, n, H, Hkv, d,
+                    P(lens.data_ptr()), P(self.cos.data_ptr()), P(self.sin.data_ptr()), self.cos.shape[0],
+                    int(cfg.use_rope), P(q.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()),
+                    _lib.DTYPE_CODES[self.dtype], kc.stride(0), kc.stride(1), kc.stride(2), self.cap, self._st()),
+                    "rope_kv")
             if use_kernel:
                 o = self._attn_kernel(q, li, lens, n, Tmax)
             else:
