@@ -180,13 +180,12 @@ int vnx_greedy_verify(const void* target, int dtype, int64_t B, int k, int rows_
 /* RoPE + KV-cache write of a q|k|v projection (vnx_rope_kv's work, done in
  * the projection's epilogue).  Projection row m is token (m / n, m % n) at
  * position lens[m / n] + m % n; heads are H query heads, then Hkv key heads,
- * then Hkv value heads of d dims (d % 32 == 0).  Queries (rotated when rope)
+ * then Hkv value heads of d dims (d % 16 == 0).  Queries (rotated when rope)
  * go to q_out (B, H, n, d) bf16; keys (rotated) and values to the bf16 caches
  * at b*c_sb + head*c_sh + pos*c_sr; rows at or past cap (and table_rows when
  * rope) are skipped.  NeoX rotate-half with the (table_rows, d) fp32 cos / sin
  * tables.  The projection weight's rows must be permuted per head (see
- * vnx_gemm_bf16_rope_kv / vnx_gemv_w4_rope_kv) so that each output tile holds
- * rotate-half pairs. */
+ * vnx_gemv_w4_rope_kv) so that each output tile holds rotate-half pairs. */
 typedef struct vnx_rope_kv_args {
   const int32_t* lens;
   int n, H, Hkv, d;
@@ -522,17 +521,6 @@ int vnx_pack_bf16(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, v
 int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
                   int64_t N, int64_t K, int batch, int epilogue, const float* comb, int64_t ldc, void* y,
                   int y_dtype, int64_t ldy, int64_t syb, void* stream);
-
-/* vnx_gemm_bf16 (batch 1, shared x) of a q|k|v projection with RoPE and the
- * KV-cache write in the epilogue (rk): the output goes to rk's q_out and
- * caches instead of a y matrix.  N = (H + 2*Hkv)*d; W's rows, before
- * vnx_pack_bf16, permuted per head in 32-row tiles: tile t of head h holds
- * dims t*16 .. t*16+15 then d/2 + t*16 .. d/2 + t*16+15 (so packed row
- * h*d + t*32 + r is source row h*d + (r < 16 ? t*16 + r : d/2 + t*16 + r - 16)).
- * Replaces vnx_gemm_bf16 followed by vnx_rope_kv (TriSparseAttention's
- * q/k/v projections and _apply_rope, tri_sparse_attn.py:182-221, :536-575). */
-int vnx_gemm_bf16_rope_kv(const void* x, int64_t ldx, const void* w_packed, int64_t M, int64_t N, int64_t K,
-                          const vnx_rope_kv_args* rk, void* stream);
 
 /* Routed MoD expert products (the expert FFNs of DensePart / Expert,
  * packages/verse_nex/verse_nex/mod.py:466-600, evaluated only on the rows

@@ -1,6 +1,6 @@
-"""GPU parity of the q|k|v projections with RoPE and the KV-cache write fused
-into their epilogues: vnx_gemm_bf16_rope_kv (bf16 weights) and
-vnx_gemv_w4_rope_kv (INT4 group-128 weights), against the fp64 projection of
+"""GPU parity of the INT4 q|k|v projection with RoPE and the KV-cache write
+fused into its epilogue (vnx_gemv_w4_rope_kv, group-128 weights), against the
+fp64 projection of
 the same rounded inputs followed by NeoX rotate-half RoPE (the reference of
 vnx_rope_kv, TriSparseAttention._apply_rope).
 
@@ -98,28 +98,8 @@ def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap):
     _say(f"  worst err / bound = {worst:.2e}")
 
 
-@pytest.mark.parametrize("B,n,H,Hkv,d,K,rope", [(32, 7, 16, 8, 64, 1024, 1), (3, 5, 4, 2, 128, 128, 1),
-                                                 (2, 3, 2, 1, 32, 64, 0), (9, 1, 6, 3, 64, 192, 1)])
-def test_gemm_rope_kv(hip, B, n, H, Hkv, d, K, rope):
-    _say(f"gemm_bf16_rope_kv B={B} n={n} H={H} Hkv={Hkv} d={d} K={K} rope={rope}")
-    dev = hip.torch_device
-    heads = H + 2 * Hkv
-    N, M, cap, T = heads * d, B * n, 48, 64
-    g = torch.Generator(device="cpu")
-    g.manual_seed(B * n + d + K)
-    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
-    W = (torch.randn((N, K), generator=g) * 0.05).to(torch.bfloat16)
-    lens, cos, sin, q, kc, vc = _setup(hip, B, n, H, Hkv, d, cap, T, seed=d + K)
-    wp = VM._pack(W[VM.rope_rows(heads, d, 16)].contiguous().to(dev), hip)
-    lens_d, cos_d, sin_d, xd = lens.to(dev), cos.to(dev), sin.to(dev), x.to(dev)
-    rk = _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, rope, cap)
-    _lib.check(_lib.lib().vnx_gemm_bf16_rope_kv(VP(xd.data_ptr()), K, VP(wp.data_ptr()), M, N, K, ctypes.byref(rk),
-                                                _st()), "gemm_bf16_rope_kv")
-    torch.cuda.synchronize()
-    _check(x.double(), W.double(), lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap)
-
-
-@pytest.mark.parametrize("B,n,H,Hkv,d,K", [(32, 1, 16, 8, 64, 1024), (20, 2, 4, 2, 64, 256), (3, 1, 2, 1, 128, 128)])
+@pytest.mark.parametrize("B,n,H,Hkv,d,K", [(32, 1, 16, 8, 64, 1024), (20, 2, 4, 2, 64, 256), (3, 1, 2, 1, 128, 128),
+                                           (40, 1, 3, 1, 16, 128)])
 def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K):
     _say(f"gemv_w4_rope_kv B={B} n={n} H={H} Hkv={Hkv} d={d} K={K}")
     dev = hip.torch_device
@@ -146,18 +126,22 @@ def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K):
 
 def test_rope_proj_rejects(hip):
     dev = hip.torch_device
-    x = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
-    wp = torch.zeros(64 * 64, dtype=torch.bfloat16, device=dev)
+    x = torch.zeros((4, 128), dtype=torch.float16, device=dev)
+    wq = torch.zeros((64, 64), dtype=torch.uint8, device=dev)
+    sc = torch.ones((64, 1), dtype=torch.float16, device=dev)
     lens = torch.zeros(4, dtype=torch.int32, device=dev)
     cs = torch.zeros((8, 16), dtype=torch.float32, device=dev)
     q = torch.zeros(4096, dtype=torch.bfloat16, device=dev)
     L = _lib.lib()
-    rk = _lib.RopeKvArgs(VP(lens.data_ptr()), 1, 2, 1, 16, VP(cs.data_ptr()), VP(cs.data_ptr()), 8, 1,
+    rk = _lib.RopeKvArgs(VP(lens.data_ptr()), 1, 2, 1, 8, VP(cs.data_ptr()), VP(cs.data_ptr()), 8, 1,
                          VP(q.data_ptr()), VP(q.data_ptr()), VP(q.data_ptr()), 64, 16, 16, 4)
-    # d = 16 is not a whole 32-row tile of rotate-half pairs
-    assert L.vnx_gemm_bf16_rope_kv(VP(x.data_ptr()), 64, VP(wp.data_ptr()), 4, 64, 64, ctypes.byref(rk),
-                                   _st()) == _lib.VNX_ERR_UNSUPPORTED
-    rk.d = 32
+    args = lambda N: (VP(x.data_ptr()), 128, VP(wq.data_ptr()), 64, VP(sc.data_ptr()), _lib.VNX_F16, 1, 4, N, 128,
+                      128, ctypes.byref(rk), _st())
+    # d = 8 is not a whole 16-row tile of rotate-half pairs
+    assert L.vnx_gemv_w4_rope_kv(*args(32)) == _lib.VNX_ERR_UNSUPPORTED
+    rk.d, rk.c_sr = 32, 32
     # N must be (H + 2 Hkv) d
-    assert L.vnx_gemm_bf16_rope_kv(VP(x.data_ptr()), 64, VP(wp.data_ptr()), 4, 96, 64, ctypes.byref(rk),
-                                   _st()) == _lib.VNX_ERR_INVALID_ARG
+    assert L.vnx_gemv_w4_rope_kv(*args(96)) == _lib.VNX_ERR_INVALID_ARG
+    # rows must be whole sequences of n tokens
+    rk.n = 3
+    assert L.vnx_gemv_w4_rope_kv(*args(128)) == _lib.VNX_ERR_INVALID_ARG

@@ -102,7 +102,6 @@ class RopeKvArgs(ctypes.Structure):
 
 
 SIGNATURES.update({
-    "vnx_gemm_bf16_rope_kv": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.POINTER(RopeKvArgs), _vp]),
     "vnx_gemv_w4_rope_kv": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
                                    ctypes.POINTER(RopeKvArgs), _vp]),
     "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),

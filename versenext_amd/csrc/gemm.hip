@@ -49,7 +49,6 @@ struct VgParams {
   int M, N, K;             // N = rows of W
   int mt, nt, ng;          // 32-row tiles of M and N; N groups of WN tiles
   int order;               // 0: M tiles of an N group on one XCD; 1: M tiles adjacent
-  RopeOut ro;              // EPI 2
 };
 
 template <int OT>
@@ -161,24 +160,6 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   if (ni >= p.nt) return;
 
   // lane holds D[row 8i + 4h + e][col r] in acc[4i + e]
-  if constexpr (EPI == 2) {
-    // RoPE + cache store: tile ni of head hh holds dims qb*16 + r (r < 16)
-    // and d/2 + qb*16 + r - 16 (r >= 16), so lanes r and r ^ 16 are partners
-    float part[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) part[i] = __shfl_xor(acc[i], 16);
-    const int hh = ni * 32 / p.ro.d;
-    const int qb = (ni * 32 - hh * p.ro.d) / 32;
-    const int dim = r < 16 ? qb * 16 + r : p.ro.d / 2 + qb * 16 + (r - 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + 8 * i + 4 * h + e;
-        if (m < p.M) rope_store(p.ro, m, hh, dim, acc[4 * i + e], part[4 * i + e]);
-      }
-    return;
-  }
   char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
   if constexpr (EPI == 0) {
     const int n = ni * 32 + r;
@@ -534,37 +515,6 @@ int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed,
   if (y_dtype == VNX_F32) go(IntC<0>{});
   else if (y_dtype == VNX_BF16) go(IntC<1>{});
   else go(IntC<2>{});
-  VNX_LAUNCH_CHECK();
-  return VNX_OK;
-}
-
-int vnx_gemm_bf16_rope_kv(const void* x, int64_t ldx, const void* w_packed, int64_t M, int64_t N, int64_t K,
-                          const vnx_rope_kv_args* rk, void* stream) {
-  if (!x || !w_packed || !rk || M < 0 || N <= 0 || K <= 0 || ldx < K) return VNX_ERR_INVALID_ARG;
-  VgParams p{};
-  const int st = rope_out_from(rk, N, &p.ro);
-  if (st) return st;
-  if (M % rk->n) return VNX_ERR_INVALID_ARG;  // rows are whole sequences of n tokens
-  if (M == 0) return VNX_OK;
-  if (K % kVgChunk || ldx % 8 || !aligned16(x) || !aligned16(w_packed)) return VNX_ERR_UNSUPPORTED;
-  if (M >= INT32_MAX || N >= INT32_MAX || K >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
-  p.x = static_cast<const uint16_t*>(x); p.w = static_cast<const uint16_t*>(w_packed);
-  p.ldx = ldx;
-  p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  p.mt = (int)((M + 31) / 32);
-  p.nt = (int)((N + 31) / 32);
-  const int64_t cus = device_cus();
-  int wn = 4;
-  while (wn > 1 && (int64_t)p.mt * ((p.nt + wn - 1) / wn) < cus * 3 / 4) wn /= 2;
-  p.ng = (p.nt + wn - 1) / wn;
-  p.order = 0;
-  const int64_t groups = (p.ng + kVgXcds - 1) / kVgXcds;
-  const int64_t wgs = groups * kVgXcds * p.mt;
-  if (wgs >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (wn == 4) hipLaunchKernelGGL((k_vgemm<1, 2, 4>), dim3((unsigned)wgs), dim3(256), 0, s, p);
-  else if (wn == 2) hipLaunchKernelGGL((k_vgemm<1, 2, 2>), dim3((unsigned)wgs), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((k_vgemm<1, 2, 1>), dim3((unsigned)wgs), dim3(256), 0, s, p);
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }

@@ -509,7 +509,7 @@ inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 int rope_out_from(const vnx_rope_kv_args* a, int64_t N, RopeOut* out) {
   if (!a || !a->lens || !a->q_out || !a->k_cache || !a->v_cache) return VNX_ERR_INVALID_ARG;
   if (a->n < 1 || a->H < 1 || a->Hkv < 1 || a->d < 2) return VNX_ERR_INVALID_ARG;
-  if (a->d % 32) return VNX_ERR_UNSUPPORTED;  // whole 32-row tiles of rotate-half pairs per head
+  if (a->d % 16) return VNX_ERR_UNSUPPORTED;  // whole 16-row tiles of rotate-half pairs per head
   if ((int64_t)(a->H + 2 * a->Hkv) * a->d != N) return VNX_ERR_INVALID_ARG;
   if (a->c_sb < 0 || a->c_sh < 0 || a->c_sr < a->d || a->cap < 1) return VNX_ERR_INVALID_ARG;
   if (a->rope && (!a->cos_table || !a->sin_table || a->table_rows < 1)) return VNX_ERR_INVALID_ARG;

@@ -407,12 +407,35 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
     const int t = blockIdx.x;
     const int hh = t * 16 / p.ro.d;
     const int qb = (t * 16 - hh * p.ro.d) / 16;
+    // one token row, four consecutive dims (all loads before any use)
+    const RopeOut& ro = p.ro;
+    const int m = (int)(p.row_off + b);  // rows < 2^31: 32-bit division
+    const int64_t bs = m / ro.n;
+    const int ti = m - (int)bs * ro.n;
+    const int64_t pos = (int64_t)ro.lens[bs] + ti;
+    if (pos < 0 || pos >= ro.cap) return;
+    const int dim0 = kq < 2 ? qb * 8 + 4 * kq : ro.d / 2 + qb * 8 + 4 * (kq - 2);
+    float y[4] = {v[0], v[1], v[2], v[3]};
+    if (ro.rope && hh < ro.H + ro.Hkv) {
+      float c[4], sn[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int rho = 4 * kq + j;
-      const int dim = rho < 8 ? qb * 8 + rho : p.ro.d / 2 + qb * 8 + (rho - 8);
-      rope_store(p.ro, p.row_off + b, hh, dim, v[j], part[j]);
+      for (int j = 0; j < 4; ++j) {
+        c[j] = ro.cos[pos * ro.d + dim0 + j];
+        sn[j] = ro.sin[pos * ro.d + dim0 + j];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // y[j] = x[j] cos[j] - x[j + d/2] sin[j];  y[j + d/2] = x[j + d/2] cos + x[j] sin
+        const float sp = kq < 2 ? -part[j] : part[j];
+        y[j] = v[j] * c[j] + sp * sn[j];
+      }
     }
+    uint16_t* dst;
+    if (hh < ro.H) dst = ro.q + ((bs * ro.H + hh) * ro.n + ti) * (int64_t)ro.d;
+    else if (hh < ro.H + ro.Hkv) dst = ro.kc + bs * ro.c_sb + (int64_t)(hh - ro.H) * ro.c_sh + pos * ro.c_sr;
+    else dst = ro.vc + bs * ro.c_sb + (int64_t)(hh - ro.H - ro.Hkv) * ro.c_sh + pos * ro.c_sr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[dim0 + j] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y[j]));
     return;
   }
   if constexpr (QE == 1) {

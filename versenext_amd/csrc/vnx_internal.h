@@ -1,5 +1,5 @@
 // Helpers shared by the vnx entry points (host side, plus the RoPE / KV-cache
-// store that the projection epilogues share).
+// arguments of the projection epilogue).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -118,27 +118,6 @@ struct RopeOut {
   int64_t c_sb, c_sh, c_sr, cap;
   int n, H, Hkv, d, rope;
 };
-
-// Stores element `dim` of head hh (q heads, then k, then v) for row m: own is
-// the projection's value at dim, partner its rotate-half partner (dim +- d/2).
-__device__ __forceinline__ void rope_store(const RopeOut& r, int64_t m, int hh, int dim, float own, float partner) {
-  const int64_t b = m / r.n;
-  const int ti = (int)(m - b * r.n);
-  const int64_t pos = (int64_t)r.lens[b] + ti;
-  if (pos < 0 || pos >= r.cap) return;
-  float y = own;
-  if (r.rope && hh < r.H + r.Hkv) {
-    // y[j] = x[j] cos[j] - x[j + d/2] sin[j];  y[j + d/2] = x[j + d/2] cos + x[j] sin
-    const float c = r.cos[pos * r.d + dim], s = r.sin[pos * r.d + dim];
-    const float sp = dim < r.d / 2 ? -partner : partner;
-    y = own * c + sp * s;
-  }
-  uint16_t* dst;
-  if (hh < r.H) dst = r.q + ((b * r.H + hh) * r.n + ti) * (int64_t)r.d;
-  else if (hh < r.H + r.Hkv) dst = r.kc + b * r.c_sb + (int64_t)(hh - r.H) * r.c_sh + pos * r.c_sr;
-  else dst = r.vc + b * r.c_sb + (int64_t)(hh - r.H - r.Hkv) * r.c_sh + pos * r.c_sr;
-  dst[dim] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y));
-}
 
 // Fills a RopeOut from the public argument block; VNX_OK or an error status.
 int rope_out_from(const vnx_rope_kv_args* a, int64_t N, RopeOut* out);

@@ -262,7 +262,7 @@ class _Linear:
 
     def __init__(self, w: torch.Tensor, dtype, hip, int4: bool, swiglu: bool = False, rope_head_dim: int = 0):
         self.N, self.K = w.shape
-        self.wp_rope = self.wq_rope = None
+        self.wq_rope = None
         self.dtype = dtype
         self.hip = hip
         self.int4 = bool(int4) and self.K % 128 == 0
@@ -277,7 +277,7 @@ class _Linear:
                 H = self.N // 2
                 self.wq_sw = wq.view(2, H // 8, 8, -1).transpose(0, 1).reshape(self.N, -1).contiguous()
                 self.sc_sw = sc.view(2, H // 8, 8, -1).transpose(0, 1).reshape(self.N, -1).contiguous()
-            if rope_head_dim and rope_head_dim % 32 == 0 and self.N % rope_head_dim == 0:
+            if rope_head_dim and rope_head_dim % 16 == 0 and self.N % rope_head_dim == 0:
                 # rows in the order of vnx_gemv_w4_rope_kv's epilogue
                 perm = rope_rows(self.N // rope_head_dim, rope_head_dim, 8).to(wq.device)
                 self.wq_rope, self.sc_rope = wq[perm].contiguous(), sc[perm].contiguous()
@@ -303,10 +303,7 @@ class _Linear:
                                            ctypes.c_void_p(self.wp.data_ptr()),
                                            ctypes.c_void_p(torch.cuda.current_stream(hip.torch_device).cuda_stream)),
                            "pack_bf16")
-                if rope_head_dim and rope_head_dim % 32 == 0 and self.N % rope_head_dim == 0:
-                    # a second packed copy in the order of vnx_gemm_bf16_rope_kv's epilogue
-                    perm = rope_rows(self.N // rope_head_dim, rope_head_dim, 16).to(self.wd.device)
-                    self.wp_rope = _pack(self.wd[perm].contiguous(), hip)
+
 
     GEMM_MAX_M = 256
 
@@ -329,17 +326,13 @@ class _Linear:
 
     def rope_kv(self, x: torch.Tensor, rk) -> bool:
         """The q|k|v projection of x with RoPE and the KV-cache write fused
-        (vnx_gemm_bf16_rope_kv for bf16 rows, M <= GEMM_MAX_M;
-        vnx_gemv_w4_rope_kv for INT4 weights, M <= 64); False (nothing done)
-        when neither applies."""
+        (vnx_gemv_w4_rope_kv, INT4 weights, M <= 64); False (nothing done)
+        when it does not apply.  (The bf16 verify projection keeps a separate
+        vnx_rope_kv: in its GEMM's epilogue the store pattern cost more than
+        the launch it saves.)"""
         M = x.shape[0]
         st = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
         L = self.hip._L
-        if self.wp_rope is not None and M <= self.GEMM_MAX_M and x.dtype == torch.bfloat16 and x.stride(1) == 1:
-            _lib.check(L.vnx_gemm_bf16_rope_kv(ctypes.c_void_p(x.data_ptr()), x.stride(0),
-                                               ctypes.c_void_p(self.wp_rope.data_ptr()), M, self.N, self.K,
-                                               ctypes.byref(rk), st), "gemm_bf16_rope_kv")
-            return True
         if self.wq_rope is not None and M <= 64:
             x16 = x.to(torch.float16).contiguous()
             _lib.check(L.vnx_gemv_w4_rope_kv(
@@ -424,7 +417,7 @@ class CometSparkGPU:
             gv = (g @ wv.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
             L = _Layer(kind=kind, norm1=W[p + "norm1.weight"], norm2=W[p + "norm2.weight"],
                        wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4,
-                                    rope_head_dim=d if dtype == torch.bfloat16 else 0),
+                                    rope_head_dim=d if dtype == torch.bfloat16 and int4 else 0),
                        proj=_Linear(W[p + "attn.proj.weight"], dtype, hip, int4),
                        gk=gk.to(dtype).contiguous(), gv=gv.to(dtype).contiguous(),
                        gates=torch.sigmoid(W[p + "attn.gate_logits"].float()).contiguous())
