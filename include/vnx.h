@@ -450,10 +450,14 @@ int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int 
  * routing weights into comb.  The router Linear (mod.py:337-440,
  * `self.gate(router_input)`) and the top-k rule in one launch.  With x_out
  * (bf16, not NULL) it also writes `copies` bf16 copies of h, copy q at
- * x_out + q*sxo (row pitch ldxo): the experts' input rows. */
-int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, int64_t M, int64_t D, int P, int E,
-                    int topk, float* comb, int64_t ldc, void* x_out, int64_t ldxo, int64_t sxo, int copies,
-                    void* stream);
+ * x_out + q*sxo (row pitch ldxo): the experts' input rows.  With norm_w
+ * (not NULL) h is the raw residual row and the routing input is its RMSNorm,
+ * RMSNorm(h) = h * rstd * norm_w, rstd = 1/sqrt(mean(h^2) + eps) (the block's
+ * norm2 fused: the products use h * norm_w and the logits are scaled by
+ * rstd; the bf16 copies are bf16(h * rstd * norm_w)). */
+int vnx_mod_route_x(const float* h, int64_t ldh, const float* norm_w, float eps, const float* wr, int64_t ldw,
+                    int64_t M, int64_t D, int P, int E, int topk, float* comb, int64_t ldc, void* x_out, int64_t ldxo,
+                    int64_t sxo, int copies, void* stream);
 
 /* The routed, weighted expert activations (DensePart / Expert,
  * mod.py:466-600): for row m and expert x < PE, with g = gu + m*ldg + x*sxg
@@ -472,9 +476,10 @@ int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, floa
  * with slots[m*E + z] >= 0, of y[z*syb + slots[m*E + z]*ldy + c], c < D: the
  * expert sum of MoDLayer.forward (mod.py:779-803) over compact per-expert
  * outputs (vnx_expert_gemm_bf16's row lists).  Equal to vnx_sum_experts of
- * the dense outputs, whose unrouted rows are zero. */
+ * the dense outputs, whose unrouted rows are zero.  accumulate != 0: out[m*ldo
+ * + c] += that sum (the block's residual add, x + sum). */
 int vnx_sum_expert_rows(const void* y, int dtype, int64_t ldy, int64_t syb, const int32_t* slots, int64_t M,
-                        int E, int64_t D, float* out, int64_t ldo, void* stream);
+                        int E, int64_t D, float* out, int64_t ldo, int accumulate, void* stream);
 
 /* Commit of one speculative round for all B sequences (the accept-and-advance
  * step of SpeculativeDecoder.verify_then_commit, packages/verse_nex/
@@ -521,6 +526,21 @@ int vnx_pack_bf16(const void* w, int64_t ldw, int64_t N, int64_t K, void* out, v
 int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
                   int64_t N, int64_t K, int batch, int epilogue, const float* comb, int64_t ldc, void* y,
                   int y_dtype, int64_t ldy, int64_t syb, void* stream);
+
+/* vnx_gemm_bf16 (batch 1) whose input is RMSNorm of the fp32 rows x (M, K),
+ * row pitch ldx (vnnn.py:593-615, the block's norm1 / norm2 fused):
+ *   acc[m, n] = rstd_m * sum_k bf16(x[m, k] * norm_w[k]) * W[n, k],
+ *   rstd_m = 1/sqrt(mean_k x[m, k]^2 + eps),
+ * then the epilogue (VNX_EPI_NONE or VNX_EPI_SWIGLU) into bf16 y.  K <= 2048;
+ * x and norm_w 16-byte aligned, ldx % 4 == 0. */
+int vnx_gemm_bf16_norm(const float* x, int64_t ldx, const float* norm_w, float eps, const void* w_packed,
+                       int64_t M, int64_t N, int64_t K, int epilogue, void* y, int64_t ldy, void* stream);
+
+/* vnx_gemm_bf16 (batch 1) with the residual add fused: res[m*ldr + n] +=
+ * acc[m, n] (fp32), the `x = x + proj(...)` of VerseNexBlock.forward
+ * (cometspark.py:236-247). */
+int vnx_gemm_bf16_residual(const void* x, int64_t ldx, const void* w_packed, int64_t M, int64_t N, int64_t K,
+                           float* res, int64_t ldr, void* stream);
 
 /* Routed MoD expert products (the expert FFNs of DensePart / Expert,
  * packages/verse_nex/verse_nex/mod.py:466-600, evaluated only on the rows

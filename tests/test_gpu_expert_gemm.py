@@ -178,9 +178,16 @@ def test_compact_second_product_and_sum(hip):
     slots = ref_slots.to(dev)
     out = torch.empty((M, N), dtype=torch.float32, device=dev)
     _lib.check(L.vnx_sum_expert_rows(VP(y.data_ptr()), _lib.VNX_BF16, N, M * N, VP(slots.data_ptr()), M, E, N,
-                                     VP(out.data_ptr()), N, _st()), "sum_rows")
+                                     VP(out.data_ptr()), N, 0, _st()), "sum_rows")
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), out_dense.cpu())
+    # accumulate: res + the sum, as the residual add rounds it
+    res = torch.randn((M, N), generator=g, device=dev)
+    res0 = res.clone()
+    _lib.check(L.vnx_sum_expert_rows(VP(y.data_ptr()), _lib.VNX_BF16, N, M * N, VP(slots.data_ptr()), M, E, N,
+                                     VP(res.data_ptr()), N, 1, _st()), "sum_rows accumulate")
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), (res0 + out_dense).cpu())
 
 
 def test_rejects(hip):

@@ -139,3 +139,68 @@ def test_rejects_bad_shapes(hip):
                            P(y.data_ptr()), _lib.VNX_F32, 64, 0, st) == _lib.VNX_ERR_INVALID_ARG
     # packing needs K a multiple of 64
     assert L.vnx_pack_bf16(P(w.data_ptr()), 64, 64, 32, P(wp.data_ptr()), st) == _lib.VNX_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(224, 2048, 1024, 0), (224, 5504, 1024, 1), (37, 96, 192, 0),
+                                       (5, 64, 2048, 1), (257, 40, 64, 0)])
+def test_norm_input(hip, M, N, K, epi):
+    """vnx_gemm_bf16_norm: the staged operand is bf16(x * w) exactly as torch
+    rounds it, so the reference is that bf16 matrix times W in fp64, scaled by
+    the fp64 rstd of the fp32 rows; the GEMM bar plus rstd's fp32 error
+    (1e-6 relative) plus one bf16 rounding of the output."""
+    _say(f"gemm norm M={M} N={N} K={K} epi={epi}")
+    dev = hip.torch_device
+    g = torch.Generator(device=dev)
+    g.manual_seed(M + N + K)
+    x = torch.randn((M, K), generator=g, device=dev) * 2.0
+    nw = torch.rand((K,), generator=g, device=dev) + 0.5
+    w = (torch.randn((1, N, K), generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wp, _ = _pack(w)
+    eps = 1e-6
+    ncols = N // 2 if epi else N
+    y = torch.empty((M, ncols), dtype=torch.bfloat16, device=dev)
+    _lib.check(_lib.lib().vnx_gemm_bf16_norm(P(x.data_ptr()), K, P(nw.data_ptr()), eps, P(wp.data_ptr()), M, N, K,
+                                             epi, P(y.data_ptr()), ncols, P(torch.cuda.current_stream().cuda_stream)),
+               "gemm_norm")
+    torch.cuda.synchronize()
+    xs = (x * nw).to(torch.bfloat16).double().cpu()                   # the staged operand
+    xd = x.double().cpu()
+    rstd = 1.0 / torch.sqrt((xd * xd).mean(dim=1, keepdim=True) + eps)
+    wd = w[0].double().cpu()
+    acc = (xs @ wd.t()) * rstd
+    mag = (xs.abs() @ wd.abs().t()) * rstd
+    if epi:
+        blk = torch.arange(N).view(-1, 32)
+        gi, ui = blk[:, :16].reshape(-1), blk[:, 16:].reshape(-1)
+        g_, u_ = acc[:, gi], acc[:, ui]
+        silu = g_ * torch.sigmoid(g_)
+        ref = silu * u_
+        tol = (RTOL + 1e-6) * (1.1 * mag[:, gi] * u_.abs() + silu.abs() * mag[:, ui]) + 2.0 ** -8 * ref.abs()
+    else:
+        ref = acc
+        tol = (RTOL + 1e-6) * mag + 2.0 ** -8 * ref.abs()
+    err = (y.double().cpu() - ref).abs()
+    worst = float((err / (tol + 1e-300)).max())
+    assert bool((err <= tol + 1e-30).all()), f"worst err / bound = {worst:.3e}"
+    _say(f"  worst err / bound = {worst:.2e}")
+
+
+@pytest.mark.parametrize("M,N,K", [(224, 1024, 1024), (224, 1024, 2752), (9, 100, 64)])
+def test_residual_epilogue(hip, M, N, K):
+    """vnx_gemm_bf16_residual: res += x . W^T in fp32; the GEMM bar plus one
+    fp32 rounding of the sum."""
+    _say(f"gemm residual M={M} N={N} K={K}")
+    x, w = _inputs(hip, 1, 1, M, N, K, seed=N + K)
+    wp, _ = _pack(w)
+    g = torch.Generator(device=hip.torch_device)
+    g.manual_seed(3)
+    res = torch.randn((M, N), generator=g, device=hip.torch_device)
+    res0 = res.double().cpu()
+    _lib.check(_lib.lib().vnx_gemm_bf16_residual(P(x.data_ptr()), K, P(wp.data_ptr()), M, N, K, P(res.data_ptr()), N,
+                                                 P(torch.cuda.current_stream().cuda_stream)), "gemm_residual")
+    torch.cuda.synchronize()
+    xd, wd = x[0].double().cpu(), w[0].double().cpu()
+    ref = res0 + xd @ wd.t()
+    mag = xd.abs() @ wd.abs().t()
+    err = (res.double().cpu() - ref).abs()
+    assert bool((err <= RTOL * mag + 2.0 ** -24 * ref.abs() + 1e-30).all())

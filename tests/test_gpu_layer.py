@@ -174,26 +174,37 @@ def test_mod_swiglu_and_sum(hip, M, PE, He, layout, odt):
         _close(s, ref_s, torch.float32, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("M,D,NP,NE,topk", [(224, 1024, 4, 4, 2), (5, 100, 2, 3, 1), (33, 64, 1, 8, 3)])
-def test_mod_route_from_hidden(hip, M, D, NP, NE, topk):
+def test_mod_route_from_hidden(hip, M, D, NP, NE, topk, norm):
     """vnx_mod_route_x (router products + routing) against torch fp32
     logits and the reference rule: softmax over all part logits, per part the
-    top-k expert logits (ties to the lower index) re-softmaxed."""
-    _say(f"mod_route_x M={M} D={D} P={NP} E={NE} topk={topk}")
+    top-k expert logits (ties to the lower index) re-softmaxed.  norm: the
+    input is the raw row and the kernel applies RMSNorm (fp64 reference of
+    x * rstd * w; the bf16 copies within one rounding)."""
+    _say(f"mod_route_x M={M} D={D} P={NP} E={NE} topk={topk} norm={norm}")
     dev = hip.torch_device
     g = _gen(hip, M + D + NP * NE)
-    h = torch.randn((M, D), generator=g, device=dev)
+    h = torch.randn((M, D), generator=g, device=dev) * (3.0 if norm else 1.0)
+    nw = torch.rand((D,), generator=g, device=dev) + 0.5
+    eps = 1e-6
     R = NP + NP * NE
     wr = torch.randn((R, D), generator=g, device=dev) * 0.02   # router init scale: logits of order 1
     comb = torch.empty((M, NP * NE), dtype=torch.float32, device=dev)
     copies = 3
     xo = torch.empty((copies, M, D), dtype=torch.bfloat16, device=dev)
-    _lib.check(_lib.lib().vnx_mod_route_x(P(h.data_ptr()), D, P(wr.data_ptr()), D, M, D, NP, NE, topk,
-                                          P(comb.data_ptr()), NP * NE, P(xo.data_ptr()), D, M * D, copies, _st()),
-               "mod_route_x")
+    _lib.check(_lib.lib().vnx_mod_route_x(P(h.data_ptr()), D, P(nw.data_ptr()) if norm else None, eps,
+                                          P(wr.data_ptr()), D, M, D, NP, NE, topk, P(comb.data_ptr()), NP * NE,
+                                          P(xo.data_ptr()), D, M * D, copies, _st()), "mod_route_x")
     torch.cuda.synchronize()
-    assert torch.equal(xo.cpu(), h.to(torch.bfloat16).cpu().unsqueeze(0).expand(copies, M, D))
-    lg = (h.double().cpu() @ wr.double().cpu().t())                       # (M, R)
+    hd = h.double().cpu()
+    if norm:
+        hd = hd / torch.sqrt((hd * hd).mean(dim=1, keepdim=True) + eps) * nw.double().cpu()
+        err = (xo.double().cpu() - hd.unsqueeze(0)).abs()
+        assert bool((err <= 2.0 ** -8 * hd.abs().unsqueeze(0) + 1e-6 * hd.abs().unsqueeze(0) + 1e-30).all())
+    else:
+        assert torch.equal(xo.cpu(), h.to(torch.bfloat16).cpu().unsqueeze(0).expand(copies, M, D))
+    lg = (hd @ wr.double().cpu().t())                                      # (M, R)
     pw = torch.softmax(lg[:, :NP], dim=-1)
     ref = torch.zeros((M, NP * NE), dtype=torch.float64)
     for p_ in range(NP):

@@ -39,6 +39,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kVgChunk = 64;  // K per chunk
 constexpr int kVgXcds = 8;    // XCDs the dispatcher deals workgroups over
 constexpr int kVgRowB = 128;  // bytes of one staged X row (64 bf16)
+constexpr int kVgNormMaxK = 2048;  // NX: K of the normalized rows (norm weight staged in LDS)
 
 struct VgParams {
   const uint16_t* x;
@@ -49,7 +50,12 @@ struct VgParams {
   int M, N, K;             // N = rows of W
   int mt, nt, ng;          // 32-row tiles of M and N; N groups of WN tiles
   int order;               // 0: M tiles of an N group on one XCD; 1: M tiles adjacent
+  const float* xf;         // NX: the fp32 rows to normalize (x unused), pitch ldx
+  const float* nw;         // NX: RMSNorm weight (K)
+  float eps;
 };
+
+
 
 template <int OT>
 __device__ __forceinline__ void vg_store(char* y, int64_t off, float v) {
@@ -69,13 +75,20 @@ __device__ __forceinline__ int xs_off(int r, int c16) { return r * kVgRowB + ((c
 
 // EPI 0: y[m, n] = acc.  EPI 1 (SwiGLU): W rows come in blocks of 32, the
 // first 16 the gate rows and the last 16 the up rows of hidden units
-// blk*16 .. +16; y[m, blk*16 + c] = comb * silu(gate) * up.
-template <int OT, int EPI, int WN>
+// blk*16 .. +16; y[m, blk*16 + c] = comb * silu(gate) * up.  EPI 3
+// (residual): y fp32, y[m, n] += acc.
+// NX: X is RMSNorm(xf) (vnnn.py:593-615): rows of xf times the norm weight
+// are staged as bf16, each thread also summing the squares of its row's
+// values, and the epilogue scales row m by rstd_m = 1/sqrt(mean x^2 + eps)
+// (the norm's per-row factor, applied to the fp32 accumulators).
+template <int OT, int EPI, int WN, bool NX = false>
 __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   constexpr int WK = 4 / WN;
   constexpr int SLAB = WK * 32 * kVgRowB;  // staged X bytes per pass (WK chunks)
   constexpr int RED = 3 * 64 * 64;         // K-split partial tiles
   __shared__ __attribute__((aligned(16))) char smem[2 * SLAB > RED ? 2 * SLAB : RED];
+  __shared__ float rsd[NX ? 32 : 1];
+  __shared__ __attribute__((aligned(16))) float nws[NX ? kVgNormMaxK : 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WN, wk = wave / WN;
   const int z = blockIdx.y;
@@ -100,23 +113,43 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   // X staging: thread tid loads, for j < WK, chunk (pass*WK + j), row
   // tid / 8, 16-byte column tid % 8.
   const int xr = tid >> 3, xc = tid & 7;
-  const uint16_t* xrow = p.x + z * p.sxb + (int64_t)min(m0 + xr, p.M - 1) * p.ldx + xc * 8;
+  const int xrc = min(m0 + xr, p.M - 1);
+  const uint16_t* xrow = p.x + z * p.sxb + (int64_t)xrc * p.ldx + xc * 8;
+  const float* xfrow = NX ? p.xf + (int64_t)xrc * p.ldx + xc * 8 : nullptr;
   const uint32_t xkeep = m0 + xr < p.M ? 0xFFFFFFFFu : 0u;
   const uint16_t* wt = p.w + z * p.swb + (int64_t)nie * nch * 2048 + lane * 8;
 
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  float ss = 0.0f;  // NX: sum of squares of this thread's values of row xr
+  // NX: the norm weight goes to LDS once per workgroup; its loads issue
+  // before the ring's first loads, so their latencies overlap
+  f32x4 nwr[NX ? kVgNormMaxK / 1024 : 1];
+  if constexpr (NX) {
+#pragma unroll
+    for (int i = 0; i < kVgNormMaxK / 1024; ++i) {
+      const int k = (tid + 256 * i) * 4;
+      nwr[i] = k < p.K ? *reinterpret_cast<const f32x4*>(p.nw + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
 
   // Loads run PD passes ahead of the math: pass ps lives in ring slot
-  // ps % PD (the loop is unrolled by PD so the slots are registers).
-  constexpr int PD = WK > 2 ? 2 : 4;
-  u32x4 xv[PD][WK], wv[PD][4];
-  auto load_pass = [&](int ps, u32x4 (&xs)[WK], u32x4 (&ws)[4]) {
+  // ps % PD (the loop is unrolled by PD so the slots are registers).  NX
+  // loads 8 fp32 per chunk instead of 8 bf16.
+  constexpr int PD = NX ? 2 : (WK > 2 ? 2 : 4);
+  constexpr int XW = NX ? 2 : 1;  // 16-byte loads per chunk
+  u32x4 xv[PD][WK][XW], wv[PD][4];
+  auto load_pass = [&](int ps, u32x4 (&xs)[WK][XW], u32x4 (&ws)[4]) {
 #pragma unroll
     for (int j = 0; j < WK; ++j) {
       const int c = min(ps * WK + j, nch - 1);
-      xs[j] = *reinterpret_cast<const u32x4*>(xrow + c * kVgChunk);
+      if constexpr (NX) {
+        xs[j][0] = *reinterpret_cast<const u32x4*>(xfrow + c * kVgChunk);
+        xs[j][1] = *reinterpret_cast<const u32x4*>(xfrow + c * kVgChunk + 4);
+      } else {
+        xs[j][0] = *reinterpret_cast<const u32x4*>(xrow + c * kVgChunk);
+      }
     }
     const int c = min(ps * WK + wk, nch - 1);
 #pragma unroll
@@ -125,14 +158,47 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   };
 #pragma unroll
   for (int j = 0; j < PD; ++j) load_pass(j, xv[j], wv[j]);
+  if constexpr (NX) {
+#pragma unroll
+    for (int i = 0; i < kVgNormMaxK / 1024; ++i) {
+      const int k = (tid + 256 * i) * 4;
+      if (k < p.K) *reinterpret_cast<f32x4*>(&nws[k]) = nwr[i];
+    }
+    __syncthreads();
+  }
   for (int ps0 = 0; ps0 < npass; ps0 += PD) {
 #pragma unroll
     for (int j = 0; j < PD; ++j) {
       const int ps = ps0 + j;
       char* buf = smem + (ps & 1) * SLAB;
 #pragma unroll
-      for (int q = 0; q < WK; ++q)
-        *reinterpret_cast<u32x4*>(buf + q * 32 * kVgRowB + xs_off(xr, xc)) = xv[j][q] & xkeep;
+      for (int q = 0; q < WK; ++q) {
+        u32x4 v;
+        if constexpr (NX) {
+          // bf16(x * w) of 8 consecutive columns; their squares into ss
+          const bool live = ps * WK + q < nch;  // clamped re-reads are not summed
+          const int c = min(ps * WK + q, nch - 1);
+          const f32x4 xa = __builtin_bit_cast(f32x4, xv[j][q][0]), xb = __builtin_bit_cast(f32x4, xv[j][q][1]);
+          const f32x4 wa = *reinterpret_cast<const f32x4*>(&nws[c * kVgChunk + xc * 8]);
+          const f32x4 wb = *reinterpret_cast<const f32x4*>(&nws[c * kVgChunk + xc * 8 + 4]);
+          float t = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t = __builtin_fmaf(xa[e], xa[e], t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t = __builtin_fmaf(xb[e], xb[e], t);
+          ss += live ? t : 0.0f;
+          bf16x8 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = static_cast<__bf16>(xa[e] * wa[e]);
+            o[4 + e] = static_cast<__bf16>(xb[e] * wb[e]);
+          }
+          v = __builtin_bit_cast(u32x4, o);
+        } else {
+          v = xv[j][q][0];
+        }
+        *reinterpret_cast<u32x4*>(buf + q * 32 * kVgRowB + xs_off(xr, xc)) = v & xkeep;
+      }
       const u32x4 wq[4] = {wv[j][0], wv[j][1], wv[j][2], wv[j][3]};
       __syncthreads();  // pass ps's X is staged; the other buffer was read before it
       load_pass(ps + PD, xv[j], wv[j]);  // past the end: clamped re-reads, never used
@@ -147,6 +213,14 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
     }
   }
 
+  if constexpr (NX) {
+    // row xr's sum of squares over its 8 threads (consecutive lanes)
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    if (xc == 0) rsd[xr] = 1.0f / __builtin_sqrtf(ss / (float)p.K + p.eps);
+    if constexpr (WK == 1) __syncthreads();  // else the K-split reduction's barriers order it
+  }
   if constexpr (WK > 1) {
     // K splits 1.. of each N tile -> LDS; split 0 adds them in split order
     __syncthreads();  // the X buffers are dead
@@ -160,7 +234,36 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   if (ni >= p.nt) return;
 
   // lane holds D[row 8i + 4h + e][col r] in acc[4i + e]
+  if constexpr (NX) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * i + e] *= rsd[8 * i + 4 * h + e];
+  }
   char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
+  if constexpr (EPI == 3) {
+    // all 16 residual values load before any is used (rows past M re-read
+    // row M-1 and are not stored), then add and store
+    const int n = ni * 32 + r;
+    if (n >= p.N) return;
+    float* yf = reinterpret_cast<float*>(ybase);
+    float old[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = min(m0 + 8 * i + 4 * h + e, p.M - 1);
+        old[4 * i + e] = yf[(int64_t)m * p.ldy + n];
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 8 * i + 4 * h + e;
+        if (m < p.M) yf[(int64_t)m * p.ldy + n] = old[4 * i + e] + acc[4 * i + e];
+      }
+    return;
+  }
   if constexpr (EPI == 0) {
     const int n = ni * 32 + r;
     if (n >= p.N) return;
@@ -437,6 +540,52 @@ __global__ __launch_bounds__(256) void k_vpack(const uint16_t* w, int64_t ldw, i
   *reinterpret_cast<u32x4*>(out + i * 8) = v;
 }
 
+// Launch shape and template dispatch of k_vgemm (p's pointers, strides and
+// M / N / K set).  epi 3 is the residual epilogue (fp32 y); nx: RMSNorm input
+// (bf16 output only).
+int vg_run(VgParams p, int batch, int epi, int y_dtype, bool nx, hipStream_t s) {
+  p.mt = (int)((p.M + 31) / 32);
+  p.nt = (int)((p.N + 31) / 32);
+  // N tiles per workgroup: the most that still keep about three quarters of
+  // the CUs busy (fewer tiles per workgroup split K over its waves instead)
+  const int64_t cus = device_cus();
+  int wn = 4;
+  while (wn > 1 && (int64_t)p.mt * ((p.nt + wn - 1) / wn) * batch < cus * 3 / 4) wn /= 2;
+  p.ng = (p.nt + wn - 1) / wn;
+  static const int order_env = [] {
+    const char* e = getenv("VNX_VG_ORDER");
+    return e ? atoi(e) : 0;
+  }();
+  p.order = order_env == 1 ? 1 : 0;
+  const int64_t groups = (p.ng + kVgXcds - 1) / kVgXcds;
+  const int64_t wgs = p.order == 0 ? groups * kVgXcds * p.mt : (int64_t)p.ng * p.mt;
+  if (wgs >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)wgs, (unsigned)batch);
+  auto launch = [&](auto ot, auto ep, auto nxc) {
+    constexpr int OT = decltype(ot)::value, EP = decltype(ep)::value;
+    constexpr bool NXC = decltype(nxc)::value;
+    if (wn == 4) hipLaunchKernelGGL((k_vgemm<OT, EP, 4, NXC>), grid, dim3(256), 0, s, p);
+    else if (wn == 2) hipLaunchKernelGGL((k_vgemm<OT, EP, 2, NXC>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((k_vgemm<OT, EP, 1, NXC>), grid, dim3(256), 0, s, p);
+  };
+  if (epi == 3) {
+    launch(IntC<0>{}, IntC<3>{}, BoolC<false>{});
+  } else if (nx) {
+    if (epi == VNX_EPI_SWIGLU) launch(IntC<1>{}, IntC<1>{}, BoolC<true>{});
+    else launch(IntC<1>{}, IntC<0>{}, BoolC<true>{});
+  } else {
+    auto by_epi = [&](auto ot) {
+      if (epi == VNX_EPI_SWIGLU) launch(ot, IntC<1>{}, BoolC<false>{});
+      else launch(ot, IntC<0>{}, BoolC<false>{});
+    };
+    if (y_dtype == VNX_F32) by_epi(IntC<0>{});
+    else if (y_dtype == VNX_BF16) by_epi(IntC<1>{});
+    else by_epi(IntC<2>{});
+  }
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
 }  // namespace
 }  // namespace vnx
 
@@ -481,42 +630,39 @@ int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed,
   p.x = static_cast<const uint16_t*>(x); p.w = static_cast<const uint16_t*>(w_packed); p.y = y; p.comb = comb;
   p.ldx = ldx; p.sxb = sxb; p.swb = swb; p.ldy = ldy; p.syb = syb; p.ldc = ldc;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  p.mt = (int)((M + 31) / 32);
-  p.nt = (int)((N + 31) / 32);
-  // N tiles per workgroup: the most that still keep about three quarters of
-  // the CUs busy (fewer tiles per workgroup split K over its waves instead)
-  const int64_t cus = device_cus();
-  int wn = 4;
-  while (wn > 1 && (int64_t)p.mt * ((p.nt + wn - 1) / wn) * batch < cus * 3 / 4) wn /= 2;
-  p.ng = (p.nt + wn - 1) / wn;
-  static const int order_env = [] {
-    const char* e = getenv("VNX_VG_ORDER");
-    return e ? atoi(e) : 0;
-  }();
-  p.order = order_env == 1 ? 1 : 0;
-  const int64_t groups = (p.ng + kVgXcds - 1) / kVgXcds;
-  const int64_t wgs = p.order == 0 ? groups * kVgXcds * p.mt : (int64_t)p.ng * p.mt;
-  if (wgs >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
-  const dim3 grid((unsigned)wgs, (unsigned)batch);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool sw = epilogue == VNX_EPI_SWIGLU;
-  auto go = [&](auto ot) {
-    constexpr int OT = decltype(ot)::value;
-    if (sw) {
-      if (wn == 4) hipLaunchKernelGGL((k_vgemm<OT, 1, 4>), grid, dim3(256), 0, s, p);
-      else if (wn == 2) hipLaunchKernelGGL((k_vgemm<OT, 1, 2>), grid, dim3(256), 0, s, p);
-      else hipLaunchKernelGGL((k_vgemm<OT, 1, 1>), grid, dim3(256), 0, s, p);
-    } else {
-      if (wn == 4) hipLaunchKernelGGL((k_vgemm<OT, 0, 4>), grid, dim3(256), 0, s, p);
-      else if (wn == 2) hipLaunchKernelGGL((k_vgemm<OT, 0, 2>), grid, dim3(256), 0, s, p);
-      else hipLaunchKernelGGL((k_vgemm<OT, 0, 1>), grid, dim3(256), 0, s, p);
-    }
-  };
-  if (y_dtype == VNX_F32) go(IntC<0>{});
-  else if (y_dtype == VNX_BF16) go(IntC<1>{});
-  else go(IntC<2>{});
-  VNX_LAUNCH_CHECK();
-  return VNX_OK;
+  return vg_run(p, batch, epilogue, y_dtype, false, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemm_bf16_norm(const float* x, int64_t ldx, const float* norm_w, float eps, const void* w_packed,
+                       int64_t M, int64_t N, int64_t K, int epilogue, void* y, int64_t ldy, void* stream) {
+  if (!x || !norm_w || !w_packed || !y || M < 0 || N < 0 || K <= 0 || !(eps >= 0.0f)) return VNX_ERR_INVALID_ARG;
+  if (epilogue != VNX_EPI_NONE && epilogue != VNX_EPI_SWIGLU) return VNX_ERR_INVALID_ARG;
+  const int64_t ncols = epilogue == VNX_EPI_SWIGLU ? N / 2 : N;
+  if (ldx < K || ldy < ncols || (epilogue == VNX_EPI_SWIGLU && N % 32)) return VNX_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return VNX_OK;
+  if (K % kVgChunk || K > kVgNormMaxK || ldx % 4 || !aligned16(x) || !aligned16(norm_w) || !aligned16(w_packed))
+    return VNX_ERR_UNSUPPORTED;
+  if (M >= INT32_MAX || N >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  VgParams p{};
+  p.xf = x; p.nw = norm_w; p.eps = eps;
+  p.x = reinterpret_cast<const uint16_t*>(x);  // not read (NX)
+  p.w = static_cast<const uint16_t*>(w_packed); p.y = y;
+  p.ldx = ldx; p.ldy = ldy;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  return vg_run(p, 1, epilogue, VNX_BF16, true, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemm_bf16_residual(const void* x, int64_t ldx, const void* w_packed, int64_t M, int64_t N, int64_t K,
+                           float* res, int64_t ldr, void* stream) {
+  if (!x || !w_packed || !res || M < 0 || N < 0 || K <= 0 || ldx < K || ldr < N) return VNX_ERR_INVALID_ARG;
+  if (M == 0 || N == 0) return VNX_OK;
+  if (K % kVgChunk || ldx % 8 || !aligned16(x) || !aligned16(w_packed)) return VNX_ERR_UNSUPPORTED;
+  if (M >= INT32_MAX || N >= INT32_MAX || K >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  VgParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.w = static_cast<const uint16_t*>(w_packed); p.y = res;
+  p.ldx = ldx; p.ldy = ldr;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  return vg_run(p, 1, 3, VNX_F32, false, static_cast<hipStream_t>(stream));
 }
 
 int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,

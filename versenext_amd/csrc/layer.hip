@@ -349,17 +349,20 @@ __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t l
 constexpr int kRouteMaxR = 32;
 
 template <int VW>
-__global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw,
-                                                     int64_t D, int P, int E, int topk, float* comb, int64_t ldc,
-                                                     __hip_bfloat16* xo, int64_t ldxo, int64_t sxo, int copies) {
+__global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh, const float* nw, float eps,
+                                                     const float* wr, int64_t ldw, int64_t D, int P, int E, int topk,
+                                                     float* comb, int64_t ldc, __hip_bfloat16* xo, int64_t ldxo,
+                                                     int64_t sxo, int copies) {
   __shared__ float red[4][kRouteMaxR];
   __shared__ float lg[kRouteMaxR];
+  __shared__ float ssr[4];
   const int64_t m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int R = P + P * E;
   float acc[kRouteMaxR];
 #pragma unroll
   for (int r = 0; r < kRouteMaxR; ++r) acc[r] = 0.0f;
+  float ss = 0.0f;  // nw: sum of squares of the raw row
   // thread tid takes columns tid*VW .. +VW of every 256*VW block
   for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
     // every row's load issued unconditionally (rows past R re-read row R-1
@@ -370,7 +373,18 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
     } else {
       x[0] = h[m * ldh + c];
     }
-    if (xo) {  // the experts' bf16 input rows, one copy per expert batch
+    if (nw) {
+      // RMSNorm input: the products use x * w; the per-row factor is applied
+      // to the reduced logits
+      float w[VW];
+      if constexpr (VW == 4) ld4(nw + c, w);
+      else w[0] = nw[c];
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        ss = __builtin_fmaf(x[e], x[e], ss);
+        x[e] *= w[e];
+      }
+    } else if (xo) {  // the experts' bf16 input rows, one copy per expert batch
       __hip_bfloat16* dst = xo + m * ldxo + c;
       for (int q = 0; q < copies; ++q) {
         if constexpr (VW == 4) st4(dst + q * sxo, x);
@@ -398,10 +412,40 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
       if (lane == 0) red[wave][r] = v;
     }
   }
+  if (nw) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, VNX_WAVE);
+    if (lane == 0) ssr[wave] = ss;
+  }
   __syncthreads();
-  if (tid < R) lg[tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+  float rstd = 1.0f;
+  if (nw) rstd = 1.0f / __builtin_sqrtf((((ssr[0] + ssr[1]) + ssr[2]) + ssr[3]) / (float)D + eps);
+  if (tid < R) {
+    const float v = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    lg[tid] = nw ? v * rstd : v;
+  }
   __syncthreads();
   if (wave == 0) route_wave(lane < R ? lg[lane] : 0.0f, P, E, topk, comb + m * ldc);
+  if (nw && xo) {
+    // the experts' bf16 input rows: bf16(x * rstd * w), as RMSNorm rounds them
+    for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
+      float x[VW], w[VW];
+      if constexpr (VW == 4) {
+        ld4(h + m * ldh + c, x);
+        ld4(nw + c, w);
+      } else {
+        x[0] = h[m * ldh + c];
+        w[0] = nw[c];
+      }
+#pragma unroll
+      for (int e = 0; e < VW; ++e) x[e] = x[e] * rstd * w[e];
+      __hip_bfloat16* dst = xo + m * ldxo + c;
+      for (int q = 0; q < copies; ++q) {
+        if constexpr (VW == 4) st4(dst + q * sxo, x);
+        else Elt<__hip_bfloat16>::st(dst + q * sxo, x[0]);
+      }
+    }
+  }
 }
 
 // Expert activations of all PE experts for every row, scaled by the routing
@@ -471,7 +515,7 @@ __global__ __launch_bounds__(256) void k_sum_experts(const TY* y, int64_t MD, in
 template <typename TY, int VW>
 __global__ __launch_bounds__(256) void k_sum_expert_rows(const TY* y, int64_t ldy, int64_t syb,
                                                          const int32_t* slots, int E, int64_t D, float* out,
-                                                         int64_t ldo) {
+                                                         int64_t ldo, int accumulate) {
   constexpr int ZB = 8;  // experts whose loads are in flight together
   const int64_t m = blockIdx.y;
   const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VW;
@@ -497,6 +541,16 @@ __global__ __launch_bounds__(256) void k_sum_expert_rows(const TY* y, int64_t ld
     for (int q = 0; q < ZB; ++q)
 #pragma unroll
       for (int e = 0; e < VW; ++e) acc[e] += sl[q] >= 0 ? v[q][e] : 0.0f;
+  }
+  if (accumulate) {  // out += the expert sum (the block's residual add)
+    if constexpr (VW == 4) {
+      float o[4];
+      ld4(out + m * ldo + c, o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = o[e] + acc[e];
+    } else {
+      acc[0] = out[m * ldo + c] + acc[0];
+    }
   }
   if constexpr (VW == 4) st4(out + m * ldo + c, acc);
   else out[m * ldo + c] = acc[0];
@@ -657,25 +711,26 @@ int vnx_mod_route(const float* logits, int64_t ld, int64_t M, int P, int E, int 
   return VNX_OK;
 }
 
-int vnx_mod_route_x(const float* h, int64_t ldh, const float* wr, int64_t ldw, int64_t M, int64_t D, int P, int E,
-                    int topk, float* comb, int64_t ldc, void* x_out, int64_t ldxo, int64_t sxo, int copies,
-                    void* stream) {
+int vnx_mod_route_x(const float* h, int64_t ldh, const float* norm_w, float eps, const float* wr, int64_t ldw,
+                    int64_t M, int64_t D, int P, int E, int topk, float* comb, int64_t ldc, void* x_out, int64_t ldxo,
+                    int64_t sxo, int copies, void* stream) {
   if (!h || !wr || !comb || M < 0 || D < 1 || P < 1 || E < 1 || topk < 1 || topk > E) return VNX_ERR_INVALID_ARG;
+  if (norm_w && !(eps >= 0.0f)) return VNX_ERR_INVALID_ARG;
   if (x_out && (ldxo < D || copies < 1 || (copies > 1 && sxo < M * ldxo))) return VNX_ERR_INVALID_ARG;
   if (P > kModMaxP || E > kModMaxE || P + P * E > kRouteMaxR) return VNX_ERR_UNSUPPORTED;
   if (ldh < D || ldw < D || ldc < (int64_t)P * E) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
   if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   const bool v4 = D % 4 == 0 && ldh % 4 == 0 && ldw % 4 == 0 && vec4_ok(h, 4) && vec4_ok(wr, 4) &&
-                  (!x_out || (ldxo % 4 == 0 && sxo % 4 == 0 && vec4_ok(x_out, 2)));
+                  (!norm_w || vec4_ok(norm_w, 4)) && (!x_out || (ldxo % 4 == 0 && sxo % 4 == 0 && vec4_ok(x_out, 2)));
   if (v4)
     hipLaunchKernelGGL((k_mod_route_x<4>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h,
-                       ldh, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo, sxo,
-                       x_out ? copies : 0);
+                       ldh, norm_w, eps, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo,
+                       sxo, x_out ? copies : 0);
   else
     hipLaunchKernelGGL((k_mod_route_x<1>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h,
-                       ldh, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo, sxo,
-                       x_out ? copies : 0);
+                       ldh, norm_w, eps, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo,
+                       sxo, x_out ? copies : 0);
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }
@@ -735,7 +790,7 @@ int vnx_sum_experts(const void* y, int dtype, int64_t M, int PE, int64_t D, floa
 }
 
 int vnx_sum_expert_rows(const void* y, int dtype, int64_t ldy, int64_t syb, const int32_t* slots, int64_t M,
-                        int E, int64_t D, float* out, int64_t ldo, void* stream) {
+                        int E, int64_t D, float* out, int64_t ldo, int accumulate, void* stream) {
   if (!y || !slots || !out || M < 0 || E < 1 || D < 1 || ldy < D || syb < 0 || ldo < D) return VNX_ERR_INVALID_ARG;
   if (M == 0) return VNX_OK;
   if (M > 65535) return VNX_ERR_UNSUPPORTED;
@@ -746,10 +801,10 @@ int vnx_sum_expert_rows(const void* y, int dtype, int64_t ldy, int64_t syb, cons
     using TY = decltype(ty);
     if (v4)
       hipLaunchKernelGGL((k_sum_expert_rows<TY, 4>), dim3(blocks_for(D / 4), (unsigned)M), dim3(256), 0, s,
-                         static_cast<const TY*>(y), ldy, syb, slots, E, D, out, ldo);
+                         static_cast<const TY*>(y), ldy, syb, slots, E, D, out, ldo, accumulate);
     else
       hipLaunchKernelGGL((k_sum_expert_rows<TY, 1>), dim3(blocks_for(D), (unsigned)M), dim3(256), 0, s,
-                         static_cast<const TY*>(y), ldy, syb, slots, E, D, out, ldo);
+                         static_cast<const TY*>(y), ldy, syb, slots, E, D, out, ldo, accumulate);
     VNX_LAUNCH_CHECK();
     return (int)VNX_OK;
   });

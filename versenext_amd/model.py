@@ -324,6 +324,34 @@ class _Linear:
             ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16")
         return y
 
+    def gemm_norm(self, x: torch.Tensor, norm_w: torch.Tensor, eps: float, epilogue: int = 0) -> Optional[torch.Tensor]:
+        """vnx_gemm_bf16_norm: RMSNorm(x) * norm_w (x (M, K) fp32 residual rows)
+        times the packed weight, (M, N) or with SwiGLU (M, N/2), bf16; None
+        when this weight or x does not qualify."""
+        M = x.shape[0]
+        if (self.wp is None or M > self.GEMM_MAX_M or x.dtype != torch.float32 or x.stride(1) != 1
+                or self.K > 2048 or (epilogue and not self.swiglu)):
+            return None
+        ncols = self.N // 2 if epilogue else self.N
+        y = torch.empty((M, ncols), dtype=torch.bfloat16, device=x.device)
+        _lib.check(self.hip._L.vnx_gemm_bf16_norm(
+            ctypes.c_void_p(x.data_ptr()), x.stride(0), ctypes.c_void_p(norm_w.data_ptr()), float(eps),
+            ctypes.c_void_p(self.wp.data_ptr()), M, self.N, self.K, int(epilogue), ctypes.c_void_p(y.data_ptr()),
+            ncols, ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16_norm")
+        return y
+
+    def gemm_residual(self, x: torch.Tensor, res: torch.Tensor) -> bool:
+        """res (M, N) fp32 += x . W^T (vnx_gemm_bf16_residual); False (nothing
+        done) when this weight or x does not qualify."""
+        M = x.shape[0]
+        if self.wp is None or M > self.GEMM_MAX_M or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+            return False
+        _lib.check(self.hip._L.vnx_gemm_bf16_residual(
+            ctypes.c_void_p(x.data_ptr()), x.stride(0), ctypes.c_void_p(self.wp.data_ptr()), M, self.N, self.K,
+            ctypes.c_void_p(res.data_ptr()), res.stride(0),
+            ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16_residual")
+        return True
+
     def rope_kv(self, x: torch.Tensor, rk) -> bool:
         """The q|k|v projection of x with RoPE and the KV-cache write fused
         (vnx_gemv_w4_rope_kv, INT4 weights, M <= 64); False (nothing done)
@@ -562,6 +590,42 @@ class CometSparkGPU:
             res = res + torch.where(use_c, Ly.gates[2] * out_c, torch.zeros_like(out_c))
         return res
 
+    def _mod_fused(self, L: _Layer, x: torch.Tensor) -> None:
+        """The MoD FFN of a verify-size forward with norm2 and the residual
+        add fused: x (M, D) fp32 residual stream += MoD(RMSNorm(x) * norm2).
+        vnx_mod_route_x normalizes, routes and writes the experts' bf16 input
+        rows; vnx_expert_gemm_bf16 runs each expert on its routed rows only
+        (gate|up with SwiGLU and routing weight fused, then down on the compact
+        rows); vnx_sum_expert_rows adds each row's experts into x."""
+        cfg = self.cfg
+        P, E, k = cfg.num_dense_parts, cfg.num_experts_per_part, cfg.top_k
+        PE, He, D = P * E, cfg.expert_hidden_eff, cfg.dim
+        M = x.shape[0]
+        P_ = ctypes.c_void_p
+        L_ = self.hip._L
+        comb = torch.empty((M, PE), dtype=torch.float32, device=self.dev)
+        wr = L.ffn["route"]                                                        # (P + PE, D) fp32
+        xh = torch.empty((M, D), dtype=torch.bfloat16, device=self.dev)
+        _lib.check(L_.vnx_mod_route_x(P_(x.data_ptr()), x.stride(0), P_(L.norm2.data_ptr()), float(cfg.eps),
+                                      P_(wr.data_ptr()), wr.stride(0), M, D, P, E, k, P_(comb.data_ptr()), PE,
+                                      P_(xh.data_ptr()), D, 0, 1, self._st()), "mod_route_x")
+        rows = torch.empty((PE, M), dtype=torch.int32, device=self.dev)
+        counts = torch.empty((PE,), dtype=torch.int32, device=self.dev)
+        slots = torch.empty((M, PE), dtype=torch.int32, device=self.dev)
+        w1p, w2p = L.ffn["w1p"], L.ffn["w2p"]
+        act = torch.empty((PE, M, He), dtype=torch.bfloat16, device=self.dev)
+        _lib.check(L_.vnx_expert_gemm_bf16(
+            P_(xh.data_ptr()), D, 0, P_(w1p.data_ptr()), w1p.stride(0), M, 2 * He, D, PE, _lib.VNX_EPI_SWIGLU,
+            P_(comb.data_ptr()), PE, 1, P_(rows.data_ptr()), P_(counts.data_ptr()), P_(slots.data_ptr()),
+            P_(act.data_ptr()), _lib.VNX_BF16, He, M * He, self._st()), "expert_gemm w1")
+        y = torch.empty((PE, M, D), dtype=torch.bfloat16, device=self.dev)
+        _lib.check(L_.vnx_expert_gemm_bf16(
+            P_(act.data_ptr()), He, M * He, P_(w2p.data_ptr()), w2p.stride(0), M, D, He, PE, _lib.VNX_EPI_NONE,
+            None, 0, 0, None, P_(counts.data_ptr()), None, P_(y.data_ptr()), _lib.VNX_BF16, D, M * D,
+            self._st()), "expert_gemm w2")
+        _lib.check(L_.vnx_sum_expert_rows(P_(y.data_ptr()), _lib.VNX_BF16, D, M * D, P_(slots.data_ptr()), M, PE,
+                                          D, P_(x.data_ptr()), x.stride(0), 1, self._st()), "sum_expert_rows")
+
     def _mod(self, L: _Layer, h: torch.Tensor) -> torch.Tensor:
         """MoD FFN on (M, D) fp32 normalized rows.  Verify-size forwards (bf16,
         M <= 256): the routing weights (vnx_mod_route_x), each expert's
@@ -585,9 +649,9 @@ class CometSparkGPU:
             # fused and its down product on its own rows only, then the sum
             # over each row's experts
             xh = torch.empty((M, D), dtype=torch.bfloat16, device=self.dev)
-            _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), P_(wr.data_ptr()), wr.stride(0), M, D, P, E,
-                                          k, P_(comb.data_ptr()), PE, P_(xh.data_ptr()), D, 0, 1, self._st()),
-                       "mod_route_x")
+            _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), None, 0.0, P_(wr.data_ptr()), wr.stride(0), M,
+                                          D, P, E, k, P_(comb.data_ptr()), PE, P_(xh.data_ptr()), D, 0, 1,
+                                          self._st()), "mod_route_x")
             rows = torch.empty((PE, M), dtype=torch.int32, device=self.dev)
             counts = torch.empty((PE,), dtype=torch.int32, device=self.dev)
             slots = torch.empty((M, PE), dtype=torch.int32, device=self.dev)
@@ -604,15 +668,15 @@ class CometSparkGPU:
                 self._st()), "expert_gemm w2")
             out = torch.empty((M, D), dtype=torch.float32, device=self.dev)
             _lib.check(L_.vnx_sum_expert_rows(P_(y.data_ptr()), _lib.VNX_BF16, D, M * D, P_(slots.data_ptr()), M, PE,
-                                              D, P_(out.data_ptr()), D, self._st()), "sum_expert_rows")
+                                              D, P_(out.data_ptr()), D, 0, self._st()), "sum_expert_rows")
             return out
         if P + PE <= 32 and self.dtype == torch.bfloat16:
             # router products and routing rule in one launch, which also
             # writes the experts' bf16 input rows (one copy per expert)
             xb = torch.empty((PE, M, D), dtype=self.dtype, device=self.dev)
-            _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), P_(wr.data_ptr()), wr.stride(0), M, D, P, E,
-                                          k, P_(comb.data_ptr()), PE, P_(xb.data_ptr()), D, M * D, PE, self._st()),
-                       "mod_route_x")
+            _lib.check(L_.vnx_mod_route_x(P_(h.data_ptr()), h.stride(0), None, 0.0, P_(wr.data_ptr()), wr.stride(0), M,
+                                          D, P, E, k, P_(comb.data_ptr()), PE, P_(xb.data_ptr()), D, M * D, PE,
+                                          self._st()), "mod_route_x")
         else:
             logits = torch.nn.functional.linear(h, wr)                             # (M, P + PE) fp32
             _lib.check(L_.vnx_mod_route(P_(logits.data_ptr()), logits.stride(0), M, P, E, k, P_(comb.data_ptr()),
@@ -683,18 +747,33 @@ class CometSparkGPU:
         use_kernel = self.kernel_attention and n <= 64 and Tmax + n <= cfg.window_size
         pending = None
         for li, L in enumerate(self.layers):
-            h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
+            # verify-size bf16 forwards: the norms and the residual adds live in
+            # the projections (vnx_gemm_bf16_norm / _residual) and in the MoD
+            # routing / expert sum, so x is the up-to-date residual stream
+            fused = (L.wqkv.wp is not None and L.proj.wp is not None and M <= _Linear.GEMM_MAX_M
+                     and self.dtype == torch.bfloat16 and D <= 2048
+                     and pending is None
+                     and ("w1p" in L.ffn if L.kind == "mod" else
+                          (L.ffn["gu"].wp is not None and L.ffn["gu"].swiglu and L.ffn["down"].wp is not None)))
+            h = None
+            qkv = None
             if li == 0:
+                h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
                 self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
+            elif fused:
+                qkv = L.wqkv.gemm_norm(x, L.norm1, cfg.eps)
             else:
+                h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
                 self._rms(x, pending, L.norm1, h)
+                pending = None
             q = torch.empty((B, H, n, d), dtype=self.dtype, device=self.dev)
             kc, vc = self.kc[li], self.vc[li]
             rk = _lib.RopeKvArgs(P(lens.data_ptr()), n, H, Hkv, d, P(self.cos.data_ptr()), P(self.sin.data_ptr()),
                                  self.cos.shape[0], int(cfg.use_rope), P(q.data_ptr()), P(kc.data_ptr()),
                                  P(vc.data_ptr()), kc.stride(0), kc.stride(1), kc.stride(2), self.cap)
-            if not L.wqkv.rope_kv(h, rk):         # projection with RoPE + cache write fused
-                qkv = L.wqkv(h)                                                      # (M, (H+2Hkv) d)
+            if qkv is not None or not L.wqkv.rope_kv(h, rk):   # INT4: projection with RoPE + cache write fused
+                if qkv is None:
+                    qkv = L.wqkv(h)                                                  # (M, (H+2Hkv) d)
                 _lib.check(L_.vnx_rope_kv(
                     P(qkv.data_ptr()), _lib.DTYPE_CODES[qkv.dtype], qkv.stride(0), B, n, H, Hkv, d,
                     P(lens.data_ptr()), P(self.cos.data_ptr()), P(self.sin.data_ptr()), self.cos.shape[0],
@@ -706,6 +785,15 @@ class CometSparkGPU:
             else:
                 o = self._attn_torch(q, li, lens, n, Tmax).permute(0, 2, 1, 3).reshape(M, H * d)
                 o = o.to(self.act_dtype).contiguous()
+            if fused and L.proj.gemm_residual(o, x):
+                # x += proj(o); then the FFN of RMSNorm(x) * norm2, added into x
+                if L.kind == "mod":
+                    self._mod_fused(L, x)
+                else:
+                    act = L.ffn["gu"].gemm_norm(x, L.norm2, cfg.eps, epilogue=_lib.VNX_EPI_SWIGLU)
+                    if act is None or not L.ffn["down"].gemm_residual(act, x):
+                        raise RuntimeError("fused FFN path unavailable for this layer")
+                continue
             a = L.proj(o)
             # MoD layers route on fp32 rows, as the reference does
             h2 = torch.empty((M, D), dtype=torch.float32 if L.kind == "mod" else self.act_dtype, device=self.dev)
