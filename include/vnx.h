@@ -229,18 +229,29 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
  * projections): W (N, K) has its rows interleaved in blocks of 16, the 8 gate
  * rows of hidden units 8t .. 8t+7 then their 8 up rows (N % 16 == 0,
  * N < 32768); y (B, N/2) fp16, row pitch ldy, y[b, j] = silu(acc[b, gate_j])
- * * acc[b, up_j] in fp32, rounded once. */
-int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
-                       int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, void* y,
-                       int64_t ldy, void* stream);
+ * * acc[b, up_j] in fp32, rounded once.
+ * norm_w (here and in vnx_gemv_w4_rope_kv): NULL, x is fp16 (B, K); else x is
+ * the fp32 residual rows (B, K), row pitch ldx, and the product's input is
+ * RMSNorm(x) * norm_w (vnnn.py:593-615, the block's norm fused): fp16(x *
+ * norm_w) times W, each row's sum scaled by rstd = 1/sqrt(mean(x^2) + eps). */
+int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const float* norm_w, float eps, const uint8_t* wq, int64_t ldw,
+                       const void* scales, int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+                       void* y, int64_t ldy, void* stream);
 
 /* vnx_gemv_w4 (group-128 fp16 scales) of a q|k|v projection with RoPE and
  * the KV-cache write in the epilogue (rk; B rows = tokens): rows of W (and of
  * its scales) permuted per head in 16-row tiles: tile t of head h holds dims
  * t*8 .. t*8+7 then d/2 + t*8 .. d/2 + t*8+7.  N = (H + 2*Hkv)*d < 32768. */
-int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
-                        int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const float* norm_w, float eps, const uint8_t* wq, int64_t ldw,
+                        const void* scales, int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
                         const vnx_rope_kv_args* rk, void* stream);
+
+/* vnx_gemv_w4 with the residual add fused: res[b*ldr + n] += (x . W^T)[b, n]
+ * (fp32; N < 32768), the `x = x + proj(...)` of VerseNexBlock.forward
+ * (cometspark.py:236-247) on a quantized projection. */
+int vnx_gemv_w4_residual(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                         int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, float* res,
+                         int64_t ldr, void* stream);
 
 /* W8: wq (N, K) int8, row pitch ldw; scale (N) fp32 per output row (the
  * per-channel INT8 of quantize_int8, quantize.py:187-214).  Replaces

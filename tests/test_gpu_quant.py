@@ -175,7 +175,7 @@ def test_gemv_swiglu_parity(hip, H, K, B):
     xt = torch.from_numpy(x16).to(dev)
     y = torch.full((B, H), float("nan"), dtype=torch.float16, device=dev)
     VP = ctypes.c_void_p
-    _lib.check(_lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0),
+    _lib.check(_lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, None, 0.0, VP(pq.data_ptr()), pq.stride(0),
                                              VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), B, N, K, 128,
                                              VP(y.data_ptr()), H, VP(torch.cuda.current_stream().cuda_stream)),
                "gemv_w4_swiglu")
@@ -192,6 +192,76 @@ def test_gemv_swiglu_parity(hip, H, K, B):
     _say(f"  worst err / bound = {worst:.2e}")
     assert np.all(err <= bound), worst
     # rejects a weight whose rows are not whole 16-row blocks
-    assert _lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0), VP(sq.data_ptr()),
-                                         _lib.VNX_F16, sq.stride(0), B, N - 8, K, 128, VP(y.data_ptr()), H,
+    assert _lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, None, 0.0, VP(pq.data_ptr()), pq.stride(0),
+                                         VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), B, N - 8, K, 128,
+                                         VP(y.data_ptr()), H,
                                          VP(torch.cuda.current_stream().cuda_stream)) == _lib.VNX_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("H,K,B", [(4096, 1024, 32), (64, 256, 17), (1000, 512, 40)])
+def test_gemv_swiglu_norm_input(hip, H, K, B):
+    """vnx_gemv_w4_swiglu with norm_w: the staged operand is fp16(x * w) as
+    numpy rounds the fp32 product, so the reference is that fp16 matrix times
+    the dequantized W in fp64, scaled by the fp64 rstd of the fp32 rows; the
+    SwiGLU bar of the plain test plus rstd's fp32 error (1e-6 relative)."""
+    import ctypes
+    from versenext_amd import _lib
+    _say(f"gemv swiglu norm H={H} K={K} B={B}")
+    N = 2 * H
+    p, s = _quantized("int4_g128", N, K, seed=H + K + 1)
+    rng = np.random.default_rng(B + 3)
+    x = (rng.normal(0, 2.0, (B, K))).astype(np.float32)
+    nw = (rng.random(K) + 0.5).astype(np.float32)
+    eps = 1e-6
+    perm = np.arange(N).reshape(2, H // 8, 8).transpose(1, 0, 2).reshape(-1)
+    dev = hip.torch_device
+    pq = torch.from_numpy(np.ascontiguousarray(p[perm])).to(dev)
+    sq = torch.from_numpy(np.ascontiguousarray(s[perm])).to(dev)
+    xt, nwt = torch.from_numpy(x).to(dev), torch.from_numpy(nw).to(dev)
+    y = torch.full((B, H), float("nan"), dtype=torch.float16, device=dev)
+    VP = ctypes.c_void_p
+    _lib.check(_lib.lib().vnx_gemv_w4_swiglu(VP(xt.data_ptr()), K, VP(nwt.data_ptr()), eps, VP(pq.data_ptr()),
+                                             pq.stride(0), VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), B, N, K,
+                                             128, VP(y.data_ptr()), H, VP(torch.cuda.current_stream().cuda_stream)),
+               "gemv_w4_swiglu norm")
+    torch.cuda.synchronize()
+    xs = (x * nw).astype(np.float16)
+    rstd = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + eps)
+    W = Q.dequantize_int4_g(p, s, (N, K), 128)
+    acc, mag = Q.gemv_ref(xs, W) * rstd, Q.gemv_abs(xs, W) * rstd
+    g, u = acc[:, :H], acc[:, H:]
+    silu = g / (1.0 + np.exp(-g))
+    ref = silu * u
+    bound = (RTOL + 1e-6) * (1.1 * mag[:, :H] * np.abs(u) + np.abs(silu) * mag[:, H:]) + 2.0 ** -11 * np.abs(ref) \
+        + 2.0 ** -25
+    err = np.abs(y.cpu().numpy().astype(np.float64) - ref)
+    worst = float(np.max(err / bound))
+    _say(f"  worst err / bound = {worst:.2e}")
+    assert np.all(err <= bound), worst
+
+
+@pytest.mark.parametrize("N,K,B", [(1024, 1024, 32), (1024, 4096, 32), (100, 256, 40)])
+def test_gemv_residual(hip, N, K, B):
+    """vnx_gemv_w4_residual: res += x . W^T (fp32); the GEMV bar plus one fp32
+    rounding of the sum."""
+    import ctypes
+    from versenext_amd import _lib
+    _say(f"gemv residual N={N} K={K} B={B}")
+    p, s = _quantized("int4_g128", N, K, seed=N + K + 2)
+    rng = np.random.default_rng(B + 5)
+    x16 = rng.normal(0, 1, (B, K)).astype(np.float16)
+    res0 = rng.normal(0, 1, (B, N)).astype(np.float32)
+    dev = hip.torch_device
+    pq, sq = torch.from_numpy(p).to(dev), torch.from_numpy(s).to(dev)
+    xt, res = torch.from_numpy(x16).to(dev), torch.from_numpy(res0).to(dev)
+    VP = ctypes.c_void_p
+    _lib.check(_lib.lib().vnx_gemv_w4_residual(VP(xt.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0),
+                                               VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), B, N, K, 128,
+                                               VP(res.data_ptr()), N, VP(torch.cuda.current_stream().cuda_stream)),
+               "gemv_w4_residual")
+    torch.cuda.synchronize()
+    W = Q.dequantize_int4_g(p, s, (N, K), 128)
+    ref = res0.astype(np.float64) + Q.gemv_ref(x16, W)
+    mag = Q.gemv_abs(x16, W)
+    err = np.abs(res.cpu().numpy().astype(np.float64) - ref)
+    assert np.all(err <= RTOL * mag + 2.0 ** -24 * np.abs(ref) + 1e-30)

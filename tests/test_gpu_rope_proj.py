@@ -54,7 +54,7 @@ def _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, rope, cap):
                            kc.stride(0), kc.stride(1), kc.stride(2), cap)
 
 
-def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap):
+def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap, rtol=RTOL):
     heads = H + 2 * Hkv
     acc = (x64 @ W64.t()).view(B, n, heads, d)
     mag = (x64.abs() @ W64.abs().t()).view(B, n, heads, d)
@@ -72,7 +72,7 @@ def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap):
     rs = rotated.view(1, 1, heads, 1)
     ref = torch.where(rs, acc * c + rot * s, acc)
     arot = torch.where(rs, (acc * c).abs() + (rot * s).abs(), acc.abs())
-    bound = torch.where(rs, RTOL * (mag * c.abs() + mrot * s.abs()), RTOL * mag) + 1e-6 * arot \
+    bound = torch.where(rs, rtol * (mag * c.abs() + mrot * s.abs()), rtol * mag) + 1e-6 * arot \
         + 2.0 ** -8 * ref.abs() + 1e-30
     qg, kg, vg = q.double().cpu(), kc.double().cpu(), vc.double().cpu()
     worst = 0.0
@@ -98,10 +98,14 @@ def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap):
     _say(f"  worst err / bound = {worst:.2e}")
 
 
+@pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("B,n,H,Hkv,d,K", [(32, 1, 16, 8, 64, 1024), (20, 2, 4, 2, 64, 256), (3, 1, 2, 1, 128, 128),
                                            (40, 1, 3, 1, 16, 128)])
-def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K):
-    _say(f"gemv_w4_rope_kv B={B} n={n} H={H} Hkv={Hkv} d={d} K={K}")
+def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K, norm):
+    """norm: x is fp32 residual rows and RMSNorm(x) * w is fused (the staged
+    operand fp16(x * w) as numpy rounds it, rows scaled by the fp64 rstd; the
+    bar grows by rstd's fp32 error, 1e-6 relative)."""
+    _say(f"gemv_w4_rope_kv B={B} n={n} H={H} Hkv={Hkv} d={d} K={K} norm={norm}")
     dev = hip.torch_device
     heads = H + 2 * Hkv
     N, M, cap, T = heads * d, B * n, 40, 48
@@ -111,17 +115,28 @@ def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K):
     perm = VM.rope_rows(heads, d, 8).numpy()
     pq = torch.from_numpy(np.ascontiguousarray(p[perm])).to(dev)
     sq = torch.from_numpy(np.ascontiguousarray(s[perm])).to(dev)
-    x16 = rng.normal(0, 1, (M, K)).astype(np.float16)
-    xd = torch.from_numpy(x16).to(dev)
     lens, cos, sin, q, kc, vc = _setup(hip, B, n, H, Hkv, d, cap, T, seed=M + d)
     lens_d, cos_d, sin_d = lens.to(dev), cos.to(dev), sin.to(dev)
     rk = _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, 1, cap)
-    _lib.check(_lib.lib().vnx_gemv_w4_rope_kv(VP(xd.data_ptr()), K, VP(pq.data_ptr()), pq.stride(0),
-                                              VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), M, N, K, 128,
-                                              ctypes.byref(rk), _st()), "gemv_w4_rope_kv")
+    if norm:
+        x = rng.normal(0, 2.0, (M, K)).astype(np.float32)
+        nw = (rng.random(K) + 0.5).astype(np.float32)
+        xd, nwd = torch.from_numpy(x).to(dev), torch.from_numpy(nw).to(dev)
+        _lib.check(_lib.lib().vnx_gemv_w4_rope_kv(VP(xd.data_ptr()), K, VP(nwd.data_ptr()), 1e-6, VP(pq.data_ptr()),
+                                                  pq.stride(0), VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), M, N,
+                                                  K, 128, ctypes.byref(rk), _st()), "gemv_w4_rope_kv norm")
+        rstd = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+        x64 = torch.from_numpy((x * nw).astype(np.float16).astype(np.float64) * rstd)
+    else:
+        x16 = rng.normal(0, 1, (M, K)).astype(np.float16)
+        xd = torch.from_numpy(x16).to(dev)
+        _lib.check(_lib.lib().vnx_gemv_w4_rope_kv(VP(xd.data_ptr()), K, None, 0.0, VP(pq.data_ptr()), pq.stride(0),
+                                                  VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), M, N, K, 128,
+                                                  ctypes.byref(rk), _st()), "gemv_w4_rope_kv")
+        x64 = torch.from_numpy(x16.astype(np.float64))
     torch.cuda.synchronize()
     Wd = torch.from_numpy(Q.dequantize_int4_g(p, s, (N, K), 128).astype(np.float64))
-    _check(torch.from_numpy(x16.astype(np.float64)), Wd, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, 1, cap)
+    _check(x64, Wd, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, 1, cap, rtol=RTOL + (1e-6 if norm else 0.0))
 
 
 def test_rope_proj_rejects(hip):
@@ -135,8 +150,8 @@ def test_rope_proj_rejects(hip):
     L = _lib.lib()
     rk = _lib.RopeKvArgs(VP(lens.data_ptr()), 1, 2, 1, 8, VP(cs.data_ptr()), VP(cs.data_ptr()), 8, 1,
                          VP(q.data_ptr()), VP(q.data_ptr()), VP(q.data_ptr()), 64, 16, 16, 4)
-    args = lambda N: (VP(x.data_ptr()), 128, VP(wq.data_ptr()), 64, VP(sc.data_ptr()), _lib.VNX_F16, 1, 4, N, 128,
-                      128, ctypes.byref(rk), _st())
+    args = lambda N: (VP(x.data_ptr()), 128, None, 0.0, VP(wq.data_ptr()), 64, VP(sc.data_ptr()), _lib.VNX_F16, 1, 4,
+                      N, 128, 128, ctypes.byref(rk), _st())
     # d = 8 is not a whole 16-row tile of rotate-half pairs
     assert L.vnx_gemv_w4_rope_kv(*args(32)) == _lib.VNX_ERR_UNSUPPORTED
     rk.d, rk.c_sr = 32, 32

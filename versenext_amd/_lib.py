@@ -62,8 +62,10 @@ SIGNATURES = {
     "vnx_gemv_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
     "vnx_gemv_w4": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
                            _vp, _c_i64, _vp, _c_sz, _vp]),
-    "vnx_gemv_w4_swiglu": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
-                                  _vp, _c_i64, _vp]),
+    "vnx_gemv_w4_swiglu": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64,
+                                  _int, _vp, _c_i64, _vp]),
+    "vnx_gemv_w4_residual": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
+                                    _vp, _c_i64, _vp]),
     "vnx_gemv_w8": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64,
                            _vp, _c_sz, _vp]),
     "vnx_dequant_w4": (_int, [_vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _c_i64, _vp]),
@@ -102,8 +104,8 @@ class RopeKvArgs(ctypes.Structure):
 
 
 SIGNATURES.update({
-    "vnx_gemv_w4_rope_kv": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
-                                   ctypes.POINTER(RopeKvArgs), _vp]),
+    "vnx_gemv_w4_rope_kv": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64,
+                                   _int, ctypes.POINTER(RopeKvArgs), _vp]),
     "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),
     "vnx_tree_attn": (_int, [ctypes.POINTER(TreeAttnArgs), _vp, _c_sz, _vp]),
     "vnx_tree_attn_plan": (_int, [_int, _int, _int, _int, _int, _int, _vp, _vp, _vp]),

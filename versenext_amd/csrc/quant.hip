@@ -56,6 +56,10 @@ struct QGemvParams {
   int64_t ldy;
   uint16_t* yh;        // SwiGLU output: fp16 bits (B, N/2), row pitch ldy (then y is unused)
   int rope_on;         // RoPE + cache store epilogue (ro; y and yh unused)
+  int resid;           // residual epilogue: y += the product (fp32)
+  const float* xf;     // NX: fp32 rows to normalize (x unused), row pitch ldx
+  const float* nw;     // NX: RMSNorm weight (K)
+  float eps;
   int64_t row_off;     // batch row of x's first row (the launch's 32-row chunks)
   RopeOut ro;
   int64_t ksplit_len;  // K per grid.y split (multiple of kGK; the launches use K)
@@ -290,8 +294,12 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
 // wave stages its group's x block (up to 32 batch rows x 128 k) through its
 // own LDS tile: coalesced 256-byte row reads in, the MFMA B-operand layout
 // out.
-// QE: 0 plain fp32 output, 1 SwiGLU (fp16), 2 RoPE + KV-cache store.
-template <int BITS, int NC, int NW, int QE = 0>
+// QE: 0 plain fp32 output, 1 SwiGLU (fp16), 2 RoPE + KV-cache store,
+// 3 residual (y += the product, fp32).  NX (W4): x is RMSNorm(xf) * nw: the
+// staged operand is fp16(xf * nw), each wave sums the squares of its groups'
+// values per row, and the epilogue scales row b by rstd_b = 1/sqrt(mean
+// xf^2 + eps) (vnnn.py:593-615, the per-row factor on the fp32 sums).
+template <int BITS, int NC, int NW, int QE = 0, bool NX = false>
 __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   constexpr int WBYTES = BITS == 4 ? 16 : 32;
   constexpr int XR = NC * 16;            // staged batch rows
@@ -302,6 +310,7 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   __shared__ __attribute__((aligned(16))) char smem[kXBytes > kRBytes ? kXBytes : kRBytes];
   auto xs_all = reinterpret_cast<uint16_t(*)[XR * XP]>(smem);
   auto red = reinterpret_cast<f32x4(*)[NC][64]>(smem);
+  __shared__ float ssp[NX ? NW : 1][NX ? XR : 1];  // NX: per-wave sums of squares per row
   const int tid = threadIdx.x;
   const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
   const int m = lane % 16, kq = lane / 16;
@@ -314,13 +323,17 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   f32x4 yacc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) yacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ss[NX ? XL : 1];  // NX: this lane's sums of squares, row (i*64 + lane) / 16
+#pragma unroll
+  for (int i = 0; i < (NX ? XL : 1); ++i) ss[i] = 0.0f;
 
   for (int g0 = wave; g0 < ngroups; g0 += 2 * NW) {
     // two groups per pass: g0 and g0 + NW (the second weighted 0 when past K)
     const int gg[2] = {g0, g0 + NW < ngroups ? g0 + NW : g0};
     const bool second = g0 + NW < ngroups;
     uint32_t wv[2][WBYTES / 4];
-    u32x4 xv[2][XL];
+    u32x4 xv[2][XL][NX ? 2 : 1];
+    u32x4 nwv[2][NX ? 2 : 1];
     float sc[2][4];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -336,7 +349,17 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
       for (int i = 0; i < XL; ++i) {
         const int b = (i * 64 + lane) / 16;
-        xv[u][i] = *reinterpret_cast<const u32x4*>(p.x + (int64_t)min(b, (int)p.B - 1) * p.ldx + k0 + m * 8);
+        if constexpr (NX) {
+          const float* src = p.xf + (int64_t)min(b, (int)p.B - 1) * p.ldx + k0 + m * 8;
+          xv[u][i][0] = *reinterpret_cast<const u32x4*>(src);
+          xv[u][i][1] = *reinterpret_cast<const u32x4*>(src + 4);
+        } else {
+          xv[u][i][0] = *reinterpret_cast<const u32x4*>(p.x + (int64_t)min(b, (int)p.B - 1) * p.ldx + k0 + m * 8);
+        }
+      }
+      if constexpr (NX) {
+        nwv[u][0] = *reinterpret_cast<const u32x4*>(p.nw + k0 + m * 8);
+        nwv[u][1] = *reinterpret_cast<const u32x4*>(p.nw + k0 + m * 8 + 4);
       }
       if constexpr (BITS == 4) {
         const unsigned col = p.gpg == 1 ? (unsigned)gg[u] : (unsigned)gg[u] / (unsigned)p.gpg;
@@ -347,10 +370,32 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       wave_lds_fence();  // the previous group's B-operand reads are done
+      const bool use = u == 0 || second;
 #pragma unroll
       for (int i = 0; i < XL; ++i) {
         const int b = (i * 64 + lane) / 16;
-        u32x4 v = b < p.B ? xv[u][i] : u32x4{0u, 0u, 0u, 0u};
+        u32x4 v;
+        if constexpr (NX) {
+          // fp16(x * w) of 8 columns; their squares into ss (counted once)
+          const f32x4 xa = __builtin_bit_cast(f32x4, xv[u][i][0]), xb = __builtin_bit_cast(f32x4, xv[u][i][1]);
+          const f32x4 wa = __builtin_bit_cast(f32x4, nwv[u][0]), wb = __builtin_bit_cast(f32x4, nwv[u][1]);
+          float t = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t = __builtin_fmaf(xa[e], xa[e], t);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) t = __builtin_fmaf(xb[e], xb[e], t);
+          ss[i] += use ? t : 0.0f;
+          half8 hv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            hv[e] = (_Float16)(xa[e] * wa[e]);
+            hv[4 + e] = (_Float16)(xb[e] * wb[e]);
+          }
+          v = __builtin_bit_cast(u32x4, hv);
+        } else {
+          v = xv[u][i][0];
+        }
+        if (b >= p.B) v = u32x4{0u, 0u, 0u, 0u};
         if constexpr (BITS == 4) v = stage_perm_w4(v);
         *reinterpret_cast<u32x4*>(&xs[b * XP + m * 8]) = v;
       }
@@ -367,7 +412,6 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
           acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc[c], 0, 0, 0);
         }
       }
-      const bool use = u == 0 || second;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
 #pragma unroll
@@ -379,6 +423,18 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
     }
   }
 
+  if constexpr (NX) {
+    // each row's sum over its 16 lanes (consecutive), one partial per wave
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      float t = ss[i];
+      t += __shfl_xor(t, 1);
+      t += __shfl_xor(t, 2);
+      t += __shfl_xor(t, 4);
+      t += __shfl_xor(t, 8);
+      if (m == 0) ssp[wave][(i * 64 + lane) / 16] = t;
+    }
+  }
   __syncthreads();  // every wave is done with its x tile
 #pragma unroll
   for (int c = 0; c < NC; ++c) red[wave][c][lane] = yacc[c];
@@ -397,6 +453,26 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   if constexpr (BITS == 8) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] *= load_scale(p, min(n0 + j, p.N - 1), 0);
+  }
+  if constexpr (NX) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += ssp[w][b];
+    const float rstd = 1.0f / __builtin_sqrtf(t / (float)p.K + p.eps);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] *= rstd;
+  }
+  if constexpr (QE == 3) {
+    float* dr = p.y + b * p.ldy + n0;
+    if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dr) & 15) == 0) {
+      const f32x4 o = *reinterpret_cast<const f32x4*>(dr);
+      *reinterpret_cast<f32x4*>(dr) = o + v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (n0 + j < p.N) dr[j] = dr[j] + v[j];
+    }
+    return;
   }
   if constexpr (QE == 2) {
     // tile t of head hh holds dims qb*8 + 0..7 (rows 0-7) and d/2 + qb*8 +
@@ -612,10 +688,14 @@ static int qgemv_check(const QGemvParams& p, int bits) {
   if (p.rope_on && (bits != 4 || p.N >= kQTileMaxN)) return VNX_ERR_UNSUPPORTED;
   // SwiGLU: blocks of 8 gate + 8 up rows, one 16-row tile each (tile kernel)
   if (p.yh && (p.N % 16 || p.N >= kQTileMaxN)) return VNX_ERR_UNSUPPORTED;
+  // residual and normalized-input forms run the tile kernel only (W4)
+  if ((p.resid || p.xf) && (bits != 4 || p.N >= kQTileMaxN)) return VNX_ERR_UNSUPPORTED;
+  if (p.xf && (!p.nw || !(p.eps >= 0.0f))) return VNX_ERR_INVALID_ARG;
   if (p.ldw < (bits == 4 ? p.K / 2 : p.K)) return VNX_ERR_INVALID_ARG;
   if (p.lds < (bits == 4 ? p.K / p.G : 1)) return VNX_ERR_INVALID_ARG;
-  // 16-byte vector loads of x and of every row's weights.
-  if (!aligned16(p.x) || p.ldx % 8 || !aligned16(p.w) || p.ldw % 16) return VNX_ERR_UNSUPPORTED;
+  // 16-byte vector loads of x (fp16, or fp32 rows to normalize) and of every row's weights.
+  if (!aligned16(p.x) || p.ldx % (p.xf ? 4 : 8) || !aligned16(p.w) || p.ldw % 16) return VNX_ERR_UNSUPPORTED;
+  if (p.xf && !aligned16(p.nw)) return VNX_ERR_UNSUPPORTED;
   return VNX_OK;
 }
 
@@ -640,6 +720,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
   for (int64_t b0 = 0; b0 < p.B; b0 += 32) {
     QGemvParams c = p;
     c.x = p.x + b0 * p.ldx;
+    if (p.xf) c.xf = p.xf + b0 * p.ldx;
     if (p.y) c.y = p.y + b0 * p.ldy;
     if (p.yh) c.yh = p.yh + b0 * p.ldy;
     c.row_off = b0;
@@ -653,14 +734,19 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       const dim3 grid((unsigned)tiles);
 #define VNX_QTILE(BITS, NC, NW) \
   hipLaunchKernelGGL((k_qgemv_tile<BITS, NC, NW>), grid, dim3(NW * 64), 0, s, c)
-#define VNX_QTILE_E(NC, NW, QE) \
-  hipLaunchKernelGGL((k_qgemv_tile<4, NC, NW, QE>), grid, dim3(NW * 64), 0, s, c)
+#define VNX_QTILE_E(NC, NW, QE, NX) \
+  hipLaunchKernelGGL((k_qgemv_tile<4, NC, NW, QE, NX>), grid, dim3(NW * 64), 0, s, c)
+#define VNX_QTILE_Q(QE, NX) \
+  do { \
+    if (two) { if (wide) VNX_QTILE_E(2, 8, QE, NX); else VNX_QTILE_E(2, 4, QE, NX); } \
+    else { if (wide) VNX_QTILE_E(1, 8, QE, NX); else VNX_QTILE_E(1, 4, QE, NX); } \
+  } while (0)
       if (c.rope_on) {
-        if (two) { if (wide) VNX_QTILE_E(2, 8, 2); else VNX_QTILE_E(2, 4, 2); }
-        else { if (wide) VNX_QTILE_E(1, 8, 2); else VNX_QTILE_E(1, 4, 2); }
+        if (c.xf) VNX_QTILE_Q(2, true); else VNX_QTILE_Q(2, false);
       } else if (c.yh) {
-        if (two) { if (wide) VNX_QTILE_E(2, 8, 1); else VNX_QTILE_E(2, 4, 1); }
-        else { if (wide) VNX_QTILE_E(1, 8, 1); else VNX_QTILE_E(1, 4, 1); }
+        if (c.xf) VNX_QTILE_Q(1, true); else VNX_QTILE_Q(1, false);
+      } else if (c.resid) {
+        VNX_QTILE_Q(3, false);
       } else if (bits == 4) {
         if (two) { if (wide) VNX_QTILE(4, 2, 8); else VNX_QTILE(4, 2, 4); }
         else { if (wide) VNX_QTILE(4, 1, 8); else VNX_QTILE(4, 1, 4); }
@@ -670,6 +756,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       }
 #undef VNX_QTILE
 #undef VNX_QTILE_E
+#undef VNX_QTILE_Q
     } else if (bits == 4 && c.G == kGK && c.sc_f16 && c.lds % 8 == 0 && aligned16(c.sc) &&
                (c.K == 512 || c.K == 1024) && !getenv("VNX_QSTREAM_OFF")) {
       // two workgroups per CU (x staged once each), tiles split evenly
@@ -728,12 +815,13 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
   return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
 }
 
-int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
-                       int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, void* y,
-                       int64_t ldy, void* stream) {
+int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const float* norm_w, float eps, const uint8_t* wq, int64_t ldw,
+                       const void* scales, int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+                       void* y, int64_t ldy, void* stream) {
   if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
   if (!y) return VNX_ERR_INVALID_ARG;
   QGemvParams p{};
+  if (norm_w) { p.xf = static_cast<const float*>(x); p.nw = norm_w; p.eps = eps; }
   p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
   p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.yh = static_cast<uint16_t*>(y);
   p.ldy = ldy; p.gpg = group / kGK;
@@ -742,17 +830,31 @@ int vnx_gemv_w4_swiglu(const void* x, int64_t ldx, const uint8_t* wq, int64_t ld
   return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
 }
 
-int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
-                        int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
+int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const float* norm_w, float eps, const uint8_t* wq, int64_t ldw,
+                        const void* scales, int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
                         const vnx_rope_kv_args* rk, void* stream) {
   if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
   QGemvParams p{};
+  if (norm_w) { p.xf = static_cast<const float*>(x); p.nw = norm_w; p.eps = eps; }
   const int rs = rope_out_from(rk, N, &p.ro);
   if (rs) return rs;
   if (B % rk->n) return VNX_ERR_INVALID_ARG;  // rows are whole sequences of n tokens
   p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
   p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.rope_on = 1;
   p.gpg = group / kGK;
+  const int st = qgemv_check(p, 4);
+  if (st) return st;
+  return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemv_w4_residual(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, const void* scales,
+                         int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group, float* res,
+                         int64_t ldr, void* stream) {
+  if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
+  QGemvParams p{};
+  p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
+  p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.y = res; p.ldy = ldr;
+  p.gpg = group / kGK; p.resid = 1;
   const int st = qgemv_check(p, 4);
   if (st) return st;
   return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));

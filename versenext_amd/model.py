@@ -352,39 +352,62 @@ class _Linear:
             ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16_residual")
         return True
 
-    def rope_kv(self, x: torch.Tensor, rk) -> bool:
-        """The q|k|v projection of x with RoPE and the KV-cache write fused
-        (vnx_gemv_w4_rope_kv, INT4 weights, M <= 64); False (nothing done)
-        when it does not apply.  (The bf16 verify projection keeps a separate
-        vnx_rope_kv: in its GEMM's epilogue the store pattern cost more than
-        the launch it saves.)"""
-        M = x.shape[0]
-        st = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
-        L = self.hip._L
-        if self.wq_rope is not None and M <= 64:
-            x16 = x.to(torch.float16).contiguous()
-            _lib.check(L.vnx_gemv_w4_rope_kv(
-                ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq_rope.data_ptr()),
-                self.wq_rope.stride(0), ctypes.c_void_p(self.sc_rope.data_ptr()), _lib.VNX_F16,
-                self.sc_rope.stride(0), M, self.N, self.K, 128, ctypes.byref(rk), st), "gemv_w4_rope_kv")
-            return True
-        return False
-
-    def gemv_swiglu(self, x: torch.Tensor) -> Optional[torch.Tensor]:
-        """silu(gate) * up (M, N/2) fp16 of a fused [gate; up] INT4 weight for
-        M <= 64 rows (vnx_gemv_w4_swiglu); None when it does not apply."""
-        M = x.shape[0]
-        if not (self.int4 and self.swiglu and M <= 64):
-            return None
+    def _gemv_x(self, x: torch.Tensor, norm_w):
+        """(x pointer, row pitch, norm pointer): fp32 residual rows when a norm
+        weight is given (the GEMV applies RMSNorm), else fp16 rows."""
+        if norm_w is not None:
+            return ctypes.c_void_p(x.data_ptr()), x.stride(0), ctypes.c_void_p(norm_w.data_ptr()), x
         x16 = x.to(torch.float16).contiguous()
+        return ctypes.c_void_p(x16.data_ptr()), self.K, None, x16
+
+    def rope_kv(self, x: torch.Tensor, rk, norm_w: Optional[torch.Tensor] = None, eps: float = 0.0) -> bool:
+        """The q|k|v projection of x with RoPE and the KV-cache write fused
+        (vnx_gemv_w4_rope_kv, INT4 weights, M <= 64; with norm_w, x is the
+        fp32 residual stream and RMSNorm(x) * norm_w is fused too); False
+        (nothing done) when it does not apply.  (The bf16 verify projection
+        keeps a separate vnx_rope_kv: in its GEMM's epilogue the store pattern
+        cost more than the launch it saves.)"""
+        M = x.shape[0]
+        if self.wq_rope is None or M > 64 or (norm_w is not None and x.dtype != torch.float32):
+            return False
+        xp, ldx, nwp, keep = self._gemv_x(x, norm_w)
+        _lib.check(self.hip._L.vnx_gemv_w4_rope_kv(
+            xp, ldx, nwp, float(eps), ctypes.c_void_p(self.wq_rope.data_ptr()), self.wq_rope.stride(0),
+            ctypes.c_void_p(self.sc_rope.data_ptr()), _lib.VNX_F16, self.sc_rope.stride(0), M, self.N, self.K, 128,
+            ctypes.byref(rk), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4_rope_kv")
+        return True
+
+    def gemv_swiglu(self, x: torch.Tensor, norm_w: Optional[torch.Tensor] = None,
+                    eps: float = 0.0) -> Optional[torch.Tensor]:
+        """silu(gate) * up (M, N/2) fp16 of a fused [gate; up] INT4 weight for
+        M <= 64 rows (vnx_gemv_w4_swiglu; with norm_w, of RMSNorm(x) * norm_w
+        of the fp32 rows x); None when it does not apply."""
+        M = x.shape[0]
+        if not (self.int4 and self.swiglu and M <= 64) or (norm_w is not None and x.dtype != torch.float32):
+            return None
+        xp, ldx, nwp, keep = self._gemv_x(x, norm_w)
         H = self.N // 2
         y = torch.empty((M, H), dtype=torch.float16, device=x.device)
         _lib.check(self.hip._L.vnx_gemv_w4_swiglu(
-            ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq_sw.data_ptr()), self.wq_sw.stride(0),
+            xp, ldx, nwp, float(eps), ctypes.c_void_p(self.wq_sw.data_ptr()), self.wq_sw.stride(0),
             ctypes.c_void_p(self.sc_sw.data_ptr()), _lib.VNX_F16, self.sc_sw.stride(0), M, self.N, self.K, 128,
             ctypes.c_void_p(y.data_ptr()), H, ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)),
             "gemv_w4_swiglu")
         return y
+
+    def gemv_residual(self, x: torch.Tensor, res: torch.Tensor) -> bool:
+        """res (M, N) fp32 += x . W^T for INT4 weights and M <= 64
+        (vnx_gemv_w4_residual); False (nothing done) when it does not apply."""
+        M = x.shape[0]
+        if not self.int4 or M > 64 or self.N >= 32768:
+            return False
+        x16 = x.to(torch.float16).contiguous()
+        _lib.check(self.hip._L.vnx_gemv_w4_residual(
+            ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq.data_ptr()), self.wq.stride(0),
+            ctypes.c_void_p(self.sc.data_ptr()), _lib.VNX_F16, self.sc.stride(0), M, self.N, self.K, 128,
+            ctypes.c_void_p(res.data_ptr()), res.stride(0),
+            ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4_residual")
+        return True
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x (M, K); returns (M, N) in the compute dtype (dense) or fp32
@@ -755,23 +778,32 @@ class CometSparkGPU:
                      and pending is None
                      and ("w1p" in L.ffn if L.kind == "mod" else
                           (L.ffn["gu"].wp is not None and L.ffn["gu"].swiglu and L.ffn["down"].wp is not None)))
+            # the INT4 draft's decode: the same fusions on its GEMVs
+            qfused = (not fused and L.kind == "trisparse" and L.wqkv.wq_rope is not None and L.proj.int4
+                      and L.ffn["gu"].int4 and L.ffn["gu"].swiglu and L.ffn["down"].int4 and M <= 64
+                      and pending is None)
             h = None
             qkv = None
-            if li == 0:
-                h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
-                self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
-            elif fused:
-                qkv = L.wqkv.gemm_norm(x, L.norm1, cfg.eps)
-            else:
-                h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
-                self._rms(x, pending, L.norm1, h)
-                pending = None
             q = torch.empty((B, H, n, d), dtype=self.dtype, device=self.dev)
             kc, vc = self.kc[li], self.vc[li]
             rk = _lib.RopeKvArgs(P(lens.data_ptr()), n, H, Hkv, d, P(self.cos.data_ptr()), P(self.sin.data_ptr()),
                                  self.cos.shape[0], int(cfg.use_rope), P(q.data_ptr()), P(kc.data_ptr()),
                                  P(vc.data_ptr()), kc.stride(0), kc.stride(1), kc.stride(2), self.cap)
-            if qkv is not None or not L.wqkv.rope_kv(h, rk):   # INT4: projection with RoPE + cache write fused
+            done = False                                   # q and the cache rows written
+            if li == 0:
+                h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
+                self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
+            elif fused:
+                qkv = L.wqkv.gemm_norm(x, L.norm1, cfg.eps)
+            elif qfused:
+                done = L.wqkv.rope_kv(x, rk, L.norm1, cfg.eps)
+            else:
+                h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
+                self._rms(x, pending, L.norm1, h)
+                pending = None
+            if not done and qkv is None:
+                done = L.wqkv.rope_kv(h, rk)               # INT4: projection with RoPE + cache write fused
+            if not done:
                 if qkv is None:
                     qkv = L.wqkv(h)                                                  # (M, (H+2Hkv) d)
                 _lib.check(L_.vnx_rope_kv(
@@ -793,6 +825,11 @@ class CometSparkGPU:
                     act = L.ffn["gu"].gemm_norm(x, L.norm2, cfg.eps, epilogue=_lib.VNX_EPI_SWIGLU)
                     if act is None or not L.ffn["down"].gemm_residual(act, x):
                         raise RuntimeError("fused FFN path unavailable for this layer")
+                continue
+            if qfused and L.proj.gemv_residual(o, x):
+                act = L.ffn["gu"].gemv_swiglu(x, L.norm2, cfg.eps)
+                if act is None or not L.ffn["down"].gemv_residual(act, x):
+                    raise RuntimeError("fused INT4 FFN path unavailable for this layer")
                 continue
             a = L.proj(o)
             # MoD layers route on fp32 rows, as the reference does
