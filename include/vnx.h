@@ -329,6 +329,23 @@ typedef struct vnx_tree_attn_args {
   int64_t seg2_strides[3];
   int T2;
   const float* gates;
+  /* RoPE and the cache write of the new rows done here (the work of
+   * vnx_rope_kv, TriSparseAttention._apply_rope, tri_sparse_attn.py:182-221):
+   * when qkv is not NULL (bf16, row pitch qkv_ld; row b*N + i holds the H
+   * query, Hkv key and Hkv value heads of tree row i), q is not read: the
+   * queries are those rows' query heads rotated at position tp_batch[b] + i,
+   * and each workgroup first writes the rows' rotated keys and their values
+   * into k_tree / v_tree at tree row tp_b + i (rows at or past cap skipped).
+   * Needs tree_follows_prefix and tp_batch; rope == 0: no rotation; cos /
+   * sin tables (table_rows, d) fp32.  NULL (or zero-initialised trailing
+   * fields): q holds the queries and the tree rows are already written. */
+  const void* qkv;
+  int64_t qkv_ld;
+  const float* cos_table;
+  const float* sin_table;
+  int64_t table_rows;
+  int rope;
+  int64_t cap;
 } vnx_tree_attn_args;
 
 size_t vnx_tree_attn_workspace(int B, int H, int Hkv, int N, int Tp, int d);

@@ -203,3 +203,73 @@ def test_rejects_bad_arguments(hip):
         hip.tree_attention(z(1, 1, 4, 96), None, None, z(1, 1, 4, 96), z(1, 1, 4, 96), np.ones(4, np.uint64))
     with pytest.raises(ValueError):  # 3 query heads over 2 kv heads
         hip.tree_attention(z(1, 3, 4, 64), None, None, z(1, 2, 4, 64), z(1, 2, 4, 64), np.ones(4, np.uint64))
+
+
+@pytest.mark.parametrize("B,H,Hkv,N,d,rope,splits", [(32, 16, 8, 7, 64, 1, None), (5, 4, 2, 3, 128, 1, None),
+                                                     (4, 8, 2, 7, 64, 0, None), (3, 4, 4, 5, 64, 1, "2")])
+def test_qkv_rows_mode_matches_rope_kv_path(hip, monkeypatch, B, H, Hkv, N, d, rope, splits):
+    """vnx_tree_attn reading the q|k|v projection rows (RoPE and the tree
+    rows' cache write inside the call) against vnx_rope_kv followed by the
+    q-input call: the same fp32 rotation rounded once to bf16, so the cache
+    rows and the outputs must agree bit for bit; rows past the cache stay
+    unwritten."""
+    import ctypes
+    from versenext_amd import _lib
+    if splits:
+        monkeypatch.setenv("VNX_TA_SPLITS", splits)
+    _say(f"tree attn qkv mode B={B} H={H} Hkv={Hkv} N={N} d={d} rope={rope} splits={splits}")
+    dev = hip.torch_device
+    g = torch.Generator(device="cpu")
+    g.manual_seed(B * N + d)
+    cap, T = 96, 120
+    heads = H + 2 * Hkv
+    qkv = (torch.randn((B * N, heads * d), generator=g) * 2).to(torch.bfloat16).to(dev)
+    lens = torch.randint(0, cap - N + 1, (B,), generator=g, dtype=torch.int32)
+    lens[0] = cap - N + 2                      # its last rows fall past the cache
+    Tp = int(lens.max())
+    lens = lens.to(dev)
+    ang = torch.rand((T, d), generator=g, dtype=torch.float64) * 6.0
+    cos, sin = torch.cos(ang).float().to(dev), torch.sin(ang).float().to(dev)
+    kc0 = torch.randn((B, Hkv, cap, d), generator=g).to(torch.bfloat16).to(dev)
+    vc0 = torch.randn((B, Hkv, cap, d), generator=g).to(torch.bfloat16).to(dev)
+    anc = torch.tensor([(1 << (i + 1)) - 1 for i in range(N)], dtype=torch.int64).to(dev)   # chain
+    L = _lib.lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def call(kc, vc, q, out, use_qkv):
+        a = _lib.TreeAttnArgs()
+        if use_qkv:
+            a.qkv = qkv.data_ptr(); a.qkv_ld = qkv.stride(0)
+            a.cos_table = cos.data_ptr(); a.sin_table = sin.data_ptr(); a.table_rows = T; a.rope = rope
+            a.cap = cap
+        else:
+            a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
+        a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = list(kc.stride()[:3])
+        a.k_tree = kc.data_ptr(); a.v_tree = vc.data_ptr(); a.tree_strides[:] = list(kc.stride()[:3])
+        a.anc = anc.data_ptr(); a.anc_batch_stride = 0
+        a.out = out.data_ptr(); a.out_dtype = _lib.VNX_BF16; a.out_strides[:] = [N * H * d, d, H * d]
+        a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, N, d
+        a.scale = 1.0 / d ** 0.5
+        a.tp_batch = lens.data_ptr(); a.tree_follows_prefix = 1
+        ws = torch.empty(max(256, L.vnx_tree_attn_workspace(B, H, Hkv, N, Tp, d)), dtype=torch.uint8, device=dev)
+        _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "tree_attn")
+
+    # reference path: vnx_rope_kv, then queries from q
+    kc_a, vc_a = kc0.clone(), vc0.clone()
+    q = torch.zeros((B, H, N, d), dtype=torch.bfloat16, device=dev)
+    _lib.check(L.vnx_rope_kv(ctypes.c_void_p(qkv.data_ptr()), _lib.VNX_BF16, qkv.stride(0), B, N, H, Hkv, d,
+                             ctypes.c_void_p(lens.data_ptr()), ctypes.c_void_p(cos.data_ptr()),
+                             ctypes.c_void_p(sin.data_ptr()), T, rope, ctypes.c_void_p(q.data_ptr()),
+                             ctypes.c_void_p(kc_a.data_ptr()), ctypes.c_void_p(vc_a.data_ptr()), _lib.VNX_BF16,
+                             kc_a.stride(0), kc_a.stride(1), kc_a.stride(2), cap, st), "rope_kv")
+    out_a = torch.zeros((B * N, H * d), dtype=torch.bfloat16, device=dev)
+    call(kc_a, vc_a, q, out_a, False)
+    kc_b, vc_b = kc0.clone(), vc0.clone()
+    out_b = torch.zeros((B * N, H * d), dtype=torch.bfloat16, device=dev)
+    call(kc_b, vc_b, None, out_b, True)
+    torch.cuda.synchronize()
+    assert torch.equal(kc_a.cpu(), kc_b.cpu()) and torch.equal(vc_a.cpu(), vc_b.cpu())
+    # rows whose positions fit the cache are compared (others are undefined in both)
+    ok = (lens.cpu().long().view(B, 1) + torch.arange(N).view(1, N)) < cap
+    oa, ob = out_a.cpu().view(B, N, H * d), out_b.cpu().view(B, N, H * d)
+    assert torch.equal(oa[ok], ob[ok])

@@ -90,6 +90,8 @@ class TreeAttnArgs(ctypes.Structure):
         ("B", _int), ("H", _int), ("Hkv", _int), ("Tp", _int), ("N", _int), ("d", _int),
         ("scale", _f32), ("tp_batch", _vp), ("tree_follows_prefix", _int),
         ("k_seg2", _vp), ("v_seg2", _vp), ("seg2_strides", _c_i64 * 3), ("T2", _int), ("gates", _vp),
+        ("qkv", _vp), ("qkv_ld", _c_i64), ("cos_table", _vp), ("sin_table", _vp), ("table_rows", _c_i64),
+        ("rope", _int), ("cap", _c_i64),
     ]
 
 

@@ -63,6 +63,14 @@ struct TreeAttnParams {
   int T2, W2;                       // rows; waves of split 0 that walk them
   const float* gates;
   float c;                          // scale * log2(e)
+  // qkv mode: queries from the projection rows (RoPE here), the tree rows'
+  // keys / values written into the cache by every workgroup first
+  const uint16_t* qkv;
+  int64_t qkv_ld;
+  const float* cos;
+  const float* sin;
+  int rope;
+  int64_t cap;                      // rows at or past it are not written (and not rotated past the table)
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -145,16 +153,74 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
   const int row0 = g * p.rows_per_group;
   const int nrows = min(p.rows_per_group, p.n_rep * p.N - row0);
 
-  // Q rows of this group -> LDS (rows past nrows are zero).
-  for (int idx = tid; idx < QT * 16 * LPR; idx += NW * 64) {
-    const int r = idx / LPR, c8 = idx - r * LPR;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (r < nrows) {
-      const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
-      const int h = kvh * p.n_rep + rep;
-      v = ldg16(p.q + b * p.q_sb + h * p.q_sh + node * p.q_sr + c8 * 8);
+  if (p.qkv) {
+    // qkv mode.  Element pairs (j, j + D/2) of a head rotate together: item
+    // (r, c) takes 8-dim chunk c < LPR/2 and its partner chunk c + LPR/2.
+    const int tpb = min(max(p.tp_batch[b], 0), p.Tp);
+    auto rot8 = [&](const uint16_t* src, int64_t pos, int c, u32x4& lo, u32x4& hi) {
+      const u32x4 a = ldg16(src + c * 8), z = ldg16(src + D / 2 + c * 8);
+      if (!p.rope) { lo = a; hi = z; return; }
+      const __bf16* av = reinterpret_cast<const __bf16*>(&a);
+      const __bf16* zv = reinterpret_cast<const __bf16*>(&z);
+      __bf16 lo8[8], hi8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = c * 8 + e;
+        const float x0 = static_cast<float>(av[e]), x1 = static_cast<float>(zv[e]);
+        const float c0 = p.cos[pos * D + j], c1 = p.cos[pos * D + j + D / 2];
+        const float s0 = p.sin[pos * D + j], s1 = p.sin[pos * D + j + D / 2];
+        lo8[e] = static_cast<__bf16>(x0 * c0 - x1 * s0);   // rotate_half(x)[j] = -x[j + D/2]
+        hi8[e] = static_cast<__bf16>(x1 * c1 + x0 * s1);   // rotate_half(x)[j + D/2] = x[j]
+      }
+      lo = __builtin_bit_cast(u32x4, lo8);
+      hi = __builtin_bit_cast(u32x4, hi8);
+    };
+    // this head's tree rows: rotated keys and values into the cache
+    for (int idx = tid; idx < p.N * LPR; idx += NW * 64) {
+      const int i = idx / LPR, c = idx - i * LPR;
+      const int64_t pos = (int64_t)tpb + i;
+      if (pos >= p.cap) continue;
+      const uint16_t* row = p.qkv + (int64_t)(b * p.N + i) * p.qkv_ld;
+      uint16_t* kd = const_cast<uint16_t*>(p.kt) + b * p.t_sb + kvh * p.t_sh + pos * p.t_sr;
+      uint16_t* vd = const_cast<uint16_t*>(p.vt) + b * p.t_sb + kvh * p.t_sh + pos * p.t_sr;
+      if (c < LPR / 2) {
+        u32x4 lo, hi;
+        rot8(row + (int64_t)(p.H + kvh) * D, pos, c, lo, hi);
+        *reinterpret_cast<u32x4*>(kd + c * 8) = lo;
+        *reinterpret_cast<u32x4*>(kd + D / 2 + c * 8) = hi;
+      } else {
+        const int cv = c - LPR / 2;  // two value chunks per item
+        const uint16_t* vs = row + (int64_t)(p.H + p.Hkv + kvh) * D;
+        *reinterpret_cast<u32x4*>(vd + cv * 8) = ldg16(vs + cv * 8);
+        *reinterpret_cast<u32x4*>(vd + D / 2 + cv * 8) = ldg16(vs + D / 2 + cv * 8);
+      }
     }
-    *reinterpret_cast<u32x4*>(s_q + r * R + c8 * 8) = v;
+    // Q rows of this group -> LDS, rotated (rows past nrows are zero)
+    for (int idx = tid; idx < QT * 16 * (LPR / 2); idx += NW * 64) {
+      const int r = idx / (LPR / 2), c = idx - r * (LPR / 2);
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      if (r < nrows) {
+        const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
+        const int h = kvh * p.n_rep + rep;
+        const int64_t pos = min((int64_t)tpb + node, p.cap - 1);
+        rot8(p.qkv + (int64_t)(b * p.N + node) * p.qkv_ld + (int64_t)h * D, pos, c, lo, hi);
+      }
+      *reinterpret_cast<u32x4*>(s_q + r * R + c * 8) = lo;
+      *reinterpret_cast<u32x4*>(s_q + r * R + D / 2 + c * 8) = hi;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the cache rows are written before any wave reads them
+  } else {
+    // Q rows of this group -> LDS (rows past nrows are zero).
+    for (int idx = tid; idx < QT * 16 * LPR; idx += NW * 64) {
+      const int r = idx / LPR, c8 = idx - r * LPR;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (r < nrows) {
+        const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
+        const int h = kvh * p.n_rep + rep;
+        v = ldg16(p.q + b * p.q_sb + h * p.q_sh + node * p.q_sr + c8 * 8);
+      }
+      *reinterpret_cast<u32x4*>(s_q + r * R + c8 * 8) = v;
+    }
   }
   // Ancestor words of this lane's query columns.
   uint64_t anc[QT];
@@ -560,7 +626,14 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   if (a->out_dtype != VNX_F32 && a->out_dtype != VNX_BF16 && a->out_dtype != VNX_F16) return VNX_ERR_UNSUPPORTED;
   if (a->T2 < 0) return VNX_ERR_INVALID_ARG;
   if (B == 0) return VNX_OK;
-  if (!a->q || !a->k_tree || !a->v_tree || !a->anc || !a->out) return VNX_ERR_INVALID_ARG;
+  if ((!a->q && !a->qkv) || !a->k_tree || !a->v_tree || !a->anc || !a->out) return VNX_ERR_INVALID_ARG;
+  if (a->qkv) {
+    // the projection rows: RoPE and the tree rows' cache write here
+    if (!a->tree_follows_prefix || !a->tp_batch || a->cap < 1) return VNX_ERR_INVALID_ARG;
+    if (a->qkv_ld < (int64_t)(H + 2 * Hkv) * d) return VNX_ERR_INVALID_ARG;
+    if (a->rope && (!a->cos_table || !a->sin_table || a->table_rows < 1)) return VNX_ERR_INVALID_ARG;
+    if (!aligned16(a->qkv) || a->qkv_ld % 8) return VNX_ERR_UNSUPPORTED;
+  }
   if (a->T2 > 0) {
     if (!a->k_seg2 || !a->v_seg2 || !a->gates || (reinterpret_cast<uintptr_t>(a->gates) & 3u))
       return VNX_ERR_INVALID_ARG;
@@ -578,7 +651,7 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
       !strides_ok(a->tree_strides[0], a->tree_strides[1], a->tree_strides[2], 8) ||
       !strides_ok(a->out_strides[0], a->out_strides[1], a->out_strides[2], 4))
     return VNX_ERR_UNSUPPORTED;
-  if (!aligned16(a->q) || !aligned16(a->k_tree) || !aligned16(a->v_tree) || !aligned16(a->out) ||
+  if ((a->q && !aligned16(a->q)) || !aligned16(a->k_tree) || !aligned16(a->v_tree) || !aligned16(a->out) ||
       (Tp > 0 && (!aligned16(a->k_cache) || !aligned16(a->v_cache))) ||
       (reinterpret_cast<uintptr_t>(a->anc) & 7u))
     return VNX_ERR_UNSUPPORTED;
@@ -612,6 +685,14 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
     p.gates = a->gates;
   }
   p.c = (float)((double)a->scale * 1.4426950408889634);
+  if (a->qkv) {
+    p.qkv = static_cast<const uint16_t*>(a->qkv);
+    p.qkv_ld = a->qkv_ld;
+    p.cos = a->cos_table;
+    p.sin = a->sin_table;
+    p.rope = a->rope ? 1 : 0;
+    p.cap = a->rope ? (a->cap < a->table_rows ? a->cap : a->table_rows) : a->cap;
+  }
   if (pl.S > 1) {
     Carve c(workspace);
     const int64_t prow = (int64_t)B * H * N * (pl.S + 1);

@@ -539,9 +539,16 @@ class CometSparkGPU:
         return w
 
     def _tree_call(self, q, kc, vc, cstr, tree_k, tree_v, tstr, anc, B, H, Hkv, Tp, n, d, tp, follows, out,
-                   seg2=None, gates=None):
+                   seg2=None, gates=None, qkv=None):
         a = _lib.TreeAttnArgs()
-        a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
+        if qkv is not None:
+            # queries from the q|k|v rows, RoPE and the cache write in the kernel
+            a.q = None; a.q_strides[:] = [0, 0, 0]
+            a.qkv = qkv.data_ptr(); a.qkv_ld = qkv.stride(0)
+            a.cos_table = self.cos.data_ptr(); a.sin_table = self.sin.data_ptr()
+            a.table_rows = self.cos.shape[0]; a.rope = int(self.cfg.use_rope); a.cap = self.cap
+        else:
+            a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
         a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = cstr
         a.k_tree = tree_k.data_ptr(); a.v_tree = tree_v.data_ptr(); a.tree_strides[:] = tstr
         a.anc = anc.data_ptr(); a.anc_batch_stride = 0
@@ -562,20 +569,22 @@ class CometSparkGPU:
         _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), self._st()),
                    "tree_attn")
 
-    def _attn_kernel(self, q, li, lens, n, Tmax):
+    def _attn_kernel(self, q, li, lens, n, Tmax, qkv=None):
         """Sliding-window and global paths in one vnx_tree_attn call: each
         row's prefix of lens[b] cache rows, then its n new rows (written in
         place right after it) under the chain mask, and the G global rows as
         the gated second segment; writes the proj input (B*n, H*d) in the
-        activation dtype.  q (B, H, n, d) bf16."""
+        activation dtype.  q (B, H, n, d) bf16, or qkv (B*n, (H+2Hkv) d) bf16
+        projection rows (RoPE and the new rows' cache write done by the
+        kernel; q unused)."""
         cfg = self.cfg
-        B, H, _, d = q.shape
+        B, H, d = self.B, cfg.n_head, cfg.head_dim
         kc, vc = self.kc[li], self.vc[li]
         Ly = self.layers[li]
         o = torch.empty((B * n, H * d), dtype=self.act_dtype, device=self.dev)
         cstr = list(kc.stride()[:3])
         self._tree_call(q, kc, vc, cstr, kc, vc, cstr, self._chain_words(n), B, H, cfg.n_kv_head, Tmax, n, d, lens,
-                        True, o, seg2=(Ly.gk, Ly.gv), gates=Ly.gates)
+                        True, o, seg2=(Ly.gk, Ly.gv), gates=Ly.gates, qkv=qkv)
         return o
 
     def _attn_torch(self, q, li, lens, n, Tmax):
@@ -803,9 +812,14 @@ class CometSparkGPU:
                 pending = None
             if not done and qkv is None:
                 done = L.wqkv.rope_kv(h, rk)               # INT4: projection with RoPE + cache write fused
+            attn_qkv = None
             if not done:
                 if qkv is None:
                     qkv = L.wqkv(h)                                                  # (M, (H+2Hkv) d)
+                if use_kernel and qkv.dtype == torch.bfloat16 and qkv.stride(1) == 1:
+                    attn_qkv = qkv                         # RoPE + cache write inside the attention call
+                    done = True
+            if not done:
                 _lib.check(L_.vnx_rope_kv(
                     P(qkv.data_ptr()), _lib.DTYPE_CODES[qkv.dtype], qkv.stride(0), B, n, H, Hkv, d,
                     P(lens.data_ptr()), P(self.cos.data_ptr()), P(self.sin.data_ptr()), self.cos.shape[0],
@@ -813,7 +827,7 @@ class CometSparkGPU:
                     _lib.DTYPE_CODES[self.dtype], kc.stride(0), kc.stride(1), kc.stride(2), self.cap, self._st()),
                     "rope_kv")
             if use_kernel:
-                o = self._attn_kernel(q, li, lens, n, Tmax)
+                o = self._attn_kernel(q, li, lens, n, Tmax, qkv=attn_qkv)
             else:
                 o = self._attn_torch(q, li, lens, n, Tmax).permute(0, 2, 1, 3).reshape(M, H * d)
                 o = o.to(self.act_dtype).contiguous()
