@@ -122,6 +122,18 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   f32x16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  // EPI 3: the residual values this lane adds to load now, under the K loop
+  // (lane holds rows 8i + 4h + e of column ni*32 + r; only split 0 stores)
+  float old[EPI == 3 ? 16 : 1];
+  if constexpr (EPI == 3) {
+    if (wk == 0) {
+      const float* yf = reinterpret_cast<const float*>(p.y) + min(ni * 32 + r, p.N - 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) old[4 * i + e] = yf[(int64_t)min(m0 + 8 * i + 4 * h + e, p.M - 1) * p.ldy];
+    }
+  }
   float ss = 0.0f;  // NX: sum of squares of this thread's values of row xr
   // NX: the norm weight goes to LDS once per workgroup; its loads issue
   // before the ring's first loads, so their latencies overlap
@@ -242,19 +254,11 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   }
   char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
   if constexpr (EPI == 3) {
-    // all 16 residual values load before any is used (rows past M re-read
-    // row M-1 and are not stored), then add and store
+    // the residual values were loaded before the K loop (rows past M re-read
+    // row M-1 and are not stored)
     const int n = ni * 32 + r;
     if (n >= p.N) return;
     float* yf = reinterpret_cast<float*>(ybase);
-    float old[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = min(m0 + 8 * i + 4 * h + e, p.M - 1);
-        old[4 * i + e] = yf[(int64_t)m * p.ldy + n];
-      }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll

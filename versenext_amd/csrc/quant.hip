@@ -323,6 +323,23 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   f32x4 yacc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) yacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // QE 3: the residual values wave c < NC adds to (row c*16 + m, columns
+  // row0 + 4*kq .. +4) load now, under the K loop
+  f32x4 rold = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (QE == 3) {
+    if (wave < NC) {
+      const int64_t rb = wave * 16 + m, rn = row0 + 4 * kq;
+      if (rb < p.B && rn < p.N) {
+        const float* src = p.y + rb * p.ldy + rn;
+        if (rn + 4 <= p.N && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+          rold = *reinterpret_cast<const f32x4*>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) rold[j] = rn + j < p.N ? src[j] : 0.0f;
+        }
+      }
+    }
+  }
   float ss[NX ? XL : 1];  // NX: this lane's sums of squares, row (i*64 + lane) / 16
 #pragma unroll
   for (int i = 0; i < (NX ? XL : 1); ++i) ss[i] = 0.0f;
@@ -465,12 +482,11 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   if constexpr (QE == 3) {
     float* dr = p.y + b * p.ldy + n0;
     if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dr) & 15) == 0) {
-      const f32x4 o = *reinterpret_cast<const f32x4*>(dr);
-      *reinterpret_cast<f32x4*>(dr) = o + v;
+      *reinterpret_cast<f32x4*>(dr) = rold + v;
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        if (n0 + j < p.N) dr[j] = dr[j] + v[j];
+        if (n0 + j < p.N) dr[j] = rold[j] + v[j];
     }
     return;
   }
