@@ -348,20 +348,20 @@ __global__ __launch_bounds__(64) void k_mod_route(const float* logits, int64_t l
 // order) and routes them.
 constexpr int kRouteMaxR = 32;
 
-template <int VW>
+template <int VW, int RM>
 __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh, const float* nw, float eps,
                                                      const float* wr, int64_t ldw, int64_t D, int P, int E, int topk,
                                                      float* comb, int64_t ldc, __hip_bfloat16* xo, int64_t ldxo,
                                                      int64_t sxo, int copies) {
-  __shared__ float red[4][kRouteMaxR];
-  __shared__ float lg[kRouteMaxR];
+  __shared__ float red[4][RM];
+  __shared__ float lg[RM];
   __shared__ float ssr[4];
   const int64_t m = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int R = P + P * E;
-  float acc[kRouteMaxR];
+  float acc[RM];
 #pragma unroll
-  for (int r = 0; r < kRouteMaxR; ++r) acc[r] = 0.0f;
+  for (int r = 0; r < RM; ++r) acc[r] = 0.0f;
   float ss = 0.0f;  // nw: sum of squares of the raw row
   // thread tid takes columns tid*VW .. +VW of every 256*VW block
   for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
@@ -391,20 +391,20 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
         else Elt<__hip_bfloat16>::st(dst + q * sxo, x[0]);
       }
     }
-    float wv[kRouteMaxR][VW];
+    float wv[RM][VW];
 #pragma unroll
-    for (int r = 0; r < kRouteMaxR; ++r) {
+    for (int r = 0; r < RM; ++r) {
       const float* wrow = wr + (int64_t)(r < R ? r : R - 1) * ldw + c;
       if constexpr (VW == 4) ld4(wrow, wv[r]);
       else wv[r][0] = wrow[0];
     }
 #pragma unroll
-    for (int r = 0; r < kRouteMaxR; ++r)
+    for (int r = 0; r < RM; ++r)
 #pragma unroll
       for (int e = 0; e < VW; ++e) acc[r] = __builtin_fmaf(x[e], r < R ? wv[r][e] : 0.0f, acc[r]);
   }
 #pragma unroll
-  for (int r = 0; r < kRouteMaxR; ++r) {
+  for (int r = 0; r < RM; ++r) {
     if (r < R) {
       float v = acc[r];
 #pragma unroll
@@ -723,14 +723,22 @@ int vnx_mod_route_x(const float* h, int64_t ldh, const float* norm_w, float eps,
   if (M >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   const bool v4 = D % 4 == 0 && ldh % 4 == 0 && ldw % 4 == 0 && vec4_ok(h, 4) && vec4_ok(wr, 4) &&
                   (!norm_w || vec4_ok(norm_w, 4)) && (!x_out || (ldxo % 4 == 0 && sxo % 4 == 0 && vec4_ok(x_out, 2)));
-  if (v4)
-    hipLaunchKernelGGL((k_mod_route_x<4>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h,
-                       ldh, norm_w, eps, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo,
-                       sxo, x_out ? copies : 0);
-  else
-    hipLaunchKernelGGL((k_mod_route_x<1>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), h,
-                       ldh, norm_w, eps, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out), ldxo,
-                       sxo, x_out ? copies : 0);
+  // router rows held per thread: P + P*E rounded up to 8 (rows past it are not loaded)
+  const int R = P + P * E;
+  auto go = [&](auto vw, auto rm) {
+    constexpr int VW = decltype(vw)::value, RM = decltype(rm)::value;
+    hipLaunchKernelGGL((k_mod_route_x<VW, RM>), dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       h, ldh, norm_w, eps, wr, ldw, D, P, E, topk, comb, ldc, static_cast<__hip_bfloat16*>(x_out),
+                       ldxo, sxo, x_out ? copies : 0);
+  };
+  auto by_r = [&](auto vw) {
+    if (R <= 8) go(vw, IntC<8>{});
+    else if (R <= 16) go(vw, IntC<16>{});
+    else if (R <= 24) go(vw, IntC<24>{});
+    else go(vw, IntC<32>{});
+  };
+  if (v4) by_r(IntC<4>{});
+  else by_r(IntC<1>{});
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }
