@@ -118,7 +118,7 @@ def _gemv_check(hip, kind, N, K, B, seed, rows=None):
 @pytest.mark.parametrize("kind", ["int8", "int4", "int4_g128"])
 @pytest.mark.parametrize("N,K,B", [(4096, 1024, 1), (1000, 384, 3), (1024, 4096, 8), (333, 512, 17),
                                    (512, 1024, 32), (256, 256, 40), (8192, 1024, 32), (1024, 4096, 32),
-                                   (40000, 256, 20)])
+                                   (40000, 256, 20), (33005, 512, 17), (40003, 1024, 32)])
 def test_gemv_parity(hip, kind, N, K, B):
     _gemv_check(hip, kind, N, K, B, seed=N + K + B)
 

@@ -560,10 +560,14 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 // Large N, W4 with group-128 fp16 scales (the tied LM head of a draft):
 // x (up to 32 batch rows x K) is staged in LDS once per workgroup, and each
 // wave streams 16-row tiles (tiles w, w + 4, ... of the workgroup's range)
-// with the next tile's weights and scales in flight while it computes the
-// current one.  KG = K / 128 groups.
-template <int NC, int KG>
+// through a ring of RS tiles in flight.  KG = K / 128 groups.  The MFMA takes
+// x as its A operand and the weights as B, so a lane's four outputs belong to
+// the one weight row it loads (batch rows 4kq .. 4kq + 3): each lane needs
+// only its own row's scales.
+template <int NC, int KG, int RS>
 __global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_per_wg) {
+  static_assert(KG == 4 || KG == 8, "K of 512 or 1024");
+  using SV = std::conditional_t<KG == 8, u32x4, uint2>;  // one row's KG fp16 scales
   constexpr int XS = KG * kGK + kXPad;  // LDS row pitch of x (fp16)
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_dyn[];
   uint16_t* xs = xs_dyn;
@@ -581,40 +585,26 @@ __global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_
   const int64_t tiles = (p.N + 15) / 16;
   const int64_t t_lo = (int64_t)blockIdx.x * tiles_per_wg;
   const int64_t t_hi = min(tiles, t_lo + tiles_per_wg);
-  // one tile's loads: weights (KG x 16 bytes per lane) and the fp16 scales of
-  // the lane's four D rows (KG halves each)
-  auto load = [&](int64_t tile, u32x4 (&wv)[KG], u32x4 (&sv)[4][KG / 8 > 0 ? KG / 8 : 1],
-                  uint2 (&sv4)[4]) {
+  // one tile's loads: the lane's weight row (KG x 16 bytes) and its scales
+  auto load = [&](int64_t tile, u32x4 (&wv)[KG], SV& sv) {
     const int64_t t = min(tile, tiles - 1);
     const int64_t ra = min(t * 16 + m, p.N - 1);
     const uint8_t* wr = p.w + ra * p.ldw + kq * 16;
 #pragma unroll
     for (int g = 0; g < KG; ++g) wv[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + g * 64));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t rd = min(t * 16 + 4 * kq + j, p.N - 1);
-      const uint16_t* srow = static_cast<const uint16_t*>(p.sc) + rd * p.lds;
-      if constexpr (KG >= 8) {
-#pragma unroll
-        for (int q = 0; q < KG / 8; ++q) sv[j][q] = *reinterpret_cast<const u32x4*>(srow + q * 8);
-      } else {
-        sv4[j] = *reinterpret_cast<const uint2*>(srow);
-      }
-    }
+    sv = *reinterpret_cast<const SV*>(static_cast<const uint16_t*>(p.sc) + ra * p.lds);
   };
-  auto scale = [&](const u32x4 (&sv)[4][KG / 8 > 0 ? KG / 8 : 1], const uint2 (&sv4)[4], int g, int j) {
+  auto scale = [&](const SV& sv, int g) {
     uint32_t wd;
-    if constexpr (KG >= 8) {
-      const u32x4 v = sv[j][g / 8];
-      const int e = (g % 8) / 2;
-      wd = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+    if constexpr (KG == 8) {
+      const int e = g / 2;
+      wd = e == 0 ? sv.x : e == 1 ? sv.y : e == 2 ? sv.z : sv.w;
     } else {
-      wd = (g / 2) == 0 ? sv4[j].x : sv4[j].y;
+      wd = (g / 2) == 0 ? sv.x : sv.y;
     }
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(wd >> (16 * (g % 2))));
   };
-  auto compute_store = [&](int64_t tile, const u32x4 (&wv)[KG], const u32x4 (&sv)[4][KG / 8 > 0 ? KG / 8 : 1],
-                           const uint2 (&sv4)[4]) {
+  auto compute_store = [&](int64_t tile, const u32x4 (&wv)[KG], const SV& sv) {
     f32x4 yacc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) yacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -626,50 +616,46 @@ __global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_
       const uint32_t wd[4] = {wv[g].x, wv[g].y, wv[g].z, wv[g].w};
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const half8 a = a_w4(wd[s4]);
+        const half8 bw = a_w4(wd[s4]);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const half8 bx = *reinterpret_cast<const half8*>(&xs[(c * 16 + m) * XS + g * kGK + kq * 32 + s4 * 8]);
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc[c], 0, 0, 0);
+          const half8 ax = *reinterpret_cast<const half8*>(&xs[(c * 16 + m) * XS + g * kGK + kq * 32 + s4 * 8]);
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bw, acc[c], 0, 0, 0);
         }
       }
+      const float sg = scale(sv, g);
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) yacc[c][j] = __builtin_fmaf(scale(sv, sv4, g, j), acc[c][j], yacc[c][j]);
+        for (int j = 0; j < 4; ++j) yacc[c][j] = __builtin_fmaf(sg, acc[c][j], yacc[c][j]);
       // one group's conversions live at a time (the scheduler would otherwise
       // hoist all of them, and the registers would cap the occupancy at one wave)
       __builtin_amdgcn_sched_barrier(0);
     }
     if (tile >= t_hi) return;
-    const int64_t n0 = tile * 16 + 4 * kq;
-    if (n0 >= p.N) return;
+    const int64_t n = tile * 16 + m;
+    if (n >= p.N) return;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int64_t b = c * 16 + m;
-      if (b >= p.B) continue;
-      float* dst = p.y + b * p.ldy + n0;
-      if (n0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-        *reinterpret_cast<f32x4*>(dst) = yacc[c];
-      } else {
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (n0 + j < p.N) dst[j] = yacc[c][j];
+      for (int j = 0; j < 4; ++j) {
+        const int64_t b = c * 16 + 4 * kq + j;
+        if (b < p.B) p.y[b * p.ldy + n] = yacc[c][j];
       }
-    }
   };
-  // two tiles per pass in a two-slot ring: slot A's loads were issued a
-  // pass earlier, slot B's before slot A's math
-  u32x4 wa[KG], wb[KG], sa[4][KG / 8 > 0 ? KG / 8 : 1], sb[4][KG / 8 > 0 ? KG / 8 : 1];
-  uint2 sa4[4], sb4[4];
-  int64_t ta = t_lo + wave;
-  load(ta, wa, sa, sa4);
-  for (; ta < t_hi; ta += 8) {
-    const int64_t tb = ta + 4;
-    load(tb, wb, sb, sb4);
-    compute_store(ta, wa, sa, sa4);
-    load(ta + 8, wa, sa, sa4);
-    compute_store(tb, wb, sb, sb4);
+  // RS slots: slot j holds tile ta + 4j; each slot is reloaded (tiles past
+  // the range load the last tile again) as soon as its math is issued
+  u32x4 wr[RS][KG];
+  SV sr[RS];
+  const int64_t t0 = t_lo + wave;
+#pragma unroll
+  for (int j = 0; j < RS; ++j) load(t0 + 4 * j, wr[j], sr[j]);
+  for (int64_t ta = t0; ta < t_hi; ta += 4 * RS) {
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+      compute_store(ta + 4 * j, wr[j], sr[j]);
+      load(ta + 4 * (j + RS), wr[j], sr[j]);
+    }
   }
 }
 
@@ -783,8 +769,9 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       const dim3 grid((unsigned)((tiles + tpw - 1) / tpw));
       const int nc = two ? 2 : 1;
       const size_t lds = (size_t)nc * 16 * (c.K + kXPad) * 2;
+      // (a ring of 4 tiles measured 1.2x slower at B = 32: 199 VGPRs)
 #define VNX_QSTREAM(NC, KG) \
-  hipLaunchKernelGGL((k_qgemv_stream<NC, KG>), grid, dim3(kQNT), lds, s, c, (int)tpw)
+  hipLaunchKernelGGL((k_qgemv_stream<NC, KG, 2>), grid, dim3(kQNT), lds, s, c, (int)tpw)
       if (c.K == 512) { if (two) VNX_QSTREAM(2, 4); else VNX_QSTREAM(1, 4); }
       else { if (two) VNX_QSTREAM(2, 8); else VNX_QSTREAM(1, 8); }
 #undef VNX_QSTREAM
