@@ -148,6 +148,34 @@ def test_bf16_kernel_path_matches_oracle(hip):
     _say(f"bf16 kernel path worst relative err {worst:.2e}")
 
 
+@pytest.mark.parametrize("int4", [True, False])
+def test_cache_only_forward_writes_the_same_cache(hip, int4):
+    """forward(cache_only=True) stops after the last layer's cache write (the
+    INT4 decode; the bf16 one writes its cache inside the attention call and
+    runs to the end): every layer's cache equals a full forward's, bit for bit."""
+    cfg = VM.ModelConfig(vocab_size=1000, dim=128, n_layer=2, n_head=2, n_kv_head=1,
+                         layer_pattern=("trisparse", "trisparse"), window_size=1024, num_global_tokens=8,
+                         use_alibi=False, use_rope=True)
+    W = VM.init_weights(cfg, seed=31)
+    dev = hip.torch_device
+    B = 4
+    ms = [VM.CometSparkGPU(cfg, W, hip, batch=B, capacity=128, dtype=torch.bfloat16, int4=int4) for _ in range(2)]
+    rng = np.random.default_rng(4)
+    prompt = torch.from_numpy(rng.integers(0, 1000, (B, 20))).to(dev)
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    for m in ms:
+        m.forward(prompt, lens, 0)
+    lens = torch.tensor([20, 17, 19, 12], dtype=torch.int32, device=dev)
+    tok = torch.from_numpy(rng.integers(0, 1000, (B, 1))).to(dev)
+    r = ms[0].forward(tok, lens, 20, cache_only=True)
+    assert (r is None) == int4
+    assert ms[1].forward(tok, lens, 20) is not None
+    torch.cuda.synchronize()
+    for li in range(cfg.n_layer):
+        assert torch.equal(ms[0].kc[li], ms[1].kc[li]), li
+        assert torch.equal(ms[0].vc[li], ms[1].vc[li]), li
+
+
 def test_kernel_and_torch_attention_paths_agree(hip):
     cfg = _toy_cfg()
     W = VM.init_weights(cfg, seed=5)

@@ -111,7 +111,9 @@ class SpecDecodeEngine:
         # the draft's positions lens_d[b] + i of all k+1 steps in one kernel
         lens_steps = self.lens_d.view(1, B) + self.steps_i32
         for i in range(k + 1):
-            h = self.d.forward(tok.view(B, 1), lens_steps[i], Tmax_d + i, out_dtype=self.d.act_dtype)
+            # the last step only writes the last draft token's cache rows
+            h = self.d.forward(tok.view(B, 1), lens_steps[i], Tmax_d + i, out_dtype=self.d.act_dtype,
+                               cache_only=i == k)
             if i == k:
                 break
             self.d.logits(h, out=self.qbuf[:, i:i + 1])

@@ -753,10 +753,14 @@ class CometSparkGPU:
 
     @torch.no_grad()
     def forward(self, tokens: torch.Tensor, lens: torch.Tensor, Tmax: Optional[int] = None,
-                out_dtype=torch.float32) -> torch.Tensor:
+                out_dtype=torch.float32, cache_only: bool = False) -> Optional[torch.Tensor]:
         """tokens (B, n) int64, lens (B,) int32 on this device; Tmax >= max(lens)
         (read back from the device when not given).  Returns (B, n, D) final-norm
-        hidden states in out_dtype (fp32 by default)."""
+        hidden states in out_dtype (fp32 by default).  cache_only: the caller
+        needs only the new rows' keys and values in every layer's cache (a
+        draft's last step of a round), so the forward stops once the last
+        layer has written them and returns None (where that layer's cache write
+        happens inside its attention call, the forward runs to the end)."""
         cfg = self.cfg
         B, n = tokens.shape
         if B != self.B:
@@ -826,6 +830,8 @@ class CometSparkGPU:
                     int(cfg.use_rope), P(q.data_ptr()), P(kc.data_ptr()), P(vc.data_ptr()),
                     _lib.DTYPE_CODES[self.dtype], kc.stride(0), kc.stride(1), kc.stride(2), self.cap, self._st()),
                     "rope_kv")
+            if cache_only and attn_qkv is None and li == len(self.layers) - 1:
+                return None                                # every layer's new cache rows are written
             if use_kernel:
                 o = self._attn_kernel(q, li, lens, n, Tmax, qkv=attn_qkv)
             else:
