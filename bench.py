@@ -166,7 +166,7 @@ def bench_gemv(args):
            "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "dtype": "int4/int8 x fp16",
            "data": "synthetic", "config": {"workload": "BASELINE config 4: weight-only dequant-GEMV"},
            "roofline": {"bound": "hbm", "achieved": best["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": best["frac"], "traffic": None, "kernel": "k_qgemv<4,*> (tied head)"},
+                        "frac": best["frac"], "traffic": None, "kernel": "k_qgemv_stream<*, 8, 2> (tied head)"},
            "results": rows}
     print(json.dumps(out), flush=True)
 
