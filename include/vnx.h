@@ -337,7 +337,8 @@ typedef struct vnx_tree_attn_args {
    * and each workgroup first writes the rows' rotated keys and their values
    * into k_tree / v_tree at tree row tp_b + i (rows at or past cap skipped).
    * Needs tree_follows_prefix and tp_batch; rope == 0: no rotation; cos /
-   * sin tables (table_rows, d) fp32.  NULL (or zero-initialised trailing
+   * sin tables (table_rows, d) fp32, 16-byte aligned (else
+   * VNX_ERR_UNSUPPORTED).  NULL (or zero-initialised trailing
    * fields): q holds the queries and the tree rows are already written. */
   const void* qkv;
   int64_t qkv_ld;

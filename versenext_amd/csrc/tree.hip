@@ -162,13 +162,19 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
       if (!p.rope) { lo = a; hi = z; return; }
       const __bf16* av = reinterpret_cast<const __bf16*>(&a);
       const __bf16* zv = reinterpret_cast<const __bf16*>(&z);
+      // the table entries of dims c*8 .. +8 and their partners: 16-byte loads
+      // (tables 16-byte aligned, D a multiple of 16)
+      f32x4 tc[4], ts[4];
+      const f32x4* cr = reinterpret_cast<const f32x4*>(p.cos + pos * D + c * 8);
+      const f32x4* sr = reinterpret_cast<const f32x4*>(p.sin + pos * D + c * 8);
+      tc[0] = cr[0]; tc[1] = cr[1]; tc[2] = cr[D / 8]; tc[3] = cr[D / 8 + 1];
+      ts[0] = sr[0]; ts[1] = sr[1]; ts[2] = sr[D / 8]; ts[3] = sr[D / 8 + 1];
       __bf16 lo8[8], hi8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int j = c * 8 + e;
         const float x0 = static_cast<float>(av[e]), x1 = static_cast<float>(zv[e]);
-        const float c0 = p.cos[pos * D + j], c1 = p.cos[pos * D + j + D / 2];
-        const float s0 = p.sin[pos * D + j], s1 = p.sin[pos * D + j + D / 2];
+        const float c0 = tc[e >> 2][e & 3], c1 = tc[2 + (e >> 2)][e & 3];
+        const float s0 = ts[e >> 2][e & 3], s1 = ts[2 + (e >> 2)][e & 3];
         lo8[e] = static_cast<__bf16>(x0 * c0 - x1 * s0);   // rotate_half(x)[j] = -x[j + D/2]
         hi8[e] = static_cast<__bf16>(x1 * c1 + x0 * s1);   // rotate_half(x)[j + D/2] = x[j]
       }
@@ -632,6 +638,7 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
     if (!a->tree_follows_prefix || !a->tp_batch || a->cap < 1) return VNX_ERR_INVALID_ARG;
     if (a->qkv_ld < (int64_t)(H + 2 * Hkv) * d) return VNX_ERR_INVALID_ARG;
     if (a->rope && (!a->cos_table || !a->sin_table || a->table_rows < 1)) return VNX_ERR_INVALID_ARG;
+    if (a->rope && (!aligned16(a->cos_table) || !aligned16(a->sin_table))) return VNX_ERR_UNSUPPORTED;
     if (!aligned16(a->qkv) || a->qkv_ld % 8) return VNX_ERR_UNSUPPORTED;
   }
   if (a->T2 > 0) {
