@@ -156,7 +156,8 @@ def test_gemv_rejects_bad_shapes(hip):
         hip.gemv_w8(x, torch.zeros((8, 100), dtype=torch.int8), torch.ones(8))  # K % 128 != 0
 
 
-@pytest.mark.parametrize("H,K,B", [(4096, 1024, 32), (4096, 1024, 1), (64, 256, 17), (1000, 512, 40)])
+@pytest.mark.parametrize("H,K,B", [(4096, 1024, 32), (4096, 1024, 1), (64, 256, 17), (1000, 512, 40),
+                                   (2056, 1024, 32), (2056, 2048, 7)])
 def test_gemv_swiglu_parity(hip, H, K, B):
     """vnx_gemv_w4_swiglu: the group-128 GEMV of a [gate; up] weight whose rows
     are interleaved in blocks of 8 gate + 8 up rows, with silu(gate) * up in
@@ -198,7 +199,7 @@ def test_gemv_swiglu_parity(hip, H, K, B):
                                          VP(torch.cuda.current_stream().cuda_stream)) == _lib.VNX_ERR_UNSUPPORTED
 
 
-@pytest.mark.parametrize("H,K,B", [(4096, 1024, 32), (64, 256, 17), (1000, 512, 40)])
+@pytest.mark.parametrize("H,K,B", [(4096, 1024, 32), (64, 256, 17), (1000, 512, 40), (2056, 1024, 20)])
 def test_gemv_swiglu_norm_input(hip, H, K, B):
     """vnx_gemv_w4_swiglu with norm_w: the staged operand is fp16(x * w) as
     numpy rounds the fp32 product, so the reference is that fp16 matrix times
@@ -240,7 +241,8 @@ def test_gemv_swiglu_norm_input(hip, H, K, B):
     assert np.all(err <= bound), worst
 
 
-@pytest.mark.parametrize("N,K,B", [(1024, 1024, 32), (1024, 4096, 32), (100, 256, 40)])
+@pytest.mark.parametrize("N,K,B", [(1024, 1024, 32), (1024, 4096, 32), (100, 256, 40), (4104, 1024, 32),
+                                   (4104, 2048, 9)])
 def test_gemv_residual(hip, N, K, B):
     """vnx_gemv_w4_residual: res += x . W^T (fp32); the GEMV bar plus one fp32
     rounding of the sum."""

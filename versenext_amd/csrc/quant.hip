@@ -299,36 +299,45 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
 // staged operand is fp16(xf * nw), each wave sums the squares of its groups'
 // values per row, and the epilogue scales row b by rstd_b = 1/sqrt(mean
 // xf^2 + eps) (vnnn.py:593-615, the per-row factor on the fp32 sums).
-template <int BITS, int NC, int NW, int QE = 0, bool NX = false>
+// TP: 16-row tiles per workgroup (2 for grids of more tiles than CUs: each
+// wave's x block is loaded and staged once for both tiles).  GP: groups per
+// pass of a wave (1 where K has at most one group per wave, or TP 2).
+template <int BITS, int NC, int NW, int QE = 0, bool NX = false, int TP = 1, int GP = 2>
 __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   constexpr int WBYTES = BITS == 4 ? 16 : 32;
   constexpr int XR = NC * 16;            // staged batch rows
   constexpr int XP = kGK + kXPad;        // LDS row pitch (fp16)
   constexpr int XL = XR * (kGK / 8) / 64;  // 16-byte x loads per lane per group
   // the per-wave x tiles, reused for the partial tiles after the K loop
-  constexpr size_t kXBytes = size_t(NW) * XR * XP * 2, kRBytes = size_t(NW) * NC * 64 * 16;
+  constexpr size_t kXBytes = size_t(NW) * XR * XP * 2, kRBytes = size_t(NW) * TP * NC * 64 * 16;
   __shared__ __attribute__((aligned(16))) char smem[kXBytes > kRBytes ? kXBytes : kRBytes];
   auto xs_all = reinterpret_cast<uint16_t(*)[XR * XP]>(smem);
-  auto red = reinterpret_cast<f32x4(*)[NC][64]>(smem);
+  auto red = reinterpret_cast<f32x4(*)[TP][NC][64]>(smem);
   __shared__ float ssp[NX ? NW : 1][NX ? XR : 1];  // NX: per-wave sums of squares per row
   const int tid = threadIdx.x;
   const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
   const int m = lane % 16, kq = lane / 16;
   uint16_t* xs = xs_all[wave];
-  const int64_t row0 = (int64_t)blockIdx.x * 16;
-  const int64_t ra = min(row0 + m, p.N - 1);     // A row (rows past N read row N-1, not stored)
-  const uint8_t* wr = p.w + ra * p.ldw;
+  const int64_t tile0 = (int64_t)blockIdx.x * TP;
+  const uint8_t* wr[TP];
+#pragma unroll
+  for (int t = 0; t < TP; ++t) {
+    const int64_t ra = min((tile0 + t) * 16 + m, p.N - 1);  // A row (rows past N read row N-1, not stored)
+    wr[t] = p.w + ra * p.ldw;
+  }
   const int ngroups = (int)(p.K / kGK);
 
-  f32x4 yacc[NC];
+  f32x4 yacc[TP][NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) yacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // QE 3: the residual values wave c < NC adds to (row c*16 + m, columns
-  // row0 + 4*kq .. +4) load now, under the K loop
+  for (int t = 0; t < TP; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) yacc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // QE 3: the residual values wave t*NC + c adds to (row c*16 + m, columns
+  // (tile0 + t)*16 + 4*kq .. +4) load now, under the K loop
   f32x4 rold = {0.f, 0.f, 0.f, 0.f};
   if constexpr (QE == 3) {
-    if (wave < NC) {
-      const int64_t rb = wave * 16 + m, rn = row0 + 4 * kq;
+    if (wave < NC * TP) {
+      const int64_t rb = (wave % NC) * 16 + m, rn = (tile0 + wave / NC) * 16 + 4 * kq;
       if (rb < p.B && rn < p.N) {
         const float* src = p.y + rb * p.ldy + rn;
         if (rn + 4 <= p.N && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
@@ -344,23 +353,27 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
   for (int i = 0; i < (NX ? XL : 1); ++i) ss[i] = 0.0f;
 
-  for (int g0 = wave; g0 < ngroups; g0 += 2 * NW) {
-    // two groups per pass: g0 and g0 + NW (the second weighted 0 when past K)
+  static_assert(GP == 1 || GP == 2, "one or two groups per pass");
+  for (int g0 = wave; g0 < ngroups; g0 += GP * NW) {
+    // GP 2: groups g0 and g0 + NW (the second weighted 0 when past K)
     const int gg[2] = {g0, g0 + NW < ngroups ? g0 + NW : g0};
     const bool second = g0 + NW < ngroups;
-    uint32_t wv[2][WBYTES / 4];
-    u32x4 xv[2][XL][NX ? 2 : 1];
-    u32x4 nwv[2][NX ? 2 : 1];
-    float sc[2][4];
+    uint32_t wv[GP][TP][WBYTES / 4];
+    u32x4 xv[GP][XL][NX ? 2 : 1];
+    u32x4 nwv[GP][NX ? 2 : 1];
+    float sc[GP][TP][4];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < GP; ++u) {
       const int64_t k0 = (int64_t)gg[u] * kGK;
-      const uint8_t* src = wr + (BITS == 4 ? k0 / 2 + kq * 16 : k0 + kq * 32);
-      const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-      wv[u][0] = v0.x; wv[u][1] = v0.y; wv[u][2] = v0.z; wv[u][3] = v0.w;
-      if constexpr (BITS == 8) {
-        const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
-        wv[u][4] = v1.x; wv[u][5] = v1.y; wv[u][6] = v1.z; wv[u][7] = v1.w;
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        const uint8_t* src = wr[t] + (BITS == 4 ? k0 / 2 + kq * 16 : k0 + kq * 32);
+        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+        wv[u][t][0] = v0.x; wv[u][t][1] = v0.y; wv[u][t][2] = v0.z; wv[u][t][3] = v0.w;
+        if constexpr (BITS == 8) {
+          const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 16));
+          wv[u][t][4] = v1.x; wv[u][t][5] = v1.y; wv[u][t][6] = v1.z; wv[u][t][7] = v1.w;
+        }
       }
       // x block: load i covers batch row (i*64 + lane) / 16, chunk lane % 16
 #pragma unroll
@@ -381,11 +394,13 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
       if constexpr (BITS == 4) {
         const unsigned col = p.gpg == 1 ? (unsigned)gg[u] : (unsigned)gg[u] / (unsigned)p.gpg;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc[u][j] = load_scale(p, min(row0 + 4 * kq + j, p.N - 1), col);
+        for (int t = 0; t < TP; ++t)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sc[u][t][j] = load_scale(p, min((tile0 + t) * 16 + 4 * kq + j, p.N - 1), col);
       }
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < GP; ++u) {
       wave_lds_fence();  // the previous group's B-operand reads are done
       const bool use = u == 0 || second;
 #pragma unroll
@@ -417,26 +432,34 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
         *reinterpret_cast<u32x4*>(&xs[b * XP + m * 8]) = v;
       }
       wave_lds_fence();
-      f32x4 acc[NC];
+      f32x4 acc[TP][NC];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < TP; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const half8 a = BITS == 4 ? a_w4(wv[u][s4]) : a_w8(wv[u][2 * s4], wv[u][2 * s4 + 1]);
+        half8 a[TP];
+#pragma unroll
+        for (int t = 0; t < TP; ++t)
+          a[t] = BITS == 4 ? a_w4(wv[u][t][s4]) : a_w8(wv[u][t][2 * s4], wv[u][t][2 * s4 + 1]);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           const half8 bx = *reinterpret_cast<const half8*>(&xs[(c * 16 + m) * XP + kq * 32 + s4 * 8]);
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, acc[c], 0, 0, 0);
+#pragma unroll
+          for (int t = 0; t < TP; ++t) acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bx, acc[t][c], 0, 0, 0);
         }
       }
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
+      for (int t = 0; t < TP; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (BITS == 4) yacc[c][j] = __builtin_fmaf(use ? sc[u][j] : 0.0f, acc[c][j], yacc[c][j]);
-          else yacc[c][j] += use ? acc[c][j] : 0.0f;
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if constexpr (BITS == 4) yacc[t][c][j] = __builtin_fmaf(use ? sc[u][t][j] : 0.0f, acc[t][c][j], yacc[t][c][j]);
+            else yacc[t][c][j] += use ? acc[t][c][j] : 0.0f;
+          }
         }
-      }
     }
   }
 
@@ -454,17 +477,21 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   }
   __syncthreads();  // every wave is done with its x tile
 #pragma unroll
-  for (int c = 0; c < NC; ++c) red[wave][c][lane] = yacc[c];
+  for (int t = 0; t < TP; ++t)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) red[wave][t][c][lane] = yacc[t][c];
   __syncthreads();
-  // wave c sums column block c over the waves, in wave order, and stores it:
-  // lane holds D[row 4*kq + j][column m]
-  if (wave >= NC) return;
-  const int c = wave;
+  // wave t*NC + c sums column block c of tile t over the waves, in wave
+  // order, and stores it: lane holds D[row 4*kq + j][column m]
+  if (wave >= NC * TP) return;
+  const int c = wave % NC;
+  const int64_t tile = tile0 + wave / NC;
+  const int64_t row0 = tile * 16;
   const int64_t b = c * 16 + m;
   if (b >= p.B) return;
-  f32x4 v = red[0][c][lane];
+  f32x4 v = red[0][wave / NC][c][lane];
 #pragma unroll
-  for (int w = 1; w < NW; ++w) v += red[w][c][lane];
+  for (int w = 1; w < NW; ++w) v += red[w][wave / NC][c][lane];
   const int64_t n0 = row0 + 4 * kq;
   if (n0 >= p.N) return;
   if constexpr (BITS == 8) {
@@ -496,7 +523,7 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
     float part[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) part[j] = __shfl_xor(v[j], 32);
-    const int t = blockIdx.x;
+    const int t = (int)tile;
     const int hh = t * 16 / p.ro.d;
     const int qb = (t * 16 - hh * p.ro.d) / 16;
     // one token row, four consecutive dims (all loads before any use)
@@ -539,7 +566,7 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) u[j] = __shfl_xor(v[j], 32);
     if (kq >= 2) return;
-    uint16_t* dh = p.yh + b * p.ldy + (int64_t)blockIdx.x * 8 + 4 * kq;
+    uint16_t* dh = p.yh + b * p.ldy + tile * 8 + 4 * kq;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float g = v[j];
@@ -738,10 +765,26 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
   hipLaunchKernelGGL((k_qgemv_tile<BITS, NC, NW>), grid, dim3(NW * 64), 0, s, c)
 #define VNX_QTILE_E(NC, NW, QE, NX) \
   hipLaunchKernelGGL((k_qgemv_tile<4, NC, NW, QE, NX>), grid, dim3(NW * 64), 0, s, c)
+#define VNX_QTILE_E1(NC, QE, NX) \
+  hipLaunchKernelGGL((k_qgemv_tile<4, NC, 8, QE, NX, 1, 1>), grid, dim3(8 * 64), 0, s, c)
+#define VNX_QTILE_E2(NC, QE, NX) \
+  hipLaunchKernelGGL((k_qgemv_tile<4, NC, 8, QE, NX, 2, 1>), grid2, dim3(8 * 64), 0, s, c)
+      // epilogue variants: beyond one tile per CU, 2 tiles per 8-wave
+      // workgroup (x loaded once for both; 2.4% of the config-5 round); one
+      // group per wave where K has at most 8 groups (no second, zero-weighted
+      // group)
+      const bool tp2 = !wide;
+      const bool g1 = c.K <= 8 * kGK;
+      const dim3 grid2((unsigned)((tiles + 1) / 2));
+#define VNX_QTILE_W(NC, QE, NX) \
+  do { \
+    if (wide) { if (g1) VNX_QTILE_E1(NC, QE, NX); else VNX_QTILE_E(NC, 8, QE, NX); } \
+    else if (tp2) VNX_QTILE_E2(NC, QE, NX); \
+    else VNX_QTILE_E(NC, 4, QE, NX); \
+  } while (0)
 #define VNX_QTILE_Q(QE, NX) \
   do { \
-    if (two) { if (wide) VNX_QTILE_E(2, 8, QE, NX); else VNX_QTILE_E(2, 4, QE, NX); } \
-    else { if (wide) VNX_QTILE_E(1, 8, QE, NX); else VNX_QTILE_E(1, 4, QE, NX); } \
+    if (two) VNX_QTILE_W(2, QE, NX); else VNX_QTILE_W(1, QE, NX); \
   } while (0)
       if (c.rope_on) {
         if (c.xf) VNX_QTILE_Q(2, true); else VNX_QTILE_Q(2, false);
@@ -758,6 +801,9 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       }
 #undef VNX_QTILE
 #undef VNX_QTILE_E
+#undef VNX_QTILE_E1
+#undef VNX_QTILE_E2
+#undef VNX_QTILE_W
 #undef VNX_QTILE_Q
     } else if (bits == 4 && c.G == kGK && c.sc_f16 && c.lds % 8 == 0 && aligned16(c.sc) &&
                (c.K == 512 || c.K == 1024) && !getenv("VNX_QSTREAM_OFF")) {
