@@ -242,7 +242,7 @@ def test_gemv_swiglu_norm_input(hip, H, K, B):
 
 
 @pytest.mark.parametrize("N,K,B", [(1024, 1024, 32), (1024, 4096, 32), (100, 256, 40), (4104, 1024, 32),
-                                   (4104, 2048, 9)])
+                                   (4104, 2048, 9), (1000, 3072, 5), (512, 8192, 17)])
 def test_gemv_residual(hip, N, K, B):
     """vnx_gemv_w4_residual: res += x . W^T (fp32); the GEMV bar plus one fp32
     rounding of the sum."""
