@@ -147,10 +147,12 @@ def mod(W, p, cfg, x):
     return out
 
 
-def forward(W, cfg, idx, return_hidden=False, last_n=None):
+def forward(W, cfg, idx, return_hidden=False, last_n=None, head=None):
     """logits (B, T, V) float32 of the tokens idx (B, T); with last_n, only
     the last last_n positions go through the head (the verifier reads k+1
-    rows, speculative.py:218-220)."""
+    rows, speculative.py:218-220).  head: the (V, D) head weight when it is
+    stored apart from the input embedding (a quantized copy of the tied
+    table), else the tied table itself (cometspark.py:396-398)."""
     idx = np.asarray(idx, dtype=np.int64)
     if idx.ndim == 1:
         idx = idx[None]
@@ -172,7 +174,52 @@ def forward(W, cfg, idx, return_hidden=False, last_n=None):
         return x
     if last_n is not None:
         x = x[:, -last_n:]
-    return x @ emb.T
+    return x @ (emb if head is None else head).T
+
+
+def bf16_round(a):
+    """float32 values rounded to bfloat16 (round to nearest, ties to even),
+    returned as float32."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(a), a, out).astype(np.float32)
+
+
+_MATRICES = ("attn.wq.weight", "attn.wk.weight", "attn.wv.weight", "attn.proj.weight", "w_gate.weight",
+             "w_up.weight", "w_down.weight")
+
+
+def stored_weights(W, int4: bool = False):
+    """The weights a GPU model holds, restated for this forward
+    (versenext_amd/model.py CometSparkGPU): every projection matrix and the
+    embedding table rounded to bfloat16; with int4, the projection matrices
+    are instead the exact dequantization q * s of their INT4 group-128
+    quantization (oracle.quant.quantize_int4_g) and the head is the
+    dequantized INT4 copy of the embedding table (returned second, else
+    None).  Norm weights, router weights, global tokens and gate logits stay
+    float32."""
+    from . import quant as OQ
+    out = {}
+    for k, v in W.items():
+        v = np.asarray(v, np.float32)
+        if k.endswith(_MATRICES):
+            if int4 and v.shape[1] % 128 == 0:
+                q, s = OQ.quantize_int4_g(v, 128)
+                out[k] = OQ.dequantize_int4_g(q, s, v.shape, 128)
+            else:
+                out[k] = bf16_round(v)
+        elif k == "tok_emb.weight":
+            out[k] = bf16_round(v)
+        else:
+            out[k] = v
+    head = None
+    if int4:
+        emb = np.asarray(W["tok_emb.weight"], np.float32)
+        q, s = OQ.quantize_int4_g(emb, 128)
+        head = OQ.dequantize_int4_g(q, s, emb.shape, 128)
+    return out, head
 
 
 def greedy_stream(W, cfg, prompt, n_new):

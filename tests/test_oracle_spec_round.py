@@ -1,0 +1,108 @@
+"""The CPU restatement of one stochastic speculative round
+(oracle/model.py spec_round_cpu: draft draws, full re-forward verify, the
+canonical acceptance), pinned by what the mathematics and the reference's own
+golden vectors fix:
+- as T -> 0 every softmax is one-hot at its argmax, so the round is the
+  reference's greedy verify (speculative.py:218-287) plus the bonus token,
+  and the committed stream is the target's greedy stream that the reference
+  wrote (tests/golden/cometspark_small.npz, greedy128);
+- a draft identical to the target has q = p at every verified position, so
+  min(1, p/q) = 1 and every draft is accepted (k+1 tokens per round);
+- a planted mistake (the verifier reading its rows one position early) fails
+  the greedy-stream check."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import model as OM
+from versenext_amd import model as VM
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cometspark_small.npz")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    z = np.load(GOLD)
+    return {k: z[k] for k in z.files}
+
+
+def _w(gold, prefix):
+    return {k[len(prefix):]: v for k, v in gold.items() if k.startswith(prefix) and not k.endswith("head.weight")}
+
+
+def _stream(gold, temperature, k=4, n=128, seed=5, round_fn=None):
+    Wt, Wd = _w(gold, "t/"), _w(gold, "d/")
+    ct, cd = VM.small_target(), VM.small_draft()
+    rng = np.random.default_rng(seed)
+    seq = [int(t) for t in gold["prompt"]]
+    out, rounds = [], 0
+    fn = round_fn or OM.spec_round_cpu
+    while len(out) < n:
+        acc = fn(Wt, ct, Wd, cd, seq, k, temperature, rng.random(k).astype(np.float32),
+                 rng.random(k + 1).astype(np.float32))
+        assert 1 <= len(acc) <= k + 1
+        seq += acc
+        out += acc
+        rounds += 1
+    return np.asarray(out[:n], np.int64), rounds
+
+
+def test_low_temperature_round_is_the_greedy_stream(gold):
+    toks, rounds = _stream(gold, 0.01)
+    assert np.array_equal(toks, gold["greedy128"])
+    assert rounds < 128  # rounds commit several tokens
+
+
+def test_identical_draft_accepts_every_position(gold):
+    Wt = _w(gold, "t/")
+    ct = VM.small_target()
+    rng = np.random.default_rng(7)
+    seq = [int(t) for t in gold["prompt"]]
+    k = 4
+    for _ in range(6):
+        ud = rng.random(k).astype(np.float32)
+        ua = (rng.random(k + 1) * 0.999).astype(np.float32)
+        acc = OM.spec_round_cpu(Wt, ct, Wt, ct, seq, k, 0.8, ud, ua)
+        assert len(acc) == k + 1
+        seq += acc
+
+
+def test_planted_early_verify_rows_fail(gold, monkeypatch):
+    """The verifier reading the rows one position early (its context missing
+    the last draft) no longer reproduces the greedy stream."""
+    real = OM.forward
+
+    def early(W, cfg, idx, return_hidden=False, last_n=None, head=None):
+        if last_n is not None and last_n > 1:
+            idx = np.asarray(idx)[:, :-1]
+        return real(W, cfg, idx, return_hidden=return_hidden, last_n=last_n, head=head)
+
+    monkeypatch.setattr(OM, "forward", early)
+    toks, _ = _stream(gold, 0.01, n=64)
+    assert not np.array_equal(toks, gold["greedy128"][:64])
+
+
+def test_stored_weights_bf16_and_int4(gold):
+    """The GPU models' weight storage restated: bf16 rounding (ties to even)
+    and exact INT4 group-128 dequantization, head kept apart for INT4."""
+    rng = np.random.default_rng(0)
+    W = VM.init_weights(VM.ModelConfig(vocab_size=300, dim=128, n_layer=1, n_head=2, n_kv_head=1,
+                                       layer_pattern=("trisparse",), window_size=64, num_global_tokens=4,
+                                       use_alibi=False, use_rope=True, mlp_hidden=256), seed=1)
+    Wn = {k: v.numpy() for k, v in W.items()}
+    s16, head = OM.stored_weights(Wn)
+    assert head is None
+    x = s16["blocks.0.attn.wq.weight"]
+    assert np.array_equal(x.view(np.uint32) & 0xFFFF, np.zeros_like(x.view(np.uint32)))
+    assert np.max(np.abs(x - Wn["blocks.0.attn.wq.weight"])) <= 2.0 ** -8 * np.max(np.abs(x))
+    assert np.array_equal(s16["norm.weight"], Wn["norm.weight"])
+    s4, head = OM.stored_weights(Wn, int4=True)
+    w = Wn["blocks.0.ffn.w_down.weight"]
+    q = s4["blocks.0.ffn.w_down.weight"]
+    g = np.abs(w.reshape(w.shape[0], -1, 128)).max(-1, keepdims=True) / 7.0
+    assert np.all(np.abs((q - w).reshape(g.shape[0], -1, 128)) <= g * 0.5 * (1 + 1e-3))
+    assert head.shape == Wn["tok_emb.weight"].shape and not np.array_equal(head, s4["tok_emb.weight"])
+    assert np.array_equal(OM.bf16_round(np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8], np.float32)),
+                          np.array([1.0, 1.0 + 2.0 ** -6], np.float32))
+    del rng

@@ -95,6 +95,8 @@ class SpecDecodeEngine:
         self.out = None
         self.n_new = 0
         self.graph = None
+        # the last round's acceptance outputs (accept_len, out_ids, flags)
+        self.last = None
         # attention prefix bound used by captured rounds
         self.bound_t = target.cap - (k + 2)
         self.bound_d = draft.cap - (k + 2)
@@ -128,9 +130,11 @@ class SpecDecodeEngine:
         self.t.logits(h, out=self.pbuf)
         if self.greedy:
             _, _, alen, ids = self.hip.greedy_verify(self.pbuf, xs, rows_t=k + 1)
+            self.last = dict(accept_len=alen, out_ids=ids, flags=None)
         else:
             res = self.hip.spec_accept(self.pbuf, self.qbuf, xs, self.u_acc, temperature=self.T)
             alen, ids = res["accept_len"], res["out_ids"]
+            self.last = res
         # commit (one launch, no data-dependent shapes, so the round can be
         # captured): ids[b, :n_b + 1] appended to out[b, count_b ...], counts,
         # cache lengths and the next round's first token advanced, and the
@@ -144,15 +148,20 @@ class SpecDecodeEngine:
 
     # ---- driver ---------------------------------------------------------
     @torch.no_grad()
-    def generate(self, prompts: torch.Tensor, n_new: int, phase_timing: bool = False):
-        """prompts (B, T0) int64 on the device.  Returns (tokens (B, n_new)
-        int64 on the device, DecodeStats).  Prefill is timed separately from
-        the decode rounds."""
+    def prefill(self, prompts: torch.Tensor, n_new: int) -> float:
+        """Runs the prompts (B, T0) int64 on the device through both models,
+        resets the round state and the output buffer for n_new tokens per
+        sequence, and returns the prefill wall time (s).  Rounds then follow
+        with step()."""
         B, T0 = prompts.shape
         if B != self.B:
             raise ValueError(f"batch {B} != {self.B}")
+        if T0 < 1:
+            raise ValueError("prompts need at least one token")
         k = self.k
         dev = self.dev
+        if T0 - 1 + n_new + 2 * (k + 1) > min(self.t.cap, self.d.cap):
+            raise ValueError("the caches cannot hold prompt + n_new tokens")
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
         self.lens_t.zero_()
@@ -170,32 +179,69 @@ class SpecDecodeEngine:
             self.graph = None
         else:
             self.out.fill_(-1)
+        self._Tmax = (T0 - 1, T0 - 1)
         torch.cuda.synchronize(dev)
-        st = DecodeStats(prefill_s=time.perf_counter() - t0)
-        if T0 - 1 + n_new + 2 * (k + 1) > min(self.t.cap, self.d.cap):
-            raise ValueError("the caches cannot hold prompt + n_new tokens")
+        return time.perf_counter() - t0
+
+    def _set_uniforms(self, uniforms) -> None:
+        """uniforms = (u_draft (k, B), u_acc (B, k+1)) float32 (host arrays or
+        tensors): u_draft[i, b] draws draft token i+1 of sequence b from
+        softmax(q_i / T); u_acc[b, :k] are its acceptance tests and
+        u_acc[b, k] its residual / bonus draw."""
+        ud, ua = uniforms
+        ud = torch.as_tensor(ud, dtype=torch.float32)
+        ua = torch.as_tensor(ua, dtype=torch.float32)
+        if tuple(ud.shape) != tuple(self.u_draft.shape) or tuple(ua.shape) != tuple(self.u_acc.shape):
+            raise ValueError(f"uniforms must be ({self.k}, {self.B}) and ({self.B}, {self.k + 1})")
+        self.u_draft.copy_(ud)
+        self.u_acc.copy_(ua)
+
+    @torch.no_grad()
+    def step(self, uniforms=None) -> torch.Tensor:
+        """One speculative round of every sequence (a graph replay once
+        captured).  uniforms: None (drawn from the engine's generator) or
+        (u_draft, u_acc) supplied by the caller (see _set_uniforms).  Returns
+        info (4,) int64 on the host: min committed count, max target / draft
+        cache length, accepted drafts summed over the batch."""
+        if self.out is None:
+            raise RuntimeError("call prefill() before step()")
+        if uniforms is None:
+            self._fill_uniforms()
+        elif not self.greedy:
+            self._set_uniforms(uniforms)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._round(*self._Tmax)
+        info = self.info.cpu()
+        Tmax_t, Tmax_d = int(info[1]), int(info[2])
+        if Tmax_t + self.k + 2 > self.t.cap or Tmax_d + self.k + 2 > self.d.cap:
+            if int(info[0]) < self.n_new:
+                raise RuntimeError("KV cache capacity exhausted")
+        self._Tmax = (Tmax_t, Tmax_d)
+        return info
+
+    @torch.no_grad()
+    def generate(self, prompts: torch.Tensor, n_new: int, phase_timing: bool = False, uniforms=None):
+        """prompts (B, T0) int64 on the device.  Returns (tokens (B, n_new)
+        int64 on the device, DecodeStats).  Prefill is timed separately from
+        the decode rounds.  uniforms: None, or a callable round_index ->
+        (u_draft, u_acc) giving each round's uniforms (see step())."""
+        B = self.B
+        st = DecodeStats(prefill_s=self.prefill(prompts, n_new))
         if self.use_graph and self.graph is None:
             self._capture()
         t1 = time.perf_counter()
-        Tmax_t = Tmax_d = T0 - 1
         while True:
             ta = time.perf_counter()
-            self._fill_uniforms()
-            if self.graph is not None:
-                self.graph.replay()
-            else:
-                self._round(Tmax_t, Tmax_d)
-            info = self.info.cpu()
+            info = self.step(None if uniforms is None else uniforms(st.rounds))
             st.rounds += 1
             st.per_round_tokens.append(int(info[3]) + B)
             if phase_timing:
                 st.draft_s += time.perf_counter() - ta
             if int(info[0]) >= n_new:
                 break
-            Tmax_t, Tmax_d = int(info[1]), int(info[2])
-            if Tmax_t + k + 2 > self.t.cap or Tmax_d + k + 2 > self.d.cap:
-                raise RuntimeError("KV cache capacity exhausted")
-        torch.cuda.synchronize(dev)
+        torch.cuda.synchronize(self.dev)
         st.decode_s = time.perf_counter() - t1
         st.emitted = B * n_new
         st.accepted_drafts = sum(st.per_round_tokens) - B * st.rounds

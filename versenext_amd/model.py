@@ -243,6 +243,12 @@ def rope_rows(heads: int, d: int, blk: int) -> torch.Tensor:
     return (torch.arange(heads).view(-1, 1) * d + blocks.view(1, -1)).reshape(-1)
 
 
+def _deq_int4(w: torch.Tensor, hip) -> torch.Tensor:
+    """fp32 q * s of w quantized to INT4 group 128 with fp16 scales (exact)."""
+    wq, sc = VQ.quantize_int4_g(w.float(), 128)
+    return hip.dequant_w4(wq, sc, w.shape[1], 128)
+
+
 def _pack(w: torch.Tensor, hip) -> torch.Tensor:
     """vnx_pack_bf16 of a contiguous (N, K) bf16 weight: the matrix-core
     operand order read by vnx_gemm_bf16 / vnx_expert_gemm_bf16."""
@@ -464,8 +470,11 @@ class CometSparkGPU:
             wq, wk, wv = W[p + "attn.wq.weight"], W[p + "attn.wk.weight"], W[p + "attn.wv.weight"]
             g = W[p + "attn.global_tokens.weight"]
             G = g.shape[0]
-            gk = (g @ wk.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
-            gv = (g @ wv.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
+            # the global sinks go through the same k / v weights as the tokens:
+            # with INT4 weights, their exact dequantization q * s
+            wk_g, wv_g = (wk, wv) if not (int4 and D % 128 == 0) else (_deq_int4(wk, hip), _deq_int4(wv, hip))
+            gk = (g @ wk_g.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
+            gv = (g @ wv_g.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
             L = _Layer(kind=kind, norm1=W[p + "norm1.weight"], norm2=W[p + "norm2.weight"],
                        wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4,
                                     rope_head_dim=d if dtype == torch.bfloat16 and int4 else 0),
