@@ -40,7 +40,9 @@ enum vnx_status {
   VNX_ERR_WORKSPACE = -2,     /* workspace missing or too small -> ValueError   */
   VNX_ERR_UNSUPPORTED = -3,   /* dtype / size outside the kernels' range        */
   VNX_ERR_HIP = -4,           /* a HIP runtime call failed      -> RuntimeError */
-  VNX_ERR_NO_DEVICE = -5      /* no gfx950 device / bad ordinal -> RuntimeError */
+  VNX_ERR_NO_DEVICE = -5,     /* no gfx950 device / bad ordinal -> RuntimeError */
+  VNX_ERR_TOO_LARGE = -6      /* input needs more than an allocation-free entry
+                                 point's fixed scratch          -> ValueError   */
 };
 
 enum vnx_dtype { VNX_F32 = 0, VNX_BF16 = 1, VNX_F16 = 2 };
@@ -141,6 +143,30 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
                     int32_t* accept_len, int64_t* out_ids, uint8_t* flags,
                     float* lse_t, float* lse_d,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free vnx_spec_accept.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory or pass a workspace (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as vnx_spec_accept
+ * without workspace / workspace_bytes: its scratch is a fixed static device
+ * array of vnx_spec_accept_noalloc_max_bytes() bytes (8 MiB) per GPU, held
+ * until the process ends.  Inputs for which vnx_spec_accept_workspace(B, k,
+ * V) exceeds that size (at V = 248,320 and k = 8: B above about 1,000)
+ * return VNX_ERR_TOO_LARGE before anything is launched.  Every call on one GPU
+ * shares that GPU's array (each call leaves it in a state the next call does
+ * not read): calls that overlap on one GPU (concurrent streams) race.  The
+ * first call with a new temperature adds one entry to the host-side
+ * temperature cache (host memory only).  vnx_init(device) resolves the
+ * array's address for that device; otherwise the first call does. */
+size_t vnx_spec_accept_noalloc_max_bytes(void);
+
+int vnx_spec_accept_noalloc(const void* target, const void* draft, int dtype,
+                            int64_t B, int k, int64_t V,
+                            int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
+                            const int64_t* draft_ids, const float* uniforms, float temperature,
+                            const float* thr_t, const float* thr_d,
+                            int32_t* accept_len, int64_t* out_ids, uint8_t* flags,
+                            float* lse_t, float* lse_d, void* stream);
 
 /* Sampling (the draft's proposals, and any caller of Sampler.sample):
  * out_ids[b] = the inverse-CDF draw with uniforms[b] from softmax(logits row

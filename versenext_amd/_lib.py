@@ -19,6 +19,7 @@ VNX_ERR_WORKSPACE = -2
 VNX_ERR_UNSUPPORTED = -3
 VNX_ERR_HIP = -4
 VNX_ERR_NO_DEVICE = -5
+VNX_ERR_TOO_LARGE = -6
 
 VNX_EPI_NONE, VNX_EPI_SWIGLU = 0, 1
 VNX_F32 = 0
@@ -59,6 +60,9 @@ SIGNATURES = {
     "vnx_spec_accept_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
     "vnx_spec_accept": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "vnx_spec_accept_noalloc_max_bytes": (_c_sz, []),
+    "vnx_spec_accept_noalloc": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                       _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vnx_gemv_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
     "vnx_gemv_w4": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
                            _vp, _c_i64, _vp, _c_sz, _vp]),
@@ -179,7 +183,7 @@ def check(status: int, what: str = "vnx call") -> None:
         return
     L = lib()
     text = L.vnx_status_string(status).decode()
-    if status in (VNX_ERR_INVALID_ARG, VNX_ERR_WORKSPACE, VNX_ERR_UNSUPPORTED):
+    if status in (VNX_ERR_INVALID_ARG, VNX_ERR_WORKSPACE, VNX_ERR_UNSUPPORTED, VNX_ERR_TOO_LARGE):
         raise ValueError(f"{what}: {text} (status {status})")
     if status == VNX_ERR_HIP:
         raise VnxError(f"{what}: {text}: {L.vnx_last_hip_error().decode()}")

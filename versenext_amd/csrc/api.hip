@@ -197,6 +197,7 @@ const char* vnx_status_string(int status) {
     case VNX_ERR_UNSUPPORTED: return "unsupported dtype or size";
     case VNX_ERR_HIP: return "HIP runtime error";
     case VNX_ERR_NO_DEVICE: return "no gfx950 device";
+    case VNX_ERR_TOO_LARGE: return "size exceeds the fixed scratch of an allocation-free entry point";
     default: return "unknown status";
   }
 }
@@ -214,7 +215,7 @@ int vnx_init(int device) {
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return VNX_ERR_NO_DEVICE;
   e = hipSetDevice(device);
   if (e != hipSuccess) return vnx::hip_fail(e);
-  return VNX_OK;
+  return vnx::spec_scratch_init(device);
 }
 
 }  // extern "C"

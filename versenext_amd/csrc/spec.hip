@@ -17,6 +17,7 @@
 // Probabilities that feed decisions use vnx_exp_canon(a - L32), a = RN(l/T),
 // L32 = RN32(row LSE), so the CPU checker reproduces them bit for bit.
 #include <algorithm>
+#include <mutex>
 
 #include "rowred.h"
 #include "vnx_internal.h"
@@ -626,6 +627,32 @@ __global__ __launch_bounds__(kCommitMaxB) void k_spec_commit(const int32_t* alen
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fixed scratch of vnx_spec_accept_noalloc (callers that cannot allocate):
+// one copy of `scratch` per GPU, held until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is a stand-in,
+// not a device address): spec_scratch_init() resolves each device's own
+// address once, with that device current, and kernels receive that pointer.
+// ---------------------------------------------------------------------------
+constexpr size_t kSpecScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kSpecScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+int spec_scratch_init(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return VNX_ERR_NO_DEVICE;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_ptr[device]) return VNX_OK;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return hip_fail(e);
+  if (!ptr) return VNX_ERR_HIP;
+  g_scratch_ptr[device] = ptr;
+  return VNX_OK;
+}
+
 }  // namespace vnx
 
 using namespace vnx;
@@ -708,6 +735,26 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype, int64_t B,
   if (k < 1) return VNX_ERR_INVALID_ARG;
   return spec_run(target, draft, dtype, B, k, V, ld_t, sb_t, ld_d, sb_d, draft_ids, uniforms, temperature,
                   thr_t, thr_d, accept_len, out_ids, flags, lse_t, lse_d, workspace, workspace_bytes, stream);
+}
+
+size_t vnx_spec_accept_noalloc_max_bytes(void) { return kSpecScratchBytes; }
+
+int vnx_spec_accept_noalloc(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
+                            int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
+                            const int64_t* draft_ids, const float* uniforms,
+                            float temperature, const float* thr_t, const float* thr_d, int32_t* accept_len,
+                            int64_t* out_ids, uint8_t* flags, float* lse_t, float* lse_d, void* stream) {
+  if (k < 1) return VNX_ERR_INVALID_ARG;
+  if (B < 0 || k > kMaxK || V <= 0) return VNX_ERR_INVALID_ARG;
+  if (B > 0 && spec_ws_bytes(B, k, V) > kSpecScratchBytes) return VNX_ERR_TOO_LARGE;
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  const int st = spec_scratch_init(dev);  // a no-op after the first call on this device
+  if (st) return st;
+  return spec_run(target, draft, dtype, B, k, V, ld_t, sb_t, ld_d, sb_d, draft_ids, uniforms, temperature,
+                  thr_t, thr_d, accept_len, out_ids, flags, lse_t, lse_d, g_scratch_ptr[dev], kSpecScratchBytes,
+                  stream);
 }
 
 size_t vnx_sample_workspace(int64_t B, int64_t V) {

@@ -14,6 +14,10 @@ namespace vnx {
 // Records the HIP error text for vnx_last_hip_error() and maps it to a status.
 int hip_fail(hipError_t e);
 
+// Resolves this device's copy of the fixed scratch of the allocation-free
+// entry point (spec.hip); the device must be current.  Idempotent.
+int spec_scratch_init(int device);
+
 #define VNX_HIP_CHECK(expr)                          \
   do {                                               \
     hipError_t _e = (expr);                          \
