@@ -8,11 +8,13 @@ are resident in HBM before the timed region.
 value = algorithmic bytes per step / mean step time, with
   bytes = 4*V*[B*(2k+1) + sum_b r_b], r_b = 2 if row b rejects (p_n and q_n
   re-read by the residual draw) else 1 (p_k re-read by the bonus draw).
-roofline = the dominant kernel, k_spec_lse (the one-pass row LSE over all
-  B*(2k+1) rows): algorithmic bytes 4*V*B*(2k+1) per launch / its mean launch
-  time, timed with HIP events the library records on the launch stream
-  (vnx_profile_begin / vnx_profile_end).  traffic = HBM bytes per launch from
-  the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary, when present.
+roofline = the acceptance path's kernel, k_spec_stage: one call is a
+  pipeline of P+2 launches of it (the row LSE streaming of part s beside the
+  accept + mass of part s-1 and the draw of part s-2); achieved = the call's
+  algorithmic bytes / the summed duration of its launches, timed with HIP
+  events the library records on the launch stream (vnx_profile_begin /
+  vnx_profile_end).  traffic = HBM bytes per call from the committed
+  rocprofv3 FETCH_SIZE / WRITE_SIZE summary, when present.
 The CPU baseline is the numpy/C checker (oracle/) on a bounded sample of the
 same workload, timed on the host's cores (threads over batch rows).
 """
@@ -32,8 +34,8 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 B, K, V, T = 64, 8, 248320, 0.8
-PHASES = ("k_spec_lse", "k_spec_accept", "k_spec_mass", "k_spec_draw")
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_spec_lse_config2_pmc.md")
+MAX_PHASES = 7  # kMaxPhases of the library's profiler
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_spec_stage_config2_pmc.md")
 
 
 def make_inputs_gpu(device):
@@ -53,17 +55,14 @@ def algorithmic_bytes(accept_len):
     return 4 * V * (B * (2 * K + 1) + r)
 
 
-LSE_BYTES = 4 * V * B * (2 * K + 1)
-
-
 def traffic_from_profile():
-    """HBM bytes per k_spec_lse launch from the committed PMC summary (the line
-    `traffic_bytes_per_launch: N`), or None."""
+    """HBM bytes per vnx_spec_accept call (all its k_spec_stage launches) from
+    the committed PMC summary (the line `traffic_bytes_per_call: N`), or None."""
     try:
         text = open(TRAFFIC_FILE).read()
     except OSError:
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    m = re.search(r"traffic_bytes_per_call:\s*([0-9]+)", text)
     return int(m.group(1)) if m else None
 
 
@@ -531,43 +530,56 @@ def bench_accept(args, emit=True):
     hip = get_backend("rocm:0")
     dev = hip.torch_device
     tgt, dft, ids, u = make_inputs_gpu(dev)
-    torch.cuda.synchronize()
+    L = _lib.lib()
+    # the C entry point on preallocated buffers, issued back to back on one
+    # stream, so the timed region holds the library's launches only
+    alen = torch.empty(B, dtype=torch.int32, device=dev)
+    out_ids = torch.empty((B, K + 1), dtype=torch.int64, device=dev)
+    flags = torch.empty((B, K + 1), dtype=torch.uint8, device=dev)
+    lse_t = torch.empty((B, K + 1), dtype=torch.float32, device=dev)
+    lse_d = torch.empty((B, K), dtype=torch.float32, device=dev)
+    ws = torch.zeros(L.vnx_spec_accept_workspace(B, K, V), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    P = ctypes.c_void_p
+    argv = (P(tgt.data_ptr()), P(dft.data_ptr()), _lib.VNX_F32, B, K, V, tgt.stride(1), tgt.stride(0),
+            dft.stride(1), dft.stride(0), P(ids.data_ptr()), P(u.data_ptr()), T, None, None,
+            P(alen.data_ptr()), P(out_ids.data_ptr()), P(flags.data_ptr()), P(lse_t.data_ptr()),
+            P(lse_d.data_ptr()), P(ws.data_ptr()), ws.numel(), P(stream.cuda_stream))
 
     def step():
-        return hip.spec_accept(tgt, dft, ids, u, temperature=T)
+        return L.vnx_spec_accept(*argv)
 
+    _lib.check(step(), "vnx_spec_accept")
     for _ in range(args.warmup):
-        res = step()
+        step()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for e0, e1 in evs:
-        e0.record(stream)
-        res = step()
-        e1.record(stream)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # Per-kernel times from a second pass of the same steps with the library's
-    # phase events (kept out of the timed pass above).
+    res = {"accept_len": alen}
+    # Per-launch times from a second pass of the same steps with the library's
+    # stage events (kept out of the timed pass above).
     L = _lib.lib()
     _lib.check(L.vnx_profile_begin(args.steps), "vnx_profile_begin")
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
-    phase = (ctypes.c_double * len(PHASES))()
+    phase = (ctypes.c_double * MAX_PHASES)()
     ncalls = ctypes.c_int(0)
-    _lib.check(L.vnx_profile_end(ctypes.cast(phase, ctypes.c_void_p), len(PHASES),
+    _lib.check(L.vnx_profile_end(ctypes.cast(phase, ctypes.c_void_p), MAX_PHASES,
                                  ctypes.cast(ctypes.pointer(ncalls), ctypes.c_void_p)), "vnx_profile_end")
-    phase_ms = {name: float(phase[i]) / max(1, ncalls.value) for i, name in enumerate(PHASES)}
-    ms = [e0.elapsed_time(e1) for e0, e1 in evs]
+    stage_ms = [float(phase[i]) / max(1, ncalls.value) for i in range(MAX_PHASES) if phase[i] > 0.0]
     alen = res["accept_len"].cpu().numpy()
     nbytes = algorithmic_bytes(alen)
-    mean_ms = float(np.mean(ms))
+    mean_ms = e0.elapsed_time(e1) / args.steps
     gbs = nbytes / (mean_ms * 1e-3) / 1e9
-    lse_gbs = LSE_BYTES / (phase_ms["k_spec_lse"] * 1e-3) / 1e9
+    call_kernel_ms = sum(stage_ms)
+    stage_gbs = nbytes / (call_kernel_ms * 1e-3) / 1e9
     emitted = int(alen.sum()) + B
 
     if args.calib_copy:
@@ -596,16 +608,15 @@ def bench_accept(args, emit=True):
                    "batch": B, "k": K, "vocab": V, "temperature": T, "top_k": None,
                    "logits": "fp32 target N(0,2), draft = target + N(0,0.5)",
                    "bytes_per_step": nbytes, "event_ms_mean": round(mean_ms, 4),
-                   "event_ms_min": round(float(np.min(ms)), 4),
-                   "event_ms_median": round(float(np.median(ms)), 4),
+                   "timing": "HIP events around the back-to-back calls of the C entry point",
                    "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(lse_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lse_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-                     "kernel": "k_spec_lse", "bytes_per_launch": LSE_BYTES,
-                     "launch_ms_mean": round(phase_ms["k_spec_lse"], 4),
-                     "timing": "HIP events recorded by the library around each launch on its stream "
-                               "(includes the gap before the next launch)",
-                     "phase_ms_mean": {k: round(v, 4) for k, v in phase_ms.items()},
+        "roofline": {"bound": "hbm", "achieved": round(stage_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(stage_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "kernel": "k_spec_stage", "launches_per_call": len(stage_ms),
+                     "bytes_per_call": nbytes, "kernel_ms_per_call": round(call_kernel_ms, 4),
+                     "timing": "HIP events recorded by the library before each launch and after the last, "
+                               "on its stream (each interval includes the gap before the next launch)",
+                     "stage_ms_mean": [round(v, 4) for v in stage_ms],
                      "profiled_calls": ncalls.value},
         "emitted_tokens_per_s": round(emitted / (mean_ms * 1e-3), 1),
         "mean_accept_len": round(float(alen.mean()), 3),

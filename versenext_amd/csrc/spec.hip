@@ -1,19 +1,29 @@
 // Stochastic speculative acceptance (Leviathan et al. 2023, Alg. 1) on the
-// (B, k+1, V) target and (B, k, V) draft logits.  Four launches, no counters:
-//   lse     grid B*(2k+1)*C: every workgroup streams one chunk of one target
-//           or draft row and writes the chunk's (max, sum 2^..) partial.  Many
-//           short workgroups let the dispatcher balance the CUs.
-//   accept  grid B: merges b's row LSEs (fp64), rounds them to fp32, runs the
-//           k acceptance tests in one wavefront (lane i tests position i; a
-//           ballot gives the first rejection n) and writes accept_len, the
-//           accepted ids, the LSEs and the draw job.
-//   mass    grid B*C2: streams p_n and q_n (or p_k for the bonus draw) with
-//           coalesced vector loads; every wave stores the draw mass
-//           sum max(0, p-q) (or sum p) of each sub-block of 64 vectors it
-//           covers (fp64).
-//   draw    grid B: sums the sub-block masses in a fixed order, walks them to
-//           the sub-block holding u_k * mass, and recomputes only that
-//           sub-block (one wave, one inclusive scan) to find the token.
+// (B, k+1, V) target and (B, k, V) draft logits, in two launches with no
+// cross-workgroup waits:
+//   A  grid B*(2k+1)*C: every workgroup streams one chunk of one target or
+//      draft row and writes the chunk's (max, sum 2^..) partial.  Many short
+//      workgroups let the dispatcher balance the CUs.  (The first ones also
+//      clear B's arrival counters.)
+//   B  grid B*C2: every workgroup of batch row b first merges b's partials
+//      into its 2k+1 row LSEs (fp64, staged through LDS, fixed lane order,
+//      so all of them get the same bits), rounds them to fp32 and runs the k
+//      acceptance tests in one wavefront (lane i tests position i; a ballot
+//      gives the first rejection n); the chunk-0 workgroup writes
+//      accept_len, the accepted ids, the LSEs and flags.  Then it streams its
+//      chunk of p_n and q_n (or p_k for the bonus draw) and publishes the
+//      draw mass sum max(0, p-q) (or sum p) of each sub-block of 64 vectors
+//      (fp64).  The workgroup completing row b (an arrival counter) sums the
+//      sub-block masses in a fixed order, walks them to the sub-block holding
+//      u_k * mass and recomputes only that sub-block (one wave, one inclusive
+//      scan) to find the token.  Published masses move through agent-scope
+//      atomic stores and loads (rowred.h arrive_last); everything else
+//      crosses the kernel boundary.
+// (Measured and dropped: the acceptance inside launch A by arrival counting
+// -- the counter round trip of 17K short workgroups slowed the streaming by
+// half; and a pipeline of row parts whose accept / mass / draw run beside
+// the next part's streaming -- launch B is latency-bound, so a tail part
+// costs nearly as much as the whole.)
 // Probabilities that feed decisions use vnx_exp_canon(a - L32), a = RN(l/T),
 // L32 = RN32(row LSE), so the CPU checker reproduces them bit for bit.
 #include <algorithm>
@@ -31,7 +41,7 @@ constexpr int kNB2 = 4;    // sub-blocks per wave in flight, mass pass
 constexpr int kMaxK = 64;
 constexpr int kMaxChunks = 256;
 constexpr int kDrawLds = 4096;  // draw: sub-block masses held in LDS (V <= 4096*64*VE)
-constexpr int kAccLds = 4096;   // accept: (2k+1)*chunks partials held in LDS
+constexpr int kAccParts = 2048; // accept: (2k+1)*chunks partials staged in LDS
 
 struct Job {
   int n;      // first rejected position (k if all accepted)
@@ -39,7 +49,7 @@ struct Job {
   float Lp;   // fp32 LSE of the target row drawn from
   float Lq;   // fp32 LSE of draft row n (mode 0)
   float u;    // uniform of the draw
-  int pad;
+  int fln;    // the acceptance flags of position n (the draw adds its own)
 };
 
 struct SpecParams {
@@ -51,8 +61,8 @@ struct SpecParams {
   int chunks;        // lse pass: chunks per row
   int64_t chunk_len; // lse pass: elements per chunk (multiple of the vector width)
   int64_t nsb;       // sub-blocks (64 vectors) per row
-  int spc;           // mass pass: sub-blocks per chunk
-  int chunks2;       // mass pass: chunks per row
+  int spc;           // launch B: sub-blocks per chunk
+  int chunks2;       // launch B: chunks per row
   TScale sc;
   const float* thr_t;
   const float* thr_d;
@@ -65,8 +75,9 @@ struct SpecParams {
   float* lse_d;
   float* part_m;   // [B*(2k+1)][chunks]
   double* part_s;  // [B*(2k+1)][chunks]
-  Job* jobs;       // [B]
   double* sbm;     // [B][nsb] sub-block draw masses
+  unsigned* cnt;   // [B] arrival counters of launch B
+  float* gath;     // [B][2k] scaled target / draft logits at the draft ids
 };
 
 // Distance test of an fp64 LSE to the rounding midpoints around its fp32 value.
@@ -98,18 +109,25 @@ __device__ __forceinline__ float row_thr(const SpecParams& p, int64_t b, int ri)
 }
 
 // ---------------------------------------------------------------------------
-// lse: one chunk of one row per workgroup.
+// lse: chunk c of row r (r = b*(2k+1) + ri) per workgroup.
 // ---------------------------------------------------------------------------
 template <typename Tin, int SM, bool THR>
-__global__ __launch_bounds__(kNT) void k_spec_lse(SpecParams p) {
-  __shared__ ReduceLds lds;
-  const int R = 2 * p.k + 1;
-  const int c = blockIdx.x % p.chunks;
-  const int64_t r = blockIdx.x / p.chunks;
+__device__ __forceinline__ void lse_work(const SpecParams& p, int64_t r, int c, ReduceLds& lds) {
+  const int k = p.k;
+  const int R = 2 * k + 1;
   const int64_t b = r / R;
   const int ri = (int)(r - b * R);
   const int64_t c0 = (int64_t)c * p.chunk_len;
   const int64_t c1 = c0 + p.chunk_len < p.V ? c0 + p.chunk_len : p.V;
+  // The chunk holding this row's draft id (target row i < k: x_i; draft row
+  // i: x_i) records the scaled logit there for the acceptance test.
+  if (ri != k) {
+    const int pos = ri < k ? ri : ri - k - 1;
+    const int64_t x = p.ids[b * k + pos];
+    if (x >= c0 && x < c1 && threadIdx.x == 0)
+      p.gath[b * 2 * k + (ri < k ? pos : k + pos)] =
+          scaled_at<Tin, SM, THR>(row_ptr<Tin>(p, b, ri), x, p.sc, row_thr<THR>(p, b, ri));
+  }
   const ChunkResult cr = reduce_chunk<Tin, SM, THR, true, false, kNT, kNB>(row_ptr<Tin>(p, b, ri), c0, c1,
                                                                            p.sc, row_thr<THR>(p, b, ri), lds);
   if (threadIdx.x == 0) {
@@ -119,116 +137,138 @@ __global__ __launch_bounds__(kNT) void k_spec_lse(SpecParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// accept: row LSEs of b from the partials, the k acceptance tests,
-// accept_len / out_ids / flags / LSEs and the draw job.
+// accept: the row LSEs of b from its chunk partials and the k acceptance
+// tests.  Every workgroup of b's mass chunks runs it and gets the same job
+// (fixed lane order, no atomics); with `write`, the workgroup also stores
+// accept_len, out_ids (accepted prefix, -1 after), flags and the LSEs.
+// pm_l / ps_l: LDS room for the row's (2k+1)*chunks partials.
 // ---------------------------------------------------------------------------
+struct AcceptLds {
+  float Ls[2 * kMaxK + 1];
+  int Ledge[2 * kMaxK + 1];
+  Job job;
+};
+
 template <typename Tin, int SM, bool THR>
-__global__ __launch_bounds__(kNT) void k_spec_accept(SpecParams p) {
-  __shared__ float pm_l[kAccLds];
-  __shared__ double ps_l[kAccLds];
-  __shared__ float rowM[2 * kMaxK + 1];
-  __shared__ float Ls[2 * kMaxK + 1];
-  __shared__ int Ledge[2 * kMaxK + 1];
-  const int64_t b = blockIdx.x;
+__device__ __forceinline__ Job accept_row(const SpecParams& p, int64_t b, bool write, AcceptLds& L, float* pm_l,
+                                          double* ps_l) {
   const int k = p.k;
   const int R = 2 * k + 1;
   const int tid = threadIdx.x;
+  const int lane = tid % VNX_WAVE, wave = tid / VNX_WAVE;
   // Lane i < k of wave 0 first issues the loads that do not depend on the
-  // LSEs (draft id, its uniform, the two logits at the id), so they overlap
-  // the partial loads below.
+  // LSEs (draft id, its uniform, the two scaled logits at the id that
+  // launch A recorded), so they overlap the partial loads below.
   int64_t x = -1;
   float u = 0.0f, a = 0.0f, bq = 0.0f;
-  bool valid = false;
   if (tid < k) {
     x = p.ids[b * k + tid];
     u = p.u[b * (k + 1) + tid];
-    valid = x >= 0 && x < p.V;
-    if (valid) {
-      a = scaled_at<Tin, SM, THR>(row_ptr<Tin>(p, b, tid), x, p.sc, row_thr<THR>(p, b, tid));
-      bq = scaled_at<Tin, SM, THR>(row_ptr<Tin>(p, b, k + 1 + tid), x, p.sc, row_thr<THR>(p, b, k + 1 + tid));
-    }
+    a = p.gath[b * 2 * k + tid];
+    bq = p.gath[b * 2 * k + k + tid];
   }
-  // The R*chunks partials of b are contiguous (row-major).  Row maxima first
-  // (one thread per row over the partial maxima in LDS), then every thread
-  // rescales its own partials to its row's maximum (one exp2 each, in
-  // parallel), then one thread per row adds its row's terms in chunk order.
-  const int total = R * p.chunks;  // <= kAccLds (host check)
-  const int64_t base = b * (int64_t)total;
+  const bool valid = x >= 0 && x < p.V;
+  // The row's partials into LDS with every load in flight at once; then
+  // segment g of 16 lanes merges rows g, g + 16, ... (every segment of the
+  // workgroup at once): the row maximum over the partial maxima, every
+  // lane's partials rescaled to it and summed in lane order, then a
+  // butterfly sum across the segment.
+  const int C = p.chunks;
+  const int total = R * C;  // <= kAccParts (host check)
+  const int64_t pbase = b * (int64_t)total;
   for (int i = tid; i < total; i += kNT) {
-    pm_l[i] = p.part_m[base + i];
-    ps_l[i] = p.part_s[base + i];
+    pm_l[i] = p.part_m[pbase + i];
+    ps_l[i] = p.part_s[pbase + i];
   }
   __syncthreads();
-  if (tid < R) {
+  constexpr int SEG = 16;
+  const int sl = tid % SEG;
+  for (int r = tid / SEG; r < R; r += kNT / SEG) {
+    const int base = r * C;
     float M = kNegInf;
-    for (int c = 0; c < p.chunks; ++c) M = fmaxf(M, pm_l[tid * p.chunks + c]);
-    rowM[tid] = M;
-  }
-  __syncthreads();
-  for (int i = tid; i < total; i += kNT) {
-    const float M = rowM[i / p.chunks], m = pm_l[i];
-    ps_l[i] = (m == kNegInf || M == kPosInf) ? 0.0 : (m == M ? ps_l[i] : rescale(ps_l[i], mt_of(m), mt_of(M)));
-  }
-  __syncthreads();
-  float M = kNegInf;
-  double S = 0.0;
-  if (tid < R) {
-    M = rowM[tid];
-    for (int c = 0; c < p.chunks; ++c) S += ps_l[tid * p.chunks + c];
-  }
-  if (tid < R) {
-    const double Lr = lse_of(M, S);
-    const float L32 = (float)Lr;
-    Ls[tid] = L32;
-    Ledge[tid] = near_f32_edge(Lr, L32, 1e-7) ? 1 : 0;
-    if (tid <= k) {
-      if (p.lse_t) p.lse_t[b * (k + 1) + tid] = L32;
-    } else if (p.lse_d) {
-      p.lse_d[b * k + (tid - k - 1)] = L32;
-    }
-  }
-  __syncthreads();
-  if (tid >= VNX_WAVE) return;
-  const int lane = tid;
-  bool acc = true;
-  uint8_t fl = 0;
-  if (lane < k) {
-    if (valid) {
-      const float pp = vnx_exp_canon(a - Ls[lane]);
-      const float qq = vnx_exp_canon(bq - Ls[k + 1 + lane]);
-      acc = (u < 1.0f) && ((double)u * (double)qq < (double)pp);
-      if (qq > 0.0f) {
-        double ratio = (double)pp / (double)qq;
-        if (ratio > 1.0) ratio = 1.0;
-        if (fabs((double)u - ratio) < 1e-6) fl |= VNX_FLAG_NEAR_TIE;
+    for (int c = sl; c < C; c += SEG) M = fmaxf(M, pm_l[base + c]);
+#pragma unroll
+    for (int o = SEG / 2; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, SEG));
+    double S = 0.0;
+    if (M < kPosInf) {
+      for (int c = sl; c < C; c += SEG) {
+        const float m = pm_l[base + c];
+        if (m > kNegInf) {
+          const double sv = ps_l[base + c];
+          S += (m == M) ? sv : rescale(sv, mt_of(m), mt_of(M));
+        }
       }
-    } else {
-      acc = false;
-      fl |= VNX_FLAG_BAD_ID;
     }
-    if (Ledge[lane] || Ledge[k + 1 + lane]) fl |= VNX_FLAG_LSE_EDGE;
+#pragma unroll
+    for (int o = SEG / 2; o > 0; o >>= 1) S += __shfl_xor(S, o, SEG);
+    if (sl == 0) {
+      const double Lr = lse_of(M, S);
+      const float L32 = (float)Lr;
+      L.Ls[r] = L32;
+      L.Ledge[r] = near_f32_edge(Lr, L32, 1e-7) ? 1 : 0;
+      if (write) {
+        if (r <= k) {
+          if (p.lse_t) p.lse_t[b * (k + 1) + r] = L32;
+        } else if (p.lse_d) {
+          p.lse_d[b * k + (r - k - 1)] = L32;
+        }
+      }
+    }
   }
-  const uint64_t rej = ~__ballot(acc);
-  int n = rej ? __builtin_ctzll(rej) : VNX_WAVE;
-  if (n > k) n = k;
-  int64_t* out = p.out_ids + b * (k + 1);
-  if (lane < k) {
-    out[lane] = lane < n ? x : -1;
-    if (p.flags) p.flags[b * (k + 1) + lane] = fl;
+  __syncthreads();
+  if (wave == 0) {
+    bool acc = true;
+    uint8_t fl = 0;
+    if (lane < k) {
+      if (valid) {
+        const float pp = vnx_exp_canon(a - L.Ls[lane]);
+        const float qq = vnx_exp_canon(bq - L.Ls[k + 1 + lane]);
+        acc = (u < 1.0f) && ((double)u * (double)qq < (double)pp);
+        if (qq > 0.0f) {
+          double ratio = (double)pp / (double)qq;
+          if (ratio > 1.0) ratio = 1.0;
+          if (fabs((double)u - ratio) < 1e-6) fl |= VNX_FLAG_NEAR_TIE;
+        }
+      } else {
+        acc = false;
+        fl |= VNX_FLAG_BAD_ID;
+      }
+      if (L.Ledge[lane] || L.Ledge[k + 1 + lane]) fl |= VNX_FLAG_LSE_EDGE;
+    }
+    const uint64_t rej = ~__ballot(acc);
+    int n = rej ? __builtin_ctzll(rej) : VNX_WAVE;
+    if (n > k) n = k;
+    const int fl_k = L.Ledge[k] ? VNX_FLAG_LSE_EDGE : 0;
+    const int fln = n < k ? __shfl((int)fl, n, VNX_WAVE) : fl_k;
+    // Position n (the drawn token and its flags) is written by the workgroup
+    // that draws, and only by it.
+    if (write) {
+      int64_t* out = p.out_ids + b * (k + 1);
+      if (lane < k && lane != n) {
+        out[lane] = lane < n ? x : -1;
+        if (p.flags) p.flags[b * (k + 1) + lane] = fl;
+      }
+      if (lane == 0) {
+        if (n < k) {
+          out[k] = -1;
+          if (p.flags) p.flags[b * (k + 1) + k] = (uint8_t)fl_k;
+        }
+        p.accept_len[b] = n;
+      }
+    }
+    if (lane == 0) {
+      Job jb;
+      jb.n = n;
+      jb.mode = n < k ? 0 : 1;
+      jb.Lp = L.Ls[n];
+      jb.Lq = n < k ? L.Ls[k + 1 + n] : 0.0f;
+      jb.u = p.u[b * (k + 1) + k];
+      jb.fln = fln;
+      L.job = jb;
+    }
   }
-  if (lane == 0) {
-    out[k] = -1;
-    if (p.flags) p.flags[b * (k + 1) + k] = Ledge[k] ? VNX_FLAG_LSE_EDGE : 0;
-    p.accept_len[b] = n;
-    Job jb;
-    jb.n = n;
-    jb.mode = n < k ? 0 : 1;
-    jb.Lp = Ls[n];
-    jb.Lq = n < k ? Ls[k + 1 + n] : 0.0f;
-    jb.u = p.u[b * (k + 1) + k];
-    jb.pad = 0;
-    p.jobs[b] = jb;
-  }
+  __syncthreads();
+  return L.job;
 }
 
 // ---------------------------------------------------------------------------
@@ -305,12 +345,12 @@ __device__ __forceinline__ double lane_weights(const Tin* P, const Tin* Q, int64
 // sub-blocks c*spc + w + kNW*j, so the workgroup's loads are contiguous.
 // ---------------------------------------------------------------------------
 template <typename Tin, int SM, bool THR, int WSEL>
-__device__ __forceinline__ void mass_chunk(const SpecParams& p, int64_t b, int c, const Tin* P, const Tin* Q,
-                                           const DrawRows& d, const Job& jb) {
+__device__ __forceinline__ void mass_chunk(const SpecParams& p, int64_t b, int c, int spc, const Tin* P,
+                                           const Tin* Q, const DrawRows& d, const Job& jb) {
   constexpr int VE = Vec<Tin>::N;
   const int wave = threadIdx.x / VNX_WAVE;
-  const int64_t s0 = (int64_t)c * p.spc;
-  const int64_t s1 = min(s0 + p.spc, p.nsb);
+  const int64_t s0 = (int64_t)c * spc;
+  const int64_t s1 = min(s0 + spc, p.nsb);
   for (int64_t sb = s0 + wave; sb < s1; sb += (int64_t)kNW * kNB2) {
     float xp[kNB2][VE], xq[kNB2][VE];
 #pragma unroll
@@ -331,45 +371,35 @@ __device__ __forceinline__ void mass_chunk(const SpecParams& p, int64_t b, int c
           m += (double)draw_weight<SM, THR>(xp[j][i], WSEL == W_RESID ? xq[j][i] : 0.0f, WSEL, p.sc, d.thr_p,
                                             d.thr_q, jb.Lp, jb.Lq);
         m = wave_sum(m);
-        if (threadIdx.x % VNX_WAVE == 0) p.sbm[b * p.nsb + sbi] = m;
+        if (threadIdx.x % VNX_WAVE == 0) st_agent(&p.sbm[b * p.nsb + sbi], m);
       }
     }
   }
-}
-
-template <typename Tin, int SM, bool THR>
-__global__ __launch_bounds__(kNT) void k_spec_mass(SpecParams p) {
-  const int c = blockIdx.x % p.chunks2;
-  const int64_t b = blockIdx.x / p.chunks2;
-  const Job jb = p.jobs[b];
-  const DrawRows d = draw_rows<THR>(p, b, jb);
-  const Tin* P = static_cast<const Tin*>(p.tgt) + d.poff;
-  const Tin* Q = static_cast<const Tin*>(p.dft) + d.qoff;
-  if (jb.mode == 0)
-    mass_chunk<Tin, SM, THR, W_RESID>(p, b, c, P, Q, d, jb);
-  else
-    mass_chunk<Tin, SM, THR, W_P>(p, b, c, P, Q, d, jb);
+  // every wave's published masses complete before the workgroup arrives
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // ---------------------------------------------------------------------------
 // draw: thread t owns sub-blocks [t*q, (t+1)*q) (q = ceil(nsb/kNT)); the
 // total is sum_t (sum_i sbm[t*q+i]) in that nested sequential order, and the
 // walk to the target follows the same order: thread, then sub-block, then
-// (one wave, lane-order inclusive scan) lane, then element.
+// (one wave, lane-order inclusive scan) lane, then element.  sh_m holds the
+// row's nsb sub-block masses (dynamic LDS), published by the other
+// workgroups of launch B (coherent loads).
 // ---------------------------------------------------------------------------
+struct DrawLds {
+  double T[kNT], E[kNT];
+  double scan[kNW];
+  double total, target, base;
+  int64_t sb;
+  int tstar, tlast;
+};
+
 template <typename Tin, int SM, bool THR>
-__global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
+__device__ __forceinline__ void draw_work(const SpecParams& p, int64_t b, const Job& jb, DrawLds& L, double* sh_m) {
   constexpr int VE = Vec<Tin>::N;
-  __shared__ double sh_m[kDrawLds];
-  __shared__ double sh_T[kNT], sh_E[kNT];
-  __shared__ double sh_scan[kNW];
-  __shared__ double sh_total, sh_target, sh_base;
-  __shared__ int64_t sh_sb;
-  __shared__ int sh_tstar, sh_tlast;
-  const int64_t b = blockIdx.x;
   const int k = p.k;
   const int tid = threadIdx.x;
-  const Job jb = p.jobs[b];
   const DrawRows d = draw_rows<THR>(p, b, jb);
   const Tin* P = static_cast<const Tin*>(p.tgt) + d.poff;
   const Tin* Q = static_cast<const Tin*>(p.dft) + d.qoff;
@@ -387,16 +417,16 @@ __global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
     __syncthreads();
     double t = 0.0;
     for (int64_t i = (int64_t)tid * q; i < min((int64_t)(tid + 1) * q, p.nsb); ++i) t += sh_m[i];
-    const double incl = block_inclusive_scan<kNT>(t, sh_scan);
-    sh_T[tid] = t;
-    sh_E[tid] = incl;
+    const double incl = block_inclusive_scan<kNT>(t, L.scan);
+    L.T[tid] = t;
+    L.E[tid] = incl;
     __syncthreads();
-    if (tid == kNT - 1) sh_total = incl;
+    if (tid == kNT - 1) L.total = incl;
     __syncthreads();
   };
-  for (int64_t i = tid; i < p.nsb; i += kNT) sh_m[i] = sbm[i];
+  for (int64_t i = tid; i < p.nsb; i += kNT) sh_m[i] = ld_agent(&sbm[i]);
   scan_totals();
-  if (!(sh_total > 0.0) && wsel == W_RESID) {
+  if (!(L.total > 0.0) && wsel == W_RESID) {
     // max(0, p_n - q_n) has no mass (p_n == q_n after rounding): draw from
     // p_n.  This workgroup recomputes the sub-block masses of p_n (rare path).
     fl |= VNX_FLAG_ZERO_RESIDUAL;
@@ -411,27 +441,27 @@ __global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
   // The thread whose range holds target = u * total (ranges of zero mass are
   // empty); if rounding leaves none, the last thread with positive mass.
   if (tid == 0) {
-    sh_tstar = kNT;  // atomicMin sentinel: no thread
-    sh_tlast = -1;
+    L.tstar = kNT;  // atomicMin sentinel: no thread
+    L.tlast = -1;
   }
   __syncthreads();
-  const double total = sh_total;
+  const double total = L.total;
   const double target = (double)jb.u * total;
   {
-    const double T = sh_T[tid], end = sh_E[tid];
-    const double start = tid ? sh_E[tid - 1] : 0.0;
-    if (T > 0.0 && start <= target && target < end) atomicMin(&sh_tstar, tid);
-    if (T > 0.0) atomicMax(&sh_tlast, tid);
+    const double T = L.T[tid], end = L.E[tid];
+    const double start = tid ? L.E[tid - 1] : 0.0;
+    if (T > 0.0 && start <= target && target < end) atomicMin(&L.tstar, tid);
+    if (T > 0.0) atomicMax(&L.tlast, tid);
   }
   __syncthreads();
   if (tid == 0) {
-    int tstar = sh_tstar;
-    if (tstar == kNT) tstar = sh_tlast;
+    int tstar = L.tstar;
+    if (tstar == kNT) tstar = L.tlast;
     int64_t sstar = -1;
     double base = 0.0;
     if (tstar >= 0) {
       // Sub-blocks of that thread, in order, from the thread's start.
-      const double b0 = tstar ? sh_E[tstar - 1] : 0.0;
+      const double b0 = tstar ? L.E[tstar - 1] : 0.0;
       double r2 = b0, b_last = b0;
       int64_t slast = -1;
       for (int64_t i = (int64_t)tstar * q; i < min((int64_t)(tstar + 1) * q, p.nsb); ++i) {
@@ -445,12 +475,12 @@ __global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
       }
       if (sstar < 0) { sstar = slast; base = b_last; }
     }
-    sh_sb = sstar;
-    sh_target = target;
-    sh_base = base;
+    L.sb = sstar;
+    L.target = target;
+    L.base = base;
   }
   __syncthreads();
-  const int64_t sstar = sh_sb;
+  const int64_t sstar = L.sb;
   if (tid >= VNX_WAVE) return;
   // Wave 0: the sub-block's weights, lane-order inclusive scan, element walk.
   int64_t token = 0;
@@ -460,12 +490,12 @@ __global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
     float w[VE];
     const double lm = lane_weights<Tin, SM, THR>(P, Q, sstar, p.V, wsel, p.sc, d, jb, w);
     const double incl = wave_inclusive_scan(lm);
-    const double start = sh_base + (incl - lm);
-    const double end = sh_base + incl;
-    const double target = sh_target;
+    const double start = L.base + (incl - lm);
+    const double end = L.base + incl;
+    const double tgt = L.target;
     // The lane whose [start, end) holds the target; if rounding leaves the
     // target past every lane, the last lane with positive mass.
-    const bool hit = lm > 0.0 && start <= target && target < end;
+    const bool hit = lm > 0.0 && start <= tgt && tgt < end;
     const uint64_t hits = __ballot(hit);
     const uint64_t pos = __ballot(lm > 0.0);
     const int lane = tid;
@@ -489,15 +519,15 @@ __global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
           lastpos = i;
           if (pick < 0) {
             const double nr = run + (double)w[i];
-            if (nr > target) { pick = i; before = run; after = nr; }
+            if (nr > tgt) { pick = i; before = run; after = nr; }
             run = nr;
           }
         }
       }
       if (pick < 0) { pick = lastpos; edge = true; }
       token = (sstar * VNX_WAVE + lane) * VE + pick;
-      const double tol = 1e-12 * sh_total;
-      if (target - before < tol || after - target < tol) edge = true;
+      const double tol = 1e-12 * L.total;
+      if (tgt - before < tol || after - tgt < tol) edge = true;
     }
     if (lstar >= 0) {
       token = __shfl(token, lstar, VNX_WAVE);
@@ -507,8 +537,51 @@ __global__ __launch_bounds__(kNT) void k_spec_draw(SpecParams p) {
   }
   if (tid == 0) {
     p.out_ids[b * (k + 1) + jb.n] = token;
-    if (p.flags) p.flags[b * (k + 1) + jb.n] |= fl;
+    if (p.flags) p.flags[b * (k + 1) + jb.n] = (uint8_t)(jb.fln | fl);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Launch A: chunk partials of every row; the first workgroups also clear the
+// arrival counters of launch B.
+// ---------------------------------------------------------------------------
+template <typename Tin, int SM, bool THR>
+__global__ __launch_bounds__(kNT) void k_spec_lse(SpecParams p) {
+  __shared__ ReduceLds lds;
+  const int64_t zc = (int64_t)blockIdx.x * kNT + threadIdx.x;
+  if (zc < p.B) p.cnt[zc] = 0u;
+  const int64_t w = blockIdx.x;
+  if (w < p.B * (2 * p.k + 1) * p.chunks) lse_work<Tin, SM, THR>(p, w / p.chunks, (int)(w % p.chunks), lds);
+}
+
+// ---------------------------------------------------------------------------
+// Launch B: accept of the row, draw masses of one chunk; the workgroup
+// completing batch row b draws its token.  Dynamic LDS: the row's partials
+// during the accept, then its sub-block masses if it draws.
+// ---------------------------------------------------------------------------
+union MassDrawLds {
+  AcceptLds acc;
+  DrawLds draw;
+};
+
+template <typename Tin, int SM, bool THR>
+__global__ __launch_bounds__(kNT) void k_spec_mass_draw(SpecParams p) {
+  __shared__ MassDrawLds lds;
+  __shared__ int last_flag;
+  extern __shared__ double dyn[];
+  const int c = blockIdx.x % p.chunks2;
+  const int64_t b = blockIdx.x / p.chunks2;
+  const int total = (2 * p.k + 1) * p.chunks;
+  const Job jb = accept_row<Tin, SM, THR>(p, b, c == 0, lds.acc, reinterpret_cast<float*>(dyn + total), dyn);
+  const DrawRows d = draw_rows<THR>(p, b, jb);
+  const Tin* P = static_cast<const Tin*>(p.tgt) + d.poff;
+  const Tin* Q = static_cast<const Tin*>(p.dft) + d.qoff;
+  if (jb.mode == 0)
+    mass_chunk<Tin, SM, THR, W_RESID>(p, b, c, p.spc, P, Q, d, jb);
+  else
+    mass_chunk<Tin, SM, THR, W_P>(p, b, c, p.spc, P, Q, d, jb);
+  if (!arrive_last(&p.cnt[b], (unsigned)p.chunks2, &last_flag)) return;
+  draw_work<Tin, SM, THR>(p, b, jb, lds.draw, dyn);
 }
 
 struct SpecPlan {
@@ -518,9 +591,9 @@ struct SpecPlan {
   int spc, chunks2;
 };
 
-// lse: chunks per row for about kLseWgs workgroups (many short workgroups;
-// the dispatcher balances them over the CUs).  mass: chunks of whole
-// sub-blocks, about kMassPerCu workgroups per CU (one resident round).
+// A: chunks per row for about kLseWgs workgroups (many short workgroups; the
+// dispatcher balances them over the CUs).  B: chunks of whole sub-blocks,
+// about kMassPerCu workgroups per CU.
 constexpr int64_t kLseWgs = 16384;
 constexpr int64_t kMassPerCu = 4;
 
@@ -530,13 +603,13 @@ static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype) {
   const int64_t rows = B * (2 * k + 1);
   // chunks of at least kNB / 2 vectors per thread: few rows (a decode batch)
   // get fewer, longer workgroups instead of thousands of one-load ones
-  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccLds / (2 * k + 1)), kLseWgs);
+  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccParts / (2 * k + 1)), kLseWgs);
   const int64_t len = ((V + c - 1) / c + ve - 1) / ve * ve;
   pl.len = len;
   pl.chunks = (int)((V + len - 1) / len);
   const int64_t sbl = (int64_t)VNX_WAVE * ve;
   pl.nsb = (V + sbl - 1) / sbl;
-  int64_t c2 = ((int64_t)device_cus() * kMassPerCu * wg_scale_pct() / 100 + B - 1) / B;
+  int64_t c2 = ((int64_t)device_cus() * kMassPerCu + B - 1) / B;
   const int64_t max_c2 = (pl.nsb + kNW - 1) / kNW;  // at least one sub-block per wave
   if (c2 > max_c2) c2 = max_c2;
   if (c2 < 1) c2 = 1;
@@ -550,10 +623,11 @@ static size_t spec_carve(void* ws, int64_t B, int k, const SpecPlan& pl, SpecPar
   const size_t n1 = (size_t)B * (2 * k + 1) * pl.chunks;
   float* pm = cv.take<float>(n1);
   double* ps = cv.take<double>(n1);
-  Job* jobs = cv.take<Job>(B);
   double* sbm = cv.take<double>((size_t)B * pl.nsb);
+  unsigned* cnt = cv.take<unsigned>((size_t)B);
+  float* gath = cv.take<float>((size_t)B * 2 * k);
   if (p) {
-    p->part_m = pm; p->part_s = ps; p->jobs = jobs; p->sbm = sbm;
+    p->part_m = pm; p->part_s = ps; p->sbm = sbm; p->cnt = cnt; p->gath = gath;
   }
   return cv.bytes();
 }
@@ -687,7 +761,7 @@ static int spec_run(const void* target, const void* draft, int dtype, int64_t B,
   if (!uniforms || !accept_len || !out_ids) return VNX_ERR_INVALID_ARG;
   const SpecPlan pl = spec_plan(B, k, V, dtype);
   if (B * (2 * k + 1) * (int64_t)pl.chunks >= INT32_MAX || B * (int64_t)pl.chunks2 >= INT32_MAX ||
-      pl.nsb > kDrawLds || (2 * k + 1) * pl.chunks > kAccLds)
+      pl.nsb > kDrawLds || (2 * k + 1) * pl.chunks > kAccParts)
     return VNX_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < spec_carve(nullptr, B, k, pl, nullptr)) return VNX_ERR_WORKSPACE;
   SpecParams p{};
@@ -699,8 +773,10 @@ static int spec_run(const void* target, const void* draft, int dtype, int64_t B,
   p.accept_len = accept_len; p.out_ids = out_ids; p.flags = flags; p.lse_t = lse_t; p.lse_d = lse_d;
   spec_carve(workspace, B, k, pl, &p);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 g1((unsigned)(B * (2 * k + 1) * pl.chunks)), gb((unsigned)B), g2((unsigned)(B * pl.chunks2));
-  hipEvent_t* ev = profile_slot(4);
+  const int64_t na = B * (2 * k + 1) * pl.chunks;
+  const dim3 ga((unsigned)std::max<int64_t>(na, (B + kNT - 1) / kNT)), gb((unsigned)(B * pl.chunks2));
+  const size_t lds_b = std::max((size_t)pl.nsb * sizeof(double), (size_t)(2 * k + 1) * pl.chunks * 12);
+  hipEvent_t* ev = profile_slot(2);
   auto mark = [&](int j) -> int {
     if (ev) VNX_HIP_CHECK(hipEventRecord(ev[j], s));
     return VNX_OK;
@@ -711,18 +787,12 @@ static int spec_run(const void* target, const void* draft, int dtype, int64_t B,
     constexpr bool THR = decltype(thrc)::value;
     int e = mark(0);
     if (e) return e;
-    hipLaunchKernelGGL((k_spec_lse<Tin, SM, THR>), g1, dim3(kNT), 0, s, p);
+    hipLaunchKernelGGL((k_spec_lse<Tin, SM, THR>), ga, dim3(kNT), 0, s, p);
     VNX_LAUNCH_CHECK();
     if ((e = mark(1))) return e;
-    hipLaunchKernelGGL((k_spec_accept<Tin, SM, THR>), gb, dim3(kNT), 0, s, p);
+    hipLaunchKernelGGL((k_spec_mass_draw<Tin, SM, THR>), gb, dim3(kNT), lds_b, s, p);
     VNX_LAUNCH_CHECK();
-    if ((e = mark(2))) return e;
-    hipLaunchKernelGGL((k_spec_mass<Tin, SM, THR>), g2, dim3(kNT), 0, s, p);
-    VNX_LAUNCH_CHECK();
-    if ((e = mark(3))) return e;
-    hipLaunchKernelGGL((k_spec_draw<Tin, SM, THR>), gb, dim3(kNT), 0, s, p);
-    VNX_LAUNCH_CHECK();
-    return mark(4);
+    return mark(2);
   });
 }
 

@@ -108,9 +108,9 @@ __host__ __device__ __forceinline__ float vnx_exp_canon(float t) {
   p = __builtin_fmaf(p, r, c2);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int k = (int)kf;
-  float two_k = __uint_as_float((uint32_t)(k + 127) << 23);
-  const float e = p * two_k;
+  // p * 2^k with k in [-125, 127]: 2^k and the product are normal numbers,
+  // so the scaling is exact (ldexp, one instruction, equals the multiply)
+  const float e = __builtin_ldexpf(p, (int)kf);
   return (t >= -86.5f) ? e : 0.0f;
 }
 
