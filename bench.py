@@ -1,22 +1,27 @@
-"""Benchmark: fused speculative acceptance on one MI355X.
+"""Benchmark of the MI355X speculative-decoding verification path.
 
-One step = one vnx_spec_accept call over B=64 rows, k=8 draft positions,
-V=248,320 (target logits (64,9,V) fp32 ~ N(0,2), draft = target[:, :8] +
-N(0,0.5), T=0.8, no top-k, draft ids drawn from q, uniforms U(0,1)); inputs
-are resident in HBM before the timed region.
+Default line (python bench.py): BASELINE.json's metric, both halves.
+- value = verified tokens/s of config 5 (end-to-end speculative decode, the
+  mate target with an INT4 draft, B = 32, k = 6, T = 0.8): one step is one
+  speculative round (a HIP graph replay); W warm-up rounds, then exactly K
+  timed rounds of one generation; value = tokens committed in the K rounds /
+  their wall time.
+- roofline = the acceptance path of config 2 (vnx_spec_accept, B = 64, k = 8,
+  V = 248,320, fp32 logits): its two kernels' launches per call, algorithmic
+  bytes 4*V*[B*(2k+1) + sum_b r_b] (r_b = 2 when row b rejects: p_n and q_n
+  re-read by the residual draw, else 1: p_k for the bonus draw) over the
+  summed launch time, timed with HIP events the library records on its
+  stream; accept_kernel = the same bytes over back-to-back calls of the C
+  entry point.
+- Extra keys carry config 1 (greedy spec decode of the small models), config
+  3 (tree verification kernels) and config 4 (INT4 / INT8 GEMV), each with
+  its CPU baseline, and a config-5 leg with the VerseNex draft (no embedding
+  scale), whose drafts the target mostly rejects.
+CPU baselines are the numpy/C restatement of the reference path (oracle/, or
+numpy written in the reference's semantics here) on a bounded sample, timed
+on the host's cores; each states its core count, CPU model and BLAS.
 
-value = algorithmic bytes per step / mean step time, with
-  bytes = 4*V*[B*(2k+1) + sum_b r_b], r_b = 2 if row b rejects (p_n and q_n
-  re-read by the residual draw) else 1 (p_k re-read by the bonus draw).
-roofline = the acceptance path's kernel, k_spec_stage: one call is a
-  pipeline of P+2 launches of it (the row LSE streaming of part s beside the
-  accept + mass of part s-1 and the draw of part s-2); achieved = the call's
-  algorithmic bytes / the summed duration of its launches, timed with HIP
-  events the library records on the launch stream (vnx_profile_begin /
-  vnx_profile_end).  traffic = HBM bytes per call from the committed
-  rocprofv3 FETCH_SIZE / WRITE_SIZE summary, when present.
-The CPU baseline is the numpy/C checker (oracle/) on a bounded sample of the
-same workload, timed on the host's cores (threads over batch rows).
+--workload accept / tree / gemv / lmhead / config1 print one config alone.
 """
 from __future__ import annotations
 
@@ -34,6 +39,34 @@ if ROOT not in sys.path:
 
 HBM_PEAK_GBS = 8000.0
 B, K, V, T = 64, 8, 248320, 0.8
+CPU_THREADS = max(1, min(16, os.cpu_count() or 1))  # the box's CPU share
+
+
+def cpu_env(threads: int) -> dict:
+    """Host facts every CPU number states: threads used, os.cpu_count(), the
+    CPU model and numpy's BLAS."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas = ""
+    try:
+        import numpy as np
+        info = np.show_config(mode="dicts")["Build Dependencies"]["blas"]
+        blas = f"{info.get('name', '')} {info.get('version', '')}".strip()
+    except Exception:
+        pass
+    return {"cores": threads, "cpu_count": os.cpu_count(), "cpu_model": model, "blas": blas}
+
+
+def _median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
 MAX_PHASES = 7  # kMaxPhases of the library's profiler
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_spec_stage_config2_pmc.md")
 
@@ -101,13 +134,50 @@ def cpu_baseline(tgt, dft, ids, u, budget_s: float = 12.0):
 GEMV_SHAPES = (("tied_head", 248320, 1024), ("w_gate_up", 4096, 1024), ("w_down", 1024, 4096))
 
 
-def bench_gemv(args):
+def cpu_gemv(packed, qtype, x_list, reps_head: int = 3, reps: int = 5):
+    """The reference's QuantizedLinear.forward, path B (quantize.py:467-504:
+    int8 weights unpacked once at load, per call cast to fp32, GEMM, scale),
+    with the group-128 INT4 format applied as its extension: per call the
+    cached int8 q times the fp16 group scales in fp32, then x @ W^T.  Median
+    of `reps` calls per batch size (reps_head for the tied head)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import quant as OQ
+
+    wq, sc = packed
+    N = wq.shape[0]
+    if qtype == "int8":
+        q8, s = wq, sc.reshape(-1).astype(np.float32)
+        K = q8.shape[1]
+    else:
+        K = wq.shape[1] * 2
+        q8 = OQ.unpack_int4(wq, (N, K))                         # load time, not timed
+        s = sc.astype(np.float32)                              # (N, K/128)
+    out = {}
+    with threadpool_limits(limits=CPU_THREADS):
+        for x in x_list:
+            ts = []
+            for _ in range(reps_head if N > 100000 else reps):
+                t0 = time.perf_counter()
+                if qtype == "int8":
+                    y = x @ q8.astype(np.float32).T
+                    y *= s
+                else:
+                    w = (q8.reshape(N, K // 128, 128).astype(np.float32) * s[:, :, None]).reshape(N, K)
+                    y = x @ w.T
+                ts.append(time.perf_counter() - t0)
+            out[x.shape[0]] = _median(ts)
+    return out
+
+
+def bench_gemv(args, emit=True):
     """weight-only INT4 (group 128, fp16 scales) and INT8
     (per-channel) GEMV, weights N(0, 0.02), fp16 activations N(0, 1), B in
     {1, 8, 32}.  bytes per launch = weight + scales + 2*B*K (fp16 x) + 4*B*N
     (fp32 y).  Time: the C entry point is called `steps` times back to back on
     preallocated buffers, between two HIP events on its stream, so the small
-    FFN layers are timed on the GPU rather than on the Python launch path."""
+    FFN layers are timed on the GPU rather than on the Python launch path.
+    The CPU leg (cpu_gemv) runs on the same quantized weights and activations."""
     import ctypes
     import numpy as np
     import torch
@@ -121,14 +191,17 @@ def bench_gemv(args):
     g = torch.Generator(device=dev)
     g.manual_seed(20)
     rows = []
+    cpu_rows = []
     for name, N, K in GEMV_SHAPES:
         w = torch.randn((N, K), generator=g, device=dev) * 0.02
         packed = {"int4_g128": VQ.quantize_int4_g(w, 128), "int8": VQ.quantize_int8(w)}
         del w
         for qtype in ("int4_g128", "int8"):
             wq, sc = packed[qtype]
+            xs = []
             for B in (1, 8, 32):
                 x = (torch.randn((B, K), generator=g, device=dev)).to(torch.float16)
+                xs.append(x)
                 y = torch.empty((B, N), dtype=torch.float32, device=dev)
                 ws = torch.zeros(max(256, L.vnx_gemv_workspace(B, N, K)), dtype=torch.uint8, device=dev)
                 stream = torch.cuda.current_stream(dev)
@@ -142,22 +215,22 @@ def bench_gemv(args):
                     call, argv = L.vnx_gemv_w4, (P(x.data_ptr()), K, P(wq.data_ptr()), wq.stride(0),
                                                  P(sc.data_ptr()), _lib.VNX_F16, sc.stride(0), B, N, K, 128,
                                                  P(y.data_ptr()), N, P(ws.data_ptr()), ws.numel(), st)
-                _lib.check(call(*argv), "gemv")
-                for _ in range(args.warmup):
-                    call(*argv)
-                torch.cuda.synchronize()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                for _ in range(args.steps):
-                    call(*argv)
-                e1.record(stream)
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) * 1e3 / args.steps
+                us = _timed(call, argv, args.steps, args.warmup, stream)
                 nbytes = VQ.weight_bytes(qtype, N, K) + 2 * B * K + 4 * B * N
                 gbs = nbytes / (us * 1e-6) / 1e9
                 rows.append({"shape": name, "N": N, "K": K, "qtype": qtype, "B": B, "us": round(us, 2),
                              "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                              "TFLOP/s": round(2 * B * N * K / (us * 1e-6) / 1e12, 2)})
+            if not args.no_cpu:
+                xs_h = [x.float().cpu().numpy() for x in xs]
+                t_cpu = cpu_gemv((wq.cpu().numpy(), sc.cpu().numpy()), qtype, xs_h)
+                for x in xs_h:
+                    Bx = x.shape[0]
+                    nbytes = VQ.weight_bytes(qtype, N, K) + 2 * Bx * K + 4 * Bx * N
+                    gpu = [r for r in rows if r["shape"] == name and r["qtype"] == qtype and r["B"] == Bx][0]
+                    cpu_rows.append({"shape": name, "qtype": qtype, "B": Bx, "ms": round(t_cpu[Bx] * 1e3, 3),
+                                     "GB/s": round(nbytes / t_cpu[Bx] / 1e9, 2),
+                                     "gpu_speedup": round(t_cpu[Bx] * 1e6 / gpu["us"], 1)})
     head = [r for r in rows if r["shape"] == "tied_head" and r["qtype"] == "int4_g128"]
     best = max(head, key=lambda r: r["GB/s"])
     out = {"metric": "quantized GEMV HBM GB/s (config 4, INT4 g128 tied head, B=1)",
@@ -167,7 +240,14 @@ def bench_gemv(args):
            "roofline": {"bound": "hbm", "achieved": best["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": best["frac"], "traffic": None, "kernel": "k_qgemv_stream<*, 8, 2> (tied head)"},
            "results": rows}
-    print(json.dumps(out), flush=True)
+    if cpu_rows:
+        out["cpu_baseline"] = dict(cpu_env(CPU_THREADS), kind="port", results=cpu_rows,
+                                   sample="QuantizedLinear.forward path B semantics (int8 cached at load; per call "
+                                          "cast, group-128 scale, BLAS GEMM): median of 5 calls (3 for the tied "
+                                          "head) per batch size, fp32 activations")
+    if emit:
+        print(json.dumps(out), flush=True)
+    return out
 
 
 def _timed(call, argv, steps, warmup, stream):
@@ -188,7 +268,7 @@ def _timed(call, argv, steps, warmup, stream):
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
-def bench_tree(args):
+def bench_tree(args, emit=True):
     """tree verification.  B = 16, tree (4,3,2) = 40 nodes,
     16 heads x 64 over a 2048-token bf16 KV prefix (N(0,1)); target logits
     (16, 41, V) and draft logits (16, 17, V) fp32 N(0, 2).  Three kernels,
@@ -281,7 +361,74 @@ def bench_tree(args):
                 "roofline": {"bound": "hbm", "achieved": greedy["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": greedy["frac"], "traffic": None, "kernel": "vnx_tree_greedy"},
                 "accept_len": alen.cpu().tolist(), "results": rows}
-    print(json.dumps(out_line), flush=True)
+    if not args.no_cpu:
+        host = dict(q=q.float().cpu().numpy(), kc=kc.float().cpu().numpy(), vc=vc.float().cpu().numpy(),
+                    kt=kt.float().cpu().numpy(), vt=vt.float().cpu().numpy(), tgt=tgt.cpu().numpy(),
+                    dft=dft.cpu().numpy(), tok=tok.cpu().numpy())
+        t_cpu = cpu_tree(host, par)
+        cpu_rows = []
+        for r in rows:
+            key = r["kernel"].split()[0]
+            t = t_cpu[key]
+            cpu_rows.append({"kernel": key, "ms": round(t * 1e3, 3), "GB/s": round(r["bytes"] / t / 1e9, 2),
+                             "gpu_speedup": round(t * 1e6 / r["us"], 1)})
+        out_line["cpu_baseline"] = dict(cpu_env(CPU_THREADS), kind="port", results=cpu_rows,
+                                        sample="numpy fp32, median of 5: top-b expansion by argpartition, "
+                                               "DeviceBackend.attention semantics (softmax(q k^T / sqrt(d) + "
+                                               "ancestor mask) v, device.py:260-270), oracle.tree.tree_greedy")
+    if emit:
+        print(json.dumps(out_line), flush=True)
+    return out_line
+
+
+def cpu_tree(h, par, reps: int = 5):
+    """Config 3 on the host, each part timed alone (median of reps): the
+    expansion (top-4 ids of the 17 parent draft rows), the ancestor-masked
+    attention in the reference's DeviceBackend.attention semantics
+    (device.py:260-270, fp32, additive 0 / -inf mask), and the greedy longest
+    accepted path (argmax of the 41 target rows + the path rule)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import tree as OT
+    from versenext_amd import tree as TR
+
+    B_, H_, N_, d_ = h["q"].shape
+    Tp_ = h["kc"].shape[2]
+    words = TR.ancestor_words(par)
+    bits = ((words[:, None] >> np.arange(N_, dtype=np.uint64)[None, :]) & np.uint64(1)).astype(bool)
+    mask = np.zeros((N_, Tp_ + N_), np.float32)
+    mask[:, Tp_:][~bits] = -np.inf
+    K_ = np.concatenate([h["kc"], h["kt"]], axis=2)
+    V_ = np.concatenate([h["vc"], h["vt"]], axis=2)
+    res = {}
+
+    def timeit(fn):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return _median(ts)
+
+    def expand():
+        x = h["dft"].reshape(-1, h["dft"].shape[-1])
+        cand = np.argpartition(x, -4, axis=-1)[:, -4:]
+        vals = np.take_along_axis(x, cand, axis=-1)
+        order = np.lexsort((cand, -vals), axis=-1)
+        return np.take_along_axis(cand, order, axis=-1)
+
+    def attend():
+        s_ = np.matmul(h["q"], K_.transpose(0, 1, 3, 2)) * np.float32(1.0 / np.sqrt(d_)) + mask
+        s_ = np.exp(s_ - s_.max(axis=-1, keepdims=True))
+        s_ /= s_.sum(axis=-1, keepdims=True)
+        return np.matmul(s_, V_)
+
+    with threadpool_limits(limits=CPU_THREADS):
+        res["vnx_row_topk"] = timeit(expand)
+        reps = min(reps, 3)  # ~1-2 s per call
+        res["vnx_tree_attn"] = timeit(attend)
+        res["vnx_tree_greedy"] = timeit(lambda: OT.tree_greedy(h["tgt"], h["tok"], par))
+    return res
 
 
 def bench_lmhead(args):
@@ -346,10 +493,12 @@ def bench_lmhead(args):
 E2E_B, E2E_K, E2E_T0, E2E_NEW, E2E_TEMP = 32, 6, 512, 256, 0.8
 
 
-def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, seed=0):
+def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, seed=0, versenex=False):
     """BASELINE config 5 models on the GPU: the CometSparkV05 mate target
     (random init, bf16) and a 2-layer mate-width draft with INT4 group-128
-    weights and head, caches for T0 + n_new + 2(k+1) positions."""
+    weights and head, caches for T0 + n_new + 2(k+1) positions.  versenex:
+    also a second draft of the same shape without the x sqrt(D) embedding
+    scale (CometSparkNexLM.forward, cometspark.py:670-690)."""
     import torch
     from versenext_amd import model as VM
     dev = hip.torch_device
@@ -360,9 +509,86 @@ def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, s
     del Wt
     Wd = VM.init_weights(dcfg, seed=seed + 1, device=dev)
     draft = VM.CometSparkGPU(dcfg, Wd, hip, batch=B, capacity=cap, dtype=torch.bfloat16, int4=True)
+    draft2 = None
+    if versenex:
+        dcfg2 = VM.mate_draft(draft_layers)
+        dcfg2.embedding_scale = False
+        dcfg2.name = dcfg.name.replace("VerseNex draft", "VerseNex draft without the embedding scale")
+        draft2 = VM.CometSparkGPU(dcfg2, Wd, hip, batch=B, capacity=cap, dtype=torch.bfloat16, int4=True)
     del Wd
     torch.cuda.empty_cache()
-    return target, draft
+    return (target, draft, draft2) if versenex else (target, draft)
+
+
+def round_floor_bytes(target, draft, B: int, k: int, ctx: float) -> dict:
+    """Algorithmic HBM bytes of one speculative round at mean context ctx
+    (committed cache rows per sequence): every weight read once per forward
+    that uses it, each cache read once per forward, the logits written once
+    and read by the kernels that need them.
+      target (one (k+1)-token forward): bf16 weights incl. the tied head,
+        fp32 router weights; K/V of ctx + k+1 rows per layer;
+      draft (k+1 one-token forwards, the last one cache-only): INT4 g128
+        linears every forward, the INT4 head k times; its K/V per forward;
+      logits: p (B, k+1, V) and q (B, k, V) fp32 written once; each of the k
+        draft draws reads its q row twice (row LSE, then the draw mass); the
+        acceptance reads p and q once and re-reads p_n and q_n (2 rows)."""
+    tc, dc = target.cfg, draft.cfg
+    V, D = tc.vocab_size, tc.dim
+
+    def attn_params(c):
+        return (c.n_head + 2 * c.n_kv_head) * c.head_dim * c.dim + c.dim * c.n_head * c.head_dim
+
+    tw = V * D * 2
+    for kind in tc.layer_pattern:
+        tw += attn_params(tc) * 2
+        if kind == "mod":
+            P, E = tc.num_dense_parts, tc.num_experts_per_part
+            tw += P * E * 3 * tc.expert_hidden_eff * D * 2 + (P + P * E) * D * 4
+        else:
+            tw += 3 * tc.ffn_hidden * D * 2
+    kv_t = tc.n_layer * B * (ctx + k + 1) * tc.n_kv_head * tc.head_dim * 2 * 2
+
+    def int4(n, kk):
+        return n * kk // 2 + 2 * n * (kk // 128)
+
+    dw_layers = dc.n_layer * (int4((dc.n_head + 2 * dc.n_kv_head) * dc.head_dim, dc.dim)
+                              + int4(dc.dim, dc.n_head * dc.head_dim) + int4(2 * dc.ffn_hidden, dc.dim)
+                              + int4(dc.dim, dc.ffn_hidden))
+    dw = (k + 1) * dw_layers + k * int4(V, D)
+    kv_d = (k + 1) * dc.n_layer * B * (ctx + k) * dc.n_kv_head * dc.head_dim * 2 * 2
+    logits = 4 * V * B * ((k + 1) + k + 2 * k + (2 * k + 1) + 2)
+    total = tw + kv_t + dw + kv_d + logits
+    return {"bytes": int(total), "target_weights": int(tw), "target_kv": int(kv_t), "draft_weights": int(dw),
+            "draft_kv": int(kv_d), "logits": int(logits), "floor_ms_at_peak": round(total / HBM_PEAK_GBS / 1e6, 4)}
+
+
+def e2e_rounds(eng, prompts, n_new, steps, warmup, mark=None):
+    """Prefill, `warmup` untimed rounds (the first captures the round's HIP
+    graph), then exactly `steps` timed rounds of the same generation (mark(),
+    when given, runs right before and right after them).  Returns (seconds,
+    tokens committed in the timed rounds, per-round token counts, prefill
+    seconds)."""
+    import torch
+    B = eng.B
+    prefill_s = eng.prefill(prompts, n_new)
+    if eng.use_graph and eng.graph is None:
+        eng._capture()
+    for _ in range(warmup):
+        eng.step()
+    torch.cuda.synchronize(eng.dev)
+    if mark:
+        mark()
+    per = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        info = eng.step()
+        per.append(int(info[3]) + B)
+    torch.cuda.synchronize(eng.dev)
+    dt = time.perf_counter() - t0
+    if mark:
+        mark()
+        torch.cuda.synchronize(eng.dev)
+    return dt, sum(per), per, prefill_s
 
 
 def cpu_baseline_e2e(Wt, Wd, prompt, budget_s: float = 15.0):
@@ -399,9 +625,9 @@ def cpu_baseline_e2e(Wt, Wd, prompt, budget_s: float = 15.0):
 
 
 def trace_summary(d: str, top: int = 40) -> None:
-    """Per-round GPU time by kernel between the two marker kernels of an
-    --e2e-mark run (rocprofv3 --kernel-trace --output-format csv): the decode
-    rounds of the last run only (no prefill, capture or warm-up)."""
+    """Per-round GPU time by kernel between the first two marker kernels of
+    an --e2e-mark run (rocprofv3 --kernel-trace --output-format csv): the
+    timed rounds only (no prefill, capture or warm-up)."""
     import collections
     import csv
     import glob
@@ -411,7 +637,7 @@ def trace_summary(d: str, top: int = 40) -> None:
     marks = [i for i, r in enumerate(rows) if "scan" in r["Kernel_Name"].lower()]
     if len(marks) < 2:
         raise SystemExit("no marker kernels in the trace (run bench.py --workload e2e --e2e-mark)")
-    win = rows[marks[-2] + 1:marks[-1]]
+    win = rows[marks[0] + 1:marks[1]]
     lm = sum(1 for r in win if "k_lm_head" in r["Kernel_Name"])  # one verify head per round
     rounds = max(1, lm)
     agg = collections.defaultdict(lambda: [0, 0.0])
@@ -428,18 +654,17 @@ def trace_summary(d: str, top: int = 40) -> None:
         print(f"{t / rounds:9.1f} us/round {c / rounds:6.1f} calls {t / c:8.1f} us  {name}")
 
 
-def bench_e2e(args):
+def bench_e2e(args, full: bool = True):
     """end-to-end speculative decode.  Target CometSparkV05
     (D 1024, 20 layers = 5 MoD + 15 TriSparse, tied 248,320 head, random init,
     bf16); draft: 2 mate-width TriSparse layers (D 1024, ffn 4096) with INT4
     group-128 weights and tied head; k = 6, batch 32, 512-token uniform-random
-    prompts, 256 new tokens per sequence, temperature 0.8.  Each decode round
-    is one HIP graph replay.
-    value = verified tokens / s = 32 * 256 committed tokens / wall time of the
-    decode rounds (prefill timed and reported separately).
-    The accept-kernel half of the metric is measured in
-    the same run after the models are freed: its k_spec_lse launch is the
-    roofline object, and its CPU leg rides along as cpu_baseline_accept."""
+    prompts, T = 0.8.  One step = one speculative round (a HIP graph replay):
+    `warmup` rounds, then `steps` timed rounds of one generation of at least
+    256 new tokens per sequence; value = tokens committed in the timed rounds
+    / their wall time (prefill reported separately).  The accept-kernel half
+    of the metric is measured in the same run after the
+    models are freed, then configs 3, 4 and 1."""
     import numpy as np
     import torch
     from versenext_amd import get_backend
@@ -448,80 +673,153 @@ def bench_e2e(args):
 
     hip = get_backend("rocm:0")
     dev = hip.torch_device
+    # config 2's 1.2 GB of logits are allocated first, while device memory is
+    # unfragmented, and stay resident until their measurement
+    acc_inputs = make_inputs_gpu(dev)
+    n_new = max(E2E_NEW, (args.warmup + args.steps + 2) * (E2E_K + 1))
     t_build = time.perf_counter()
     Wt_host = Wd_host = None
     if not args.no_cpu:
         Wt_host = {k: v.cpu().numpy() for k, v in VM.init_weights(VM.mate_target(), seed=0, device=dev).items()}
         Wd_host = {k: v.cpu().numpy() for k, v in VM.init_weights(VM.mate_draft(2), seed=1, device=dev).items()}
-    target, draft = build_e2e(hip)
+    target, draft, draft2 = build_e2e(hip, n_new=n_new, versenex=True)
     build_s = time.perf_counter() - t_build
     g = torch.Generator(device=dev)
     g.manual_seed(30)
     prompts = torch.randint(0, V, (E2E_B, E2E_T0), generator=g, device=dev)
     eng = SpecDecodeEngine(target, draft, hip, k=E2E_K, temperature=E2E_TEMP, seed=31,
                            use_graph=not args.e2e_eager)
-    runs = []
-    nruns = max(1, args.e2e_runs)
-    mark = torch.ones(64, dtype=torch.int16, device=dev) if args.e2e_mark else None
-    if mark is not None:
-        # marker kernels (an int16 scan, used nowhere else) bracket the last
-        # run's decode rounds in a kernel trace: one after its prefill, one
-        # after its last round (see --trace-summary)
-        fill = eng._fill_uniforms
-        armed = {"on": False}
+    mark = None
+    if args.e2e_mark:
+        # marker kernels (an int16 scan, used nowhere else) bracket the timed
+        # rounds in a kernel trace (see --trace-summary)
+        mvec = torch.ones(64, dtype=torch.int16, device=dev)
 
-        def fill_marked():
-            if armed["on"]:
-                torch.cumsum(mark, 0)
-                armed["on"] = False
-            fill()
-        eng._fill_uniforms = fill_marked
-    for r in range(nruns):
-        if mark is not None and r == nruns - 1:
-            armed["on"] = True
-        toks, st = eng.generate(prompts, E2E_NEW)
-        if mark is not None and r == nruns - 1:
-            torch.cumsum(mark, 0)
-            torch.cuda.synchronize()
-        runs.append(st)
-        print(json.dumps({"e2e_run": r, "rounds": st.rounds, "decode_s": round(st.decode_s, 4),
-                          "prefill_s": round(st.prefill_s, 4), "tokens_per_s": round(st.tokens_per_s, 1),
-                          "graph": eng.graph is not None}), flush=True)
-    timed = runs[-1]
+        def mark():
+            torch.cumsum(mvec, 0)
+    dt, toks, per, prefill_s = e2e_rounds(eng, prompts, n_new, args.steps, args.warmup, mark)
     graphed = eng.graph is not None
+    ms_round = dt * 1e3 / args.steps
+    ctx = E2E_T0 + (args.warmup + args.steps / 2) * float(np.mean(per)) / E2E_B
+    floor = round_floor_bytes(target, draft, E2E_B, E2E_K, ctx)
+    floor["frac_of_round"] = round(floor["floor_ms_at_peak"] / ms_round, 4)
+    floor["mean_context"] = round(ctx, 1)
+    # the whole 256-token generation, for continuity with earlier runs
+    toks_gen, st = eng.generate(prompts, E2E_NEW)
+    gen = {"tokens_per_s": round(st.tokens_per_s, 1), "rounds": st.rounds, "decode_s": round(st.decode_s, 4),
+           "new_tokens_per_seq": E2E_NEW}
+    del toks_gen
+    # the same round with the VerseNex draft (no embedding scale)
+    eng2 = SpecDecodeEngine(target, draft2, hip, k=E2E_K, temperature=E2E_TEMP, seed=31,
+                            use_graph=not args.e2e_eager)
+    dt2, toks2, per2, _ = e2e_rounds(eng2, prompts, n_new, args.steps, args.warmup)
+    versenex = {"draft": draft2.cfg.name + ", INT4 g128", "tokens_per_s": round(toks2 / dt2, 1),
+                "ms_per_round": round(dt2 * 1e3 / args.steps, 3),
+                "mean_tokens_per_round_per_seq": round(toks2 / args.steps / E2E_B, 3)}
     tcfg_name, dcfg_name = target.cfg.name, draft.cfg.name
     prompt0 = prompts[0].cpu().numpy()
-    mean_tokens_round = float(np.mean(timed.per_round_tokens)) / E2E_B
-    del eng, target, draft, toks
+    del eng, eng2, target, draft, draft2
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
 
-    acc = bench_accept(args, emit=False)
-    out = {"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(timed.tokens_per_s, 1),
-           "unit": "tokens/s", "n_gpus": 1, "steps": timed.rounds, "warmup": len(runs) - 1,
-           "ms_per_step": round(timed.decode_s * 1e3 / timed.rounds, 3), "higher_is_better": True,
+    if not full:
+        print(json.dumps({"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(toks / dt, 1),
+                          "unit": "tokens/s", "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": round(ms_round, 3),
+                          "mean_tokens_per_round_per_seq": round(toks / args.steps / E2E_B, 3),
+                          "round_floor": floor, "e2e_versenex_draft": versenex}), flush=True)
+        return
+    acc = bench_accept(args, emit=False, inputs=acc_inputs)
+    del acc_inputs
+    tree = bench_tree(args, emit=False)
+    gemv = bench_gemv(args, emit=False)
+    c1 = bench_config1(args, emit=False)
+    out = {"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(toks / dt, 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(ms_round, 3), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16 target / int4 draft / f32 logits",
            "data": "synthetic (random-init weights, uniform-random prompts)",
            "config": {"workload": "BASELINE config 5: end-to-end speculative decode", "batch": E2E_B, "k": E2E_K,
                       "rounds_as": "HIP graph replays" if graphed else "eager launches",
-                      "prompt": E2E_T0, "new_tokens": E2E_NEW, "temperature": E2E_TEMP,
+                      "prompt": E2E_T0, "new_tokens": n_new, "temperature": E2E_TEMP,
                       "target": tcfg_name, "draft": dcfg_name + ", INT4 g128",
                       "step": "one speculative round: 7 draft forwards + 6 draws, one 7-token target verify "
                               "+ LM head, acceptance, commit"},
-           "prefill_s": round(timed.prefill_s, 4), "build_s": round(build_s, 2),
-           "mean_tokens_per_round_per_seq": round(mean_tokens_round, 3),
+           "prefill_s": round(prefill_s, 4), "build_s": round(build_s, 2),
+           "mean_tokens_per_round_per_seq": round(toks / args.steps / E2E_B, 3),
+           "acceptance_rate": round((toks / args.steps / E2E_B - 1) / E2E_K, 4),
+           "round_floor": floor, "generation_256": gen, "e2e_versenex_draft": versenex,
            "roofline": acc["roofline"],
            "accept_kernel": {"metric": acc["metric"], "value": acc["value"], "unit": acc["unit"],
                              "workload": acc["config"]["workload"], "frac_of_hbm_peak":
-                             acc["config"]["frac_of_hbm_peak"], "ms_per_call": acc["config"]["event_ms_mean"]}}
+                             acc["config"]["frac_of_hbm_peak"], "ms_per_call": acc["config"]["event_ms_mean"]},
+           "config3_tree": {k: tree.get(k) for k in ("value", "unit", "ms_per_step", "results", "cpu_baseline")},
+           "config4_gemv": {k: gemv.get(k) for k in ("value", "unit", "results", "cpu_baseline")},
+           "config1": c1}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_e2e(Wt_host, Wd_host, prompt0)
         out["cpu_baseline_accept"] = acc.get("cpu_baseline")
     print(json.dumps(out), flush=True)
 
 
-def bench_accept(args, emit=True):
-    """one vnx_spec_accept call per step (module docstring)."""
+def bench_config1(args, emit=True):
+    """greedy speculative decode of the CometSparkV05Small
+    target (V 256, D 64, 2 layers) with the 1-layer D = 32 draft, k = 4, one
+    sequence, the 16-token prompt and 128 new tokens, with the weights the
+    reference itself wrote (tests/golden/cometspark_small.npz, np.random.seed
+    (0) construction).  GPU: SpecDecodeEngine, fp32, greedy verify, rounds as
+    graph replays; CPU: the reference's loop restated in numpy
+    (oracle.model.spec_decode_greedy: draft argmax by re-forward, full
+    re-forward verify, speculative.py:230-310), the full 128 tokens."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from oracle import model as OM
+    from versenext_amd import get_backend
+    from versenext_amd import model as VM
+    from versenext_amd.e2e import SpecDecodeEngine
+
+    hip = get_backend("rocm:0")
+    z = np.load(os.path.join(ROOT, "tests", "golden", "cometspark_small.npz"))
+    gold = {k: z[k] for k in z.files}
+
+    def w(prefix):
+        return {k[len(prefix):]: v for k, v in gold.items() if k.startswith(prefix) and not k.endswith("head.weight")}
+
+    Wt, Wd = w("t/"), w("d/")
+    ct, cd = VM.small_target(), VM.small_draft()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    t = VM.CometSparkGPU(ct, Wt, hip, batch=1, capacity=256, dtype=torch.float32)
+    d = VM.CometSparkGPU(cd, Wd, hip, batch=1, capacity=256, dtype=torch.float32)
+    eng = SpecDecodeEngine(t, d, hip, k=4, temperature=0.0, use_graph=True)
+    prompt = torch.from_numpy(gold["prompt"][None].astype(np.int64)).to(hip.torch_device)
+    eng.generate(prompt, 128)                                   # captures the graph
+    runs = [eng.generate(prompt, 128) for _ in range(3)]
+    toks, st = runs[-1]
+    ok = bool(np.array_equal(toks.cpu().numpy()[0], gold["greedy128"]))
+    out = {"workload": "BASELINE config 1: greedy spec decode, CometSparkV05Small target + 1-layer draft, k=4, "
+                       "128 tokens", "gpu_tokens_per_s": round(_median([r[1].tokens_per_s for r in runs]), 1),
+           "gpu_rounds": st.rounds, "gpu_stream_equals_reference_greedy128": ok}
+    if not args.no_cpu:
+        with threadpool_limits(limits=CPU_THREADS):
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                ctoks, steps = OM.spec_decode_greedy(Wt, ct, Wd, cd, gold["prompt"], 128, 4)
+                ts.append(time.perf_counter() - t0)
+        tc = _median(ts)
+        out["cpu_baseline"] = dict(cpu_env(CPU_THREADS), kind="port", value=round(128 / tc, 2), unit="tokens/s",
+                                   sample=f"the full 128-token run (median of 3), {steps} verify rounds, "
+                                          f"stream equals greedy128: {bool(np.array_equal(ctoks, gold['greedy128']))}")
+        out["gpu_speedup"] = round(out["gpu_tokens_per_s"] / out["cpu_baseline"]["value"], 2)
+    if emit:
+        print(json.dumps(out), flush=True)
+    return out
+
+
+def bench_accept(args, emit=True, inputs=None):
+    """one vnx_spec_accept call per step (module docstring).
+    inputs: (target, draft, ids, uniforms) already on the device (make_inputs_gpu)."""
     import numpy as np
     import torch
     from versenext_amd import get_backend
@@ -529,7 +827,7 @@ def bench_accept(args, emit=True):
 
     hip = get_backend("rocm:0")
     dev = hip.torch_device
-    tgt, dft, ids, u = make_inputs_gpu(dev)
+    tgt, dft, ids, u = inputs if inputs is not None else make_inputs_gpu(dev)
     L = _lib.lib()
     # the C entry point on preallocated buffers, issued back to back on one
     # stream, so the timed region holds the library's launches only
@@ -632,10 +930,9 @@ def bench_accept(args, emit=True):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--e2e-runs", type=int, default=2, help="e2e: decode runs (the last is reported)")
     ap.add_argument("--e2e-eager", action="store_true", help="e2e: launch every round eagerly (no HIP graph)")
     ap.add_argument("--e2e-mark", action="store_true",
                     help="e2e: bracket the last run's decode rounds with marker kernels for a kernel trace")
@@ -644,10 +941,11 @@ def main():
                          "(DIR holds *kernel_trace.csv) and exit")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
-    ap.add_argument("--workload", default="e2e", choices=("e2e", "accept", "gemv", "tree", "lmhead"),
-                    help="e2e: BASELINE config 5 verified tokens/s with the config-2 accept-kernel roofline "
-                         "(the bench line); accept: config 2 alone; gemv: config 4; tree: config 3; "
-                         "lmhead: the verify-pass LM head")
+    ap.add_argument("--workload", default="all",
+                    choices=("all", "e2e", "accept", "gemv", "tree", "lmhead", "config1"),
+                    help="all: the bench line (config 5 verified tokens/s, the config-2 accept-kernel "
+                         "roofline, configs 1, 3 and 4 as extra keys); e2e: config 5 alone; accept: config 2; "
+                         "gemv: config 4; tree: config 3; config1: config 1; lmhead: the verify-pass LM head")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
@@ -665,8 +963,11 @@ def main():
     if args.workload == "lmhead":
         bench_lmhead(args)
         return
-    if args.workload == "e2e":
-        bench_e2e(args)
+    if args.workload == "config1":
+        bench_config1(args)
+        return
+    if args.workload in ("all", "e2e"):
+        bench_e2e(args, full=args.workload == "all")
         return
 
     bench_accept(args)
