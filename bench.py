@@ -68,7 +68,7 @@ def _median(xs):
     xs = sorted(xs)
     return xs[len(xs) // 2]
 MAX_PHASES = 7  # kMaxPhases of the library's profiler
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_spec_stage_config2_pmc.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "vnx_spec_accept_config2.md")
 
 
 def make_inputs_gpu(device):
@@ -910,7 +910,7 @@ def bench_accept(args, emit=True, inputs=None):
                    "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(stage_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(stage_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-                     "kernel": "k_spec_stage", "launches_per_call": len(stage_ms),
+                     "kernel": "k_spec_lse + k_spec_mass_draw", "launches_per_call": len(stage_ms),
                      "bytes_per_call": nbytes, "kernel_ms_per_call": round(call_kernel_ms, 4),
                      "timing": "HIP events recorded by the library before each launch and after the last, "
                                "on its stream (each interval includes the gap before the next launch)",
