@@ -144,6 +144,36 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
                     float* lse_t, float* lse_d,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Sampler.sample, one call per batch of rows: out_ids[b] = the token the
+ * reference's Sampler draws from logits row b with temperature, top_k, top_p
+ * and the uniform uniforms[b] in place of its RNG
+ * (packages/verse_infra/verse_infra/verse_inference/sampler.py:70-138):
+ * temperature 0 -> numpy.argmax of the raw row; a = RN(l/T); top_k in (0, V):
+ * kth = the kth largest a (numpy.partition order, NaN largest), a = a >= kth ?
+ * a : -inf; max(a) not finite -> numpy.argmax of the raw row; p =
+ * vnx_exp_canon(a - RN32(row LSE)); top_p < 1: the first cutoff + 1 tokens
+ * in (p descending, id ascending) order, cutoff = the first position whose
+ * cumulative floor(p * 2^60) reaches floor(top_p * 2^60), at most V - 1;
+ * the draw is the inverse CDF over the kept p (numpy's Generator.choice
+ * rule).  One workgroup per row, no workspace.  Optional outputs (NULL to
+ * skip): flags (VNX_FLAG_CDF_EDGE / LSE_EDGE), lse = RN32(row LSE), kth (the
+ * top-k threshold, -inf if off), p_star / j_star (the last kept token's
+ * probability and id, -1 if top_p is off).  Errors: temperature < 0 or not
+ * finite, top_k < 0, top_p outside (0, 1] -> VNX_ERR_INVALID_ARG (the
+ * reference's ValueError, sampler.py:54-59). */
+int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float temperature,
+                       int64_t top_k, float top_p, const float* uniforms, int64_t* out_ids, uint8_t* flags,
+                       float* lse, float* kth, float* p_star, int64_t* j_star, void* stream);
+
+/* Logit calibration of VMPC-compressed models
+ * (CometSparkNexLM._apply_logit_calibration, packages/verse_nex/verse_nex/
+ * cometspark.py:922-948): out row b = logits row b / sqrt(var + eps) *
+ * calib_factor, var the row's population variance (taken in fp64, then
+ * rounded to fp32; the rest in fp32 in the reference's order).  out is fp32
+ * (it may alias fp32 logits with ld_out == ld); var (B) fp64 may be NULL. */
+int vnx_logit_calibrate(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float calib_factor,
+                        float eps, float* out, int64_t ld_out, double* var, void* stream);
+
 /* Allocation-free vnx_spec_accept.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory or pass a workspace (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -1,0 +1,138 @@
+"""vnx_sampler_sample and vnx_logit_calibrate against the CPU restatement
+(oracle/sampler.py) through the C ABI: the kth value and the nucleus (p*, j*)
+bit for bit, the drawn token bit for bit except rows the kernel flags
+(CDF_EDGE: the target within 1e-12 of a bucket edge; LSE_EDGE: the fp64 LSE
+within 1e-7 of an fp32 rounding midpoint), on 248,320-wide rows, with ties,
+NaN and -inf rows, fp32 and bf16 logits."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampler as OS
+from oracle.model import bf16_round
+from versenext_amd import _lib
+from versenext_amd.sampler import Sampler
+
+pytestmark = pytest.mark.gpu
+
+V = 248320
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _check(hip, x, T, top_k, top_p, u, dtype=torch.float32):
+    """x (B, V) float32 host rows (already representable in dtype)."""
+    B = x.shape[0]
+    res = hip.sampler_sample(torch.from_numpy(x).to(dtype), torch.from_numpy(u), T, top_k, top_p, return_all=True)
+    torch.cuda.synchronize()
+    ids = res["ids"].cpu().numpy()
+    flags = res["flags"].cpu().numpy()
+    kth = res["kth"].cpu().numpy()
+    ps = res["p_star"].cpu().numpy()
+    js = res["j_star"].cpu().numpy()
+    bad = 0
+    for b in range(B):
+        ref, rflags, info = OS.sample(x[b], T, top_k, top_p, u[b])
+        if "kth" in info:
+            assert (np.isnan(kth[b]) and np.isnan(info["kth"])) or kth[b] == info["kth"], (b, kth[b], info["kth"])
+        lse_edge = flags[b] & _lib.FLAG_LSE_EDGE
+        if "p_star" in info and not (ps[b] == info["p_star"] and js[b] == info["j_star"]):
+            # a flagged LSE may round to the neighbouring float32 and shift every p by an ulp
+            assert lse_edge, (b, ps[b], js[b], info)
+        if ids[b] != ref:
+            assert flags[b] != 0 or rflags != 0, (b, ids[b], ref, T, top_k, top_p)
+            bad += 1
+    return ids, flags, bad
+
+
+@pytest.mark.parametrize("T,top_k,top_p", [(0.8, 0, 1.0), (0.7, 50, 1.0), (1.0, 0, 0.9), (0.8, 20, 0.95),
+                                           (1.3, 1000, 0.5), (0.6, 64, 0.99), (0.8, 1, 1.0), (0.0, 0, 1.0)])
+def test_sampler_matches_oracle_full_vocab(hip, T, top_k, top_p):
+    rng = np.random.default_rng(int(T * 10 + top_k + top_p * 100))
+    B = 12
+    x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    ids, flags, bad = _check(hip, x, T, top_k, top_p, u)
+    _say(f"T={T} top_k={top_k} top_p={top_p}: ids {ids[:6].tolist()} flagged {int((flags != 0).sum())}, "
+         f"differing {bad}")
+    assert bad <= 1
+
+
+def test_sampler_ties_and_bf16(hip):
+    """Logits on a coarse grid: many equal values at the kth value and in the
+    nucleus; bf16 rows."""
+    rng = np.random.default_rng(5)
+    B = 8
+    x = (np.round(rng.normal(0, 2.0, (B, V)) * 4) / 4).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    for (T, k, p) in ((1.0, 200, 1.0), (1.0, 0, 0.8), (1.0, 30, 0.7), (0.5, 0, 0.3)):
+        ids, flags, bad = _check(hip, x, T, k, p, u)
+        assert bad <= 1, (T, k, p)
+    xb = bf16_round(rng.normal(0, 2.0, (B, V)).astype(np.float32))
+    ids, flags, bad = _check(hip, xb, 0.8, 40, 0.9, u, dtype=torch.bfloat16)
+    assert bad <= 1
+
+
+def test_sampler_special_rows(hip):
+    """NaN without top-k, all -inf, more NaN than k, top_k >= V, tiny top_p,
+    a short odd-width vocabulary."""
+    rng = np.random.default_rng(8)
+    B = 6
+    x = rng.normal(0, 2.0, (B, 1003)).astype(np.float32)
+    x[0, 17] = np.nan
+    x[1, :] = -np.inf
+    x[2, [3, 9, 11]] = np.nan
+    u = rng.random(B).astype(np.float32)
+    for (T, k, p) in ((0.8, 0, 1.0), (0.8, 2, 1.0), (0.8, 5000, 1.0), (0.8, 0, 1e-6), (0.9, 7, 0.6)):
+        ids, flags, bad = _check(hip, x, T, k, p, u)
+        assert bad == 0, (T, k, p)
+    assert hip.sampler_sample(torch.from_numpy(x), torch.from_numpy(u), 0.8)[0].item() == 17
+
+
+def test_sampler_errors_match_the_reference(hip):
+    x = torch.zeros((1, 16))
+    u = torch.zeros(1)
+    for kw in (dict(temperature=-0.1), dict(top_k=-1), dict(top_p=0.0), dict(top_p=1.01)):
+        with pytest.raises(ValueError):
+            hip.sampler_sample(x, u, **kw)
+    with pytest.raises(ValueError):
+        Sampler(top_p=0.0)
+
+
+def test_sampler_class_reproduces_numpy_choice_stream(hip):
+    """The Sampler class with a seed draws its uniform from default_rng(seed):
+    with top_k 0 / top_p 1 the tokens equal numpy's Generator.choice on the
+    canonical probabilities (the reference's sampler.py:135-137 rule)."""
+    rng = np.random.default_rng(2)
+    s = Sampler(temperature=0.9, seed=123)
+    gen = np.random.default_rng(123)
+    for _ in range(5):
+        x = rng.normal(0, 2.0, 5000).astype(np.float32)
+        tok = s.sample(x)
+        _, _, p = OS.probabilities(x, 0.9)
+        q = p.astype(np.float64) / p.astype(np.float64).sum()
+        assert tok == gen.choice(q.size, p=q)
+
+
+def test_logit_calibration_matches_oracle(hip):
+    rng = np.random.default_rng(3)
+    x = rng.normal(0.3, 2.5, (6, V)).astype(np.float32)
+    out, var = hip.logit_calibrate(torch.from_numpy(x), 1.5, return_var=True)
+    torch.cuda.synchronize()
+    ref, var64 = OS.logit_calibrate(x, 1.5)
+    var = var.cpu().numpy()
+    assert np.max(np.abs(var - var64) / var64) < 1e-12
+    got = out.cpu().numpy()
+    for b in range(6):
+        # the fp32 rounding of var decides every output bit; skip a row whose
+        # fp64 variance sits within reassociation error of a rounding midpoint
+        v32 = np.float32(var64[b])
+        mid = (float(v32) + float(np.nextafter(v32, np.float32(np.inf)))) / 2
+        if abs(var64[b] - mid) < 1e-13 * var64[b]:
+            continue
+        assert np.array_equal(got[b], ref[b]), b
+    xb = bf16_round(x)
+    outb = hip.logit_calibrate(torch.from_numpy(xb).to(torch.bfloat16), 0.7).cpu().numpy()
+    assert np.max(np.abs(outb - OS.logit_calibrate(xb, 0.7)[0])) <= 1e-6

@@ -287,6 +287,56 @@ class HipBackend(DeviceBackend):
             return dict(ids=ids, flags=flags, lse=lse)
         return ids
 
+    def sampler_sample(self, logits, uniforms, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
+                       return_all: bool = False):
+        """Sampler.sample for every row of logits (B, V) (vnx_sampler_sample):
+        temperature / top_k / top_p with the reference's semantics, one host
+        uniform per row in place of the RNG.  Returns ids (B,) int64, or with
+        return_all a dict with ids, flags, lse, kth, p_star, j_star."""
+        if temperature < 0.0:
+            raise ValueError(f"temperature must be >= 0, got {temperature}")
+        if top_k < 0:
+            raise ValueError(f"top_k must be >= 0, got {top_k}")
+        if not 0.0 < top_p <= 1.0:
+            raise ValueError(f"top_p must be in (0, 1], got {top_p}")
+        dev = self._torch_device
+        lg = self._rows2d(logits)
+        B, V = lg.shape
+        u = _to_tensor(uniforms, dev, torch.float32).reshape(-1).contiguous()
+        if u.numel() != B:
+            raise ValueError(f"uniforms must have {B} entries")
+        ids = torch.empty(B, dtype=torch.int64, device=dev)
+        extra = None
+        if return_all:
+            extra = dict(flags=torch.empty(B, dtype=torch.uint8, device=dev),
+                         lse=torch.empty(B, dtype=torch.float32, device=dev),
+                         kth=torch.empty(B, dtype=torch.float32, device=dev),
+                         p_star=torch.empty(B, dtype=torch.float32, device=dev),
+                         j_star=torch.empty(B, dtype=torch.int64, device=dev))
+        g = (lambda k: _ptr(extra[k])) if extra else (lambda k: None)
+        _lib.check(self._L.vnx_sampler_sample(
+            _ptr(lg), _LOGIT_DTYPES[lg.dtype], B, V, lg.stride(0), float(temperature), int(top_k), float(top_p),
+            _ptr(u), _ptr(ids), g("flags"), g("lse"), g("kth"), g("p_star"), g("j_star"),
+            ctypes.c_void_p(self._stream().cuda_stream)), "sampler_sample")
+        if return_all:
+            return dict(ids=ids, **extra)
+        return ids
+
+    def logit_calibrate(self, logits, calib_factor: float, eps: float = 1e-8, return_var: bool = False):
+        """CometSparkNexLM._apply_logit_calibration along the last axis
+        (vnx_logit_calibrate): logits / sqrt(var + eps) * calib_factor, fp32."""
+        t = self._logits(logits)
+        shape = t.shape
+        x2 = self._rows2d(t)
+        R, V = x2.shape
+        out = torch.empty((R, V), dtype=torch.float32, device=self._torch_device)
+        var = torch.empty(R, dtype=torch.float64, device=self._torch_device)
+        _lib.check(self._L.vnx_logit_calibrate(_ptr(x2), _LOGIT_DTYPES[x2.dtype], R, V, x2.stride(0),
+                                               float(calib_factor), float(eps), _ptr(out), V, _ptr(var),
+                                               ctypes.c_void_p(self._stream().cuda_stream)), "logit_calibrate")
+        out = out.reshape(shape)
+        return (out, var) if return_var else out
+
     # ---- weight-only quantized GEMV -------------------------------------------
     def _acts(self, x, K: int) -> torch.Tensor:
         """(..., K) activations -> contiguous (B, K) fp16 on this device."""
