@@ -155,15 +155,31 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
  * in (p descending, id ascending) order, cutoff = the first position whose
  * cumulative floor(p * 2^60) reaches floor(top_p * 2^60), at most V - 1;
  * the draw is the inverse CDF over the kept p (numpy's Generator.choice
- * rule).  One workgroup per row, no workspace.  Optional outputs (NULL to
- * skip): flags (VNX_FLAG_CDF_EDGE / LSE_EDGE), lse = RN32(row LSE), kth (the
- * top-k threshold, -inf if off), p_star / j_star (the last kept token's
- * probability and id, -1 if top_p is off).  Errors: temperature < 0 or not
- * finite, top_k < 0, top_p outside (0, 1] -> VNX_ERR_INVALID_ARG (the
- * reference's ValueError, sampler.py:54-59). */
+ * rule).  One workgroup per row, no workspace.
+ * mode (bit flags) selects the sampling step of CometSparkNexLM's
+ * _generate_with_logits (packages/verse_nex/verse_nex/cometspark.py:868-910):
+ *   VNX_SAMPLE_CALIBRATE  l -> l / sqrt(var(l) + calib_eps) * calib_factor
+ *                         first (cometspark.py:922-948, fused: two more passes
+ *                         over the row, the same arithmetic as
+ *                         vnx_logit_calibrate), greedy included;
+ *   VNX_SAMPLE_EXACT_K    argpartition(-a, k-1)[:k]: exactly k tokens, NaN
+ *                         ranked below every value, ties at the kth value
+ *                         taken by lower id (numpy leaves them open); the
+ *                         draw runs over the kept ids in id order.
+ * Optional outputs (NULL to skip): flags (VNX_FLAG_CDF_EDGE / LSE_EDGE), lse
+ * = RN32(row LSE), kth (the top-k threshold, -inf if off), p_star / j_star
+ * (the last kept token's probability and id, -1 if top_p is off), k_star (the
+ * id of the last kept tie at kth under VNX_SAMPLE_EXACT_K, else -1).  Errors:
+ * temperature < 0 or not finite, top_k < 0, top_p outside (0, 1], unknown
+ * mode bits, a calibration factor that is not finite or eps < 0 ->
+ * VNX_ERR_INVALID_ARG (the reference's ValueError, sampler.py:54-59). */
+#define VNX_SAMPLE_EXACT_K 1
+#define VNX_SAMPLE_CALIBRATE 2
+
 int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float temperature,
-                       int64_t top_k, float top_p, const float* uniforms, int64_t* out_ids, uint8_t* flags,
-                       float* lse, float* kth, float* p_star, int64_t* j_star, void* stream);
+                       int64_t top_k, float top_p, int mode, float calib_factor, float calib_eps,
+                       const float* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
+                       float* p_star, int64_t* j_star, int64_t* k_star, void* stream);
 
 /* Logit calibration of VMPC-compressed models
  * (CometSparkNexLM._apply_logit_calibration, packages/verse_nex/verse_nex/

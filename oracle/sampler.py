@@ -7,7 +7,10 @@ float32 numpy results are not reproducible bit for bit:
 1. temperature 0: numpy.argmax of the raw logits (:88-90);
 2. a = RN(l / T) in float32 (:93);
 3. top-k (0 < k < V): kth = np.partition(a, -k)[-k]; a = where(a >= kth, a,
-   -inf), so ties keep more than k and NaN drops out (:96-102);
+   -inf), so ties keep more than k and NaN drops out (:96-102).  CometSpark's
+   exactly-k rule instead keeps argpartition(-a, k-1)[:k] (packages/verse_nex/
+   verse_nex/cometspark.py:896-898): exactly k tokens, NaN ranked below every
+   value, ties at the kth value taken by lower id (numpy leaves them open);
 4. M = max(a); if M is not finite, numpy.argmax of the raw logits (:105-108);
 5. probabilities p = E(a - L32), E = the canonical exp, L32 = RN32 of the
    fp64 row log-sum-exp (the reference's exp / sum, :109-111);
@@ -19,7 +22,13 @@ float32 numpy results are not reproducible bit for bit:
    cutoff + 1 tokens are kept;
 7. the draw: numpy's Generator.choice rule on the kept probabilities with
    the given uniform (first j with C_j > u * C_V over fp64 cumulative sums,
-   :135-137; oracle/canon.c vnx_ref_icdf).
+   :135-137; oracle/canon.c vnx_ref_icdf), over token ids in increasing order
+   (CometSpark draws over argpartition's output order, which numpy does not
+   fix: the distribution is the same, the token for a given uniform is not).
+
+CometSpark's sampling step (_generate_with_logits, cometspark.py:868-910) is
+sample(..., exact_k=True, calib_factor=f): the calibration first, then
+temperature 0 -> argmax of the calibrated row, else the steps above.
 
 The logit calibration of VMPC-compressed models (packages/verse_nex/
 verse_nex/cometspark.py:922-948): logits / sqrt(var(logits) + 1e-8) *
@@ -66,13 +75,31 @@ def nucleus(p: np.ndarray, top_p: float):
     return keep, np.float32(p[j_star]), j_star, cutoff
 
 
-def probabilities(logits, temperature: float, top_k: int = 0):
+def exact_k_keep(a: np.ndarray, k: int):
+    """(keep mask, kth value, k_star) of argpartition(-a, k-1)[:k] with the
+    order fixed: value descending (NaN below every value, -0 == +0), then id
+    ascending; k_star is the id of the last kept token."""
+    a = np.asarray(a, np.float32)
+    V = a.size
+    nan = np.isnan(a)
+    neg = np.where(nan, 0.0, -a.astype(np.float64))
+    order = np.lexsort((np.arange(V), neg, nan))
+    keep = np.zeros(V, bool)
+    keep[order[:k]] = True
+    last = int(order[k - 1])
+    return keep, np.float32(a[last]), last
+
+
+def probabilities(logits, temperature: float, top_k: int = 0, exact_k: bool = False):
     """(a masked, L32, p) of steps 2-5, or None when step 4 falls back to argmax."""
     x = np.asarray(logits, np.float32)
     V = x.size
     a = rows.scale(x, temperature)
     if 0 < top_k < V:
-        a = rows.apply_threshold(a, kth_largest(a, top_k))
+        if exact_k:
+            a = np.where(exact_k_keep(a, top_k)[0], a, np.float32(-np.inf)).astype(np.float32)
+        else:
+            a = rows.apply_threshold(a, kth_largest(a, top_k))
     M = np.max(a)
     if not np.isfinite(M):
         return None
@@ -81,17 +108,24 @@ def probabilities(logits, temperature: float, top_k: int = 0):
     return a, L32, p
 
 
-def sample(logits, temperature: float, top_k: int, top_p: float, u: float):
-    """Sampler.sample restated: (token, flags, info).  info holds the kth value,
-    L32 and the nucleus (p_star, j_star) when they apply."""
+def sample(logits, temperature: float, top_k: int, top_p: float, u: float, exact_k: bool = False,
+           calib_factor=None, eps: float = 1e-8):
+    """Sampler.sample restated: (token, flags, info).  info holds the kth value
+    (and k_star under exact_k), L32 and the nucleus (p_star, j_star) when they
+    apply.  calib_factor (not None) calibrates the row first."""
     x = np.asarray(logits, np.float32).reshape(-1)
+    if calib_factor is not None:
+        x = logit_calibrate(x, calib_factor, eps)[0]
     V = x.size
     info = {}
     if temperature == 0.0:
         return int(np.argmax(x)), 0, info
     if 0 < top_k < V:
-        info["kth"] = kth_largest(rows.scale(x, temperature), top_k)
-    pr = probabilities(x, temperature, top_k)
+        if exact_k:
+            _, info["kth"], info["k_star"] = exact_k_keep(rows.scale(x, temperature), top_k)
+        else:
+            info["kth"] = kth_largest(rows.scale(x, temperature), top_k)
+    pr = probabilities(x, temperature, top_k, exact_k)
     if pr is None:
         return int(np.argmax(x)), 0, info
     a, L32, p = pr

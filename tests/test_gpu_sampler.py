@@ -22,21 +22,25 @@ def _say(*a):
     print(*a, flush=True)
 
 
-def _check(hip, x, T, top_k, top_p, u, dtype=torch.float32):
+def _check(hip, x, T, top_k, top_p, u, dtype=torch.float32, exact_k=False, calib_factor=None):
     """x (B, V) float32 host rows (already representable in dtype)."""
     B = x.shape[0]
-    res = hip.sampler_sample(torch.from_numpy(x).to(dtype), torch.from_numpy(u), T, top_k, top_p, return_all=True)
+    res = hip.sampler_sample(torch.from_numpy(x).to(dtype), torch.from_numpy(u), T, top_k, top_p, return_all=True,
+                             exact_k=exact_k, calib_factor=calib_factor)
     torch.cuda.synchronize()
     ids = res["ids"].cpu().numpy()
     flags = res["flags"].cpu().numpy()
     kth = res["kth"].cpu().numpy()
     ps = res["p_star"].cpu().numpy()
     js = res["j_star"].cpu().numpy()
+    ks = res["k_star"].cpu().numpy()
     bad = 0
     for b in range(B):
-        ref, rflags, info = OS.sample(x[b], T, top_k, top_p, u[b])
+        ref, rflags, info = OS.sample(x[b], T, top_k, top_p, u[b], exact_k=exact_k, calib_factor=calib_factor)
         if "kth" in info:
             assert (np.isnan(kth[b]) and np.isnan(info["kth"])) or kth[b] == info["kth"], (b, kth[b], info["kth"])
+        if "k_star" in info:
+            assert ks[b] == info["k_star"], (b, ks[b], info["k_star"])
         lse_edge = flags[b] & _lib.FLAG_LSE_EDGE
         if "p_star" in info and not (ps[b] == info["p_star"] and js[b] == info["j_star"]):
             # a flagged LSE may round to the neighbouring float32 and shift every p by an ulp
@@ -136,3 +140,68 @@ def test_logit_calibration_matches_oracle(hip):
     xb = bf16_round(x)
     outb = hip.logit_calibrate(torch.from_numpy(xb).to(torch.bfloat16), 0.7).cpu().numpy()
     assert np.max(np.abs(outb - OS.logit_calibrate(xb, 0.7)[0])) <= 1e-6
+
+
+@pytest.mark.parametrize("k", [1, 64, 1000, 50000])
+def test_exact_k_matches_oracle(hip, k):
+    """CometSpark's exactly-k top-k: kth value, the last kept tie k*, the token."""
+    rng = np.random.default_rng(20 + k)
+    B = 6
+    x = rng.normal(0, 2.0, (B, V)).astype(np.float32)
+    x[1] = (np.round(x[1] * 2) / 2).astype(np.float32)  # heavy ties, -0 and +0 among them
+    x[2, rng.integers(0, V, 9)] = np.nan
+    u = rng.random(B).astype(np.float32)
+    ids, flags, bad = _check(hip, x, 0.9, k, 1.0, u, exact_k=True)
+    _say(f"exact k={k}: ids {ids.tolist()} flagged {int((flags != 0).sum())}, differing {bad}")
+    assert bad <= 1
+
+
+def test_exact_k_with_ties_split_at_the_kth_value(hip):
+    """Values on a grid of 1/4: k falls inside a run of ties, so k* decides
+    which of them are kept; bf16 rows too."""
+    rng = np.random.default_rng(31)
+    B = 4
+    x = (np.round(rng.normal(0, 1.5, (B, V)) * 4) / 4).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    for k in (7, 333, 4096):
+        _check(hip, x, 1.0, k, 1.0, u, exact_k=True)
+    xb = bf16_round(rng.normal(0, 2.0, (B, V)).astype(np.float32))
+    _check(hip, xb, 0.7, 100, 1.0, u, dtype=torch.bfloat16, exact_k=True)
+
+
+def test_fused_calibration_matches_oracle(hip):
+    """VNX_SAMPLE_CALIBRATE: the CometSpark step (calibrate, then greedy or
+    exactly-k sampling) and the Sampler rules on calibrated rows."""
+    rng = np.random.default_rng(41)
+    B = 8
+    x = rng.normal(0.4, 3.0, (B, V)).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    ids, _, _ = _check(hip, x, 0.0, 0, 1.0, u, calib_factor=1.7)
+    assert ids.tolist() == [int(np.argmax(OS.logit_calibrate(x[b], 1.7)[0])) for b in range(B)]
+    for (T, k, p, ex) in ((0.8, 50, 1.0, True), (1.0, 0, 0.9, False), (0.7, 64, 0.95, False)):
+        ids, flags, bad = _check(hip, x, T, k, p, u, exact_k=ex, calib_factor=1.7)
+        assert bad <= 1, (T, k, p, ex)
+    xb = bf16_round(x)
+    ids, flags, bad = _check(hip, xb, 0.9, 200, 1.0, u, dtype=torch.bfloat16, exact_k=True, calib_factor=0.6)
+    assert bad <= 1
+
+
+def test_cometspark_sample_step(hip):
+    """cometspark_sample: greedy with calibration, and exactly-k draws with
+    host uniforms, against the oracle's CometSpark step."""
+    from versenext_amd.sampler import cometspark_sample
+    rng = np.random.default_rng(51)
+    x = rng.normal(0, 2.5, (4, V)).astype(np.float32)
+    xt = torch.from_numpy(x)
+    g = cometspark_sample(hip, xt, 0.0, 40, calib_factor=1.2).cpu().numpy()
+    assert g.tolist() == [OS.sample(x[b], 0.0, 0, 1.0, 0.0, calib_factor=1.2)[0] for b in range(4)]
+    u = rng.random(4).astype(np.float32)
+    t = cometspark_sample(hip, xt, 0.85, 30, calib_factor=1.2, uniforms=u).cpu().numpy()
+    for b in range(4):
+        ref, fl, _ = OS.sample(x[b], 0.85, 30, 1.0, u[b], exact_k=True, calib_factor=1.2)
+        assert t[b] == ref or fl, b
+    # the reference's top_k=None means no top-k
+    t2 = cometspark_sample(hip, xt, 0.85, None, uniforms=u).cpu().numpy()
+    for b in range(4):
+        ref, fl, _ = OS.sample(x[b], 0.85, 0, 1.0, u[b])
+        assert t2[b] == ref or fl, b

@@ -129,3 +129,65 @@ def test_logit_calibration_matches_the_reference_formula():
     ref = x / np.sqrt(np.var(x, axis=-1, keepdims=True) + 1e-8) * 1.7  # cometspark.py:946-948, float32 numpy
     assert np.max(np.abs(out - ref) / np.abs(ref)) < 2e-6
     assert np.allclose(np.std(out.astype(np.float64), axis=-1), 1.7, rtol=1e-5)
+
+
+def test_exact_k_is_numpy_argpartition_set():
+    """Distinct values (with NaN present): the kept set equals
+    argpartition(-a, k-1)[:k] (cometspark.py:896-898), NaN never kept while k
+    non-NaN values exist."""
+    rng = np.random.default_rng(12)
+    for k in (1, 5, 64, 300, 999):
+        a = rng.normal(0, 2, 3000).astype(np.float32)
+        a[rng.integers(0, 3000, 7)] = np.nan
+        keep, kth, kstar = OS.exact_k_keep(a, k)
+        ref = np.zeros(a.size, bool)
+        ref[np.argpartition(-a, kth=k - 1)[:k]] = True
+        assert np.array_equal(keep, ref), k
+        assert keep.sum() == k and not np.isnan(a[keep]).any()
+        assert kth == np.min(a[keep]) and a[kstar] == kth
+
+
+def test_exact_k_ties_go_by_lower_id():
+    rng = np.random.default_rng(13)
+    for trial in range(30):
+        a = (rng.integers(-6, 6, 800) / 2).astype(np.float32)
+        a[a == 0] = np.float32(-0.0) if trial % 2 else np.float32(0.0)  # -0 and +0 tie
+        k = int(rng.integers(1, 800))
+        keep, kth, kstar = OS.exact_k_keep(a, k)
+        assert keep.sum() == k
+        # every kept token outranks every dropped one by (value desc, id asc)
+        kept, dropped = np.flatnonzero(keep), np.flatnonzero(~keep)
+        assert np.all((a[kept] > kth) | ((a[kept] == kth) & (kept <= kstar)))
+        assert np.all((a[dropped] < kth) | ((a[dropped] == kth) & (dropped > kstar)))
+        # a planted tie rule that takes the highest ids breaks the property whenever ties are split
+        ties = np.flatnonzero(a == kth)
+        need = k - int(np.sum(a > kth))
+        if 0 < need < ties.size:
+            bad = (a > kth)
+            bad[ties[-need:]] = True
+            assert not np.array_equal(bad, keep)
+
+
+def test_cometspark_step_calibrates_then_draws_exactly_k():
+    """sample(exact_k=True, calib_factor=f): greedy is the argmax of the
+    calibrated row; the draw is Generator.choice over the softmax of the k kept
+    values (cometspark.py:896-904), the kept ids in increasing order."""
+    rng = np.random.default_rng(14)
+    agree = 0
+    for seed in range(20):
+        x = rng.normal(0, 3, 2000).astype(np.float32)
+        f = 1.3
+        xc = OS.logit_calibrate(x, f)[0]
+        assert OS.sample(x, 0.0, 40, 1.0, 0.5, exact_k=True, calib_factor=f)[0] == int(np.argmax(xc))
+        u = np.random.default_rng(seed).random()
+        tok, flags, info = OS.sample(x, 0.8, 40, 1.0, np.float32(u), exact_k=True, calib_factor=f)
+        a = (xc / np.float32(0.8)).astype(np.float64)
+        idx = np.sort(np.argpartition(-a, 39)[:40])
+        q = np.exp(a[idx] - a[idx].max())
+        q /= q.sum()
+        ref = idx[np.random.default_rng(seed).choice(40, p=q)]
+        if flags == 0 and abs(float(np.float32(u)) - u) < 1e-7:
+            agree += tok == ref
+            assert tok == ref, (seed, tok, ref)
+        assert info["k_star"] in idx
+    assert agree >= 15

@@ -4,11 +4,18 @@
 //
 // k_sampler: one workgroup of kST threads per row, every step of the
 // reference in one launch, nothing outside LDS:
-//   T == 0      numpy.argmax of the raw row;
+//   calibrate   (CometSpark mode) l = RN(RN(l / s) * f), s = RN(sqrt(RN32(var)
+//               + eps)) with var the fp64 population variance of the row
+//               (cometspark.py:922-948), two extra passes;
+//   T == 0      numpy.argmax of the row;
 //   a = RN(l/T) (the exact scaling of vnx_common.h);
-//   top-k       kth = the kth largest a (numpy.partition order, NaN largest)
-//               by a radix select over order-preserving 32-bit keys, four
-//               8-bit digits, per-wave LDS histograms; a = a >= kth ? a : -inf;
+//   top-k       kth = the kth largest a by a radix select over order-preserving
+//               32-bit keys, four 8-bit digits, per-wave LDS histograms.
+//               Sampler rule (sampler.py:96-102): NaN ranks largest
+//               (numpy.partition) and a = a >= kth ? a : -inf keeps every tie.
+//               Exactly-k rule (cometspark.py:896-904, argpartition(-a)[:k]):
+//               NaN ranks smallest and the ties at kth are taken by lower id
+//               until k are kept (a rank pass finds the last one, k*);
 //   softmax     M = max a (not finite -> numpy.argmax of the raw row), the row
 //               LSE in fp64, L32 = RN32(LSE), p = vnx_exp_canon(a - L32);
 //   top-p       the nucleus on p ordered by (p descending, id ascending), with
@@ -22,7 +29,9 @@
 //               order (first j with C_j > u * C_V, fp64 sums): sub-block
 //               masses in LDS, a thread-order scan to the sub-block, one wave
 //               rescans it.
-// The CPU checker oracle/sampler.py restates the same rules.
+// The CPU checker oracle/sampler.py restates the same rules.  The exactly-k
+// draw runs over the kept tokens in id order: argpartition's output order,
+// which the reference draws over, is implementation-defined.
 #include <algorithm>
 
 #include "rowred.h"
@@ -43,6 +52,9 @@ struct SamplerParams {
   TScale sc;
   int greedy;
   int64_t top_k;           // 0: off
+  int exact_k;             // CometSpark's exactly-k rule
+  int calib;               // fused logit calibration
+  float cf, ceps;          // calibration factor and eps
   int use_p;               // top_p < 1
   uint64_t p_target;       // floor(top_p * 2^60)
   const float* u;
@@ -52,6 +64,7 @@ struct SamplerParams {
   float* kth;
   float* p_star;
   int64_t* j_star;
+  int64_t* k_star;
 };
 
 struct SamplerLds {
@@ -75,6 +88,7 @@ struct SamplerLds {
   uint32_t prefix, pmask;
   unsigned long long rem;
   int64_t jstar;
+  unsigned long long rank;
   double total, target, base;
   int64_t sb;
   int tstar, tlast;
@@ -89,8 +103,12 @@ __device__ __forceinline__ uint32_t okey(float a) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The exactly-k order (argpartition of -a): NaN below every value, -0 and +0
+// one value (a + 0 turns -0 into +0), so equal values tie and go by id.
+__device__ __forceinline__ uint32_t okey_lo(float a) { return __builtin_isnan(a) ? 0u : okey(a + 0.0f); }
+
 __device__ __forceinline__ float okey_value(uint32_t k) {
-  if (k == 0xFFFFFFFFu) return __builtin_nanf("");
+  if (k == 0xFFFFFFFFu || k == 0u) return __builtin_nanf("");
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
   return __uint_as_float(u);
 }
@@ -153,12 +171,6 @@ __device__ __forceinline__ void seg_visit(const Tin* row, int64_t j0, int64_t j1
   for (int64_t j = j0 + nv * VE; j < j1; ++j) f(j, Vec<Tin>::load1(row + j));
 }
 
-template <typename Tin, int SM>
-__device__ __forceinline__ float masked_scaled(float raw, const SamplerParams& p, bool use_thr, float thr) {
-  const float a = tscale<SM>(raw, p.sc);
-  return use_thr ? (a >= thr ? a : kNegInf) : a;
-}
-
 __device__ __forceinline__ void hist_clear(SamplerLds& L) {
   __syncthreads();
   for (int i = threadIdx.x; i < kHist * kBins; i += kST) {
@@ -186,16 +198,59 @@ __device__ __forceinline__ void hist_merge(SamplerLds& L) {
   __syncthreads();
 }
 
-// numpy.argmax of the raw row (NaN first, then the lowest index of the max).
-template <typename Tin>
-__device__ int64_t row_argmax(const Tin* row, int64_t V, SamplerLds& L) {
+// numpy.argmax of the row g(l) (NaN first, then the lowest index of the max).
+template <typename Tin, typename G>
+__device__ __forceinline__ int64_t row_argmax(const Tin* row, int64_t V, SamplerLds& L, G&& g) {
   float bv = kNegInf;
   int64_t bi = INT64_MAX;
   for_row<Tin>(row, V, [&](int64_t j, float x) {
-    if (bi == INT64_MAX || argmax_better(x, j, bv, bi)) { bv = x; bi = j; }
+    const float v = g(x);
+    if (bi == INT64_MAX || argmax_better(v, j, bv, bi)) { bv = v; bi = j; }
   });
   block_argmax<kST>(bv, bi, L.f, L.i);
   return bi == INT64_MAX ? 0 : bi;
+}
+
+// The id of the m-th element (1-based, id order) of the row for which
+// pred(j, raw) holds, -1 if there are fewer.  Thread t owns the contiguous
+// range [t*seg, (t+1)*seg) (seg a multiple of the vector width): counts, a
+// scan in thread order, then the owner of the m-th match walks its range.
+template <typename Tin, typename P>
+__device__ __forceinline__ int64_t nth_match(const Tin* row, int64_t V, unsigned long long m, SamplerLds& L, P&& pred) {
+  constexpr int VE = Vec<Tin>::N;
+  const int tid = threadIdx.x;
+  const int64_t seg = ((V + kST - 1) / kST + VE - 1) / VE * VE;
+  const int64_t j0 = min((int64_t)tid * seg, V), j1 = min(j0 + seg, V);
+  unsigned long long c = 0;
+  seg_visit<Tin>(row, j0, j1, [&](int64_t j, float x) { c += pred(j, x) ? 1ull : 0ull; });
+  __syncthreads();
+  L.u.d.seg[tid] = c;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long run = 0;
+    int owner = -1;
+    for (int t = 0; t < kST; ++t) {
+      if (run + L.u.d.seg[t] >= m) { owner = t; break; }
+      run += L.u.d.seg[t];
+    }
+    L.tstar = owner;
+    L.rank = m - run;  // rank of the match inside the owner's range
+    L.jstar = -1;
+  }
+  __syncthreads();
+  if (tid == L.tstar) {
+    const unsigned long long want = L.rank;
+    unsigned long long r = 0;
+    int64_t found = -1;
+    seg_visit<Tin>(row, j0, j1, [&](int64_t j, float x) {
+      if (found < 0 && pred(j, x) && ++r == want) found = j;
+    });
+    L.jstar = found;
+  }
+  __syncthreads();
+  const int64_t res = L.jstar;
+  __syncthreads();
+  return res;
 }
 
 template <typename Tin, int SM>
@@ -208,24 +263,46 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
   const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
   const Tin* row = static_cast<const Tin*>(p.x) + b * p.ld;
   const int64_t V = p.V;
-  uint8_t fl = 0;
+  int fl = 0;
+  int64_t kstar = -1;
   auto finish = [&](int64_t token, float lse, float kth, float ps, int64_t js) {
     if (tid == 0) {
       p.out[b] = token;
-      if (p.flags) p.flags[b] = fl;
+      if (p.flags) p.flags[b] = (uint8_t)fl;
       if (p.lse) p.lse[b] = lse;
       if (p.kth) p.kth[b] = kth;
       if (p.p_star) p.p_star[b] = ps;
       if (p.j_star) p.j_star[b] = js;
+      if (p.k_star) p.k_star[b] = kstar;
     }
   };
+  // ---- calibration: s = sqrt(RN32(var) + eps), l -> RN(RN(l / s) * f) ----
+  float sd = 1.0f;
+  if (p.calib) {
+    double s1 = 0.0;
+    for_row<Tin>(row, V, [&](int64_t, float x) { s1 += (double)x; });
+    const double mean = block_sum<kST>(s1, L.dd) / (double)V;
+    double s2 = 0.0;
+    for_row<Tin>(row, V, [&](int64_t, float x) {
+      const double d = (double)x - mean;
+      s2 += d * d;
+    });
+    const double var = block_sum<kST>(s2, L.dd) / (double)V;
+    sd = sqrtf((float)var + p.ceps);
+  }
+  // small lambdas capture by value so every closure stays in registers
+  auto val = [calib = p.calib != 0, sd, cf = p.cf](float x) -> float { return calib ? (x / sd) * cf : x; };
   if (p.greedy) {
-    finish(row_argmax<Tin>(row, V, L), __builtin_nanf(""), kNegInf, -1.0f, -1);
+    finish(row_argmax<Tin>(row, V, L, val), __builtin_nanf(""), kNegInf, -1.0f, -1);
     return;
   }
+  auto scaled = [val, sc = p.sc](float x) -> float { return tscale<SM>(val(x), sc); };
+  const bool exact = p.exact_k != 0;
+  auto key = [exact](float a) -> uint32_t { return exact ? okey_lo(a) : okey(a); };
   // ---- top-k: radix select of the kth largest scaled value ----
   const bool use_thr = p.top_k > 0 && p.top_k < V;
   float thr = kNegInf;
+  uint32_t tkey = 0u;
   if (use_thr) {
     if (tid == 0) { L.prefix = 0u; L.pmask = 0u; L.rem = (unsigned long long)p.top_k; }
     for (int pass = 0; pass < 4; ++pass) {
@@ -233,7 +310,7 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
       const int shift = 24 - 8 * pass;
       const uint32_t prefix = L.prefix, pmask = L.pmask;
       for_row<Tin>(row, V, [&](int64_t, float x) {
-        const uint32_t k = okey(tscale<SM>(x, p.sc));
+        const uint32_t k = key(scaled(x));
         if ((k & pmask) == prefix) atomicAdd(&L.u.h.cnt[wave % kHist][(k >> shift) & 0xFFu], 1u);
       });
       hist_merge(L);
@@ -250,13 +327,27 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
       }
       __syncthreads();
     }
-    thr = okey_value(L.prefix);
+    tkey = L.prefix;
+    thr = okey_value(tkey);
+    if (exact) {
+      // L.rem ties at the kth key complete the k: the last kept one is the
+      // L.rem-th tie in id order
+      const unsigned long long m = L.rem;
+      kstar = nth_match<Tin>(row, V, m, L, [key, scaled, tkey](int64_t, float x) { return key(scaled(x)) == tkey; });
+    }
   }
+  auto masked = [scaled, key, use_thr, exact, thr, tkey, kstar](int64_t j, float x) -> float {
+    const float a = scaled(x);
+    if (!use_thr) return a;
+    if (!exact) return a >= thr ? a : kNegInf;
+    const uint32_t k = key(a);
+    return (k > tkey || (k == tkey && j <= kstar)) ? a : kNegInf;
+  };
   // ---- softmax: max, row LSE (fp64), L32 ----
   float M = kNegInf;
   bool nan = false;
-  for_row<Tin>(row, V, [&](int64_t, float x) {
-    const float a = masked_scaled<Tin, SM>(x, p, use_thr, thr);
+  for_row<Tin>(row, V, [&](int64_t j, float x) {
+    const float a = masked(j, x);
     nan |= __builtin_isnan(a);
     M = fmaxf(M, a);
   });
@@ -264,15 +355,15 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
     const float bm = block_max<kST>(nan ? kPosInf : M, L.f);
     M = bm;
   }
-  if (!(M > kNegInf && M < kPosInf)) {  // np.max not finite: numpy.argmax of the raw row
+  if (!(M > kNegInf && M < kPosInf)) {  // np.max not finite: numpy.argmax of the row
     __syncthreads();
-    finish(row_argmax<Tin>(row, V, L), __builtin_nanf(""), thr, -1.0f, -1);
+    finish(row_argmax<Tin>(row, V, L, val), __builtin_nanf(""), thr, -1.0f, -1);
     return;
   }
   const float mt = mt_of(M);
   double s = 0.0;
-  for_row<Tin>(row, V, [&](int64_t, float x) {
-    const float a = masked_scaled<Tin, SM>(x, p, use_thr, thr);
+  for_row<Tin>(row, V, [&](int64_t j, float x) {
+    const float a = masked(j, x);
     if (a > kNegInf) s += (double)exp2_term(a, mt);
   });
   s = block_sum<kST>(s, L.dd);
@@ -283,10 +374,7 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
     const double mu = 0.5 * ((double)L32 + up), md = 0.5 * ((double)L32 + dn);
     if (fabs(Lr - mu) < 1e-7 || fabs(Lr - md) < 1e-7) fl |= VNX_FLAG_LSE_EDGE;
   }
-  auto prob = [&](float x) -> float {
-    const float a = masked_scaled<Tin, SM>(x, p, use_thr, thr);
-    return vnx_exp_canon(a - L32);
-  };
+  auto prob = [masked, L32](int64_t j, float x) -> float { return vnx_exp_canon(masked(j, x) - L32); };
   // ---- top-p: nucleus value p*, tie count, j* ----
   float pstar = -1.0f;
   int64_t jstar = -1;
@@ -296,8 +384,8 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
       hist_clear(L);
       const int shift = 24 - 8 * pass;
       const uint32_t prefix = L.prefix, pmask = L.pmask;
-      for_row<Tin>(row, V, [&](int64_t, float x) {
-        const float pp = prob(x);
+      for_row<Tin>(row, V, [&](int64_t j, float x) {
+        const float pp = prob(j, x);
         const uint32_t k = __float_as_uint(pp);
         if ((k & pmask) == prefix) {
           const int d = (k >> shift) & 0xFFu;
@@ -329,42 +417,12 @@ __global__ __launch_bounds__(kST) void k_sampler(SamplerParams p) {
       // m = the smallest number of ties whose fixed-point mass reaches rem
       const unsigned long long P = fix60(pstar);  // > 0: a zero-mass bin is never chosen
       const unsigned long long m = (L.rem + P - 1) / P;
-      // rank pass in id order: thread t owns the contiguous range
-      // [t*seg, (t+1)*seg) (seg a multiple of the vector width); counts,
-      // then a scan in thread order, then the owner finds the tie
-      const int64_t seg = ((V + kST - 1) / kST + VE - 1) / VE * VE;
-      const int64_t j0 = min((int64_t)tid * seg, V), j1 = min(j0 + seg, V);
-      unsigned long long c = 0;
-      seg_visit<Tin>(row, j0, j1, [&](int64_t, float x) { c += (prob(x) == pstar) ? 1ull : 0ull; });
-      L.u.d.seg[tid] = c;
-      __syncthreads();
-      if (tid == 0) {
-        unsigned long long run = 0;
-        int owner = -1;
-        for (int t = 0; t < kST; ++t) {
-          if (run + L.u.d.seg[t] >= m) { owner = t; break; }
-          run += L.u.d.seg[t];
-        }
-        L.tstar = owner;
-        L.rem = m - run;  // rank of the tie inside the owner's range
-        L.jstar = -1;
-      }
-      __syncthreads();
-      if (tid == L.tstar) {
-        unsigned long long r = 0;
-        int64_t found = -1;
-        seg_visit<Tin>(row, j0, j1, [&](int64_t j, float x) {
-          if (found < 0 && prob(x) == pstar && ++r == L.rem) found = j;
-        });
-        L.jstar = found;
-      }
-      __syncthreads();
-      jstar = L.jstar;
+      jstar = nth_match<Tin>(row, V, m, L, [prob, pstar](int64_t j, float x) { return prob(j, x) == pstar; });
     }
     __syncthreads();
   }
-  auto weight = [&](int64_t j, float x) -> float {
-    const float pp = prob(x);
+  auto weight = [prob, pstar, jstar](int64_t j, float x) -> float {
+    const float pp = prob(j, x);
     if (pstar >= 0.0f && !(pp > pstar || (pp == pstar && j <= jstar))) return 0.0f;
     return pp;
   };
@@ -537,10 +595,14 @@ using namespace vnx;
 extern "C" {
 
 int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float temperature,
-                       int64_t top_k, float top_p, const float* uniforms, int64_t* out_ids, uint8_t* flags,
-                       float* lse, float* kth, float* p_star, int64_t* j_star, void* stream) {
+                       int64_t top_k, float top_p, int mode, float calib_factor, float calib_eps,
+                       const float* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
+                       float* p_star, int64_t* j_star, int64_t* k_star, void* stream) {
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
   if (B < 0 || V <= 0 || top_k < 0) return VNX_ERR_INVALID_ARG;
+  if (mode & ~(VNX_SAMPLE_EXACT_K | VNX_SAMPLE_CALIBRATE)) return VNX_ERR_INVALID_ARG;
+  if ((mode & VNX_SAMPLE_CALIBRATE) && (!__builtin_isfinite(calib_factor) || !(calib_eps >= 0.0f)))
+    return VNX_ERR_INVALID_ARG;
   if (!(temperature >= 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
   if (!(top_p > 0.0f && top_p <= 1.0f)) return VNX_ERR_INVALID_ARG;
   if (B == 0) return VNX_OK;
@@ -554,9 +616,14 @@ int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int6
   p.greedy = temperature == 0.0f;
   const int sm = p.greedy ? SM_ID : make_scale(temperature, &p.sc);
   p.top_k = top_k;
+  p.exact_k = (mode & VNX_SAMPLE_EXACT_K) != 0;
+  p.calib = (mode & VNX_SAMPLE_CALIBRATE) != 0;
+  p.cf = calib_factor;
+  p.ceps = calib_eps;
   p.use_p = top_p < 1.0f;
   p.p_target = (uint64_t)floor((double)top_p * 1152921504606846976.0);
   p.u = uniforms; p.out = out_ids; p.flags = flags; p.lse = lse; p.kth = kth; p.p_star = p_star; p.j_star = j_star;
+  p.k_star = k_star;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const size_t lds = (size_t)nsb * sizeof(double);
   return dispatch_tsm(dtype, sm, false, [&](auto tin, auto smc, auto) {

@@ -288,17 +288,21 @@ class HipBackend(DeviceBackend):
         return ids
 
     def sampler_sample(self, logits, uniforms, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0,
-                       return_all: bool = False):
+                       return_all: bool = False, exact_k: bool = False, calib_factor=None, calib_eps: float = 1e-8):
         """Sampler.sample for every row of logits (B, V) (vnx_sampler_sample):
         temperature / top_k / top_p with the reference's semantics, one host
-        uniform per row in place of the RNG.  Returns ids (B,) int64, or with
-        return_all a dict with ids, flags, lse, kth, p_star, j_star."""
+        uniform per row in place of the RNG.  exact_k takes CometSpark's
+        exactly-k top-k (argpartition, ties by lower id); calib_factor (not
+        None) first applies its logit calibration with eps calib_eps.  Returns
+        ids (B,) int64, or with return_all a dict with ids, flags, lse, kth,
+        p_star, j_star, k_star."""
         if temperature < 0.0:
             raise ValueError(f"temperature must be >= 0, got {temperature}")
         if top_k < 0:
             raise ValueError(f"top_k must be >= 0, got {top_k}")
         if not 0.0 < top_p <= 1.0:
             raise ValueError(f"top_p must be in (0, 1], got {top_p}")
+        mode = (_lib.SAMPLE_EXACT_K if exact_k else 0) | (_lib.SAMPLE_CALIBRATE if calib_factor is not None else 0)
         dev = self._torch_device
         lg = self._rows2d(logits)
         B, V = lg.shape
@@ -312,11 +316,13 @@ class HipBackend(DeviceBackend):
                          lse=torch.empty(B, dtype=torch.float32, device=dev),
                          kth=torch.empty(B, dtype=torch.float32, device=dev),
                          p_star=torch.empty(B, dtype=torch.float32, device=dev),
-                         j_star=torch.empty(B, dtype=torch.int64, device=dev))
+                         j_star=torch.empty(B, dtype=torch.int64, device=dev),
+                         k_star=torch.empty(B, dtype=torch.int64, device=dev))
         g = (lambda k: _ptr(extra[k])) if extra else (lambda k: None)
         _lib.check(self._L.vnx_sampler_sample(
             _ptr(lg), _LOGIT_DTYPES[lg.dtype], B, V, lg.stride(0), float(temperature), int(top_k), float(top_p),
-            _ptr(u), _ptr(ids), g("flags"), g("lse"), g("kth"), g("p_star"), g("j_star"),
+            mode, float(calib_factor if calib_factor is not None else 1.0), float(calib_eps),
+            _ptr(u), _ptr(ids), g("flags"), g("lse"), g("kth"), g("p_star"), g("j_star"), g("k_star"),
             ctypes.c_void_p(self._stream().cuda_stream)), "sampler_sample")
         if return_all:
             return dict(ids=ids, **extra)

@@ -54,8 +54,10 @@ class Sampler:
         return int(ids.cpu()[0])
 
     def greedy(self, logits) -> int:
-        """argmax of the logits."""
-        return int(np.argmax(np.asarray(logits).flatten()))
+        """argmax of the logits (numpy.argmax order), on the device."""
+        x = np.asarray(logits, dtype=np.float32).reshape(1, -1) if not hasattr(logits, "device") else logits
+        ids = self._hip().sampler_sample(x.reshape(1, -1), np.zeros(1, np.float32), 0.0)
+        return int(ids.cpu()[0])
 
     def __repr__(self) -> str:
         return (f"Sampler(temperature={self.temperature}, top_k={self.top_k}, "
@@ -72,4 +74,26 @@ class GreedySampler(Sampler):
         return self.greedy(logits)
 
 
-__all__ = ["Sampler", "GreedySampler"]
+def cometspark_sample(hip, logits, temperature: float, top_k: Optional[int] = None, calib_factor=None,
+                      uniforms=None, rng=None):
+    """The per-step sampling of CometSparkNexLM._generate_with_logits
+    (packages/verse_nex/verse_nex/cometspark.py:886-910) for logits (B, V), in
+    one vnx_sampler_sample launch: the logit calibration when calib_factor is
+    not None (a VMPC-compressed model, :922-948), temperature <= 0 -> argmax,
+    else logits / max(temperature, 1e-8), top_k > 0 -> exactly min(top_k, V)
+    tokens (argpartition, ties by lower id), softmax, one draw per row with
+    uniforms[b] (drawn from rng, default numpy.random.default_rng(), when
+    None).  Returns the (B,) int64 token ids on the device."""
+    x = logits
+    B = x.shape[0]
+    T = float(temperature)
+    k = int(top_k) if top_k else 0
+    if T <= 0:
+        u = np.zeros(B, np.float32)
+        return hip.sampler_sample(x, u, 0.0, calib_factor=calib_factor)
+    if uniforms is None:
+        uniforms = (rng if rng is not None else np.random.default_rng()).random(B).astype(np.float32)
+    return hip.sampler_sample(x, uniforms, max(T, 1e-8), k, 1.0, exact_k=True, calib_factor=calib_factor)
+
+
+__all__ = ["Sampler", "GreedySampler", "cometspark_sample"]
