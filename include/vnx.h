@@ -419,9 +419,39 @@ typedef struct vnx_tree_attn_args {
   int64_t table_rows;
   int rope;
   int64_t cap;
+  /* TriSparse's sliding window and ALiBi paths (tri_sparse_attn.py:258-378,
+   * :489-530).  Positions: node i of batch row b sits at tp_b + depth(i)
+   * (depth = its ancestor count, 0 for a root; a chain's row i at tp_b + i),
+   * prefix row j at j, tree row j at tp_b + depth(j).
+   * window > 0: the prefix + tree attention keeps only keys with
+   *   pos(i) - pos(key) < window (needs window >= N, else
+   *   VNX_ERR_UNSUPPORTED: the tree keys then always fall inside it).
+   * alibi_slopes (device array of H fp32, e.g. m_h = 2^(-h/H), h = 1..H) not
+   *   NULL: a third softmax over the same prefix + tree keys, no window, with
+   *   scores + -m_h * (pos(i) - pos(key)), added as gates[2] * it for batch
+   *   rows with tp_b + N <= alibi_max_keys (the reference's T_k <= 1024 rule,
+   *   :600-607); gates then holds 3 fp32 (gates[1] unused without a second
+   *   segment) and out = gates[0] * path A + gates[1] * path B + gates[2] *
+   *   path C.
+   * Zero (the zero-initialised default): no window, no ALiBi. */
+  int window;
+  const float* alibi_slopes;
+  int alibi_max_keys;
+  /* Tuning: force_splits >= 1 fixes the key splits, force_waves (4, 5 = 4
+   * with prefetch, 8, 16) the workgroup shape where the query tile fits;
+   * 0: the launch plan's choice.  (Size the workspace with
+   * vnx_tree_attn_workspace_args when forcing splits.) */
+  int force_splits;
+  int force_waves;
 } vnx_tree_attn_args;
 
+/* Workspace bytes of the automatic plan without a window (an upper bound for
+ * any window and for ALiBi). */
 size_t vnx_tree_attn_workspace(int B, int H, int Hkv, int N, int Tp, int d);
+
+/* Workspace bytes of exactly this call (forced splits, window, ALiBi
+ * included); 256 for invalid arguments. */
+size_t vnx_tree_attn_workspace_args(const vnx_tree_attn_args* args);
 
 int vnx_tree_attn(const vnx_tree_attn_args* args, void* workspace, size_t workspace_bytes,
                   void* stream);

@@ -12,8 +12,10 @@ reference's verifier calls the model (speculative.py:202-213):
 - TriSparseAttention.forward (packages/verse_nex/verse_nex/tri_sparse_attn.py
   :536-613): projections, RoPE (:167-221), repeat_kv adjacent copies,
   sliding-window path (:260-400; written here as one masked softmax over the
-  window, which the chunked form equals), global path (:469-495), ALiBi path
-  when use_alibi and T <= 1024 (:501-534), sigmoid gates (:585-608);
+  window, which the chunked form equals: tests/test_oracle_swa_replay.py
+  replays the reference's parallel-vs-serial cases against it), global path
+  (:469-495), ALiBi path when use_alibi and T <= 1024 (:501-534), sigmoid
+  gates (:585-608);
 - SwiGLUMLP (vnnn.py:779-807); MoDLayer / DensePart / Router / Expert
   (packages/verse_nex/verse_nex/mod.py:142-213, :337-440, :466-803):
   argsort(-logits)[:k] selection, softmax over the selected logits.
@@ -76,6 +78,42 @@ def _attend(q, k, v, bias):
     return _softmax(s) @ v
 
 
+def alibi_slopes(H):
+    """m_h = 1 / 2^(h / H), h = 1..H (tri_sparse_attn.py:151-155)."""
+    return (1.0 / (2.0 ** (np.arange(1, H + 1, dtype=F32) / H))).astype(F32)
+
+
+def swa_attention(q, k, v, window, offset=0):
+    """Path A (tri_sparse_attn.py:258-448) as one masked softmax: queries at
+    positions offset + i, keys at 0 .. Tk-1, key j visible iff j <= pos and
+    pos - j < window; masked scores get -1e9.  (B, H, Tq, d)."""
+    Tq, Tk = q.shape[2], k.shape[2]
+    i = np.arange(Tq)[:, None] + offset
+    j = np.arange(Tk)[None, :]
+    ok = (j <= i) & ((i - j) < window)
+    return _attend(q, k, v, np.where(ok, F32(0.0), F32(-1e9)).astype(F32)[None, None])
+
+
+def alibi_attention(q, k, v, slopes, offset=0):
+    """Path C (tri_sparse_attn.py:501-534): causal, bias -m_h * (pos - j)."""
+    Tq, Tk = q.shape[2], k.shape[2]
+    i = np.arange(Tq)[:, None] + offset
+    j = np.arange(Tk)[None, :]
+    dist = (i - j).astype(F32)
+    bias = np.where((j <= i)[None], -slopes[:, None, None] * dist[None], F32(-1e9)).astype(F32)
+    return _attend(q, k, v, bias[None])
+
+
+def trisparse_heads(q, k, v, kg, vg, gate, cfg, offset=0):
+    """The gated paths before the output projection (tri_sparse_attn.py:
+    585-608): q (B, H, Tq, d); k, v (B, H, Tk, d) after repeat_kv; kg, vg the
+    global rows (1, H, G, d); gate = sigmoid(gate_logits)."""
+    out = gate[0] * swa_attention(q, k, v, cfg.window_size, offset) + gate[1] * _attend(q, kg, vg, None)
+    if cfg.use_alibi and k.shape[2] <= 1024:
+        out = out + gate[2] * alibi_attention(q, k, v, alibi_slopes(q.shape[1]), offset)
+    return out
+
+
 def trisparse(W, p, cfg, x):
     B, T, D = x.shape
     H, Hkv = cfg.n_head, cfg.n_kv_head
@@ -90,24 +128,12 @@ def trisparse(W, p, cfg, x):
     k = np.repeat(k, rep, axis=2).transpose(0, 2, 1, 3)
     v = np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)
     q = q.transpose(0, 2, 1, 3)
-    i = np.arange(T)[:, None]
-    j = np.arange(T)[None, :]
-    causal = j <= i
-    neg = F32(-1e9)
-    swa_mask = np.where(causal & ((i - j) < cfg.window_size), F32(0.0), neg).astype(F32)
-    swa = _attend(q, k, v, swa_mask[None, None])
     g = W[p + "attn.global_tokens.weight"]
     G = g.shape[0]
     kg = np.repeat((g @ W[p + "attn.wk.weight"].T).reshape(1, G, Hkv, d), rep, axis=2).transpose(0, 2, 1, 3)
     vg = np.repeat((g @ W[p + "attn.wv.weight"].T).reshape(1, G, Hkv, d), rep, axis=2).transpose(0, 2, 1, 3)
-    glob = _attend(q, kg, vg, None)
     gate = _sigmoid(W[p + "attn.gate_logits"].astype(F32))
-    out = gate[0] * swa + gate[1] * glob
-    if cfg.use_alibi and T <= 1024:
-        slopes = (1.0 / (2.0 ** (np.arange(1, H + 1, dtype=F32) / H))).astype(F32)
-        dist = (i - j).astype(F32)
-        bias = np.where(causal[None], -slopes[:, None, None] * dist[None], neg).astype(F32)
-        out = out + gate[2] * _attend(q, k, v, bias[None])
+    out = trisparse_heads(q, k, v, kg, vg, gate, cfg)
     out = out.transpose(0, 2, 1, 3).reshape(B, T, H * d)
     return out @ W[p + "attn.proj.weight"].T
 

@@ -11,6 +11,13 @@ Attention (the kernel vnx_tree_attn):
 - `tree_attention_gathered`: the same quantity computed node by node over
   the keys it may see, collected by walking its parent chain; a formulation
   that shares no mask code with `tree_attention`, used to pin it.
+- `tree_attention_paths`: TriSparseAttention's gated paths over a cache
+  plus tree rows (tri_sparse_attn.py:585-608): node i of batch row b sits at
+  position tp_b + depth(i) (depth 0 for a root), prefix row j at j, tree row
+  j at tp_b + depth(j); path A the sliding window (pos - key pos < window,
+  :258-378), path B the global rows (all visible, :469-495), path C ALiBi
+  (bias -m_h * (pos - key pos), no window, only where tp_b + N <= 1024,
+  :489-530, :600-607); out = g0 A + g1 B + g2 C.
 
 Greedy tree verification (vnx_tree_greedy; no reference function — the
 reference's verifier is the chain case, speculative.py:202-223 and :277-287):
@@ -33,6 +40,10 @@ all-visible mask == plain prefix attention; tree_attention ==
 tree_attention_gathered on random trees; tree_greedy == brute force on random
 trees and == the reference-pinned chain rule (oracle.speculative
 .greedy_verify_batched) on chains; topk_rows == a full stable sort.
+tree_attention_paths on a chain == the last rows of oracle.model
+.trisparse_heads (itself pinned by reference-written golden logits) with the
+window crossed, with and without ALiBi (tests/test_oracle_swa_replay.py), and
+on trees == tree_attention where the paths reduce to it.
 """
 from __future__ import annotations
 
@@ -97,6 +108,70 @@ def tree_attention(q, k_cache, v_cache, k_tree, v_tree, anc, scale=None):
     den = e.sum(axis=-1, keepdims=True)
     p = np.divide(e, den, out=np.zeros_like(e), where=den > 0)
     return np.matmul(p, V), np.matmul(p, np.abs(V))
+
+
+def tree_attention_paths(q, k_cache, v_cache, k_tree, v_tree, anc, tp=None, window=0, slopes=None,
+                         alibi_max=1024, seg2=None, gates=None, scale=None):
+    """(out, mag) (B, H, N, d) fp64 of the gated TriSparse paths over each
+    batch row's first tp[b] cache rows and its N tree rows (see the module
+    docstring).  tp: (B,) prefix lengths (default: all Tp rows); seg2 = (k2,
+    v2) (B or 1, Hkv, T2, d); gates (3,) fp32; slopes (H,) or None."""
+    q = _f64(q)
+    kt, vt = _f64(k_tree), _f64(v_tree)
+    B, H, N, d = q.shape
+    Hkv = kt.shape[1]
+    rep = H // Hkv
+    Tp = 0 if k_cache is None else np.asarray(k_cache).shape[2]
+    kc = None if k_cache is None else _f64(k_cache)
+    vc = None if v_cache is None else _f64(v_cache)
+    tp = np.full(B, Tp, np.int64) if tp is None else np.clip(np.asarray(tp, np.int64), 0, Tp)
+    sc = 1.0 / np.sqrt(d) if scale is None else float(scale)
+    w = _words(anc, B, N)
+    g = None if gates is None else np.asarray(gates, np.float32).astype(np.float64)
+    out = np.zeros((B, H, N, d))
+    mag = np.zeros((B, H, N, d))
+
+    def soft(scores, ok, V):
+        s = np.where(ok, scores, -np.inf)
+        mx = s.max(axis=-1, keepdims=True)
+        mx = np.where(np.isfinite(mx), mx, 0.0)
+        e = np.exp(s - mx)
+        den = e.sum(axis=-1, keepdims=True)
+        pr = np.divide(e, den, out=np.zeros_like(e), where=den > 0)
+        return pr @ V, pr @ np.abs(V)
+
+    for b in range(B):
+        t = int(tp[b])
+        bits = ((w[b][:, None] >> np.arange(N, dtype=np.uint64)[None, :]) & np.uint64(1)).astype(bool)  # (N, N)
+        depth = bits.sum(axis=1) - 1
+        qpos = t + depth                                                     # (N,)
+        kpos = np.concatenate([np.arange(t), t + depth])                    # (t + N,)
+        vis = np.concatenate([np.ones((N, t), bool), bits], axis=1)         # (N, t + N)
+        dist = qpos[:, None] - kpos[None, :]
+        K = np.concatenate([kc[b, :, :t], kt[b]], axis=1) if t else kt[b]
+        V = np.concatenate([vc[b, :, :t], vt[b]], axis=1) if t else vt[b]
+        K = np.repeat(K, rep, axis=0)
+        V = np.repeat(V, rep, axis=0)
+        scores = q[b] @ K.transpose(0, 2, 1) * sc                           # (H, N, t + N)
+        okA = vis & (dist < window) if window else vis
+        oA, mA = soft(scores, okA[None], V)
+        if g is None:
+            out[b], mag[b] = oA, mA
+            continue
+        o, m = g[0] * oA, g[0] * mA
+        if seg2 is not None:
+            k2 = _f64(seg2[0])
+            v2 = _f64(seg2[1])
+            k2 = np.repeat(k2[b if k2.shape[0] > 1 else 0], rep, axis=0)
+            v2 = np.repeat(v2[b if v2.shape[0] > 1 else 0], rep, axis=0)
+            oB, mB = soft(q[b] @ k2.transpose(0, 2, 1) * sc, np.ones((1, 1, k2.shape[1]), bool), v2)
+            o, m = o + g[1] * oB, m + g[1] * mB
+        if slopes is not None and t + N <= alibi_max:
+            sl = np.asarray(slopes, np.float32).astype(np.float64)
+            oC, mC = soft(scores - sl[:, None, None] * dist[None], vis[None], V)
+            o, m = o + g[2] * oC, m + g[2] * mC
+        out[b], mag[b] = o, m
+    return out, mag
 
 
 def tree_attention_gathered(q, k_cache, v_cache, k_tree, v_tree, parent, scale=None):

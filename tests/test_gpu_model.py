@@ -107,17 +107,20 @@ def test_ragged_lengths_roll_back(hip, gold):
         lens += torch.tensor(adv, dtype=torch.int32, device=dev)
 
 
-def _toy_cfg():
+def _toy_cfg(window=1024, alibi=False):
     return VM.ModelConfig(vocab_size=1000, dim=256, n_layer=2, n_head=4, n_kv_head=2,
-                          layer_pattern=("mod", "trisparse"), window_size=1024, num_global_tokens=8,
-                          use_alibi=False, use_rope=True, num_dense_parts=2, num_experts_per_part=4, top_k=2)
+                          layer_pattern=("mod", "trisparse"), window_size=window, num_global_tokens=8,
+                          use_alibi=alibi, use_rope=True, num_dense_parts=2, num_experts_per_part=4, top_k=2)
 
 
-def test_bf16_kernel_path_matches_oracle(hip):
-    """head_dim 64, RoPE, no ALiBi: the new rows attend through vnx_tree_attn
-    (per-row prefix lengths, rows written in place) and the head runs on
-    vnx_lm_head; compared with the fp32 oracle on each row's sequence."""
-    cfg = _toy_cfg()
+@pytest.mark.parametrize("window,alibi", [(1024, False), (48, False), (48, True), (1024, True)])
+def test_bf16_kernel_path_matches_oracle(hip, window, alibi):
+    """head_dim 64, RoPE, with and without a window the contexts cross and
+    ALiBi: the new rows attend through vnx_tree_attn (per-row prefix
+    lengths, rows written in place) and the head runs on vnx_lm_head;
+    compared with the fp32 oracle on each row's sequence."""
+    _say(f"bf16 kernel path window={window} alibi={alibi}")
+    cfg = _toy_cfg(window, alibi)
     W = VM.init_weights(cfg, seed=3)
     Wn = {k: v.numpy() for k, v in W.items()}
     for k_ in list(Wn):
@@ -176,8 +179,9 @@ def test_cache_only_forward_writes_the_same_cache(hip, int4):
         assert torch.equal(ms[0].vc[li], ms[1].vc[li]), li
 
 
-def test_kernel_and_torch_attention_paths_agree(hip):
-    cfg = _toy_cfg()
+@pytest.mark.parametrize("window,alibi", [(1024, False), (20, True)])
+def test_kernel_and_torch_attention_paths_agree(hip, window, alibi):
+    cfg = _toy_cfg(window, alibi)
     W = VM.init_weights(cfg, seed=5)
     dev = hip.torch_device
     B = 3

@@ -45,9 +45,9 @@ def _check(out, ref, mag, bf16=False):
 
 
 def _run(hip, B, H, Hkv, N, Tp, d, parent=None, seed=0, out_dtype=torch.float32, per_batch=False,
-         cache_extra=0, inplace=False, std=1.0, T2=0, gates=(0.3, 0.8)):
+         cache_extra=0, inplace=False, std=1.0, T2=0, gates=(0.3, 0.8), waves=0, splits=0):
     _say(f"tree_attn B={B} H={H} Hkv={Hkv} N={N} Tp={Tp} d={d} out={out_dtype} per_batch={per_batch} "
-         f"cache_extra={cache_extra} inplace={inplace} T2={T2}")
+         f"cache_extra={cache_extra} inplace={inplace} T2={T2} waves={waves} splits={splits}")
     rng = np.random.default_rng(seed)
     par = T.tree_from_branching((4, 3, 2)) if parent is None else np.asarray(parent, np.int32)
     assert par.size == N
@@ -72,7 +72,8 @@ def _run(hip, B, H, Hkv, N, Tp, d, parent=None, seed=0, out_dtype=torch.float32,
     if T2:
         seg2 = (_bf16(rng, (1, Hkv, T2, d), std).to(dev), _bf16(rng, (1, Hkv, T2, d)).to(dev))
     out = hip.tree_attention(q, kc if Tp else None, vc if Tp else None, kt, vt, words, out_dtype=out_dtype,
-                             seg2=seg2, gates=np.asarray(gates, np.float32) if T2 else None)
+                             seg2=seg2, gates=np.asarray(gates, np.float32) if T2 else None,
+                             force_waves=waves, force_splits=splits)
     torch.cuda.synchronize()
     ref, mag = OT.tree_attention(_np(q), _np(kc) if Tp else None, _np(vc) if Tp else None, _np(kt), _np(vt),
                                  words)
@@ -142,16 +143,15 @@ def test_splits_cover_one_and_many(hip):
 @pytest.mark.parametrize("waves", ["4", "5", "8", "16"])
 @pytest.mark.parametrize("B,H,Hkv,N,Tp,d", [(8, 16, 8, 1, 640, 64), (8, 16, 8, 7, 301, 64),
                                             (2, 16, 16, 40, 700, 64), (2, 4, 2, 20, 300, 128)])
-def test_workgroup_shapes(hip, monkeypatch, waves, B, H, Hkv, N, Tp, d):
+def test_workgroup_shapes(hip, waves, B, H, Hkv, N, Tp, d):
     """Every workgroup shape (4 waves, 4 with prefetch, 8, 16; a shape that
     does not fit the query tile falls back to the default) on decode-like
     (N 1, 7) and verify-like (N 40) calls."""
-    monkeypatch.setenv("VNX_TA_WAVES", waves)
     par = T.chain(N) if N < 40 else None
     if N == 20:
         rng = np.random.default_rng(5)
         par = np.array([-1] + [int(rng.integers(-1, i)) for i in range(1, N)], np.int32)
-    _run(hip, B, H, Hkv, N, Tp, d, parent=par, seed=N + Tp)
+    _run(hip, B, H, Hkv, N, Tp, d, parent=par, seed=N + Tp, waves=int(waves))
 
 
 @pytest.mark.parametrize("waves,splits,out_dtype,N,T2,d", [
@@ -159,15 +159,13 @@ def test_workgroup_shapes(hip, monkeypatch, waves, B, H, Hkv, N, Tp, d):
     ("5", None, torch.float16, 7, 100, 64), ("4", "3", torch.float32, 7, 128, 64),
     ("16", "2", torch.float16, 1, 40, 64), ("8", None, torch.float32, 7, 128, 128),
     ("4", "2", torch.bfloat16, 40, 64, 64)])
-def test_gated_second_segment(hip, monkeypatch, waves, splits, out_dtype, N, T2, d):
+def test_gated_second_segment(hip, waves, splits, out_dtype, N, T2, d):
     """TriSparse's fused sliding-window + global paths: out = g1 * tree
     attention + g2 * attention over the T2 shared rows, with and without key
     splits (the second segment then merges through its own slot)."""
-    monkeypatch.setenv("VNX_TA_WAVES", waves)
-    if splits:
-        monkeypatch.setenv("VNX_TA_SPLITS", splits)
     par = T.chain(N) if N < 40 else None
-    _run(hip, 6, 16, 8, N, 500, d, parent=par, seed=N + T2, out_dtype=out_dtype, T2=T2)
+    _run(hip, 6, 16, 8, N, 500, d, parent=par, seed=N + T2, out_dtype=out_dtype, T2=T2, waves=int(waves),
+         splits=int(splits) if splits else 0)
 
 
 def test_large_scores(hip):
@@ -207,7 +205,7 @@ def test_rejects_bad_arguments(hip):
 
 @pytest.mark.parametrize("B,H,Hkv,N,d,rope,splits", [(32, 16, 8, 7, 64, 1, None), (5, 4, 2, 3, 128, 1, None),
                                                      (4, 8, 2, 7, 64, 0, None), (3, 4, 4, 5, 64, 1, "2")])
-def test_qkv_rows_mode_matches_rope_kv_path(hip, monkeypatch, B, H, Hkv, N, d, rope, splits):
+def test_qkv_rows_mode_matches_rope_kv_path(hip, B, H, Hkv, N, d, rope, splits):
     """vnx_tree_attn reading the q|k|v projection rows (RoPE and the tree
     rows' cache write inside the call) against vnx_rope_kv followed by the
     q-input call: the same fp32 rotation rounded once to bf16, so the cache
@@ -215,8 +213,6 @@ def test_qkv_rows_mode_matches_rope_kv_path(hip, monkeypatch, B, H, Hkv, N, d, r
     unwritten."""
     import ctypes
     from versenext_amd import _lib
-    if splits:
-        monkeypatch.setenv("VNX_TA_SPLITS", splits)
     _say(f"tree attn qkv mode B={B} H={H} Hkv={Hkv} N={N} d={d} rope={rope} splits={splits}")
     dev = hip.torch_device
     g = torch.Generator(device="cpu")
@@ -251,7 +247,8 @@ def test_qkv_rows_mode_matches_rope_kv_path(hip, monkeypatch, B, H, Hkv, N, d, r
         a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, N, d
         a.scale = 1.0 / d ** 0.5
         a.tp_batch = lens.data_ptr(); a.tree_follows_prefix = 1
-        ws = torch.empty(max(256, L.vnx_tree_attn_workspace(B, H, Hkv, N, Tp, d)), dtype=torch.uint8, device=dev)
+        a.force_splits = int(splits) if splits else 0
+        ws = torch.empty(max(256, L.vnx_tree_attn_workspace_args(ctypes.byref(a))), dtype=torch.uint8, device=dev)
         _lib.check(L.vnx_tree_attn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "tree_attn")
 
     # reference path: vnx_rope_kv, then queries from q
@@ -273,3 +270,73 @@ def test_qkv_rows_mode_matches_rope_kv_path(hip, monkeypatch, B, H, Hkv, N, d, r
     ok = (lens.cpu().long().view(B, 1) + torch.arange(N).view(1, N)) < cap
     oa, ob = out_a.cpu().view(B, N, H * d), out_b.cpu().view(B, N, H * d)
     assert torch.equal(oa[ok], ob[ok])
+
+
+def _run_paths(hip, B, H, Hkv, N, Tp, d, tp, window, alibi, parent=None, T2=0, seed=0, out_dtype=torch.float32,
+               alibi_max=1024, waves=0, splits=0):
+    """vnx_tree_attn with a sliding window and / or ALiBi against
+    oracle.tree.tree_attention_paths (the gated TriSparse paths)."""
+    _say(f"tree_attn paths B={B} H={H} Hkv={Hkv} N={N} Tp={Tp} d={d} window={window} alibi={alibi} T2={T2} "
+         f"alibi_max={alibi_max} waves={waves} splits={splits}")
+    rng = np.random.default_rng(seed)
+    par = T.chain(N) if parent is None else np.asarray(parent, np.int32)
+    dev = hip.torch_device
+    q = _bf16(rng, (B, H, N, d), 2.0).to(dev)
+    kc = _bf16(rng, (B, Hkv, Tp, d), 2.0).to(dev)
+    vc = _bf16(rng, (B, Hkv, Tp, d)).to(dev)
+    kt = _bf16(rng, (B, Hkv, N, d), 2.0).to(dev)
+    vt = _bf16(rng, (B, Hkv, N, d)).to(dev)
+    words = T.ancestor_words(par)
+    gates = np.asarray([0.55, 0.3, 0.7], np.float32)
+    seg2 = None
+    if T2:
+        seg2 = (_bf16(rng, (1, Hkv, T2, d)).to(dev), _bf16(rng, (1, Hkv, T2, d)).to(dev))
+    slopes = (1.0 / (2.0 ** (np.arange(1, H + 1, dtype=np.float32) / H))).astype(np.float32) if alibi else None
+    out = hip.tree_attention(q, kc, vc, kt, vt, words, out_dtype=out_dtype, seg2=seg2,
+                             gates=gates if (T2 or alibi) else None, tp=np.asarray(tp, np.int32), window=window,
+                             alibi_slopes=slopes, alibi_max_keys=alibi_max, force_waves=waves, force_splits=splits)
+    torch.cuda.synchronize()
+    ref, mag = OT.tree_attention_paths(_np(q), _np(kc), _np(vc), _np(kt), _np(vt), words, tp=tp, window=window,
+                                       slopes=slopes, alibi_max=alibi_max,
+                                       seg2=(_np(seg2[0]), _np(seg2[1])) if T2 else None,
+                                       gates=gates if (T2 or alibi) else None)
+    worst = _check(out, ref, mag, bf16=out_dtype == torch.bfloat16)
+    _say(f"  worst err / sum p|v| = {worst:.2e}")
+
+
+@pytest.mark.parametrize("window,splits", [(64, 0), (100, 0), (37, 0), (64, 3), (200, 2)])
+def test_sliding_window_crossed_by_ragged_rows(hip, window, splits):
+    """Path A with the window crossed: ragged prefixes (some shorter than the
+    window, some far longer), a chain of 7 new rows, the global rows gated;
+    key splits over the windowed range."""
+    tp = [300, 12, 63, 64, 299, 150]
+    _run_paths(hip, 6, 16, 8, 7, 300, 64, tp, window, False, T2=16, seed=window + splits, splits=splits)
+
+
+@pytest.mark.parametrize("waves,d,out_dtype", [(4, 64, torch.float32), (8, 64, torch.bfloat16),
+                                               (4, 128, torch.float32), (8, 128, torch.float16)])
+def test_alibi_path_with_window_and_global_rows(hip, waves, d, out_dtype):
+    """All three gated paths (config-1's layout: window, global rows, ALiBi)
+    at bf16 head sizes; one row's keys exceed alibi_max, so its ALiBi path
+    drops out as in the reference."""
+    tp = [90, 5, 40, 61]
+    _run_paths(hip, 4, 8, 4, 5, 90, d, tp, 32, True, T2=8, seed=d + waves, out_dtype=out_dtype,
+               alibi_max=70, waves=waves)
+
+
+def test_alibi_without_window_on_a_tree(hip):
+    """ALiBi over a token tree (key positions from the tree depths), no
+    window and no global rows, and a tree with a window."""
+    par = T.tree_from_branching((3, 2, 2))
+    N = par.size
+    _run_paths(hip, 3, 4, 2, N, 50, 64, [50, 0, 17], 0, True, parent=par, seed=1)
+    _run_paths(hip, 3, 4, 2, N, 50, 64, [50, 0, 17], N + 3, True, parent=par, seed=2)
+    _run_paths(hip, 3, 4, 2, N, 80, 64, [80, 20, 45], N, False, parent=par, seed=3, T2=4)
+
+
+def test_window_smaller_than_the_tree_is_rejected(hip):
+    dev = hip.torch_device
+    z = lambda *s: torch.zeros(s, dtype=torch.bfloat16, device=dev)  # noqa: E731
+    with pytest.raises(ValueError):
+        hip.tree_attention(z(1, 2, 8, 64), z(1, 2, 10, 64), z(1, 2, 10, 64), z(1, 2, 8, 64), z(1, 2, 8, 64),
+                           T.ancestor_words(T.chain(8)), window=7)

@@ -102,6 +102,8 @@ class TreeAttnArgs(ctypes.Structure):
         ("k_seg2", _vp), ("v_seg2", _vp), ("seg2_strides", _c_i64 * 3), ("T2", _int), ("gates", _vp),
         ("qkv", _vp), ("qkv_ld", _c_i64), ("cos_table", _vp), ("sin_table", _vp), ("table_rows", _c_i64),
         ("rope", _int), ("cap", _c_i64),
+        ("window", _int), ("alibi_slopes", _vp), ("alibi_max_keys", _int),
+        ("force_splits", _int), ("force_waves", _int),
     ]
 
 
@@ -119,6 +121,7 @@ SIGNATURES.update({
     "vnx_gemv_w4_rope_kv": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64,
                                    _int, ctypes.POINTER(RopeKvArgs), _vp]),
     "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),
+    "vnx_tree_attn_workspace_args": (_c_sz, [ctypes.POINTER(TreeAttnArgs)]),
     "vnx_tree_attn": (_int, [ctypes.POINTER(TreeAttnArgs), _vp, _c_sz, _vp]),
     "vnx_tree_attn_plan": (_int, [_int, _int, _int, _int, _int, _int, _vp, _vp, _vp]),
     "vnx_tree_greedy_workspace": (_c_sz, [_c_i64, _int, _c_i64]),

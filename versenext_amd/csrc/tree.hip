@@ -28,6 +28,19 @@
 // Waves merge their (m, l, O) through LDS; with several key splits the
 // partial (m, l, O) go to the workspace and k_tree_merge combines them (a
 // kernel boundary instead of cross-XCD fences).
+//
+// TriSparseAttention's paths (tri_sparse_attn.py:585-608) ride on the same
+// walk: the global rows are a second key segment with waves of their own
+// (softmax normalised apart, gated); with EXT the sliding window masks the
+// keys of segment 1 whose position is window or more behind the query's
+// (node i of batch row b sits at tp_b + depth(i), prefix row j at j; the
+// first max(0, tp_b - window + 1) rows are skipped outright), and ALiBi is a
+// third group of waves that walks segment 1's keys again without the window,
+// adding -m_h * (query position - key position) to each score (the bias is
+// per column, a multiply-add in the exp2 domain), its softmax gated by
+// gates[2].
+#include <climits>
+
 #include "vnx_internal.h"
 
 namespace vnx {
@@ -63,6 +76,12 @@ struct TreeAttnParams {
   int T2, W2;                       // rows; waves of split 0 that walk them
   const float* gates;
   float c;                          // scale * log2(e)
+  // EXT: sliding window (0: none) and ALiBi (slopes != NULL; the launch then
+  // has one key split and W3 waves walking the third segment, for batch rows
+  // with tp_b + N <= alibi_max)
+  int window;
+  const float* slopes;
+  int alibi_max, W3;
   // qkv mode: queries from the projection rows (RoPE here), the tree rows'
   // keys / values written into the cache by every workgroup first
   const uint16_t* qkv;
@@ -131,7 +150,7 @@ constexpr bool ta_variant_ok(int D, int QT, int NW, bool PF) {
 // One workgroup of NW waves per (b, kv head, query group, key split).  PF:
 // issue the loads of a wave's next key step before the current step's math
 // (more registers; for grids of at most one workgroup per CU).
-template <int D, int QT, int OT, int NW, bool PF>
+template <int D, int QT, int OT, int NW, bool PF, bool EXT>
 __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
   constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
   constexpr int DT = D / 16;          // 16-wide dimension tiles of O
@@ -241,18 +260,25 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
   }
   __syncthreads();
 
-  // The segment this wave walks: split 0 gives its last W2 waves the second
-  // segment (wave-uniform, so the selects below are scalar).
-  const bool has2 = p.T2 > 0 && s == 0;
-  const int nw1 = has2 ? NW - p.W2 : NW;
-  const bool seg2 = has2 && w >= nw1;
-  const int wi = seg2 ? w - nw1 : w;   // index among the segment's waves
-  const int nws = seg2 ? p.W2 : nw1;   // waves walking the segment
   // Segment 1: this batch row's prefix of Tp rows, or tp_batch[b] (clamped
   // to [0, Tp]) when the rows of a batch have different committed lengths,
-  // then the N tree rows.  Segment 2: T2 rows, no tree.
+  // then the N tree rows.  Segment 2: T2 rows, no tree.  Segment 3 (EXT with
+  // ALiBi): segment 1's keys again.
   int Tp = p.Tp;
   if (p.tp_batch) Tp = min(max(p.tp_batch[b], 0), p.Tp);
+  // The segment this wave walks: split 0 gives its last W2 waves the second
+  // segment and, with ALiBi, the W3 before them the third (wave-uniform, so
+  // the selects below are scalar).
+  const bool has2 = p.T2 > 0 && s == 0;
+  const bool alibi = EXT && p.slopes != nullptr;
+  const bool has3 = alibi && Tp + p.N <= p.alibi_max;
+  const int w2 = has2 ? p.W2 : 0, w3 = alibi ? p.W3 : 0;
+  const int nw1 = NW - w2 - w3;
+  const bool seg3 = alibi && w >= nw1 && w < nw1 + w3;
+  const bool seg2 = has2 && w >= nw1 + w3;
+  const int wi = seg2 ? w - nw1 - w3 : seg3 ? w - nw1 : w;  // index among the segment's waves
+  const int nws = seg2 ? w2 : seg3 ? w3 : nw1;               // waves walking the segment
+  const bool win = EXT && p.window > 0 && !seg2 && !seg3;
   const uint16_t* kc = seg2 ? p.k2 : p.kc;
   const uint16_t* vc = seg2 ? p.v2 : p.vc;
   const int64_t cbase = seg2 ? b * p.s2_sb + kvh * p.s2_sh : b * p.c_sb + kvh * p.c_sh;
@@ -280,9 +306,31 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
   }
 
   uint16_t* vt_w = s_v + w * 32 * R;  // this wave's 32-key V tile
-  const int k_lo = seg2 ? 0 : s * p.chunk;
-  const int k_hi = seg2 ? p.T2 : min(KT, k_lo + p.chunk);
-  const int nsteps = (k_hi - k_lo + 31) >> 5;
+  // segment 1 under a window starts at the first row any node can see
+  const int kbase = win ? max(0, Tp - p.window + 1) : 0;
+  const int k_lo = (seg2 || seg3) ? 0 : kbase + s * p.chunk;
+  const int k_hi = seg2 ? p.T2 : seg3 ? (has3 ? KT : 0) : min(KT, k_lo + p.chunk);
+  const int nsteps = k_hi > k_lo ? (k_hi - k_lo + 31) >> 5 : 0;
+  // Per query column: its position (prefix rows + depth), the window's first
+  // visible key, the ALiBi slope times -log2(e).
+  int qpos[EXT ? QT : 1], kmin[EXT ? QT : 1];
+  float cb[EXT ? QT : 1];
+  if constexpr (EXT) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int r = qt * 16 + col;
+      const int dep = r < nrows ? __builtin_popcountll(anc[qt]) - 1 : 0;
+      qpos[qt] = Tp + dep;
+      kmin[qt] = win ? qpos[qt] - p.window + 1 : INT_MIN;
+      cb[qt] = 0.0f;
+      if (seg3 && r < nrows) {
+        const int h = kvh * p.n_rep + (row0 + r) / p.N;
+        cb[qt] = -p.slopes[h] * 1.4426950408889634f;
+      }
+    }
+  }
+  // the last key index below some column's window start
+  const int wlim = win ? Tp + p.N - p.window : INT_MIN;
 
   // One step's loads: K fragments (A rows = keys base + kt*16 + col, k = dims
   // ks*32 + grp*8 .. +8) and V rows, coalesced (load v covers keys
@@ -327,7 +375,21 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
       for (int e = 0; e < 8; ++e) e8[e] = vt_w[((e < 4 ? 0 : 16) + grp * 4 + (e & 3)) * R + dt * 16 + col];
       va[dt] = __builtin_bit_cast(bf16x8, e8);
     }
-    const bool edge = base + 32 > Tpe;  // the step reaches tree keys or the end
+    // masks: the step reaches tree keys or the end, or keys below a window
+    const bool edge = base + 32 > Tpe || (EXT && base < wlim);
+    int kpos[EXT ? 8 : 1];
+    if constexpr (EXT) {
+      if (seg3) {
+        // key positions: prefix row j at j, tree row j at Tp + depth(j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = base + (e < 4 ? 0 : 16) + grp * 4 + (e & 3);
+          const int j = key - Tpe;
+          kpos[e] = key < Tpe ? key
+                              : (j < p.N ? Tp + __builtin_popcountll(p.anc[b * p.anc_sb + j]) - 1 : Tp);
+        }
+      }
+    }
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       f32x4 sa[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -340,12 +402,19 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
       float x[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = sa[e >> 2][e & 3] * p.c;
+      if constexpr (EXT) {
+        if (seg3) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = __builtin_fmaf(cb[qt], (float)(qpos[qt] - kpos[e]), x[e]);
+        }
+      }
       if (edge) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int key = base + (e < 4 ? 0 : 16) + grp * 4 + (e & 3);
           bool vis = key < k_hi;
           if (key >= Tpe) vis = vis && ((anc[qt] >> (key - Tpe)) & 1ull);
+          else if (EXT) vis = vis && key >= kmin[qt];
           x[e] = vis ? x[e] : kNegInf;
         }
       }
@@ -406,8 +475,9 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
     if (grp == 0) s_ml[(w * QT + qt) * 16 + col] = make_float2(m[qt], l[qt]);
   }
   __syncthreads();
-  const float g1 = has2 && p.S == 1 ? p.gates[0] : 1.0f;
+  const float g1 = (has2 || alibi) && p.S == 1 ? p.gates[0] : 1.0f;
   const float g2 = has2 && p.S == 1 ? p.gates[1] : 0.0f;
+  const float g3 = has3 ? p.gates[2] : 0.0f;  // ALiBi launches have one split
   for (int t = w; t < QT * DT; t += NW) {
     const int qt = t / DT, dt = t - qt * DT;
     // (M, L, O) of waves [a, e) for this lane's column and 4 dimensions.
@@ -424,10 +494,11 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
         O += s_o[((i * QT + qt) * DT + dt) * 64 + lane] * f;
       }
     };
-    float M1, L1, M2 = kNegInf, L2 = 0.0f;
-    f32x4 O1, O2 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float M1, L1, M2 = kNegInf, L2 = 0.0f, M3 = kNegInf, L3 = 0.0f;
+    f32x4 O1, O2 = {0.0f, 0.0f, 0.0f, 0.0f}, O3 = {0.0f, 0.0f, 0.0f, 0.0f};
     combine(0, nw1, M1, L1, O1);
-    if (has2) combine(nw1, NW, M2, L2, O2);
+    if (has3) combine(nw1, nw1 + w3, M3, L3, O3);
+    if (has2) combine(nw1 + w3, NW, M2, L2, O2);
     const int r = qt * 16 + col;
     if (r >= nrows) continue;
     const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
@@ -435,6 +506,7 @@ __global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
     if (p.S == 1) {
       f32x4 v = O1 * (L1 > 0.0f ? g1 / L1 : 0.0f);
       if (has2) v += O2 * (L2 > 0.0f ? g2 / L2 : 0.0f);
+      if (has3) v += O3 * (L3 > 0.0f ? g3 / L3 : 0.0f);
       ta_store4<OT>(p.out, b * p.o_sb + h * p.o_sh + node * p.o_sr + dt * 16 + grp * 4, v);
     } else {
       const int64_t prow = ((int64_t)(b * p.H + h) * p.N + node) * (p.S + 1);
@@ -490,25 +562,18 @@ struct TaPlan {
   int G, rows_per_group, QT, S, chunk;
 };
 
-static int env_int(const char* name) {
-  const char* e = getenv(name);
-  const int x = e ? atoi(e) : 0;
-  return x > 0 ? x : 0;
-}
-
-// VNX_TA_SPLITS (>= 1) fixes the key splits and VNX_TA_WAVES (4, 8, 16; 5 =
-// 4 waves with prefetch) the workgroup shape, for tuning sweeps.
-static int ta_splits_override() { return env_int("VNX_TA_SPLITS"); }
-static int ta_waves_override() { return env_int("VNX_TA_WAVES"); }
-
-static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d) {
+// force_splits (>= 1) fixes the key splits (the args' field; 0: the plan's).
+// window > 0: only the last window - 1 prefix rows (plus the tree) are walked.
+// alibi: one split (the third segment walks all keys in split 0).
+static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d, int force_splits = 0, int window = 0,
+                      bool alibi = false) {
   TaPlan pl{};
   const int qmax = d == 64 ? 64 : 32;  // query rows per group (register budget of O)
   const int rows = (H / Hkv) * N;
   pl.G = (rows + qmax - 1) / qmax;
   pl.rows_per_group = (rows + pl.G - 1) / pl.G;
   pl.QT = (pl.rows_per_group + 15) / 16;
-  const int KT = Tp + N;
+  const int KT = (window > 0 && Tp > window - 1 ? window - 1 : Tp) + N;
   const int steps = (KT + 31) / 32;
   const int64_t base = (int64_t)B * Hkv * pl.G;
   const int64_t target = (int64_t)device_cus() * 4 * wg_scale_pct() / 100;
@@ -519,7 +584,8 @@ static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d) {
   const int sby_work = steps / 24 > 1 ? steps / 24 : 1;
   S = S < sby_work ? S : sby_work;
   const int smax = (steps + 3) / 4;  // at least one 32-key step per wave
-  if (ta_splits_override()) S = ta_splits_override();
+  if (force_splits > 0) S = force_splits;
+  if (alibi) S = 1;
   S = S < 1 ? 1 : (S > smax ? smax : S);
   const int steps_per = (steps + S - 1) / S;
   pl.chunk = steps_per * 32;
@@ -539,13 +605,15 @@ static size_t ta_ws_bytes(const TaPlan& pl, int B, int H, int N, int d) {
 // Waves per workgroup (5: 4 with prefetch).  A grid of at most one workgroup
 // per CU gets 8 waves (16 when 8 does not fit the query tile), so each wave
 // walks few key steps and more loads are in flight per CU; larger grids keep
-// 4 waves.
-static int ta_waves(int D, int QT, int64_t nwg) {
+// 4 waves.  force (the args' force_waves: 4, 5, 8, 16) overrides the choice
+// where the shape fits.  EXT launches (window / ALiBi) have 4 or 8 waves.
+static int ta_waves(int D, int QT, int64_t nwg, int force, bool ext) {
   auto ok = [&](int nw) {
+    if (ext && nw != 4 && nw != 8) return false;
     return nw == 5 ? ta_variant_ok(D, QT, 4, true) : ta_variant_ok(D, QT, nw, false);
   };
-  const int o = ta_waves_override();
-  if (o && ok(o)) return o;
+  if (force && ok(force)) return force;
+  if (ext) return ok(8) && nwg <= 2 * device_cus() ? 8 : 4;
   const int64_t cus = device_cus();
   if (nwg <= cus) {
     if (ok(8)) return 8;  // (measured at least as fast as 16 at decode shapes, with twice the registers)
@@ -556,30 +624,34 @@ static int ta_waves(int D, int QT, int64_t nwg) {
   return 4;
 }
 
-template <int D, int OT, int NW, bool PF>
+template <int D, int OT, int NW, bool PF, bool EXT>
 static void ta_launch_qt(const TreeAttnParams& p, int QT, dim3 grid, hipStream_t st) {
   const dim3 block(NW * 64);
   switch (QT) {
     case 1:
-      if constexpr (ta_variant_ok(D, 1, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 1, OT, NW, PF>), grid, block, 0, st, p);
+      if constexpr (ta_variant_ok(D, 1, NW, PF))
+        hipLaunchKernelGGL((k_tree_attn<D, 1, OT, NW, PF, EXT>), grid, block, 0, st, p);
       break;
     case 2:
-      if constexpr (ta_variant_ok(D, 2, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 2, OT, NW, PF>), grid, block, 0, st, p);
+      if constexpr (ta_variant_ok(D, 2, NW, PF))
+        hipLaunchKernelGGL((k_tree_attn<D, 2, OT, NW, PF, EXT>), grid, block, 0, st, p);
       break;
     case 3:
-      if constexpr (ta_variant_ok(D, 3, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 3, OT, NW, PF>), grid, block, 0, st, p);
+      if constexpr (ta_variant_ok(D, 3, NW, PF))
+        hipLaunchKernelGGL((k_tree_attn<D, 3, OT, NW, PF, EXT>), grid, block, 0, st, p);
       break;
     default:
-      if constexpr (ta_variant_ok(D, 4, NW, PF)) hipLaunchKernelGGL((k_tree_attn<D, 4, OT, NW, PF>), grid, block, 0, st, p);
+      if constexpr (ta_variant_ok(D, 4, NW, PF))
+        hipLaunchKernelGGL((k_tree_attn<D, 4, OT, NW, PF, EXT>), grid, block, 0, st, p);
       break;
   }
 }
 
 template <int D, int OT>
-static int ta_launch_d(TreeAttnParams p, int QT, hipStream_t st, hipEvent_t* ev) {
+static int ta_launch_d(TreeAttnParams p, int QT, bool ext, int force_waves, hipStream_t st, hipEvent_t* ev) {
   const int64_t nwg = (int64_t)p.B * p.Hkv * p.G * p.S;
   const dim3 grid((unsigned)nwg);
-  const int nw = ta_waves(D, QT, nwg);
+  const int nw = ta_waves(D, QT, nwg, force_waves, ext);
   const int waves = nw == 5 ? 4 : nw;
   if (p.T2 > 0) {
     // split 0's share of waves for the second segment: a quarter, at most
@@ -588,12 +660,22 @@ static int ta_launch_d(TreeAttnParams p, int QT, hipStream_t st, hipEvent_t* ev)
     p.W2 = waves / 4 < steps2 ? waves / 4 : steps2;
     if (p.W2 < 1) p.W2 = 1;
   }
+  if (p.slopes) {
+    // the ALiBi segment walks as many keys as segment 1: half the rest
+    p.W3 = (waves - (p.T2 > 0 ? p.W2 : 0)) / 2;
+    if (p.W3 < 1) p.W3 = 1;
+  }
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[0], st));
-  switch (nw) {
-    case 16: ta_launch_qt<D, OT, 16, false>(p, QT, grid, st); break;
-    case 8: ta_launch_qt<D, OT, 8, false>(p, QT, grid, st); break;
-    case 5: ta_launch_qt<D, OT, 4, true>(p, QT, grid, st); break;
-    default: ta_launch_qt<D, OT, 4, false>(p, QT, grid, st); break;
+  if (ext) {
+    if (nw == 8) ta_launch_qt<D, OT, 8, false, true>(p, QT, grid, st);
+    else ta_launch_qt<D, OT, 4, false, true>(p, QT, grid, st);
+  } else {
+    switch (nw) {
+      case 16: ta_launch_qt<D, OT, 16, false, false>(p, QT, grid, st); break;
+      case 8: ta_launch_qt<D, OT, 8, false, false>(p, QT, grid, st); break;
+      case 5: ta_launch_qt<D, OT, 4, true, false>(p, QT, grid, st); break;
+      default: ta_launch_qt<D, OT, 4, false, false>(p, QT, grid, st); break;
+    }
   }
   VNX_LAUNCH_CHECK();
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[1], st));
@@ -624,6 +706,18 @@ size_t vnx_tree_attn_workspace(int B, int H, int Hkv, int N, int Tp, int d) {
   return n < 256 ? 256 : n;
 }
 
+size_t vnx_tree_attn_workspace_args(const vnx_tree_attn_args* a) {
+  if (!a) return 256;
+  const int B = a->B, H = a->H, Hkv = a->Hkv, N = a->N, Tp = a->Tp, d = a->d;
+  if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || N <= 0 || N > kTaMaxN || Tp < 0 || (d != 64 && d != 128) ||
+      a->window < 0 || a->force_splits < 0)
+    return 256;
+  const bool ext = a->alibi_slopes || (a->window > 0 && Tp + N > a->window);
+  const TaPlan pl = ta_plan(B, H, Hkv, N, Tp, d, a->force_splits, ext ? a->window : 0, a->alibi_slopes != nullptr);
+  const size_t n = ta_ws_bytes(pl, B, H, N, d);
+  return n < 256 ? 256 : n;
+}
+
 int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   if (!a) return VNX_ERR_INVALID_ARG;
   const int B = a->B, H = a->H, Hkv = a->Hkv, N = a->N, Tp = a->Tp, d = a->d;
@@ -641,6 +735,12 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
     if (a->rope && (!aligned16(a->cos_table) || !aligned16(a->sin_table))) return VNX_ERR_UNSUPPORTED;
     if (!aligned16(a->qkv) || a->qkv_ld % 8) return VNX_ERR_UNSUPPORTED;
   }
+  if (a->window < 0 || a->alibi_max_keys < 0 || a->force_splits < 0 || a->force_waves < 0)
+    return VNX_ERR_INVALID_ARG;
+  if (a->window > 0 && a->window < N) return VNX_ERR_UNSUPPORTED;  // tree keys always inside the window
+  if (a->alibi_slopes && (!a->gates || (reinterpret_cast<uintptr_t>(a->gates) & 3u) ||
+                          (reinterpret_cast<uintptr_t>(a->alibi_slopes) & 3u)))
+    return VNX_ERR_INVALID_ARG;
   if (a->T2 > 0) {
     if (!a->k_seg2 || !a->v_seg2 || !a->gates || (reinterpret_cast<uintptr_t>(a->gates) & 3u))
       return VNX_ERR_INVALID_ARG;
@@ -662,7 +762,10 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
       (Tp > 0 && (!aligned16(a->k_cache) || !aligned16(a->v_cache))) ||
       (reinterpret_cast<uintptr_t>(a->anc) & 7u))
     return VNX_ERR_UNSUPPORTED;
-  const TaPlan pl = ta_plan(B, H, Hkv, N, Tp, d);
+  // EXT variant: ALiBi, or a window some row's keys reach past
+  const bool ext = a->alibi_slopes || (a->window > 0 && Tp + N > a->window);
+  const int window = ext ? a->window : 0;
+  const TaPlan pl = ta_plan(B, H, Hkv, N, Tp, d, a->force_splits, window, a->alibi_slopes != nullptr);
   if ((int64_t)B * Hkv * pl.G * pl.S >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   const size_t need = ta_ws_bytes(pl, B, H, N, d);
   if (need && (!workspace || workspace_bytes < need)) return VNX_ERR_WORKSPACE;
@@ -692,6 +795,10 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
     p.gates = a->gates;
   }
   p.c = (float)((double)a->scale * 1.4426950408889634);
+  p.window = window;
+  p.slopes = a->alibi_slopes;
+  p.alibi_max = a->alibi_max_keys;
+  if (p.slopes) p.gates = a->gates;
   if (a->qkv) {
     p.qkv = static_cast<const uint16_t*>(a->qkv);
     p.qkv_ld = a->qkv_ld;
@@ -709,11 +816,14 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipEvent_t* ev = profile_slot(2);
   const int ot = a->out_dtype == VNX_F32 ? 0 : a->out_dtype == VNX_BF16 ? 1 : 2;
+  const int fw = a->force_waves;
   if (d == 64)
-    return ot == 0 ? ta_launch_d<64, 0>(p, pl.QT, st, ev)
-                   : ot == 1 ? ta_launch_d<64, 1>(p, pl.QT, st, ev) : ta_launch_d<64, 2>(p, pl.QT, st, ev);
-  return ot == 0 ? ta_launch_d<128, 0>(p, pl.QT, st, ev)
-                 : ot == 1 ? ta_launch_d<128, 1>(p, pl.QT, st, ev) : ta_launch_d<128, 2>(p, pl.QT, st, ev);
+    return ot == 0   ? ta_launch_d<64, 0>(p, pl.QT, ext, fw, st, ev)
+           : ot == 1 ? ta_launch_d<64, 1>(p, pl.QT, ext, fw, st, ev)
+                     : ta_launch_d<64, 2>(p, pl.QT, ext, fw, st, ev);
+  return ot == 0   ? ta_launch_d<128, 0>(p, pl.QT, ext, fw, st, ev)
+         : ot == 1 ? ta_launch_d<128, 1>(p, pl.QT, ext, fw, st, ev)
+                   : ta_launch_d<128, 2>(p, pl.QT, ext, fw, st, ev);
 }
 
 int vnx_tree_attn_plan(int B, int H, int Hkv, int N, int Tp, int d, int* splits, int* groups, int* chunk) {

@@ -436,7 +436,9 @@ class HipBackend(DeviceBackend):
         return t
 
     def tree_attention(self, q, k_cache, v_cache, k_tree, v_tree, anc, scale: float | None = None,
-                       out_dtype=torch.float32, seg2=None, gates=None) -> torch.Tensor:
+                       out_dtype=torch.float32, seg2=None, gates=None, tp=None, window: int = 0,
+                       alibi_slopes=None, alibi_max_keys: int = 1024, force_splits: int = 0,
+                       force_waves: int = 0) -> torch.Tensor:
         """Tree-verify attention (vnx_tree_attn).
 
         q (B, H, N, d); k_cache / v_cache (B, Hkv, Tp, d) or None (Tp = 0);
@@ -445,7 +447,12 @@ class HipBackend(DeviceBackend):
         in out_dtype (torch.float32, torch.bfloat16 or torch.float16).
         seg2 = (k2, v2), each (B or 1, Hkv, T2, d), with gates (2,) adds
         TriSparse's gated global path: out = gates[0] * (the tree attention)
-        + gates[1] * (attention over the T2 rows, all visible)."""
+        + gates[1] * (attention over the T2 rows, all visible).  tp (B,)
+        int32: per-row prefix lengths (ragged caches).  window > 0 keeps
+        keys less than window positions behind each node; alibi_slopes (H,)
+        with gates (3,) adds the ALiBi path as gates[2] * it for rows with
+        tp_b + N <= alibi_max_keys.  force_splits / force_waves pin the launch
+        shape (tuning and tests)."""
         dev = self._torch_device
         qt = self._heads_bf16(q, "q")
         kt = self._heads_bf16(k_tree, "k_tree")
@@ -499,6 +506,27 @@ class HipBackend(DeviceBackend):
         args.B, args.H, args.Hkv, args.Tp, args.N, args.d = B, H, Hkv, Tp, N, d
         args.scale = sc
         keep = []
+        if tp is not None:
+            tpt = _to_tensor(tp, dev, torch.int32).reshape(-1).contiguous()
+            if tpt.numel() != B:
+                raise ValueError(f"tp must have {B} entries")
+            keep.append(tpt)
+            args.tp_batch = tpt.data_ptr()
+        args.window = int(window)
+        args.force_splits, args.force_waves = int(force_splits), int(force_waves)
+        if alibi_slopes is not None:
+            sl = _to_tensor(alibi_slopes, dev, torch.float32).reshape(-1).contiguous()
+            if sl.numel() != H:
+                raise ValueError(f"alibi_slopes must have {H} entries")
+            if gates is None:
+                raise ValueError("the ALiBi path needs three gates")
+            g3 = _to_tensor(gates, dev, torch.float32).reshape(-1).contiguous()
+            if g3.numel() < 3:
+                raise ValueError("gates must hold three values with ALiBi")
+            keep += [sl, g3]
+            args.alibi_slopes = sl.data_ptr()
+            args.alibi_max_keys = int(alibi_max_keys)
+            args.gates = g3.data_ptr()
         if seg2 is not None:
             k2 = self._heads_bf16(seg2[0], "k_seg2")
             v2 = self._heads_bf16(seg2[1], "v_seg2")
@@ -511,12 +539,12 @@ class HipBackend(DeviceBackend):
             g = _to_tensor(gates, dev, torch.float32).reshape(-1).contiguous()
             if g.numel() < 2:
                 raise ValueError("gates must hold two values")
-            keep = [k2, v2, g]
+            keep += [k2, v2, g]
             args.k_seg2, args.v_seg2 = k2.data_ptr(), v2.data_ptr()
             args.seg2_strides[:] = [0 if k2.shape[0] == 1 else k2.stride(0), k2.stride(1), k2.stride(2)]
             args.T2 = k2.shape[2]
             args.gates = g.data_ptr()
-        ws = self._workspace(self._L.vnx_tree_attn_workspace(B, H, Hkv, N, Tp, d))
+        ws = self._workspace(self._L.vnx_tree_attn_workspace_args(ctypes.byref(args)))
         _lib.check(self._L.vnx_tree_attn(ctypes.byref(args), _ptr(ws), ws.numel(),
                                          ctypes.c_void_p(self._stream().cuda_stream)), "tree_attn")
         del keep

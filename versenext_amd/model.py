@@ -520,7 +520,9 @@ class CometSparkGPU:
         self.vc = [torch.zeros((self.B, Hkv, self.cap, d), dtype=dtype, device=dev) for _ in self.layers]
         self._words = {}
         self._neg = torch.full((), -1e9, dtype=torch.float32, device=dev)  # the reference's mask value
-        self.kernel_attention = (dtype == torch.bfloat16 and d in (64, 128) and not cfg.use_alibi)
+        # vnx_tree_attn covers all three paths (window, global rows, ALiBi) for
+        # bf16 heads of 64 / 128
+        self.kernel_attention = dtype == torch.bfloat16 and d in (64, 128)
         # dtype of the activations fed to the projections: fp16 for the INT4
         # GEMVs, else the compute dtype
         self.act_dtype = torch.float16 if int4 else dtype
@@ -565,6 +567,9 @@ class CometSparkGPU:
         a.out = out.data_ptr(); a.out_dtype = _lib.DTYPE_CODES[out.dtype]; a.out_strides[:] = [n * H * d, d, H * d]
         a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, n, d
         a.scale = 1.0 / math.sqrt(d)
+        a.window = self.cfg.window_size
+        if self.cfg.use_alibi:
+            a.alibi_slopes = self.slopes.data_ptr(); a.alibi_max_keys = 1024; a.gates = gates.data_ptr()
         a.tp_batch = tp.data_ptr() if tp is not None else None
         a.tree_follows_prefix = 1 if follows else 0
         if seg2 is not None:
@@ -789,7 +794,7 @@ class CometSparkGPU:
             x = (self.emb[tok].float() * self.emb_scale).contiguous()
         else:
             x = torch.empty((M, D), dtype=torch.float32, device=self.dev)                # fp32 residual stream
-        use_kernel = self.kernel_attention and n <= 64 and Tmax + n <= cfg.window_size
+        use_kernel = self.kernel_attention and n <= 64 and n <= cfg.window_size
         pending = None
         for li, L in enumerate(self.layers):
             # verify-size bf16 forwards: the norms and the residual adds live in
