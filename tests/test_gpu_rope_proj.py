@@ -100,7 +100,10 @@ def _check(x64, W64, lens, cos, sin, q, kc, vc, B, n, H, Hkv, d, rope, cap, rtol
 
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("B,n,H,Hkv,d,K", [(32, 1, 16, 8, 64, 1024), (20, 2, 4, 2, 64, 256), (3, 1, 2, 1, 128, 128),
-                                           (40, 1, 3, 1, 16, 128)])
+                                           (40, 1, 3, 1, 16, 128),
+                                           # (H + 2Hkv) d = 4608 rows: more 16-row tiles than CUs, so
+                                           # the two-tiles-per-workgroup epilogue variant runs
+                                           (8, 1, 56, 8, 64, 512), (24, 1, 56, 8, 64, 1024)])
 def test_gemv_w4_rope_kv(hip, B, n, H, Hkv, d, K, norm):
     """norm: x is fp32 residual rows and RMSNorm(x) * w is fused (the staged
     operand fp16(x * w) as numpy rounds it, rows scaled by the fp64 rstd; the

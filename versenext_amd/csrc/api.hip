@@ -91,19 +91,7 @@ int device_cus() {
   return n;
 }
 
-// VNX_WG_SCALE (a percentage, read once) scales every launch's workgroup
-// target for tuning sweeps; the default is 100.
-int64_t wg_scale_pct() {
-  static const int64_t t = [] {
-    const char* e = getenv("VNX_WG_SCALE");
-    const long long v = e ? atoll(e) : 0;
-    return (int64_t)(v >= 1 && v <= 10000 ? v : 100);
-  }();
-  return t;
-}
-
 int pick_chunks(int64_t rows, int64_t V, int vec_elems, int max_chunks, int64_t target_wgs) {
-  target_wgs = target_wgs * wg_scale_pct() / 100;
   int64_t c = (target_wgs + rows - 1) / rows;
   int64_t max_by_len = V / (256 * (int64_t)vec_elems);
   if (max_by_len < 1) max_by_len = 1;

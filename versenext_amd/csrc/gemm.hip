@@ -49,7 +49,6 @@ struct VgParams {
   int64_t ldx, sxb, swb, ldy, syb, ldc;
   int M, N, K;             // N = rows of W
   int mt, nt, ng;          // 32-row tiles of M and N; N groups of WN tiles
-  int order;               // 0: M tiles of an N group on one XCD; 1: M tiles adjacent
   const float* xf;         // NX: the fp32 rows to normalize (x unused), pitch ldx
   const float* nw;         // NX: RMSNorm weight (K)
   float eps;
@@ -93,15 +92,10 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   const int wn = wave % WN, wk = wave / WN;
   const int z = blockIdx.y;
   const int t = blockIdx.x;
-  int gi, mi;
-  if (p.order == 0) {
-    const int grp = t / (kVgXcds * p.mt), rem = t - grp * (kVgXcds * p.mt);
-    gi = grp * kVgXcds + rem % kVgXcds;
-    mi = rem / kVgXcds;
-  } else {
-    gi = t / p.mt;
-    mi = t - gi * p.mt;
-  }
+  // the M tiles of one N group on one XCD (ids t, t + 8, ...)
+  const int grp = t / (kVgXcds * p.mt), rem = t - grp * (kVgXcds * p.mt);
+  const int gi = grp * kVgXcds + rem % kVgXcds;
+  const int mi = rem / kVgXcds;
   if (gi >= p.ng) return;  // uniform over the workgroup
   const int m0 = mi * 32;
   const int ni = gi * WN + wn;             // this wave's N tile (past nt: computes, never stores)
@@ -127,7 +121,7 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   float old[EPI == 3 ? 16 : 1];
   if constexpr (EPI == 3) {
     if (wk == 0) {
-      const float* yf = reinterpret_cast<const float*>(p.y) + min(ni * 32 + r, p.N - 1);
+      const float* yf = reinterpret_cast<const float*>(p.y) + (int64_t)z * p.syb + min(ni * 32 + r, p.N - 1);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -556,13 +550,8 @@ int vg_run(VgParams p, int batch, int epi, int y_dtype, bool nx, hipStream_t s) 
   int wn = 4;
   while (wn > 1 && (int64_t)p.mt * ((p.nt + wn - 1) / wn) * batch < cus * 3 / 4) wn /= 2;
   p.ng = (p.nt + wn - 1) / wn;
-  static const int order_env = [] {
-    const char* e = getenv("VNX_VG_ORDER");
-    return e ? atoi(e) : 0;
-  }();
-  p.order = order_env == 1 ? 1 : 0;
   const int64_t groups = (p.ng + kVgXcds - 1) / kVgXcds;
-  const int64_t wgs = p.order == 0 ? groups * kVgXcds * p.mt : (int64_t)p.ng * p.mt;
+  const int64_t wgs = groups * kVgXcds * p.mt;
   if (wgs >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
   const dim3 grid((unsigned)wgs, (unsigned)batch);
   auto launch = [&](auto ot, auto ep, auto nxc) {

@@ -733,16 +733,6 @@ static int qgemv_check(const QGemvParams& p, int bits) {
 // columns, and N fills the GPU anyway, else 1), whole K.  Smaller N: the
 // tile kernel, one 16-row tile per workgroup with K split over its waves.
 
-// VNX_QTPW (1 or 4) overrides the tiles per wave for tuning sweeps.
-static int tpw_override() {
-  static const int t = [] {
-    const char* e = getenv("VNX_QTPW");
-    const int v = e ? atoi(e) : 0;
-    return (v == 1 || v == 4) ? v : 0;
-  }();
-  return t;
-}
-
 static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
   if (p.B == 0 || p.N == 0) return VNX_OK;
   // Batch columns in chunks of 32 (two MFMA column blocks) or one of 16.
@@ -773,14 +763,12 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       // workgroup (x loaded once for both; 2.4% of the config-5 round); one
       // group per wave where K has at most 8 groups (no second, zero-weighted
       // group)
-      const bool tp2 = !wide;
       const bool g1 = c.K <= 8 * kGK;
       const dim3 grid2((unsigned)((tiles + 1) / 2));
 #define VNX_QTILE_W(NC, QE, NX) \
   do { \
     if (wide) { if (g1) VNX_QTILE_E1(NC, QE, NX); else VNX_QTILE_E(NC, 8, QE, NX); } \
-    else if (tp2) VNX_QTILE_E2(NC, QE, NX); \
-    else VNX_QTILE_E(NC, 4, QE, NX); \
+    else VNX_QTILE_E2(NC, QE, NX); \
   } while (0)
 #define VNX_QTILE_Q(QE, NX) \
   do { \
@@ -806,7 +794,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
 #undef VNX_QTILE_W
 #undef VNX_QTILE_Q
     } else if (bits == 4 && c.G == kGK && c.sc_f16 && c.lds % 8 == 0 && aligned16(c.sc) &&
-               (c.K == 512 || c.K == 1024) && !getenv("VNX_QSTREAM_OFF")) {
+               (c.K == 512 || c.K == 1024)) {
       // two workgroups per CU (x staged once each), tiles split evenly
       const int64_t tiles = (c.N + 15) / 16;
       const int64_t wgs_target = 2 * device_cus();
@@ -822,7 +810,7 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       else { if (two) VNX_QSTREAM(2, 8); else VNX_QSTREAM(1, 8); }
 #undef VNX_QSTREAM
     } else {
-      const int tpw = tpw_override() ? tpw_override() : (c.B > 16 && c.N >= 256 * kQTargetWgs ? 4 : 1);
+      const int tpw = c.B > 16 && c.N >= 256 * kQTargetWgs ? 4 : 1;
       const dim3 grid((unsigned)((c.N + 64 * tpw - 1) / (64 * tpw)));
 #define VNX_QLAUNCH(BITS, NC, TPW) hipLaunchKernelGGL((k_qgemv<BITS, NC, TPW>), grid, dim3(kQNT), 0, s, c)
       if (bits == 4) {

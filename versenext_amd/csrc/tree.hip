@@ -576,7 +576,7 @@ static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d, int force_spl
   const int KT = (window > 0 && Tp > window - 1 ? window - 1 : Tp) + N;
   const int steps = (KT + 31) / 32;
   const int64_t base = (int64_t)B * Hkv * pl.G;
-  const int64_t target = (int64_t)device_cus() * 4 * wg_scale_pct() / 100;
+  const int64_t target = (int64_t)device_cus() * 4;
   int S = (int)((target + base - 1) / base);
   // A split must carry enough keys to pay for the merge launch: at least 24
   // 32-key steps each (the config-3 sweep: 2 splits of 33 steps beat 4 of

@@ -87,10 +87,6 @@ hipEvent_t* profile_slot(int nphase);
 // Compute units of the current device (cached per device ordinal).
 int device_cus();
 
-// Percentage applied to every launch's workgroup target (VNX_WG_SCALE,
-// default 100; a tuning knob read once).
-int64_t wg_scale_pct();
-
 // Chunks per row for the streaming row kernels: about target_wgs workgroups
 // in the launch, chunks no shorter than one 256-thread x 16-byte pass, at most
 // max_chunks per row.
