@@ -332,6 +332,20 @@ int vnx_gemv_w8(const void* x, int64_t ldx, const int8_t* wq, int64_t ldw, const
                 int64_t B, int64_t N, int64_t K, float* y, int64_t ldy, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* INT4 group-128 quantization on the device (the writer of the format above;
+ * quantize_int4_g of the product's quant.py, restating the group variant of
+ * QuantizedLinear's INT4 path, quantize.py:231-258, with fp16 group scales):
+ * rows w (N, K) in dtype VNX_F32 / VNX_BF16 / VNX_F16, row pitch ldw
+ * elements -> packed (N, K/2) bytes (pitch ldp) and fp16 scales (N, K/128)
+ * (pitch lds); per group s = RN16(RN32(max|w| / 7)) (1/7 for an all-zero
+ * group), q = clamp(rint(w / s), -8, 7).  group must be 128, K a multiple of
+ * it.  bad_groups (device int32, zeroed by the caller; NULL to skip) counts
+ * groups with a non-finite weight or a scale that underflows fp16 (the
+ * host-side quantizer's ValueError).  Used to stream .vn weights into the
+ * GEMV buffers chunk by chunk without a full-precision copy. */
+int vnx_quantize_w4_g(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, int group, uint8_t* packed,
+                      int64_t ldp, void* scales, int64_t lds, int32_t* bad_groups, void* stream);
+
 /* out[n][k] = q[n][k] * s (fp32, one rounded multiply): the weights the GEMV
  * kernels use.  Replaces dequantize_int4 (quantize.py:261-274) and
  * dequantize_int8 (quantize.py:216-224). */

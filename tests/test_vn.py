@@ -1,0 +1,116 @@
+"""The streamed .vn reader (versenext_amd/vn.py) against the libraries that
+define the two weight payloads: every tensor, read in row chunks, equals
+safetensors' own loader (fp32, fp16, bf16, int64) and numpy's .npy reader
+(the npz fallback); VNFileReader's checks (vn_format.py:557-620) hold; the
+config maps to the model's."""
+import json
+import zipfile
+
+import numpy as np
+import pytest
+import torch
+
+from versenext_amd import vn as VN
+from versenext_amd.model import ModelConfig
+from tests.vn_fixture import write_vn
+
+
+def _state(rng):
+    return {
+        "tok_emb.weight": rng.normal(0, 1, (300, 256)).astype(np.float32),
+        "blocks.0.attn.wq.weight": rng.normal(0, 1, (256, 256)).astype(np.float32),
+        "blocks.0.norm1.weight": rng.random(256).astype(np.float32),
+        "blocks.0.attn.gate_logits": np.zeros(3, np.float32),
+        "half": rng.normal(0, 1, (7, 33)).astype(np.float16),
+        "ids": np.arange(10, dtype=np.int64),
+        "scalar": np.array(2.5, np.float32),
+    }
+
+
+def _read_all(path, rows_per_chunk=5):
+    out = {}
+    with VN.VNReader(path) as r:
+        for t in r.tensors():
+            parts = []
+            left = t.rows
+            buf = bytearray(max(1, rows_per_chunk) * t.row_bytes)
+            while left:
+                n = min(rows_per_chunk, left)
+                parts.append(bytes(t.read_into(memoryview(buf), n)))
+                left -= n
+            out[t.name] = (t.dtype, t.shape, b"".join(parts))
+    return out
+
+
+@pytest.mark.parametrize("fmt", ["safetensors", "npz"])
+def test_streamed_tensors_equal_the_library_loaders(tmp_path, fmt):
+    rng = np.random.default_rng(0)
+    st = _state(rng)
+    p = tmp_path / f"m_{fmt}.vn"
+    write_vn(p, st, {"dim": 256}, fmt=fmt)
+    got = _read_all(p)
+    with zipfile.ZipFile(p) as zf:
+        payload = zf.read("model.safetensors" if fmt == "safetensors" else "model.npz")
+    if fmt == "safetensors":
+        from safetensors.numpy import load
+        ref = load(payload)
+    else:
+        import io
+        ref = dict(np.load(io.BytesIO(payload), allow_pickle=False))
+    assert set(got) == set(ref) == set(st)
+    for k, (dt, shape, raw) in got.items():
+        r = ref[k]
+        assert shape == r.shape, k
+        assert raw == np.ascontiguousarray(r).tobytes(), k
+
+
+def test_bf16_payload_equals_safetensors_torch(tmp_path):
+    rng = np.random.default_rng(1)
+    st = {"a": rng.normal(0, 1, (64, 128)).astype(np.float32), "b": rng.normal(0, 1, (5, 128)).astype(np.float32)}
+    p = tmp_path / "bf.vn"
+    write_vn(p, st, {"dim": 128}, bf16_names=("a",))
+    got = _read_all(p, rows_per_chunk=7)
+    with zipfile.ZipFile(p) as zf:
+        from safetensors.torch import load
+        ref = load(zf.read("model.safetensors"))
+    assert got["a"][0] == "BF16" and got["b"][0] == "F32"
+    for k in st:
+        assert got[k][2] == ref[k].contiguous().view(torch.uint8).numpy().tobytes(), k
+
+
+def test_reader_checks_match_the_reference(tmp_path):
+    st = {"w": np.ones((2, 128), np.float32)}
+    ok1 = tmp_path / "v1.vn"
+    write_vn(ok1, st, {"dim": 128}, version=None)        # v1: no version field
+    with VN.VNReader(ok1) as r:
+        assert r.read_meta()["weight_format"] == "safetensors" and r.vn_format_version == 1
+    bad = tmp_path / "v3.vn"
+    write_vn(bad, st, {"dim": 128}, version=3)
+    with pytest.raises(ValueError):
+        VN.VNReader(bad).read_meta()
+    for drop in ("meta", "config", "weights"):
+        q = tmp_path / f"no_{drop}.vn"
+        write_vn(q, st, {"dim": 128}, drop=(drop,))
+        with VN.VNReader(q) as r, pytest.raises(ValueError):
+            if drop == "config":
+                r.read_config()
+            else:
+                list(r.tensors())
+
+
+def test_config_mapping_both_flavours():
+    W = {"blocks.1.ffn.w_gate.weight": VN.Int4Weight(torch.zeros((4096, 512), dtype=torch.uint8),
+                                                      torch.zeros((4096, 8), dtype=torch.float16))}
+    nex = {"vocab_size": 248320, "dim": 1024, "n_layer": 2, "n_head": 16, "n_kv_head": 8,
+           "layer_pattern": ["mod", "trisparse"], "max_seq_len": 2048, "tie_weights": True, "window_size": 1024,
+           "num_global_tokens": 128, "use_alibi": False, "use_rope": True, "rope_theta": 10000.0,
+           "num_dense_parts": 4, "num_experts_per_part": 4, "top_k": 2, "expert_hidden": None}
+    c = VN.config_from_vn(nex, W)
+    assert isinstance(c, ModelConfig) and c.dim == 1024 and not c.embedding_scale and c.ffn_hidden == 4096
+    assert c.layer_pattern == ("mod", "trisparse")
+    v05 = {"arch": "versenex", "vocab_size": 256, "n_layer": 8, "n_embd": 64, "n_head": 4, "n_kv_head": None,
+           "layer_pattern": None, "mod_every": 4, "window_size": 32, "num_global_tokens": 4, "use_alibi": True,
+           "use_rope": False, "embedding_scale": True}
+    c5 = VN.config_from_vn(v05, {})
+    assert c5.dim == 64 and c5.n_kv_head == 4 and c5.embedding_scale
+    assert c5.layer_pattern == ("mod", "trisparse", "trisparse", "trisparse") * 2

@@ -70,6 +70,7 @@ SIGNATURES = {
     "vnx_spec_accept_noalloc": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vnx_gemv_workspace": (_c_sz, [_c_i64, _c_i64, _c_i64]),
+    "vnx_quantize_w4_g": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _int, _vp, _c_i64, _vp, _c_i64, _vp, _vp]),
     "vnx_gemv_w4": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,
                            _vp, _c_i64, _vp, _c_sz, _vp]),
     "vnx_gemv_w4_swiglu": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -28,6 +28,8 @@
 // a group is a permutation shared by A and B, so the dot product is unchanged).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "vnx_internal.h"
 
 namespace vnx {
@@ -827,6 +829,52 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
   return VNX_OK;
 }
 
+// ---------------------------------------------------------------------------
+// INT4 group-128 quantization on the device: the writer of the format the
+// GEMVs read (quantize_int4_g: per group of 128 columns s = RN16(RN32(max|w|
+// / 7)), 1/7 for an all-zero group; q = clamp(rint(w / f32(s)), -8, 7); two q
+// per byte, the even column in the low nibble).  One wave per group, lane l
+// holding columns 2l and 2l + 1: a wave max, then one packed byte per lane.
+// A group with a non-finite weight or a scale that underflows fp16 is
+// counted in *bad (the host turns it into an error).
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float qw_load(const T* p) {
+  if constexpr (std::is_same<T, float>::value) {
+    return *p;
+  } else if constexpr (std::is_same<T, __half>::value) {
+    return __half2float(*p);
+  } else {
+    return __uint_as_float((uint32_t)(*reinterpret_cast<const uint16_t*>(p)) << 16);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_quantize_w4_g(const T* __restrict__ w, int64_t N, int64_t K, int64_t ldw,
+                                                       uint8_t* __restrict__ out, int64_t ldo,
+                                                       __half* __restrict__ sc, int64_t lds, int* bad) {
+  const int lane = threadIdx.x & 63;
+  const int64_t groups = K / kGK;
+  const int64_t gid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gid >= N * groups) return;  // uniform over the wave
+  const int64_t row = gid / groups, g = gid - row * groups;
+  const T* src = w + row * ldw + g * kGK + 2 * lane;
+  const float a0 = qw_load(src), a1 = qw_load(src + 1);
+  const bool nonfinite = !__builtin_isfinite(a0) || !__builtin_isfinite(a1);
+  const float m = wave_max(fmaxf(fabsf(a0), fabsf(a1)));
+  const float safe = m > 0.0f ? m : 1.0f;
+  const __half s16 = __float2half_rn(safe / 7.0f);
+  const float s = __half2float(s16);
+  const int q0 = (int)fminf(fmaxf(rintf(a0 / s), -8.0f), 7.0f);
+  const int q1 = (int)fminf(fmaxf(rintf(a1 / s), -8.0f), 7.0f);
+  out[row * ldo + g * (kGK / 2) + lane] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+  const bool flag = __ballot(nonfinite) != 0 || s == 0.0f;
+  if (lane == 0) {
+    sc[row * lds + g] = s16;
+    if (flag && bad) atomicAdd(bad, 1);
+  }
+}
+
 }  // namespace vnx
 
 using namespace vnx;
@@ -922,6 +970,31 @@ int vnx_dequant_w4(const uint8_t* wq, int64_t ldw, const void* scales, int scale
   const int64_t n = N * K;
   hipLaunchKernelGGL(k_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), p, 4, out, ldo);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_quantize_w4_g(const void* w, int dtype, int64_t N, int64_t K, int64_t ldw, int group, uint8_t* packed,
+                      int64_t ldp, void* scales, int64_t lds, int32_t* bad_groups, void* stream) {
+  if (dtype != VNX_F32 && dtype != VNX_BF16 && dtype != VNX_F16) return VNX_ERR_UNSUPPORTED;
+  if (group != kGK) return VNX_ERR_UNSUPPORTED;
+  if (!w || !packed || !scales || N < 0 || K <= 0 || K % kGK || ldw < K || ldp < K / 2 || lds < K / kGK)
+    return VNX_ERR_INVALID_ARG;
+  if (N == 0) return VNX_OK;
+  const int64_t waves = N * (K / kGK);
+  if ((waves + 3) / 4 >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  __half* sc = static_cast<__half*>(scales);
+  if (dtype == VNX_F32)
+    hipLaunchKernelGGL(k_quantize_w4_g<float>, grid, dim3(256), 0, s, static_cast<const float*>(w), N, K, ldw,
+                       packed, ldp, sc, lds, bad_groups);
+  else if (dtype == VNX_F16)
+    hipLaunchKernelGGL(k_quantize_w4_g<__half>, grid, dim3(256), 0, s, static_cast<const __half*>(w), N, K, ldw,
+                       packed, ldp, sc, lds, bad_groups);
+  else
+    hipLaunchKernelGGL(k_quantize_w4_g<__hip_bfloat16>, grid, dim3(256), 0, s,
+                       static_cast<const __hip_bfloat16*>(w), N, K, ldw, packed, ldp, sc, lds, bad_groups);
   VNX_LAUNCH_CHECK();
   return VNX_OK;
 }

@@ -44,6 +44,7 @@ import torch
 
 from . import _lib
 from . import quant as VQ
+from .vn import Int4Weight
 
 
 # ---------------------------------------------------------------------------
@@ -243,10 +244,21 @@ def rope_rows(heads: int, d: int, blk: int) -> torch.Tensor:
     return (torch.arange(heads).view(-1, 1) * d + blocks.view(1, -1)).reshape(-1)
 
 
-def _deq_int4(w: torch.Tensor, hip) -> torch.Tensor:
-    """fp32 q * s of w quantized to INT4 group 128 with fp16 scales (exact)."""
+def _deq_int4(w, hip) -> torch.Tensor:
+    """fp32 q * s of w quantized to INT4 group 128 with fp16 scales (exact);
+    w a dense tensor or an Int4Weight already in that format."""
+    if isinstance(w, Int4Weight):
+        return hip.dequant_w4(w.wq, w.sc, w.shape[1], 128)
     wq, sc = VQ.quantize_int4_g(w.float(), 128)
     return hip.dequant_w4(wq, sc, w.shape[1], 128)
+
+
+def _cat(ws):
+    """Row concatenation of dense tensors or of Int4Weights (per-row groups,
+    so the packed rows and scales concatenate as they are)."""
+    if isinstance(ws[0], Int4Weight):
+        return Int4Weight.cat(ws)
+    return torch.cat(ws, 0)
 
 
 def _pack(w: torch.Tensor, hip) -> torch.Tensor:
@@ -266,16 +278,17 @@ class _Linear:
     M <= 64 rows and a dequantized copy (bit-exact q * s) for larger M
     (prefill)."""
 
-    def __init__(self, w: torch.Tensor, dtype, hip, int4: bool, swiglu: bool = False, rope_head_dim: int = 0):
+    def __init__(self, w, dtype, hip, int4: bool, swiglu: bool = False, rope_head_dim: int = 0):
         self.N, self.K = w.shape
         self.wq_rope = None
         self.dtype = dtype
         self.hip = hip
-        self.int4 = bool(int4) and self.K % 128 == 0
+        pre = isinstance(w, Int4Weight)  # already quantized (streamed from a .vn file)
+        self.int4 = pre or (bool(int4) and self.K % 128 == 0)
         self.wp = None
         self.swiglu = bool(swiglu) and self.N % 32 == 0
         if self.int4:
-            wq, sc = VQ.quantize_int4_g(w.float(), 128)
+            wq, sc = (w.wq, w.sc) if pre else VQ.quantize_int4_g(w.float(), 128)
             self.wq, self.sc = wq.contiguous(), sc.contiguous()
             if self.swiglu:
                 # rows reordered for vnx_gemv_w4_swiglu: blocks of 8 gate +
@@ -287,7 +300,13 @@ class _Linear:
                 # rows in the order of vnx_gemv_w4_rope_kv's epilogue
                 perm = rope_rows(self.N // rope_head_dim, rope_head_dim, 8).to(wq.device)
                 self.wq_rope, self.sc_rope = wq[perm].contiguous(), sc[perm].contiguous()
-            self.wd = hip.dequant_w4(self.wq, self.sc, self.K, 128).to(dtype)
+            # the dense copy for prefill-size products, dequantized in row
+            # blocks so no fp32 copy of a large matrix (the tied head) exists
+            self.wd = torch.empty((self.N, self.K), dtype=dtype, device=hip.torch_device)
+            rb = max(1, (8 << 20) // (4 * self.K))
+            for r0 in range(0, self.N, rb):
+                r1 = min(self.N, r0 + rb)
+                self.wd[r0:r1] = hip.dequant_w4(self.wq[r0:r1], self.sc[r0:r1], self.K, 128)
             L = hip._L
             self._ws = torch.zeros(max(256, L.vnx_gemv_workspace(64, self.N, self.K)), dtype=torch.uint8,
                                    device=hip.torch_device)
@@ -458,12 +477,21 @@ class CometSparkGPU:
         self.B = int(batch)
         self.cap = int(capacity)
         dev, D, d = self.dev, cfg.dim, cfg.head_dim
-        W = {k: (v if isinstance(v, torch.Tensor) else torch.from_numpy(np.asarray(v))).to(dev, torch.float32)
+        # Int4Weight entries (a .vn file streamed by load_vn_weights) stay as
+        # they are; everything else becomes fp32 on the device
+        W = {k: v if isinstance(v, Int4Weight) else
+             (v if isinstance(v, torch.Tensor) else torch.from_numpy(np.asarray(v))).to(dev, torch.float32)
              for k, v in weights.items()}
-        self.emb = W["tok_emb.weight"].to(dtype).contiguous()
+        E = W["tok_emb.weight"]
+        if isinstance(E, Int4Weight):
+            if not int4:
+                raise ValueError("an INT4 embedding needs int4=True")
+            self.emb = (E.dense if E.dense is not None else _deq_int4(E, hip)).to(dtype).contiguous()
+        else:
+            self.emb = E.to(dtype).contiguous()
         self.emb_scale = math.sqrt(D) if cfg.embedding_scale else 1.0
         self.norm = W["norm.weight"]
-        self.head = _Linear(W["tok_emb.weight"], dtype, hip, int4) if int4 else None
+        self.head = _Linear(E, dtype, hip, int4) if int4 else None
         self.layers = []
         for i, kind in enumerate(cfg.layer_pattern):
             p = f"blocks.{i}."
@@ -476,13 +504,13 @@ class CometSparkGPU:
             gk = (g @ wk_g.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
             gv = (g @ wv_g.t()).reshape(G, cfg.n_kv_head, d).permute(1, 0, 2).unsqueeze(0)
             L = _Layer(kind=kind, norm1=W[p + "norm1.weight"], norm2=W[p + "norm2.weight"],
-                       wqkv=_Linear(torch.cat([wq, wk, wv], 0), dtype, hip, int4,
+                       wqkv=_Linear(_cat([wq, wk, wv]), dtype, hip, int4,
                                     rope_head_dim=d if dtype == torch.bfloat16 and int4 else 0),
                        proj=_Linear(W[p + "attn.proj.weight"], dtype, hip, int4),
                        gk=gk.to(dtype).contiguous(), gv=gv.to(dtype).contiguous(),
                        gates=torch.sigmoid(W[p + "attn.gate_logits"].float()).contiguous())
             if kind == "trisparse":
-                L.ffn["gu"] = _Linear(torch.cat([W[p + "ffn.w_gate.weight"], W[p + "ffn.w_up.weight"]], 0),
+                L.ffn["gu"] = _Linear(_cat([W[p + "ffn.w_gate.weight"], W[p + "ffn.w_up.weight"]]),
                                       dtype, hip, int4, swiglu=True)
                 L.ffn["down"] = _Linear(W[p + "ffn.w_down.weight"], dtype, hip, int4)
             else:
@@ -526,6 +554,27 @@ class CometSparkGPU:
         # dtype of the activations fed to the projections: fp16 for the INT4
         # GEMVs, else the compute dtype
         self.act_dtype = torch.float16 if int4 else dtype
+
+    @classmethod
+    def from_vn(cls, path: str, hip, batch: int, capacity: int, dtype=torch.bfloat16, int4: bool = True,
+                chunk_bytes: int = 64 << 20, cfg: Optional[ModelConfig] = None) -> "CometSparkGPU":
+        """The model saved in a .vn file (CometSparkNexLM.save_vn /
+        CometSparkV05LM.save_vn, cometspark.py:1014-1060; loaded by the
+        reference through VNFileReader, spark/mate/model/model.py:271-285),
+        its weights streamed onto the device: with int4 the projections, the
+        trisparse FFNs and the tied head are quantized chunk by chunk into
+        their INT4 group-128 buffers on the GPU (vnx_quantize_w4_g), never
+        held in full precision.  The untied copy 'head.weight' of a tied
+        model is skipped (the head is the embedding)."""
+        from .vn import VNReader, config_from_vn, int4_matrix, load_vn_weights
+        with VNReader(path) as r:
+            r.read_meta()
+            conf = r.read_config()
+            W = load_vn_weights(r, hip, quantize=int4_matrix if int4 else (lambda n, s: False), dense_dtype=dtype,
+                                chunk_bytes=chunk_bytes, skip=lambda n: n == "head.weight")
+        if cfg is None:
+            cfg = config_from_vn(conf, W, name=f"{path} (.vn)")
+        return cls(cfg, W, hip, batch, capacity, dtype, int4)
 
     # ---- pieces ---------------------------------------------------------
     def _st(self) -> ctypes.c_void_p:
