@@ -491,6 +491,10 @@ def bench_lmhead(args):
 
 
 E2E_B, E2E_K, E2E_T0, E2E_NEW, E2E_TEMP = 32, 6, 512, 256, 0.8
+# final-norm weight scale of the partial-acceptance draft: its logits shrink
+# by this factor, so it puts about 0.7 of its mass on the token both random-
+# init models favour (repeating the current one) instead of ~1.0
+PARTIAL_ALPHA = 0.5
 
 
 def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, seed=0, versenex=False):
@@ -498,7 +502,9 @@ def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, s
     (random init, bf16) and a 2-layer mate-width draft with INT4 group-128
     weights and head, caches for T0 + n_new + 2(k+1) positions.  versenex:
     also a second draft of the same shape without the x sqrt(D) embedding
-    scale (CometSparkNexLM.forward, cometspark.py:670-690)."""
+    scale (CometSparkNexLM.forward, cometspark.py:670-690), and a third whose
+    final-norm weight is scaled by PARTIAL_ALPHA (a flatter draft, so
+    acceptance is partial)."""
     import torch
     from versenext_amd import model as VM
     dev = hip.torch_device
@@ -515,9 +521,13 @@ def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, s
         dcfg2.embedding_scale = False
         dcfg2.name = dcfg.name.replace("VerseNex draft", "VerseNex draft without the embedding scale")
         draft2 = VM.CometSparkGPU(dcfg2, Wd, hip, batch=B, capacity=cap, dtype=torch.bfloat16, int4=True)
+        dcfg3 = VM.mate_draft(draft_layers)
+        dcfg3.name = dcfg.name.replace("VerseNex draft", f"VerseNex draft, final norm x {PARTIAL_ALPHA}")
+        Wd["norm.weight"] = Wd["norm.weight"] * PARTIAL_ALPHA
+        draft3 = VM.CometSparkGPU(dcfg3, Wd, hip, batch=B, capacity=cap, dtype=torch.bfloat16, int4=True)
     del Wd
     torch.cuda.empty_cache()
-    return (target, draft, draft2) if versenex else (target, draft)
+    return (target, draft, draft2, draft3) if versenex else (target, draft)
 
 
 def round_floor_bytes(target, draft, B: int, k: int, ctx: float) -> dict:
@@ -682,7 +692,7 @@ def bench_e2e(args, full: bool = True):
     if not args.no_cpu:
         Wt_host = {k: v.cpu().numpy() for k, v in VM.init_weights(VM.mate_target(), seed=0, device=dev).items()}
         Wd_host = {k: v.cpu().numpy() for k, v in VM.init_weights(VM.mate_draft(2), seed=1, device=dev).items()}
-    target, draft, draft2 = build_e2e(hip, n_new=n_new, versenex=True)
+    target, draft, draft2, draft3 = build_e2e(hip, n_new=n_new, versenex=True)
     build_s = time.perf_counter() - t_build
     g = torch.Generator(device=dev)
     g.manual_seed(30)
@@ -716,9 +726,18 @@ def bench_e2e(args, full: bool = True):
     versenex = {"draft": draft2.cfg.name + ", INT4 g128", "tokens_per_s": round(toks2 / dt2, 1),
                 "ms_per_round": round(dt2 * 1e3 / args.steps, 3),
                 "mean_tokens_per_round_per_seq": round(toks2 / args.steps / E2E_B, 3)}
+    # and with the flatter draft: acceptance between none and all
+    eng3 = SpecDecodeEngine(target, draft3, hip, k=E2E_K, temperature=E2E_TEMP, seed=31,
+                            use_graph=not args.e2e_eager)
+    dt3, toks3, per3, _ = e2e_rounds(eng3, prompts, n_new, args.steps, args.warmup)
+    partial = {"draft": draft3.cfg.name + ", INT4 g128", "tokens_per_s": round(toks3 / dt3, 1),
+               "ms_per_round": round(dt3 * 1e3 / args.steps, 3),
+               "mean_tokens_per_round_per_seq": round(toks3 / args.steps / E2E_B, 3),
+               "acceptance_rate": round((toks3 / args.steps / E2E_B - 1) / E2E_K, 4),
+               "tokens_per_round_min_max": [min(per3), max(per3)]}
     tcfg_name, dcfg_name = target.cfg.name, draft.cfg.name
     prompt0 = prompts[0].cpu().numpy()
-    del eng, eng2, target, draft, draft2
+    del eng, eng2, eng3, target, draft, draft2, draft3
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
 
@@ -727,13 +746,15 @@ def bench_e2e(args, full: bool = True):
                           "unit": "tokens/s", "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": round(ms_round, 3),
                           "mean_tokens_per_round_per_seq": round(toks / args.steps / E2E_B, 3),
-                          "round_floor": floor, "e2e_versenex_draft": versenex}), flush=True)
+                          "round_floor": floor, "e2e_versenex_draft": versenex,
+                          "e2e_partial_accept": partial}), flush=True)
         return
     acc = bench_accept(args, emit=False, inputs=acc_inputs)
     del acc_inputs
     tree = bench_tree(args, emit=False)
     gemv = bench_gemv(args, emit=False)
     c1 = bench_config1(args, emit=False)
+    samp = bench_sampler(args, emit=False)
     out = {"metric": "verified tokens/s (mate target, k=6, bs32)", "value": round(toks / dt, 1),
            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(ms_round, 3), "higher_is_better": True,
@@ -749,17 +770,75 @@ def bench_e2e(args, full: bool = True):
            "mean_tokens_per_round_per_seq": round(toks / args.steps / E2E_B, 3),
            "acceptance_rate": round((toks / args.steps / E2E_B - 1) / E2E_K, 4),
            "round_floor": floor, "generation_256": gen, "e2e_versenex_draft": versenex,
+           "e2e_partial_accept": partial,
            "roofline": acc["roofline"],
            "accept_kernel": {"metric": acc["metric"], "value": acc["value"], "unit": acc["unit"],
                              "workload": acc["config"]["workload"], "frac_of_hbm_peak":
                              acc["config"]["frac_of_hbm_peak"], "ms_per_call": acc["config"]["event_ms_mean"]},
            "config3_tree": {k: tree.get(k) for k in ("value", "unit", "ms_per_step", "results", "cpu_baseline")},
            "config4_gemv": {k: gemv.get(k) for k in ("value", "unit", "results", "cpu_baseline")},
-           "config1": c1}
+           "config1": c1,
+           "sampler": {k: samp.get(k) for k in ("value", "unit", "results", "cpu_baseline")}}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_e2e(Wt_host, Wd_host, prompt0)
         out["cpu_baseline_accept"] = acc.get("cpu_baseline")
     print(json.dumps(out), flush=True)
+
+
+def bench_sampler(args, emit=True):
+    """Sampler.sample on the GPU (vnx_sampler_sample), config-5 batch: 32 rows
+    of 248,320 fp32 logits N(0, 2), T 0.8, three settings: top-k 50 (the
+    radix select), top-p 0.9 (the nucleus), top-k 50 + top-p 0.9; and the
+    CometSpark step (calibration + exactly-k 50).  One workgroup per row
+    streams the row once per pass (about 10 passes, L2-resident after the
+    first); bytes = the row read once, 4 V per row.  CPU: the reference's
+    numpy Sampler (partition, exp / sum, argsort / cumsum / searchsorted,
+    choice) per row, restated in oracle/sampler.py, 8 rows."""
+    import numpy as np
+    import torch
+    from versenext_amd import get_backend, _lib
+    from oracle import sampler as OS
+
+    hip = get_backend("rocm:0")
+    L = _lib.lib()
+    dev = hip.torch_device
+    Bs = E2E_B
+    g = torch.Generator(device=dev)
+    g.manual_seed(41)
+    x = torch.randn((Bs, V), generator=g, device=dev) * 2.0
+    u = torch.rand((Bs,), generator=g, device=dev)
+    ids = torch.empty(Bs, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    st = ctypes.c_void_p(stream.cuda_stream)
+    P = ctypes.c_void_p
+    rows = []
+    nb = 4 * V * Bs
+    settings = [("top_k 50", 50, 1.0, 0), ("top_p 0.9", 0, 0.9, 0), ("top_k 50 + top_p 0.9", 50, 0.9, 0),
+                ("CometSpark: calibrate + exactly-k 50", 50, 1.0, _lib.SAMPLE_EXACT_K | _lib.SAMPLE_CALIBRATE)]
+    for name, k, p, mode in settings:
+        us = _timed(L.vnx_sampler_sample, (P(x.data_ptr()), _lib.VNX_F32, Bs, V, V, 0.8, k, p, mode, 1.2, 1e-8,
+                                           P(u.data_ptr()), P(ids.data_ptr()), None, None, None, None, None, None,
+                                           st), args.steps, args.warmup, stream)
+        rows.append({"setting": name, "us": round(us, 2), "rows_per_s": round(Bs / us * 1e6, 1),
+                     "GB/s": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
+    out = {"metric": "sampled rows/s (config-5 batch, V=248320)", "value": rows[2]["rows_per_s"],
+           "unit": "rows/s", "steps": args.steps, "warmup": args.warmup, "results": rows,
+           "config": {"workload": "Sampler.sample, 32 x 248320 fp32 rows, T 0.8", "bytes_per_call": nb}}
+    if not args.no_cpu:
+        xs = x[:8].cpu().numpy()
+        us_ = u[:8].cpu().numpy()
+        cpu_rows = []
+        for name, k, p, mode in settings[:3]:
+            t0 = time.perf_counter()
+            for b in range(8):
+                OS.sample(xs[b], 0.8, k, p, us_[b])
+            dt = time.perf_counter() - t0
+            cpu_rows.append({"setting": name, "rows_per_s": round(8 / dt, 2)})
+        out["cpu_baseline"] = dict(cpu_env(1), kind="port", value=cpu_rows[2]["rows_per_s"], unit="rows/s",
+                                   results=cpu_rows, sample="8 of the 32 rows, numpy on one thread")
+    if emit:
+        print(json.dumps(out), flush=True)
+    return out
 
 
 def bench_config1(args, emit=True):
@@ -942,7 +1021,7 @@ def main():
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 1 GiB device copy (the known-size kernel that scales PMC counters)")
     ap.add_argument("--workload", default="all",
-                    choices=("all", "e2e", "accept", "gemv", "tree", "lmhead", "config1"),
+                    choices=("all", "e2e", "accept", "gemv", "tree", "lmhead", "config1", "sampler"),
                     help="all: the bench line (config 5 verified tokens/s, the config-2 accept-kernel "
                          "roofline, configs 1, 3 and 4 as extra keys); e2e: config 5 alone; accept: config 2; "
                          "gemv: config 4; tree: config 3; config1: config 1; lmhead: the verify-pass LM head")
@@ -962,6 +1041,9 @@ def main():
         return
     if args.workload == "lmhead":
         bench_lmhead(args)
+        return
+    if args.workload == "sampler":
+        bench_sampler(args)
         return
     if args.workload == "config1":
         bench_config1(args)

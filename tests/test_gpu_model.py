@@ -299,3 +299,23 @@ def test_graph_rounds_match_eager_rounds(hip, gold):
     agree = (res[0] == res[1]).float().mean().item()
     _say(f"graph vs eager greedy agreement {agree:.3f}")
     assert agree >= 0.9
+
+
+def test_verify_forward_is_reproducible(hip):
+    """test_mod_complete.py:451-461 (two eval forwards of the same input agree)
+    on the GPU verify path: the routed MoD expert products, the attention and
+    the head return the same bits when the same rows are verified twice."""
+    cfg = _toy_cfg()
+    W = VM.init_weights(cfg, seed=61)
+    dev = hip.torch_device
+    B = 4
+    m = VM.CometSparkGPU(cfg, W, hip, batch=B, capacity=128, dtype=torch.bfloat16)
+    rng = np.random.default_rng(61)
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    m.forward(torch.from_numpy(rng.integers(0, 1000, (B, 30))).to(dev), lens, 0)
+    lens = torch.tensor([30, 22, 27, 30], dtype=torch.int32, device=dev)
+    new = torch.from_numpy(rng.integers(0, 1000, (B, 7))).to(dev)
+    h1 = m.logits(m.forward(new, lens, 30)).clone()
+    h2 = m.logits(m.forward(new, lens, 30))
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2)
