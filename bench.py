@@ -789,9 +789,11 @@ def bench_sampler(args, emit=True):
     """Sampler.sample on the GPU (vnx_sampler_sample), config-5 batch: 32 rows
     of 248,320 fp32 logits N(0, 2), T 0.8, three settings: top-k 50 (the
     radix select), top-p 0.9 (the nucleus), top-k 50 + top-p 0.9; and the
-    CometSpark step (calibration + exactly-k 50).  One workgroup per row
-    streams the row once per pass (about 10 passes, L2-resident after the
-    first); bytes = the row read once, 4 V per row.  CPU: the reference's
+    CometSpark step (calibration + exactly-k 50).  Each row is split over
+    32 workgroups: with top-k one read of the row and a per-row candidate
+    search (2 launches, 4 with the calibration sums); top-p alone 7 launches,
+    the passes after the first mostly from the L2 / MALL; bytes = the row
+    read once, 4 V per row.  CPU: the reference's
     numpy Sampler (partition, exp / sum, argsort / cumsum / searchsorted,
     choice) per row, restated in oracle/sampler.py, 8 rows."""
     import numpy as np
@@ -815,10 +817,11 @@ def bench_sampler(args, emit=True):
     nb = 4 * V * Bs
     settings = [("top_k 50", 50, 1.0, 0), ("top_p 0.9", 0, 0.9, 0), ("top_k 50 + top_p 0.9", 50, 0.9, 0),
                 ("CometSpark: calibrate + exactly-k 50", 50, 1.0, _lib.SAMPLE_EXACT_K | _lib.SAMPLE_CALIBRATE)]
+    ws = torch.empty(L.vnx_sampler_workspace(Bs, V, _lib.VNX_F32), dtype=torch.uint8, device=dev)
     for name, k, p, mode in settings:
         us = _timed(L.vnx_sampler_sample, (P(x.data_ptr()), _lib.VNX_F32, Bs, V, V, 0.8, k, p, mode, 1.2, 1e-8,
                                            P(u.data_ptr()), P(ids.data_ptr()), None, None, None, None, None, None,
-                                           st), args.steps, args.warmup, stream)
+                                           P(ws.data_ptr()), ws.numel(), st), args.steps, args.warmup, stream)
         rows.append({"setting": name, "us": round(us, 2), "rows_per_s": round(Bs / us * 1e6, 1),
                      "GB/s": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4)})
     out = {"metric": "sampled rows/s (config-5 batch, V=248320)", "value": rows[2]["rows_per_s"],

@@ -155,7 +155,10 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
  * in (p descending, id ascending) order, cutoff = the first position whose
  * cumulative floor(p * 2^60) reaches floor(top_p * 2^60), at most V - 1;
  * the draw is the inverse CDF over the kept p (numpy's Generator.choice
- * rule).  One workgroup per row, no workspace.
+ * rule).  Each row is split over several workgroups (a short chain of
+ * launches: with 0 < top_k <= 256 a candidate search, one read of the row;
+ * the workspace of vnx_sampler_workspace(B, V, dtype) bytes, no
+ * initialisation, holds the candidates, histograms and partials).
  * mode (bit flags) selects the sampling step of CometSparkNexLM's
  * _generate_with_logits (packages/verse_nex/verse_nex/cometspark.py:868-910):
  *   VNX_SAMPLE_CALIBRATE  l -> l / sqrt(var(l) + calib_eps) * calib_factor
@@ -176,10 +179,13 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
 #define VNX_SAMPLE_EXACT_K 1
 #define VNX_SAMPLE_CALIBRATE 2
 
+size_t vnx_sampler_workspace(int64_t B, int64_t V, int dtype);
+
 int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float temperature,
                        int64_t top_k, float top_p, int mode, float calib_factor, float calib_eps,
                        const float* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
-                       float* p_star, int64_t* j_star, int64_t* k_star, void* stream);
+                       float* p_star, int64_t* j_star, int64_t* k_star, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* Logit calibration of VMPC-compressed models
  * (CometSparkNexLM._apply_logit_calibration, packages/verse_nex/verse_nex/

@@ -319,11 +319,13 @@ class HipBackend(DeviceBackend):
                          j_star=torch.empty(B, dtype=torch.int64, device=dev),
                          k_star=torch.empty(B, dtype=torch.int64, device=dev))
         g = (lambda k: _ptr(extra[k])) if extra else (lambda k: None)
+        dt = _LOGIT_DTYPES[lg.dtype]
+        ws = self._workspace(self._L.vnx_sampler_workspace(B, V, dt))
         _lib.check(self._L.vnx_sampler_sample(
-            _ptr(lg), _LOGIT_DTYPES[lg.dtype], B, V, lg.stride(0), float(temperature), int(top_k), float(top_p),
+            _ptr(lg), dt, B, V, lg.stride(0), float(temperature), int(top_k), float(top_p),
             mode, float(calib_factor if calib_factor is not None else 1.0), float(calib_eps),
             _ptr(u), _ptr(ids), g("flags"), g("lse"), g("kth"), g("p_star"), g("j_star"), g("k_star"),
-            ctypes.c_void_p(self._stream().cuda_stream)), "sampler_sample")
+            _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "sampler_sample")
         if return_all:
             return dict(ids=ids, **extra)
         return ids
