@@ -17,14 +17,13 @@
 //              smallest; -0 == +0), takes t = the kth largest of its 256
 //              per-thread maxima (at most its own kth largest key) and
 //              publishes every key >= t with its id.  Every token the global
-//              cut keeps is among them.  The chunk also records numpy.argmax
-//              of the row's (calibrated) logits;
+//              cut keeps is among them;
 //   cand       one 1024-thread workgroup per row, in LDS: the candidates
 //              with key >= the largest chunk threshold (a lower bound of the
 //              row's kth key), sorted by (key desc, id asc); the global cut
 //              (Sampler: a >= kth; exactly-k: argpartition(-a)[:k], ties at
 //              the kth value by lower id), max(a) (not finite: numpy.argmax of
-//              the row), the fp64 LSE and L32 = RN32(LSE), p =
+//              the row, one more read of it), the fp64 LSE and L32 = RN32(LSE), p =
 //              vnx_exp_canon(a - L32), the nucleus (a sort by (p desc, id
 //              asc), exact fixed-point cumulative sums floor(p * 2^60), the
 //              first cutoff + 1 kept), the kept tokens sorted by id, and the
@@ -62,7 +61,7 @@ constexpr int kSNT = 256;              // threads per workgroup (chunk kernels)
 constexpr int kSNW = kSNT / VNX_WAVE;
 constexpr int kST = 1024;              // threads per workgroup (per-row kernels)
 constexpr int kSW = kST / VNX_WAVE;
-constexpr int kSNB = 8;                // vectors in flight per thread
+constexpr int kSNB = 4;                // vectors in flight per thread
 constexpr int kBins = 256;             // 8-bit digits
 constexpr int kSMaxC = 64;             // chunks per row (one wave merges their partials)
 constexpr int64_t kChunkMax = 8192;    // elements per chunk (the local kernel's LDS keys)
@@ -376,11 +375,15 @@ struct RowCtx {
   int64_t jbound;
 };
 
-template <int SM>
+// CAL: the logit calibration (l -> RN(RN(l/s) * f)) is on.
+template <int SM, bool CAL>
 struct RowFns {
   const SampParams& p;
   const RowCtx& r;
-  __device__ __forceinline__ float val(float x) const { return p.calib ? (x / r.sd) * p.cf : x; }
+  __device__ __forceinline__ float val(float x) const {
+    if constexpr (CAL) return (x / r.sd) * p.cf;
+    return x;
+  }
   __device__ __forceinline__ float scaled(float x) const { return tscale<SM>(val(x), p.sc); }
   __device__ __forceinline__ float prob(float x) const { return vnx_exp_canon(scaled(x) - r.L32); }
   __device__ __forceinline__ float weight(int64_t j, float x) const {
@@ -494,8 +497,6 @@ __global__ __launch_bounds__(kSNT) void k_samp_calib(SampParams p) {
 struct LocalLds {
   uint32_t keys[kChunkMax];
   uint32_t mx[kSNT];
-  float f[kSNW];
-  int64_t i[kSNW];
   uint32_t t;
   unsigned n;
 };
@@ -510,7 +511,7 @@ __device__ __forceinline__ unsigned lane_rank(uint64_t m) {
 // t is the kth largest of the 256 per-thread maxima: k threads hold a key
 // >= t, so the chunk holds at least k keys >= t.  For rows of independent
 // logits about k(1 + 1/e) keys pass.
-template <typename Tin, int SM>
+template <typename Tin, int SM, bool CAL>
 __global__ __launch_bounds__(kSNT) void k_samp_local(SampParams p) {
   __shared__ LocalLds L;
   const int64_t b = blockIdx.x / p.C;
@@ -521,15 +522,11 @@ __global__ __launch_bounds__(kSNT) void k_samp_local(SampParams p) {
   const int n = (int)(j1 - j0);  // <= kChunkMax (host plan)
   RowCtx r;
   ctx_init(p, b, r);
-  const RowFns<SM> fn{p, r};
+  const RowFns<SM, CAL> fn{p, r};
   const bool ex = p.exact != 0;
-  float av = kNegInf;
-  int64_t ai = INT64_MAX;
   uint32_t mx = 0u;
   for_range<Tin, kSNT>(row, j0, j1, [&](int64_t j, float x) {
-    const float v = fn.val(x);
-    if (ai == INT64_MAX || argmax_better(v, j, av, ai)) { av = v; ai = j; }
-    const float a = tscale<SM>(v, p.sc);
+    const float a = fn.scaled(x);
     // -0 and +0 one value in both orders (the Sampler rule compares values)
     const uint32_t k = ex ? okey_lo(a) : okey(a + 0.0f);
     L.keys[j - j0] = k;
@@ -537,11 +534,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_local(SampParams p) {
   });
   L.mx[tid] = mx;
   if (tid == 0) L.n = 0u;
-  block_argmax<kSNT>(av, ai, L.f, L.i);  // its barriers publish mx and the keys
-  if (tid == 0) {
-    p.pav[b * p.C + c] = av;
-    p.pai[b * p.C + c] = ai;
-  }
+  __syncthreads();
   if (tid < VNX_WAVE) {
     // the kth largest maximum, bit by bit from the top: the largest t with
     // at least k maxima >= t (t stays 0, every key, when fewer than k)
@@ -585,7 +578,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_local(SampParams p) {
   }
 }
 
-template <typename Tin, int SM>
+template <typename Tin, int SM, bool CAL>
 __global__ __launch_bounds__(kSNT) void k_samp_lse(SampParams p) {
   __shared__ SampLds L;
   const int64_t b = blockIdx.x / p.C;
@@ -594,7 +587,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_lse(SampParams p) {
   const int64_t j0 = c * p.clen, j1 = min(j0 + p.clen, p.V);
   RowCtx r;
   ctx_init(p, b, r);
-  const RowFns<SM> fn{p, r};
+  const RowFns<SM, CAL> fn{p, r};
   // chunk max (NaN -> +inf) and numpy.argmax of the (calibrated) row
   float M = kNegInf, av = kNegInf;
   bool nan = false;
@@ -627,7 +620,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_lse(SampParams p) {
   }
 }
 
-template <typename Tin, int SM, int PASS>
+template <typename Tin, int SM, bool CAL, int PASS>
 __global__ __launch_bounds__(kSNT) void k_samp_ppass(SampParams p) {
   __shared__ SampLds L;
   const int64_t b = blockIdx.x / p.C;
@@ -639,7 +632,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_ppass(SampParams p) {
   ctx_init(p, b, r);
   ctx_lse(p, b, r, L);
   if (r.fallback) return;  // uniform over the workgroup
-  const RowFns<SM> fn{p, r};
+  const RowFns<SM, CAL> fn{p, r};
   RadixState s = p.stp[b * 5 + (PASS > 0 ? PASS - 1 : 0)];
   if (PASS > 0) {
     s = p_step(s, PASS - 1, p.phm + (b * 4 + PASS - 1) * kBins, L);
@@ -675,7 +668,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_ppass(SampParams p) {
   if (PASS == 3) p.lp[(b * p.C + c) * kBins + t] = cn;
 }
 
-template <typename Tin, int SM>
+template <typename Tin, int SM, bool CAL>
 __global__ __launch_bounds__(kSNT) void k_samp_mass(SampParams p) {
   __shared__ SampLds L;
   extern __shared__ double sh_m[];  // the draw: the row's sub-block masses
@@ -690,7 +683,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_mass(SampParams p) {
   RowCtx r;
   ctx_init(p, b, r);
   if (!p.greedy) ctx_lse(p, b, r, L);
-  const RowFns<SM> fn{p, r};
+  const RowFns<SM, CAL> fn{p, r};
   const bool draw = !p.greedy && !r.fallback;
   if (draw && p.use_p) {
     RadixState s = p_step(p.stp[b * 5 + 3], 3, p.phm + (b * 4 + 3) * kBins, L);
@@ -1450,12 +1443,18 @@ __global__ __launch_bounds__(kST) void k_samp_cand(SampParams p) {
   }
   M = block_max<kST>(nan ? kPosInf : M, L.f);
   if (!(M > kNegInf && M < kPosInf)) {
-    // np.max not finite: numpy.argmax of the row (the local kernel's partials)
-    int64_t am = 0;
-    if (tid < VNX_WAVE) am = merged_argmax(p, b);
-    if (tid == 0) L.token = am;
-    __syncthreads();
-    row_finish(p, b, L.token, 0, __builtin_nanf(""), thr, -1.0f, -1, kstar);
+    // np.max not finite: numpy.argmax of the (calibrated) row
+    const Tin* row = static_cast<const Tin*>(p.x) + b * p.ld;
+    const bool cal = p.calib != 0;
+    const float cf = p.cf;
+    float bv = kNegInf;
+    int64_t bi = INT64_MAX;
+    for_range<Tin, kST>(row, 0, p.V, [&](int64_t j, float x) {
+      const float v = cal ? (x / sd) * cf : x;
+      if (bi == INT64_MAX || argmax_better(v, j, bv, bi)) { bv = v; bi = j; }
+    });
+    block_argmax<kST>(bv, bi, L.f, L.i);
+    row_finish(p, b, bi == INT64_MAX ? 0 : bi, 0, __builtin_nanf(""), thr, -1.0f, -1, kstar);
     return;
   }
   const float mt = mt_of(M);
@@ -1764,24 +1763,29 @@ int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int6
   return dispatch_tsm(dtype, sm, false, [&](auto tin, auto smc, auto) {
     using Tin = decltype(tin);
     constexpr int SM = decltype(smc)::value;
-    if (p.calib) {
-      hipLaunchKernelGGL((k_samp_calib<Tin, 0>), grid, blk, 0, s, p);
-      hipLaunchKernelGGL((k_samp_calib<Tin, 1>), grid, blk, 0, s, p);
-    }
-    if (cand) {
-      p.single = !local;
-      if (local) hipLaunchKernelGGL((k_samp_local<Tin, SM>), grid, blk, 0, s, p);
-      hipLaunchKernelGGL((k_samp_cand<Tin, SM>), dim3((unsigned)B), dim3(kST), 0, s, p);
-    } else {
-      hipLaunchKernelGGL((k_samp_lse<Tin, SM>), grid, blk, 0, s, p);
-      if (p.use_p && !p.greedy) {
-        hipLaunchKernelGGL((k_samp_ppass<Tin, SM, 0>), grid, blk, 0, s, p);
-        hipLaunchKernelGGL((k_samp_ppass<Tin, SM, 1>), grid, blk, 0, s, p);
-        hipLaunchKernelGGL((k_samp_ppass<Tin, SM, 2>), grid, blk, 0, s, p);
-        hipLaunchKernelGGL((k_samp_ppass<Tin, SM, 3>), grid, blk, 0, s, p);
+    auto run = [&](auto calc) {
+      constexpr bool CAL = decltype(calc)::value;
+      if (CAL) {
+        hipLaunchKernelGGL((k_samp_calib<Tin, 0>), grid, blk, 0, s, p);
+        hipLaunchKernelGGL((k_samp_calib<Tin, 1>), grid, blk, 0, s, p);
       }
-      hipLaunchKernelGGL((k_samp_mass<Tin, SM>), grid, blk, (size_t)pl.nsb * sizeof(double), s, p);
-    }
+      if (cand) {
+        p.single = !local;
+        if (local) hipLaunchKernelGGL((k_samp_local<Tin, SM, CAL>), grid, blk, 0, s, p);
+        hipLaunchKernelGGL((k_samp_cand<Tin, SM>), dim3((unsigned)B), dim3(kST), 0, s, p);
+      } else {
+        hipLaunchKernelGGL((k_samp_lse<Tin, SM, CAL>), grid, blk, 0, s, p);
+        if (p.use_p && !p.greedy) {
+          hipLaunchKernelGGL((k_samp_ppass<Tin, SM, CAL, 0>), grid, blk, 0, s, p);
+          hipLaunchKernelGGL((k_samp_ppass<Tin, SM, CAL, 1>), grid, blk, 0, s, p);
+          hipLaunchKernelGGL((k_samp_ppass<Tin, SM, CAL, 2>), grid, blk, 0, s, p);
+          hipLaunchKernelGGL((k_samp_ppass<Tin, SM, CAL, 3>), grid, blk, 0, s, p);
+        }
+        hipLaunchKernelGGL((k_samp_mass<Tin, SM, CAL>), grid, blk, (size_t)pl.nsb * sizeof(double), s, p);
+      }
+    };
+    if (p.calib) run(BoolC<true>{});
+    else run(BoolC<false>{});
     VNX_LAUNCH_CHECK();
     return (int)VNX_OK;
   });
