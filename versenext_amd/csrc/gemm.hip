@@ -321,6 +321,7 @@ struct XgParams {
   int64_t ldx, sxb, swb, ldy, syb, ldc;
   int M, N, K, E;
   int nt, ng;
+  int xcd_group;           // the workgroups of one expert on one XCD
 };
 
 constexpr int kXgRows = 128;  // rows per pass
@@ -337,12 +338,22 @@ __global__ __launch_bounds__(256) void k_xgemm(XgParams p) {
   __shared__ unsigned long long wmask[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WN, wk = wave / WN;
-  // expert-major order: consecutive workgroups (dealt round-robin over the
-  // XCDs) are N groups of one expert, so every XCD gets an even share of the
-  // work however unevenly the rows are routed (giving each XCD whole experts
-  // measured up to 1.6x slower under skewed routing)
-  const int z = blockIdx.x / p.ng;
-  const int gi = blockIdx.x % p.ng;
+  // Workgroup t runs on XCD t % 8 (the dispatcher deals them round-robin;
+  // gridDim.x is a multiple of 8 whenever xcd_group is set).  xcd_group:
+  // the N groups of experts x, x + 8, ... run on XCD x, so each expert's X
+  // rows are fetched into one L2 only (balanced routing, MoD's training
+  // target).  Otherwise expert-major order: consecutive workgroups are N
+  // groups of one expert, spread over every XCD, which keeps an even share
+  // per XCD however unevenly the rows are routed.
+  int z, gi;
+  if (p.xcd_group) {
+    const int t = blockIdx.x, slot = t >> 3;
+    z = (t & 7) + 8 * (slot / p.ng);
+    gi = slot % p.ng;
+  } else {
+    z = blockIdx.x / p.ng;
+    gi = blockIdx.x % p.ng;
+  }
 
   int cnt;
   if constexpr (ROUTE) {
@@ -690,6 +701,9 @@ int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_
   const int64_t cus = device_cus();
   const int wn = (int64_t)((p.nt + 3) / 4) * experts >= cus ? 4 : 2;
   p.ng = (p.nt + wn - 1) / wn;
+  // the down product (its X rows are K = expert hidden wide) groups an
+  // expert's workgroups on one XCD; the routed gate-up keeps them spread
+  p.xcd_group = (experts % 8 == 0 && route == 0) ? 1 : 0;
   const int64_t wgs = (int64_t)experts * p.ng;
   const int64_t passes = (M + kXgRows - 1) / kXgRows;
   if (wgs >= INT32_MAX || passes > 65535) return VNX_ERR_UNSUPPORTED;
