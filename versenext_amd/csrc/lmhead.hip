@@ -32,10 +32,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kLhWaves = 4;
-constexpr int kLhThreads = 64 * kLhWaves;
-constexpr int kLhTiles = 2;                        // 32-row A tiles per wave
-constexpr int kLhRows = 32 * kLhTiles * kLhWaves;  // vocab rows per workgroup (256)
+constexpr int kLhRows = 256;                       // vocab rows per workgroup
 constexpr int kLhSlab = 64;                        // k per slab (four MFMA k steps)
 constexpr int kLhPitch = kLhSlab + 8;              // LDS row pitch of X (bf16)
 constexpr int kLhOutPitch = kLhRows + 4;           // LDS row pitch of the output tile (fp32)
@@ -65,9 +62,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 }
 
 // MT: 32-column position tiles (M <= 32*MT); RING: W slabs held in registers
-// (RING - 1 in flight ahead of the math), a divisor of K / 64.
-template <int MT, int RING, bool OUT_BF16>
-__global__ __launch_bounds__(kLhThreads, 1) void k_lm_head(LhParams p) {
+// (RING - 1 in flight ahead of the math), a divisor of K / 64; WAVES x TILES
+// = 8: waves per workgroup and 32-row A tiles per wave (4 x 2: one wave per
+// SIMD, each X fragment feeding two MFMAs; 8 x 1: two waves per SIMD).
+template <int MT, int RING, bool OUT_BF16, int WAVES, int TILES>
+__global__ __launch_bounds__(64 * WAVES, WAVES / 4) void k_lm_head(LhParams p) {
+  static_assert(WAVES * TILES * 32 == kLhRows, "a workgroup covers kLhRows vocab rows");
+  constexpr int kLhThreads = 64 * WAVES;
+  constexpr int kLhTiles = TILES;
   constexpr size_t kXBytes = size_t(2) * MT * 32 * kLhPitch * 2;
   constexpr size_t kOBytes = size_t(32) * kLhOutPitch * 4;
   __shared__ __align__(16) char smem[kXBytes > kOBytes ? kXBytes : kOBytes];
@@ -188,14 +190,15 @@ __global__ __launch_bounds__(kLhThreads, 1) void k_lm_head(LhParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 v = {acc[t][m][4 * i], acc[t][m][4 * i + 1], acc[t][m][4 * i + 2], acc[t][m][4 * i + 3]};
-        *reinterpret_cast<f32x4*>(so + r32 * kLhOutPitch + w * 64 + t * 32 + 8 * i + 4 * h) = v;
+        *reinterpret_cast<f32x4*>(so + r32 * kLhOutPitch + w * (32 * kLhTiles) + t * 32 + 8 * i + 4 * h) = v;
       }
     __syncthreads();
     if constexpr (OUT_BF16) {
-      // 32 positions x 256 values = 4 passes of 8 rows; a thread converts 8 values.
+      // 32 positions x 256 values in passes of kLhThreads / 32 rows; a thread converts 8 values.
+      constexpr int RPP = kLhThreads / 32;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int rr = q * 8 + (tid >> 5), c = (tid & 31) * 8;
+      for (int q = 0; q < 32 / RPP; ++q) {
+        const int rr = q * RPP + (tid >> 5), c = (tid & 31) * 8;
         const int r = m * 32 + rr;
         const int64_t n = nw + c;
         if (r < p.M && n < p.V) {
@@ -214,10 +217,11 @@ __global__ __launch_bounds__(kLhThreads, 1) void k_lm_head(LhParams p) {
         }
       }
     } else {
-      // 32 positions x 256 values = 8 passes of 4 rows; a thread writes 4 values.
+      // 32 positions x 256 values in passes of kLhThreads / 64 rows; a thread writes 4 values.
+      constexpr int RPP = kLhThreads / 64;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int rr = q * 4 + (tid >> 6), c = (tid & 63) * 4;
+      for (int q = 0; q < 32 / RPP; ++q) {
+        const int rr = q * RPP + (tid >> 6), c = (tid & 63) * 4;
         const int r = m * 32 + rr;
         const int64_t n = nw + c;
         if (r < p.M && n < p.V) {
@@ -235,13 +239,16 @@ __global__ __launch_bounds__(kLhThreads, 1) void k_lm_head(LhParams p) {
   }
 }
 
+constexpr int kLhWaves = 8;  // 8 x 1 (two waves per SIMD) or 4 x 2
+
 template <int MT, int RING>
 void launch_ring(const LhParams& p, bool bf16_out, hipStream_t s) {
+  constexpr int TILES = 8 / kLhWaves;
   const dim3 grid((unsigned)((p.V + kLhRows - 1) / kLhRows));
   if (bf16_out)
-    hipLaunchKernelGGL((k_lm_head<MT, RING, true>), grid, dim3(kLhThreads), 0, s, p);
+    hipLaunchKernelGGL((k_lm_head<MT, RING, true, kLhWaves, TILES>), grid, dim3(64 * kLhWaves), 0, s, p);
   else
-    hipLaunchKernelGGL((k_lm_head<MT, RING, false>), grid, dim3(kLhThreads), 0, s, p);
+    hipLaunchKernelGGL((k_lm_head<MT, RING, false, kLhWaves, TILES>), grid, dim3(64 * kLhWaves), 0, s, p);
 }
 
 // The ring depth divides the slab count: 4 when it can (3 slabs in flight;
