@@ -486,7 +486,7 @@ def bench_lmhead(args):
                       "config": {"workload": "config 5 verify pass: tied LM head over B*(k+1) = 224 rows"},
                       "roofline": {"bound": "hbm", "achieved": main_row["GB/s"], "peak": HBM_PEAK_GBS,
                                    "unit": "GB/s", "frac": main_row["frac_hbm"], "traffic": None,
-                                   "kernel": "k_lm_head<14, false>"},
+                                   "kernel": "k_lm_head<7, 4, false, 8, 1>"},
                       "results": rows}), flush=True)
 
 
