@@ -169,6 +169,25 @@ def test_exact_k_with_ties_split_at_the_kth_value(hip):
     _check(hip, xb, 0.7, 100, 1.0, u, dtype=torch.bfloat16, exact_k=True)
 
 
+def test_top_k_outside_the_candidate_search(hip):
+    """The single-workgroup form behind the candidate search: rows longer than
+    64 chunks of 8192 logits, and rows whose ties at the chunk thresholds
+    overflow the candidate segments (a flat row with a few larger values)."""
+    rng = np.random.default_rng(51)
+    xw = rng.normal(0, 2.0, (2, 600_000)).astype(np.float32)
+    uw = rng.random(2).astype(np.float32)
+    for (T, k, p, ex) in ((0.8, 50, 1.0, False), (0.8, 50, 0.9, False), (1.0, 40, 1.0, True)):
+        ids, flags, bad = _check(hip, xw, T, k, p, uw, exact_k=ex)
+        assert bad == 0 or (flags != 0).any(), (T, k, p, ex)
+    xf = np.ones((3, V), np.float32)
+    xf[:, rng.choice(V, 10, replace=False)] = 2.0
+    xf[2, :1000] = 0.5
+    uf = rng.random(3).astype(np.float32)
+    for (T, k, p, ex) in ((1.0, 50, 1.0, False), (1.0, 50, 1.0, True), (0.9, 20, 0.5, False)):
+        ids, flags, bad = _check(hip, xf, T, k, p, uf, exact_k=ex)
+        assert bad == 0 or (flags != 0).any(), (T, k, p, ex)
+
+
 def test_fused_calibration_matches_oracle(hip):
     """VNX_SAMPLE_CALIBRATE: the CometSpark step (calibrate, then greedy or
     exactly-k sampling) and the Sampler rules on calibrated rows."""
