@@ -494,7 +494,7 @@ E2E_B, E2E_K, E2E_T0, E2E_NEW, E2E_TEMP = 32, 6, 512, 256, 0.8
 # final-norm weight scale of the partial-acceptance draft: its logits shrink
 # by this factor, so it puts about 0.7 of its mass on the token both random-
 # init models favour (repeating the current one) instead of ~1.0
-PARTIAL_ALPHA = 0.5
+PARTIAL_ALPHA = 0.6
 
 
 def build_e2e(hip, B=E2E_B, k=E2E_K, T0=E2E_T0, n_new=E2E_NEW, draft_layers=2, seed=0, versenex=False):
