@@ -28,7 +28,8 @@
 //              asc), exact fixed-point cumulative sums floor(p * 2^60), the
 //              first cutoff + 1 kept), the kept tokens sorted by id, and the
 //              draw (numpy's Generator.choice rule: first j with
-//              C_j > u * C_V, fp64 sums).
+//              C_j > u * C_V, fp64 sums); with at most 64 survivors one wave
+//              does all of it in registers.
 //              A row whose candidates overflow (many ties at a threshold),
 //              a larger k or a longer row runs the whole algorithm over the
 //              row in the same workgroup instead (single-workgroup form).
@@ -1276,6 +1277,119 @@ __device__ __forceinline__ void lds_sort(unsigned long long* a, int n, bool desc
   }
 }
 
+// Bitonic sort of one u64 per lane across a wave (ascending, or descending
+// when desc): register exchanges only.
+__device__ __forceinline__ unsigned long long wave_sort_u64(unsigned long long v, bool desc) {
+  const int l = threadIdx.x % VNX_WAVE;
+#pragma unroll
+  for (int k = 2; k <= VNX_WAVE; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const unsigned long long o = __shfl_xor(v, j, VNX_WAVE);
+      const bool up = ((l & k) == 0) != desc;  // this pair's order: ascending
+      const bool take_min = ((l & j) == 0) == up;
+      v = take_min ? (o < v ? o : v) : (o > v ? o : v);
+    }
+  return v;
+}
+
+__device__ __forceinline__ unsigned long long wave_scan_u64(unsigned long long v) {
+  const int l = threadIdx.x % VNX_WAVE;
+#pragma unroll
+  for (int o = 1; o < VNX_WAVE; o <<= 1) {
+    const unsigned long long n = __shfl_up(v, o, VNX_WAVE);
+    if (l >= o) v += n;
+  }
+  return v;
+}
+
+// The per-row step after the compaction when at most 64 candidates remain
+// (the usual case for small k): the cut, LSE, nucleus and draw of the
+// workgroup form, in one wave with register exchanges instead of LDS sorts
+// and barriers.  Returns true when max(a) is not finite (the caller then
+// takes numpy.argmax of the row; thr and k* are left in L.f[0] / L.i[0]).
+__device__ __forceinline__ bool cand_wave(const SampParams& p, int64_t b, int n, CandLds& L) {
+  const int lane = threadIdx.x % VNX_WAVE;
+  const bool ex = p.exact != 0;
+  // (key << 32 | ~id), descending: key descending, id ascending
+  unsigned long long e = lane < n ? L.a[lane] : 0ull;
+  e = wave_sort_u64(e, true);
+  const int kk = (int)p.top_k;  // <= n
+  const unsigned long long ek = __shfl(e, kk - 1, VNX_WAVE);
+  const uint32_t tkey = (uint32_t)(ek >> 32);
+  const float thr = okey_value(tkey);
+  const int64_t kstar = ex ? (int64_t)(0xFFFFFFFFu - (uint32_t)ek) : -1;
+  const uint32_t id = 0xFFFFFFFFu - (uint32_t)e;
+  const float a = okey_value((uint32_t)(e >> 32));  // -0 read as +0: the same value
+  const bool keep = lane < n && (ex ? lane < kk : a >= thr);
+  const bool anynan = __ballot(keep && __builtin_isnan(a)) != 0;
+  const float M = anynan ? kPosInf : wave_max(keep ? a : kNegInf);
+  if (!(M > kNegInf && M < kPosInf)) {
+    if (lane == 0) {
+      L.f[0] = thr;
+      L.i[0] = kstar;
+    }
+    return true;
+  }
+  double sd = keep ? (double)exp2_term(a, mt_of(M)) : 0.0;
+  sd = wave_sum(sd);
+  RowCtx rc;
+  rc.fl = 0;
+  set_l32(rc, lse_of(M, sd));
+  const float L32 = rc.L32;
+  int fl = rc.fl;
+  const float pp = keep ? vnx_exp_canon(a - L32) : 0.0f;
+  // kept tokens: a prefix of the sorted order (keys >= the kth, or the first k)
+  const int nk = __builtin_popcountll(__ballot(keep));
+  int ncut = nk;
+  float pstar = -1.0f;
+  int64_t jstar = -1;
+  unsigned long long d;  // the draw's entries (id << 32 | p bits), ascending
+  if (p.use_p) {
+    // (p desc, id asc), exact fixed-point prefix sums, the first to reach top_p
+    unsigned long long q = keep ? ((unsigned long long)__float_as_uint(pp) << 32) | (0xFFFFFFFFu - id) : 0ull;
+    q = wave_sort_u64(q, true);
+    const float pq = __uint_as_float((uint32_t)(q >> 32));
+    const unsigned long long incl = wave_scan_u64(lane < nk ? fix60(pq) : 0ull);
+    const uint64_t reach = __ballot(lane < nk && incl >= p.p_target);
+    if (reach) {
+      const int cut = __builtin_ctzll(reach);
+      ncut = cut + 1;
+      const unsigned long long qc = __shfl(q, cut, VNX_WAVE);
+      pstar = __uint_as_float((uint32_t)(qc >> 32));
+      jstar = (int64_t)(0xFFFFFFFFu - (uint32_t)qc);
+    }
+    d = lane < ncut ? ((unsigned long long)(0xFFFFFFFFu - (uint32_t)q) << 32) | (q >> 32) : ~0ull;
+  } else {
+    d = keep ? ((unsigned long long)id << 32) | __float_as_uint(pp) : ~0ull;
+  }
+  d = wave_sort_u64(d, false);
+  const float w = lane < ncut ? __uint_as_float((uint32_t)d) : 0.0f;
+  const double incl = wave_inclusive_scan((double)w);
+  const double total = __shfl(incl, VNX_WAVE - 1, VNX_WAVE);
+  const double target = (double)p.u[b] * total;
+  int64_t token = 0;
+  if (!(total > 0.0)) {
+    fl |= VNX_FLAG_ZERO_RESIDUAL;
+  } else {
+    const double before = incl - (double)w;
+    const uint64_t hits = __ballot(w > 0.0f && before <= target && target < incl);
+    int pick;
+    if (hits) {
+      pick = __builtin_ctzll(hits);
+    } else {
+      pick = 63 - __builtin_clzll(__ballot(w > 0.0f));  // rounding left the target past every weight
+      fl |= VNX_FLAG_CDF_EDGE;
+    }
+    const double tol = 1e-12 * total;
+    const bool edge = (target - before < tol || incl - target < tol);
+    if (__shfl((int)edge, pick, VNX_WAVE)) fl |= VNX_FLAG_CDF_EDGE;
+    token = (int64_t)(__shfl(d, pick, VNX_WAVE) >> 32);
+  }
+  row_finish(p, b, token, fl, L32, thr, pstar, jstar, kstar);
+  return false;
+}
+
 __device__ __forceinline__ int pow2_at_least(int n) {
   int m = 1;
   while (m < n) m <<= 1;
@@ -1404,6 +1518,30 @@ __global__ __launch_bounds__(kST) void k_samp_cand(SampParams p) {
     __syncthreads();
   }
   const int n = (int)L.n;  // >= k
+  if (n <= VNX_WAVE) {
+    // one wave finishes the row; the others wait only for the rare argmax
+    if (tid < VNX_WAVE) {
+      const bool fb = cand_wave(p, b, n, L);
+      if (tid == 0) L.hit = fb ? 1 : 0;
+    }
+    __syncthreads();
+    if (!L.hit) return;  // uniform
+    const float thr = L.f[0];
+    const int64_t kstar = L.i[0];
+    __syncthreads();
+    const Tin* row = static_cast<const Tin*>(p.x) + b * p.ld;
+    const bool cal = p.calib != 0;
+    const float cf = p.cf;
+    float bv = kNegInf;
+    int64_t bi = INT64_MAX;
+    for_range<Tin, kST>(row, 0, p.V, [&](int64_t j, float x) {
+      const float v = cal ? (x / sd) * cf : x;
+      if (bi == INT64_MAX || argmax_better(v, j, bv, bi)) { bv = v; bi = j; }
+    });
+    block_argmax<kST>(bv, bi, L.f, L.i);
+    row_finish(p, b, bi == INT64_MAX ? 0 : bi, 0, __builtin_nanf(""), thr, -1.0f, -1, kstar);
+    return;
+  }
   const int np = pow2_at_least(n);
   // sort key: (cut key << 32) | ~id, descending = key descending, id ascending
   for (int i = n + tid; i < np; i += kST) L.a[i] = 0ull;
