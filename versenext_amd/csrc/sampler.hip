@@ -38,7 +38,8 @@
 //              2^(a*log2e - mt), and numpy.argmax of the row;
 //   ppass 0..3 (top-p) every workgroup merges the C LSE partials (one wave,
 //              fixed order) into L32 and radix-selects the nucleus value p*
-//              over the keys of p with (count, fixed-point mass) histograms,
+//              over the keys of p with fixed-point mass histograms (the last
+//              pass also counts per chunk, for ranking the ties),
 //              one 8-bit digit per launch: per-wave LDS histograms, nonzero
 //              bins added to the row's global histogram, the digit derived by
 //              the next launch (a block scan) and recorded by its chunk 0;
@@ -100,7 +101,6 @@ struct SampParams {
   int64_t* j_star;
   int64_t* k_star;
   // workspace
-  uint32_t* phc;              // [B][4][256]
   unsigned long long* phm;    // [B][4][256]
   uint32_t* lp;               // [B][C][256] the last p pass's per-chunk counts
   RadixState* stp;            // [B][5] top-p state before pass i
@@ -462,10 +462,7 @@ __device__ __forceinline__ int64_t merged_argmax(const SampParams& p, int64_t b)
 __global__ __launch_bounds__(kSNT) void k_samp_init(SampParams p) {
   const int64_t b = blockIdx.x;
   const int t = threadIdx.x;
-  for (int i = t; i < 4 * kBins; i += kSNT) {
-    p.phc[b * 4 * kBins + i] = 0u;
-    p.phm[b * 4 * kBins + i] = 0ull;
-  }
+  for (int i = t; i < 4 * kBins; i += kSNT) p.phm[b * 4 * kBins + i] = 0ull;
   if (t == 0) {
     p.cnt[b] = 0u;
     p.stp[b * 5] = RadixState{0u, 0u, (unsigned long long)p.p_target, 0, 0};
@@ -651,7 +648,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_ppass(SampParams p) {
     const uint32_t k = __float_as_uint(pp);
     if ((k & s.pmask) == s.prefix) {
       const int d = (k >> shift) & 0xFFu;
-      atomicAdd(&L.hc[wave][d], 1u);
+      if (PASS == 3) atomicAdd(&L.hc[wave][d], 1u);  // the last digit's ties are ranked by count
       atomicAdd(&L.hm[wave][d], fix60(pp));
     }
   });
@@ -661,10 +658,9 @@ __global__ __launch_bounds__(kSNT) void k_samp_ppass(SampParams p) {
   unsigned long long m = 0;
 #pragma unroll
   for (int w = 0; w < kSNW; ++w) {
-    cn += L.hc[w][t];
+    if (PASS == 3) cn += L.hc[w][t];
     m += L.hm[w][t];
   }
-  if (cn) atomicAdd(p.phc + (b * 4 + PASS) * kBins + t, cn);
   if (m) atomicAdd(p.phm + (b * 4 + PASS) * kBins + t, m);
   if (PASS == 3) p.lp[(b * p.C + c) * kBins + t] = cn;
 }
@@ -1815,7 +1811,6 @@ static SampPlan samp_plan(int64_t B, int64_t V, int dtype, bool local) {
 static size_t samp_carve(void* ws, int64_t B, const SampPlan& pl, SampParams* p) {
   Carve cv(ws);
   const size_t nb = (size_t)B * 4 * kBins, nc = (size_t)B * pl.C;
-  uint32_t* phc = cv.take<uint32_t>(nb);
   unsigned long long* phm = cv.take<unsigned long long>(nb);
   uint32_t* lp = cv.take<uint32_t>(nc * kBins);
   RadixState* stp = cv.take<RadixState>((size_t)B * 5);
@@ -1832,7 +1827,7 @@ static size_t samp_carve(void* ws, int64_t B, const SampPlan& pl, SampParams* p)
   unsigned* nct = cv.take<unsigned>(nc);
   uint32_t* tc = cv.take<uint32_t>(nc);
   if (p) {
-    p->phc = phc; p->phm = phm; p->lp = lp; p->stp = stp;
+    p->phm = phm; p->lp = lp; p->stp = stp;
     p->cs1 = cs1; p->cs2 = cs2; p->pm = pm; p->ps = ps; p->pav = pav; p->pai = pai;
     p->jstar = jstar; p->sbm = sbm; p->cnt = cnt; p->cand = cand; p->nct = nct; p->tc = tc;
   }
