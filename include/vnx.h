@@ -463,6 +463,14 @@ typedef struct vnx_tree_attn_args {
    * vnx_tree_attn_workspace_args when forcing splits.) */
   int force_splits;
   int force_waves;
+  /* fp32 rows (nonzero): q, the cache and tree rows and the second segment
+   * are fp32 (TriSparse on fp32 weights, tri_sparse_attn.py:258-378,
+   * :469-530), d in {8, 16, 32}, strides multiples of 4 elements, pointers
+   * 16-byte aligned; qkv must be NULL and no workspace is used.  anc may be
+   * NULL: a chain (node i sees tree rows j <= i and sits at tp_b + i), and
+   * then any N >= 1 (prefill chunks); the window may be shorter than N.
+   * Zero: the bf16 rows above. */
+  int f32_rows;
 } vnx_tree_attn_args;
 
 /* Workspace bytes of the automatic plan without a window (an upper bound for

@@ -115,7 +115,8 @@ def tree_attention_paths(q, k_cache, v_cache, k_tree, v_tree, anc, tp=None, wind
     """(out, mag) (B, H, N, d) fp64 of the gated TriSparse paths over each
     batch row's first tp[b] cache rows and its N tree rows (see the module
     docstring).  tp: (B,) prefix lengths (default: all Tp rows); seg2 = (k2,
-    v2) (B or 1, Hkv, T2, d); gates (3,) fp32; slopes (H,) or None."""
+    v2) (B or 1, Hkv, T2, d); gates (3,) fp32; slopes (H,) or None.  anc None:
+    a chain of any length (node i sees tree rows j <= i)."""
     q = _f64(q)
     kt, vt = _f64(k_tree), _f64(v_tree)
     B, H, N, d = q.shape
@@ -126,7 +127,7 @@ def tree_attention_paths(q, k_cache, v_cache, k_tree, v_tree, anc, tp=None, wind
     vc = None if v_cache is None else _f64(v_cache)
     tp = np.full(B, Tp, np.int64) if tp is None else np.clip(np.asarray(tp, np.int64), 0, Tp)
     sc = 1.0 / np.sqrt(d) if scale is None else float(scale)
-    w = _words(anc, B, N)
+    w = None if anc is None else _words(anc, B, N)
     g = None if gates is None else np.asarray(gates, np.float32).astype(np.float64)
     out = np.zeros((B, H, N, d))
     mag = np.zeros((B, H, N, d))
@@ -142,7 +143,10 @@ def tree_attention_paths(q, k_cache, v_cache, k_tree, v_tree, anc, tp=None, wind
 
     for b in range(B):
         t = int(tp[b])
-        bits = ((w[b][:, None] >> np.arange(N, dtype=np.uint64)[None, :]) & np.uint64(1)).astype(bool)  # (N, N)
+        if w is None:
+            bits = np.tril(np.ones((N, N), bool))
+        else:
+            bits = ((w[b][:, None] >> np.arange(N, dtype=np.uint64)[None, :]) & np.uint64(1)).astype(bool)  # (N, N)
         depth = bits.sum(axis=1) - 1
         qpos = t + depth                                                     # (N,)
         kpos = np.concatenate([np.arange(t), t + depth])                    # (t + N,)

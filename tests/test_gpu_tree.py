@@ -340,3 +340,58 @@ def test_window_smaller_than_the_tree_is_rejected(hip):
     with pytest.raises(ValueError):
         hip.tree_attention(z(1, 2, 8, 64), z(1, 2, 10, 64), z(1, 2, 10, 64), z(1, 2, 8, 64), z(1, 2, 8, 64),
                            T.ancestor_words(T.chain(8)), window=7)
+
+
+def _run_rows_f32(hip, B, H, Hkv, N, Tp, d, tp, window, alibi, parent="chain", T2=0, seed=0,
+                  out_dtype=torch.float32, alibi_max=1024):
+    """vnx_tree_attn's fp32-rows path (f32_rows: fp32 q / cache / tree rows,
+    d 8 / 16 / 32) against oracle.tree.tree_attention_paths; parent "chain"
+    passes anc=None (a chain of any length N)."""
+    _say(f"tree_attn fp32 rows B={B} H={H} Hkv={Hkv} N={N} Tp={Tp} d={d} window={window} alibi={alibi} "
+         f"T2={T2} alibi_max={alibi_max} out={out_dtype} tree={parent if isinstance(parent, str) else 'words'}")
+    rng = np.random.default_rng(seed)
+    dev = hip.torch_device
+    f = lambda *s: torch.from_numpy(rng.normal(0, 1.5, s).astype(np.float32)).to(dev)  # noqa: E731
+    q, kt, vt = f(B, H, N, d), f(B, Hkv, N, d), f(B, Hkv, N, d)
+    kc, vc = (f(B, Hkv, Tp, d), f(B, Hkv, Tp, d)) if Tp else (None, None)
+    words = None if isinstance(parent, str) else T.ancestor_words(np.asarray(parent, np.int32))
+    gates = np.asarray([0.55, 0.3, 0.7], np.float32)
+    seg2 = (f(1, Hkv, T2, d), f(1, Hkv, T2, d)) if T2 else None
+    slopes = (1.0 / (2.0 ** (np.arange(1, H + 1, dtype=np.float32) / H))).astype(np.float32) if alibi else None
+    out = hip.tree_attention(q, kc, vc, kt, vt, words, out_dtype=out_dtype, seg2=seg2,
+                             gates=gates if (T2 or alibi) else None, tp=np.asarray(tp, np.int32), window=window,
+                             alibi_slopes=slopes, alibi_max_keys=alibi_max, fp32_rows=True)
+    torch.cuda.synchronize()
+    ref, mag = OT.tree_attention_paths(_np(q), _np(kc), _np(vc), _np(kt), _np(vt), words, tp=tp, window=window,
+                                       slopes=slopes, alibi_max=alibi_max,
+                                       seg2=(_np(seg2[0]), _np(seg2[1])) if T2 else None,
+                                       gates=gates if (T2 or alibi) else None)
+    worst = _check(out, ref, mag, bf16=out_dtype == torch.bfloat16)
+    _say(f"  worst err / sum p|v| = {worst:.2e}")
+
+
+@pytest.mark.parametrize("d,out_dtype", [(16, torch.float32), (8, torch.float32), (32, torch.bfloat16),
+                                         (16, torch.float16)])
+def test_fp32_rows_config1_layout(hip, d, out_dtype):
+    """The config-1 target's layout (4 heads / 2 kv, window 32, 4 global rows,
+    ALiBi) on fp32 rows: a verify chain of 5 over ragged prefixes, one of
+    them past alibi_max so its ALiBi path drops out."""
+    _run_rows_f32(hip, 3, 4, 2, 5, 150, d, [150, 0, 31], 32, True, T2=4, seed=d, out_dtype=out_dtype,
+                  alibi_max=100)
+
+
+@pytest.mark.parametrize("N,Tp,window,alibi,d", [(66, 84, 32, True, 16), (100, 0, 32, False, 32),
+                                                 (150, 0, 32, True, 8), (40, 16, 16, True, 16)])
+def test_fp32_rows_long_chains(hip, N, Tp, window, alibi, d):
+    """Prefill chunks: chains longer than one mask word and longer than the
+    window (anc=None), with and without a cache before them."""
+    _run_rows_f32(hip, 2, 4, 2, N, Tp, d, [Tp, Tp // 2], window, alibi, T2=4, seed=N + d)
+
+
+def test_fp32_rows_on_a_tree(hip):
+    """Ancestor words on the fp32 path: tree positions from the depths, a
+    window wider than the tree, ALiBi, no global rows; and no paths at all."""
+    par = T.tree_from_branching((3, 2, 2))
+    N = par.size
+    _run_rows_f32(hip, 3, 4, 2, N, 50, 16, [50, 0, 17], N + 3, True, parent=par, seed=5)
+    _run_rows_f32(hip, 2, 2, 1, N, 20, 8, [20, 3], 0, False, parent=par, seed=6)

@@ -130,10 +130,11 @@ class OM_cfg:
 
 
 @pytest.mark.parametrize("T,n,W,alibi", [(40, 5, 8, True), (70, 9, 16, False), (30, 1, 32, True),
-                                         (100, 7, 64, True)])
+                                         (100, 7, 64, True), (150, 66, 32, True), (100, 100, 32, False)])
 def test_tree_paths_on_a_chain_equal_the_model_paths(T, n, W, alibi):
     """A cache of T - n rows, then n new rows in a chain: the gated paths of
-    the new rows equal the last n rows of the whole-sequence restatement."""
+    the new rows equal the last n rows of the whole-sequence restatement.
+    Chains longer than one mask word (and prefill, n = T) pass anc=None."""
     rng = np.random.default_rng(T + n)
     B, H, Hkv, d, G = 2, 4, 2, 16, 4
     q, k, v = _qkv(rng, B, T, H, Hkv, d)
@@ -144,7 +145,7 @@ def test_tree_paths_on_a_chain_equal_the_model_paths(T, n, W, alibi):
                              OM_cfg(W, alibi))[:, :, T - n:]
     kc = k[:, ::H // Hkv]
     vc = v[:, ::H // Hkv]
-    words = np.array([(1 << (i + 1)) - 1 for i in range(n)], np.uint64)
+    words = np.array([(1 << (i + 1)) - 1 for i in range(n)], np.uint64) if n <= 64 else None
     out, _ = OT.tree_attention_paths(q[:, :, T - n:], kc[:, :, :T - n], vc[:, :, :T - n], kc[:, :, T - n:],
                                      vc[:, :, T - n:], words, window=W,
                                      slopes=OM.alibi_slopes(H) if alibi else None, seg2=(k2, v2), gates=gate)

@@ -105,7 +105,7 @@ class TreeAttnArgs(ctypes.Structure):
         ("qkv", _vp), ("qkv_ld", _c_i64), ("cos_table", _vp), ("sin_table", _vp), ("table_rows", _c_i64),
         ("rope", _int), ("cap", _c_i64),
         ("window", _int), ("alibi_slopes", _vp), ("alibi_max_keys", _int),
-        ("force_splits", _int), ("force_waves", _int),
+        ("force_splits", _int), ("force_waves", _int), ("f32_rows", _int),
     ]
 
 

@@ -693,6 +693,281 @@ static bool strides_ok(int64_t sb, int64_t sh, int64_t sr, int unit) {
   return sb >= 0 && sh >= 0 && sr >= 0 && sb % unit == 0 && sh % unit == 0 && sr % unit == 0;
 }
 
+// ---------------------------------------------------------------------------
+// fp32 rows with small heads (d = 8 / 16 / 32: the fp32 TriSparse models).
+// One wave per query row (b, h, node i).  The lanes walk the row's keys 64
+// apart, each lane keeping its own online softmax (running max m, sum l,
+// output o[D]) for path A (prefix + tree keys inside the window) and path C
+// (the same keys, no window, score + -(m_h * distance): ALiBi), sharing
+// every key's q . k; the wave then merges the 64 lane states.  The second
+// segment (path B, the global rows) follows in a loop of its own.  A chain
+// (anc == NULL) lets node i see tree rows j <= i, so N is not held to one
+// mask word and prefill chunks of any length run here.  Scores follow the
+// reference's fp32 computation (tri_sparse_attn.py:258-378 window,
+// :469-495 global rows, :489-530 ALiBi, mixed as :585-608).
+
+struct F32RowsParams {
+  const float* q;
+  const float* kc;
+  const float* vc;
+  const float* kt;
+  const float* vt;
+  const uint64_t* anc;   // NULL: chain
+  void* out;
+  int64_t q_sb, q_sh, q_sr;
+  int64_t c_sb, c_sh, c_sr;
+  int64_t t_sb, t_sh, t_sr;
+  int64_t o_sb, o_sh, o_sr;
+  int64_t anc_sb;
+  const float* k2;
+  const float* v2;
+  int64_t s2_sb, s2_sh, s2_sr;
+  int T2;
+  const float* gates;
+  const float* slopes;
+  int alibi_max, window;
+  const int32_t* tp_batch;
+  int follows;
+  int B, H, N, Tp, n_rep;
+  float scale;
+};
+
+template <int D>
+struct RowSoftmax {
+  float m, l;
+  float o[D];
+};
+
+template <int D>
+__device__ __forceinline__ void rs_init(RowSoftmax<D>& a) {
+  a.m = -INFINITY;
+  a.l = 0.0f;
+#pragma unroll
+  for (int d = 0; d < D; ++d) a.o[d] = 0.0f;
+}
+
+// e^x for x <= 0 on the transcendental unit
+__device__ __forceinline__ float rs_exp(float x) { return ex2(x * 1.4426950408889634f); }
+
+template <int D>
+__device__ __forceinline__ void rs_add(RowSoftmax<D>& a, float s, const float (&v)[D]) {
+  if (s > a.m) {
+    const float c = rs_exp(a.m - s);  // 0 while a.m is -inf
+    a.l *= c;
+#pragma unroll
+    for (int d = 0; d < D; ++d) a.o[d] *= c;
+    a.m = s;
+  }
+  const float e = rs_exp(s - a.m);
+  a.l += e;
+#pragma unroll
+  for (int d = 0; d < D; ++d) a.o[d] = fmaf(e, v[d], a.o[d]);
+}
+
+__device__ __forceinline__ float rs_wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// Merges the 64 lane states; every lane returns the row's softmax output
+// (sum_j e_j v_j / sum_j e_j), zeros when no lane saw a key.
+template <int D>
+__device__ __forceinline__ void rs_merge(RowSoftmax<D>& a) {
+  float M = a.m;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  const float c = a.m == -INFINITY ? 0.0f : rs_exp(a.m - M);
+  const float L = rs_wave_sum(a.l * c);
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+  for (int d = 0; d < D; ++d) a.o[d] = rs_wave_sum(a.o[d] * c) * inv;
+}
+
+template <int D>
+__device__ __forceinline__ void load_row_f32(const float* src, float (&r)[D]) {
+#pragma unroll
+  for (int d = 0; d < D; d += 4) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(src + d);
+    r[d] = t[0]; r[d + 1] = t[1]; r[d + 2] = t[2]; r[d + 3] = t[3];
+  }
+}
+
+template <int D>
+__device__ __forceinline__ float dot_f32(const float (&q)[D], const float (&k)[D]) {
+  float s = 0.0f;
+#pragma unroll
+  for (int d = 0; d < D; ++d) s = fmaf(q[d], k[d], s);
+  return s;
+}
+
+template <int D, int OT>
+__global__ __launch_bounds__(256) void k_attn_rows_f32(F32RowsParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= (int64_t)p.B * p.H * p.N) return;  // whole waves leave; no barriers below
+  const int i = (int)(r % p.N);
+  const int h = (int)((r / p.N) % p.H);
+  const int b = (int)(r / ((int64_t)p.N * p.H));
+  const int kvh = h / p.n_rep;
+  int tp = p.Tp;
+  if (p.tp_batch) {
+    const int t = p.tp_batch[b];
+    tp = t < 0 ? 0 : t > p.Tp ? p.Tp : t;
+  }
+  float q[D];
+  load_row_f32<D>(p.q + b * p.q_sb + h * p.q_sh + i * p.q_sr, q);
+  const uint64_t* anc = p.anc ? p.anc + b * p.anc_sb : nullptr;
+  const uint64_t w = anc ? anc[i] : 0;
+  const int pos_i = tp + (anc ? __popcll(w) - 1 : i);
+  const int nk = tp + (anc ? p.N : i + 1);
+  const bool alibi = p.slopes && tp + p.N <= p.alibi_max;
+  const float slope = alibi ? p.slopes[h] : 0.0f;
+  // prefix rows (position = index) a window leaves out are skipped outright
+  int lo = 0;
+  if (p.window > 0 && !alibi) {
+    lo = pos_i - p.window + 1;
+    lo = lo < 0 ? 0 : lo > tp ? tp : lo;
+  }
+  RowSoftmax<D> A, C;
+  rs_init(A);
+  rs_init(C);
+  for (int t = lo + lane; t < nk; t += 64) {
+    int64_t off;
+    const float* kb;
+    const float* vb;
+    int kpos;
+    if (t < tp) {
+      off = b * p.c_sb + kvh * p.c_sh + t * p.c_sr;
+      kb = p.kc;
+      vb = p.vc;
+      kpos = t;
+    } else {
+      const int j = t - tp;
+      if (anc && !((w >> j) & 1ull)) continue;
+      off = b * p.t_sb + kvh * p.t_sh + (int64_t)(p.follows ? tp + j : j) * p.t_sr;
+      kb = p.kt;
+      vb = p.vt;
+      kpos = tp + (anc ? __popcll(anc[j]) - 1 : j);
+    }
+    float k[D], v[D];
+    load_row_f32<D>(kb + off, k);
+    load_row_f32<D>(vb + off, v);
+    const float s = dot_f32<D>(q, k) * p.scale;
+    const int dist = pos_i - kpos;
+    if (p.window <= 0 || dist < p.window) rs_add<D>(A, s, v);
+    if (alibi) rs_add<D>(C, s + -(slope * (float)dist), v);
+  }
+  rs_merge<D>(A);
+  if (alibi) rs_merge<D>(C);
+  const bool has2 = p.T2 > 0;
+  const float g1 = (has2 || p.slopes) ? p.gates[0] : 1.0f;
+  RowSoftmax<D> S2;
+  rs_init(S2);
+  if (has2) {
+    const int64_t base = b * p.s2_sb + kvh * p.s2_sh;
+    for (int t = lane; t < p.T2; t += 64) {
+      float k[D], v[D];
+      load_row_f32<D>(p.k2 + base + t * p.s2_sr, k);
+      load_row_f32<D>(p.v2 + base + t * p.s2_sr, v);
+      rs_add<D>(S2, dot_f32<D>(q, k) * p.scale, v);
+    }
+    rs_merge<D>(S2);
+  }
+  if (lane != 0) return;
+  const float g2 = has2 ? p.gates[1] : 0.0f;
+  const float g3 = alibi ? p.gates[2] : 0.0f;
+  const int64_t ob = b * p.o_sb + h * p.o_sh + i * p.o_sr;
+#pragma unroll
+  for (int d = 0; d < D; d += 4) {
+    f32x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float t = g1 * A.o[d + e];
+      if (has2) t = t + g2 * S2.o[d + e];
+      if (alibi) t = t + g3 * C.o[d + e];
+      y[e] = t;
+    }
+    ta_store4<OT>(p.out, ob + d, y);
+  }
+}
+
+template <int D>
+static void attn_rows_launch(const F32RowsParams& p, int ot, hipStream_t st) {
+  const int64_t rows = (int64_t)p.B * p.H * p.N;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (ot == 0) hipLaunchKernelGGL((k_attn_rows_f32<D, 0>), grid, dim3(256), 0, st, p);
+  else if (ot == 1) hipLaunchKernelGGL((k_attn_rows_f32<D, 1>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((k_attn_rows_f32<D, 2>), grid, dim3(256), 0, st, p);
+}
+
+// vnx_tree_attn with f32_rows set: the argument checks of that path, then one
+// launch (no workspace).
+static int tree_attn_f32(const vnx_tree_attn_args* a, void* stream) {
+  const int B = a->B, H = a->H, Hkv = a->Hkv, N = a->N, Tp = a->Tp, d = a->d;
+  if (d != 8 && d != 16 && d != 32) return VNX_ERR_UNSUPPORTED;
+  if (a->qkv) return VNX_ERR_UNSUPPORTED;  // queries and rows come in ready
+  if (a->anc && N > kTaMaxN) return VNX_ERR_UNSUPPORTED;
+  if (a->window < 0 || a->alibi_max_keys < 0 || a->T2 < 0) return VNX_ERR_INVALID_ARG;
+  if (B == 0) return VNX_OK;
+  if (!a->q || !a->k_tree || !a->v_tree || !a->out) return VNX_ERR_INVALID_ARG;
+  if (Tp > 0 && (!a->k_cache || !a->v_cache)) return VNX_ERR_INVALID_ARG;
+  if ((a->T2 > 0 || a->alibi_slopes) && (!a->gates || (reinterpret_cast<uintptr_t>(a->gates) & 3u)))
+    return VNX_ERR_INVALID_ARG;
+  if (a->alibi_slopes && (reinterpret_cast<uintptr_t>(a->alibi_slopes) & 3u)) return VNX_ERR_INVALID_ARG;
+  if (a->T2 > 0 && (!a->k_seg2 || !a->v_seg2)) return VNX_ERR_INVALID_ARG;
+  if (a->tp_batch && (reinterpret_cast<uintptr_t>(a->tp_batch) & 3u)) return VNX_ERR_INVALID_ARG;
+  if (!(a->scale > 0.0f) || !__builtin_isfinite(a->scale)) return VNX_ERR_INVALID_ARG;
+  if (a->anc_batch_stride < 0) return VNX_ERR_INVALID_ARG;
+  if ((int64_t)B * H * N > (int64_t)INT32_MAX * 2) return VNX_ERR_UNSUPPORTED;
+  // 16-byte loads of fp32 rows; 4-element output stores
+  if (!strides_ok(a->q_strides[0], a->q_strides[1], a->q_strides[2], 4) ||
+      !strides_ok(a->cache_strides[0], a->cache_strides[1], a->cache_strides[2], 4) ||
+      !strides_ok(a->tree_strides[0], a->tree_strides[1], a->tree_strides[2], 4) ||
+      !strides_ok(a->out_strides[0], a->out_strides[1], a->out_strides[2], 4) ||
+      (a->T2 > 0 && !strides_ok(a->seg2_strides[0], a->seg2_strides[1], a->seg2_strides[2], 4)))
+    return VNX_ERR_UNSUPPORTED;
+  if (!aligned16(a->q) || !aligned16(a->k_tree) || !aligned16(a->v_tree) || !aligned16(a->out) ||
+      (Tp > 0 && (!aligned16(a->k_cache) || !aligned16(a->v_cache))) ||
+      (a->T2 > 0 && (!aligned16(a->k_seg2) || !aligned16(a->v_seg2))) ||
+      (a->anc && (reinterpret_cast<uintptr_t>(a->anc) & 7u)))
+    return VNX_ERR_UNSUPPORTED;
+  F32RowsParams p{};
+  p.q = static_cast<const float*>(a->q);
+  p.kc = static_cast<const float*>(Tp > 0 ? a->k_cache : a->k_tree);
+  p.vc = static_cast<const float*>(Tp > 0 ? a->v_cache : a->v_tree);
+  p.kt = static_cast<const float*>(a->k_tree);
+  p.vt = static_cast<const float*>(a->v_tree);
+  p.anc = a->anc;
+  p.out = a->out;
+  p.q_sb = a->q_strides[0]; p.q_sh = a->q_strides[1]; p.q_sr = a->q_strides[2];
+  p.c_sb = a->cache_strides[0]; p.c_sh = a->cache_strides[1]; p.c_sr = a->cache_strides[2];
+  p.t_sb = a->tree_strides[0]; p.t_sh = a->tree_strides[1]; p.t_sr = a->tree_strides[2];
+  p.o_sb = a->out_strides[0]; p.o_sh = a->out_strides[1]; p.o_sr = a->out_strides[2];
+  p.anc_sb = a->anc_batch_stride;
+  if (a->T2 > 0) {
+    p.k2 = static_cast<const float*>(a->k_seg2);
+    p.v2 = static_cast<const float*>(a->v_seg2);
+    p.s2_sb = a->seg2_strides[0]; p.s2_sh = a->seg2_strides[1]; p.s2_sr = a->seg2_strides[2];
+    p.T2 = a->T2;
+  }
+  p.gates = a->gates;
+  p.slopes = a->alibi_slopes;
+  p.alibi_max = a->alibi_max_keys;
+  p.window = a->window;
+  p.tp_batch = a->tp_batch;
+  p.follows = a->tree_follows_prefix ? 1 : 0;
+  p.B = B; p.H = H; p.N = N; p.Tp = Tp; p.n_rep = H / Hkv;
+  p.scale = a->scale;
+  const int ot = a->out_dtype == VNX_F32 ? 0 : a->out_dtype == VNX_BF16 ? 1 : 2;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d == 8) attn_rows_launch<8>(p, ot, st);
+  else if (d == 16) attn_rows_launch<16>(p, ot, st);
+  else attn_rows_launch<32>(p, ot, st);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
 }  // namespace vnx
 
 using namespace vnx;
@@ -722,8 +997,9 @@ int vnx_tree_attn(const vnx_tree_attn_args* a, void* workspace, size_t workspace
   if (!a) return VNX_ERR_INVALID_ARG;
   const int B = a->B, H = a->H, Hkv = a->Hkv, N = a->N, Tp = a->Tp, d = a->d;
   if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv || N < 1 || Tp < 0) return VNX_ERR_INVALID_ARG;
-  if (N > kTaMaxN || (d != 64 && d != 128)) return VNX_ERR_UNSUPPORTED;
   if (a->out_dtype != VNX_F32 && a->out_dtype != VNX_BF16 && a->out_dtype != VNX_F16) return VNX_ERR_UNSUPPORTED;
+  if (a->f32_rows) return tree_attn_f32(a, stream);
+  if (N > kTaMaxN || (d != 64 && d != 128)) return VNX_ERR_UNSUPPORTED;
   if (a->T2 < 0) return VNX_ERR_INVALID_ARG;
   if (B == 0) return VNX_OK;
   if ((!a->q && !a->qkv) || !a->k_tree || !a->v_tree || !a->anc || !a->out) return VNX_ERR_INVALID_ARG;

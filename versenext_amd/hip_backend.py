@@ -427,20 +427,22 @@ class HipBackend(DeviceBackend):
         return out
 
     # ---- tree-verify attention ------------------------------------------------
-    def _heads_bf16(self, x, name: str) -> torch.Tensor:
-        """(B, heads, rows, d) bf16 view with the head dimension contiguous and
-        16-byte aligned strides (copied when it is not)."""
-        t = _to_tensor(x, self._torch_device, torch.bfloat16)
+    def _heads_bf16(self, x, name: str, dtype=torch.bfloat16) -> torch.Tensor:
+        """(B, heads, rows, d) view in dtype (bf16, or fp32 for the fp32-rows
+        path) with the head dimension contiguous and 16-byte aligned strides
+        (copied when it is not)."""
+        t = _to_tensor(x, self._torch_device, dtype)
         if t.dim() != 4:
             raise ValueError(f"{name} must be (B, heads, rows, d), got shape {tuple(t.shape)}")
-        if t.stride(-1) != 1 or t.data_ptr() % 16 or any(st % 8 for st in t.stride()[:3]):
+        unit = 16 // t.element_size()
+        if t.stride(-1) != 1 or t.data_ptr() % 16 or any(st % unit for st in t.stride()[:3]):
             t = t.contiguous()
         return t
 
     def tree_attention(self, q, k_cache, v_cache, k_tree, v_tree, anc, scale: float | None = None,
                        out_dtype=torch.float32, seg2=None, gates=None, tp=None, window: int = 0,
                        alibi_slopes=None, alibi_max_keys: int = 1024, force_splits: int = 0,
-                       force_waves: int = 0) -> torch.Tensor:
+                       force_waves: int = 0, fp32_rows: bool = False) -> torch.Tensor:
         """Tree-verify attention (vnx_tree_attn).
 
         q (B, H, N, d); k_cache / v_cache (B, Hkv, Tp, d) or None (Tp = 0);
@@ -454,11 +456,14 @@ class HipBackend(DeviceBackend):
         keys less than window positions behind each node; alibi_slopes (H,)
         with gates (3,) adds the ALiBi path as gates[2] * it for rows with
         tp_b + N <= alibi_max_keys.  force_splits / force_waves pin the launch
-        shape (tuning and tests)."""
+        shape (tuning and tests).  fp32_rows: inputs read as fp32 (d in 8 /
+        16 / 32, the fp32 models' path), and anc may be None for a chain of
+        any length N."""
         dev = self._torch_device
-        qt = self._heads_bf16(q, "q")
-        kt = self._heads_bf16(k_tree, "k_tree")
-        vt = self._heads_bf16(v_tree, "v_tree")
+        rows = torch.float32 if fp32_rows else torch.bfloat16
+        qt = self._heads_bf16(q, "q", rows)
+        kt = self._heads_bf16(k_tree, "k_tree", rows)
+        vt = self._heads_bf16(v_tree, "v_tree", rows)
         B, H, N, d = qt.shape
         if kt.shape != vt.shape or kt.shape[0] != B or kt.shape[2] != N or kt.shape[3] != d:
             raise ValueError(f"tree rows {tuple(kt.shape)} / {tuple(vt.shape)} do not match q {tuple(qt.shape)}")
@@ -472,8 +477,8 @@ class HipBackend(DeviceBackend):
             Tp = 0
             cstr = (0, 0, 0)
         else:
-            kc = self._heads_bf16(k_cache, "k_cache")
-            vc = self._heads_bf16(v_cache, "v_cache")
+            kc = self._heads_bf16(k_cache, "k_cache", rows)
+            vc = self._heads_bf16(v_cache, "v_cache", rows)
             if kc.shape != vc.shape or kc.shape[0] != B or kc.shape[1] != Hkv or kc.shape[3] != d:
                 raise ValueError(f"cache {tuple(kc.shape)} / {tuple(vc.shape)} does not match the tree rows")
             if kc.stride() != vc.stride():
@@ -482,11 +487,16 @@ class HipBackend(DeviceBackend):
             cstr = kc.stride()[:3]
             if Tp == 0:
                 kc = vc = None
-        a = anc.detach().cpu().numpy() if isinstance(anc, torch.Tensor) else np.asarray(anc)
-        a = np.ascontiguousarray(a.astype(np.uint64) if a.dtype != np.uint64 else a)
-        if a.shape not in ((N,), (B, N)):
-            raise ValueError(f"anc must be ({N},) or ({B}, {N}), got {a.shape}")
-        anc_t = torch.from_numpy(a.view(np.int64)).to(dev)
+        if anc is None:
+            if not fp32_rows:
+                raise ValueError("anc=None (a chain) needs fp32_rows")
+            a = anc_t = None
+        else:
+            a = anc.detach().cpu().numpy() if isinstance(anc, torch.Tensor) else np.asarray(anc)
+            a = np.ascontiguousarray(a.astype(np.uint64) if a.dtype != np.uint64 else a)
+            if a.shape not in ((N,), (B, N)):
+                raise ValueError(f"anc must be ({N},) or ({B}, {N}), got {a.shape}")
+            anc_t = torch.from_numpy(a.view(np.int64)).to(dev)
         if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
             raise ValueError("out_dtype must be torch.float32, torch.bfloat16 or torch.float16")
         out = torch.empty((B, H, N, d), dtype=out_dtype, device=dev)
@@ -500,8 +510,9 @@ class HipBackend(DeviceBackend):
         args.k_tree = kt.data_ptr()
         args.v_tree = vt.data_ptr()
         args.tree_strides[:] = list(kt.stride()[:3])
-        args.anc = anc_t.data_ptr()
-        args.anc_batch_stride = N if a.ndim == 2 else 0
+        args.anc = anc_t.data_ptr() if anc_t is not None else None
+        args.anc_batch_stride = N if a is not None and a.ndim == 2 else 0
+        args.f32_rows = int(fp32_rows)
         args.out = out.data_ptr()
         args.out_dtype = _lib.DTYPE_CODES[out_dtype]
         args.out_strides[:] = list(out.stride()[:3])
@@ -530,8 +541,8 @@ class HipBackend(DeviceBackend):
             args.alibi_max_keys = int(alibi_max_keys)
             args.gates = g3.data_ptr()
         if seg2 is not None:
-            k2 = self._heads_bf16(seg2[0], "k_seg2")
-            v2 = self._heads_bf16(seg2[1], "v_seg2")
+            k2 = self._heads_bf16(seg2[0], "k_seg2", rows)
+            v2 = self._heads_bf16(seg2[1], "v_seg2", rows)
             if k2.shape != v2.shape or k2.shape[0] not in (1, B) or k2.shape[1] != Hkv or k2.shape[3] != d:
                 raise ValueError(f"second segment {tuple(k2.shape)} / {tuple(v2.shape)} does not match")
             if k2.stride() != v2.stride():

@@ -549,8 +549,10 @@ class CometSparkGPU:
         self._words = {}
         self._neg = torch.full((), -1e9, dtype=torch.float32, device=dev)  # the reference's mask value
         # vnx_tree_attn covers all three paths (window, global rows, ALiBi) for
-        # bf16 heads of 64 / 128
-        self.kernel_attention = dtype == torch.bfloat16 and d in (64, 128)
+        # bf16 heads of 64 / 128 (verify-size chunks) and fp32 heads of 8 / 16 /
+        # 32 (chunks of any length)
+        self.f32_rows = dtype == torch.float32 and d in (8, 16, 32)
+        self.kernel_attention = (dtype == torch.bfloat16 and d in (64, 128)) or self.f32_rows
         # dtype of the activations fed to the projections: fp16 for the INT4
         # GEMVs, else the compute dtype
         self.act_dtype = torch.float16 if int4 else dtype
@@ -611,7 +613,8 @@ class CometSparkGPU:
             a.q = q.data_ptr(); a.q_strides[:] = list(q.stride()[:3])
         a.k_cache = kc.data_ptr(); a.v_cache = vc.data_ptr(); a.cache_strides[:] = cstr
         a.k_tree = tree_k.data_ptr(); a.v_tree = tree_v.data_ptr(); a.tree_strides[:] = tstr
-        a.anc = anc.data_ptr(); a.anc_batch_stride = 0
+        a.anc = anc.data_ptr() if anc is not None else None; a.anc_batch_stride = 0   # None: a chain (fp32 rows)
+        a.f32_rows = int(self.f32_rows)
         # output rows in (B, n, H, d) order: the proj input layout
         a.out = out.data_ptr(); a.out_dtype = _lib.DTYPE_CODES[out.dtype]; a.out_strides[:] = [n * H * d, d, H * d]
         a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, n, d
@@ -637,7 +640,9 @@ class CometSparkGPU:
         row's prefix of lens[b] cache rows, then its n new rows (written in
         place right after it) under the chain mask, and the G global rows as
         the gated second segment; writes the proj input (B*n, H*d) in the
-        activation dtype.  q (B, H, n, d) bf16, or qkv (B*n, (H+2Hkv) d) bf16
+        activation dtype.  fp32 models with heads of 8 / 16 / 32 take the
+        kernel's fp32-rows path (a chain of any n, no mask words).  q (B, H,
+        n, d) in the model dtype, or qkv (B*n, (H+2Hkv) d) bf16
         projection rows (RoPE and the new rows' cache write done by the
         kernel; q unused)."""
         cfg = self.cfg
@@ -646,13 +651,15 @@ class CometSparkGPU:
         Ly = self.layers[li]
         o = torch.empty((B * n, H * d), dtype=self.act_dtype, device=self.dev)
         cstr = list(kc.stride()[:3])
-        self._tree_call(q, kc, vc, cstr, kc, vc, cstr, self._chain_words(n), B, H, cfg.n_kv_head, Tmax, n, d, lens,
+        anc = None if self.f32_rows else self._chain_words(n)
+        self._tree_call(q, kc, vc, cstr, kc, vc, cstr, anc, B, H, cfg.n_kv_head, Tmax, n, d, lens,
                         True, o, seg2=(Ly.gk, Ly.gv), gates=Ly.gates, qkv=qkv)
         return o
 
     def _attn_torch(self, q, li, lens, n, Tmax):
-        """The same three paths with explicit fp32 masks (any head size,
-        ALiBi, windows shorter than the context, prefill).  q (B, H, n, d)."""
+        """The same three paths with explicit fp32 masks: bf16 prefill chunks
+        longer than 64 rows or than the window, and head sizes the kernel does
+        not take.  q (B, H, n, d)."""
         cfg = self.cfg
         B, H, _, d = q.shape
         rep = H // cfg.n_kv_head
@@ -843,7 +850,7 @@ class CometSparkGPU:
             x = (self.emb[tok].float() * self.emb_scale).contiguous()
         else:
             x = torch.empty((M, D), dtype=torch.float32, device=self.dev)                # fp32 residual stream
-        use_kernel = self.kernel_attention and n <= 64 and n <= cfg.window_size
+        use_kernel = self.kernel_attention and (self.f32_rows or (n <= 64 and n <= cfg.window_size))
         pending = None
         for li, L in enumerate(self.layers):
             # verify-size bf16 forwards: the norms and the residual adds live in
