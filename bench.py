@@ -575,9 +575,10 @@ def round_floor_bytes(target, draft, B: int, k: int, ctx: float) -> dict:
 def e2e_rounds(eng, prompts, n_new, steps, warmup, mark=None):
     """Prefill, `warmup` untimed rounds (the first captures the round's HIP
     graph), then exactly `steps` timed rounds of the same generation (mark(),
-    when given, runs right before and right after them).  Returns (seconds,
-    tokens committed in the timed rounds, per-round token counts, prefill
-    seconds)."""
+    when given, runs right before and right after them), each enqueued
+    before the previous round's info is read (SpecDecodeEngine.run_rounds).
+    Returns (seconds, tokens committed in the timed rounds, per-round token
+    counts, prefill seconds)."""
     import torch
     B = eng.B
     prefill_s = eng.prefill(prompts, n_new)
@@ -588,11 +589,8 @@ def e2e_rounds(eng, prompts, n_new, steps, warmup, mark=None):
     torch.cuda.synchronize(eng.dev)
     if mark:
         mark()
-    per = []
     t0 = time.perf_counter()
-    for _ in range(steps):
-        info = eng.step()
-        per.append(int(info[3]) + B)
+    per = [int(info[3]) + B for info in eng.run_rounds(steps)]
     torch.cuda.synchronize(eng.dev)
     dt = time.perf_counter() - t0
     if mark:

@@ -268,6 +268,44 @@ def test_stochastic_spec_decode_runs_and_commits_consistently(hip):
     _say(f"stochastic: {st.rounds} rounds, {st.accepted_drafts} drafts accepted")
 
 
+def test_pipelined_rounds_match_one_round_at_a_time(hip):
+    """generate() and run_rounds() enqueue a round before reading the previous
+    round's info; the committed streams, the round count and the per-round
+    infos equal those of one step() at a time from the same seed (stochastic
+    rounds, graph replays, draws from the engine's generator)."""
+    cfg = _toy_cfg()
+    dcfg = VM.ModelConfig(vocab_size=1000, dim=128, n_layer=1, n_head=2, n_kv_head=1, layer_pattern=("trisparse",),
+                          window_size=1024, num_global_tokens=8, use_alibi=False, use_rope=True)
+    Wt, Wd = VM.init_weights(cfg, seed=41), VM.init_weights(dcfg, seed=42)
+    dev = hip.torch_device
+    B, n_new = 4, 60
+    prompt = torch.from_numpy(np.random.default_rng(5).integers(0, 1000, (B, 24))).to(dev)
+    tt = VM.CometSparkGPU(cfg, Wt, hip, batch=B, capacity=200, dtype=torch.bfloat16)
+    dd = VM.CometSparkGPU(dcfg, Wd, hip, batch=B, capacity=200, dtype=torch.bfloat16)
+    eng = SpecDecodeEngine(tt, dd, hip, k=4, temperature=0.8, seed=7, use_graph=True)
+    eng.generate(prompt, n_new)                     # captures the graph
+    eng.gen.manual_seed(7)
+    toks_p, st_p = eng.generate(prompt, n_new)      # pipelined
+    eng.gen.manual_seed(7)
+    eng.prefill(prompt, n_new)
+    infos = []
+    while True:                                     # one round at a time
+        infos.append(eng.step())
+        if int(infos[-1][0]) >= n_new:
+            break
+    toks_s = eng.out[:, :n_new].clone()
+    _say(f"pipelined {st_p.rounds} rounds, sequential {len(infos)} rounds")
+    assert st_p.rounds == len(infos)
+    assert st_p.per_round_tokens == [int(i[3]) + B for i in infos]
+    assert torch.equal(toks_p, toks_s)
+    # run_rounds: the same infos as the sequential rounds
+    eng.gen.manual_seed(7)
+    eng.prefill(prompt, n_new)
+    got = eng.run_rounds(len(infos))
+    assert [list(map(int, g)) for g in got] == [list(map(int, i)) for i in infos]
+    assert torch.equal(eng.out[:, :n_new], toks_s)
+
+
 def test_graph_rounds_match_eager_rounds(hip, gold):
     """The captured round (HIP graph, cache-bound prefix maxima) commits the
     same streams as eager rounds: config 1 reproduces the reference's greedy

@@ -91,6 +91,11 @@ class SpecDecodeEngine:
         self.lens_d = torch.zeros(B, dtype=torch.int32, device=dev)
         self.count = torch.zeros(B, dtype=torch.int64, device=dev)
         self.info = torch.zeros(4, dtype=torch.int64, device=dev)
+        # pinned host slots the rounds' info is copied into (two rounds in
+        # flight), with the event each copy completes
+        self.info_host = [torch.zeros(4, dtype=torch.int64, pin_memory=True) for _ in range(2)]
+        self.info_ev = [torch.cuda.Event() for _ in range(2)]
+        self._slot = 0
         self.steps_i32 = torch.arange(k + 1, dtype=torch.int32, device=dev).view(k + 1, 1)
         self.out = None
         self.n_new = 0
@@ -196,13 +201,9 @@ class SpecDecodeEngine:
         self.u_draft.copy_(ud)
         self.u_acc.copy_(ua)
 
-    @torch.no_grad()
-    def step(self, uniforms=None) -> torch.Tensor:
-        """One speculative round of every sequence (a graph replay once
-        captured).  uniforms: None (drawn from the engine's generator) or
-        (u_draft, u_acc) supplied by the caller (see _set_uniforms).  Returns
-        info (4,) int64 on the host: min committed count, max target / draft
-        cache length, accepted drafts summed over the batch."""
+    def _launch(self, uniforms=None) -> int:
+        """Enqueues one round (a graph replay once captured) and the copy of
+        its info into a pinned host slot; returns the slot."""
         if self.out is None:
             raise RuntimeError("call prefill() before step()")
         if uniforms is None:
@@ -213,7 +214,17 @@ class SpecDecodeEngine:
             self.graph.replay()
         else:
             self._round(*self._Tmax)
-        info = self.info.cpu()
+        slot = self._slot
+        self._slot ^= 1
+        self.info_host[slot].copy_(self.info, non_blocking=True)
+        self.info_ev[slot].record(torch.cuda.current_stream(self.dev))
+        return slot
+
+    def _collect(self, slot: int) -> torch.Tensor:
+        """Waits for the round whose info went to slot and returns that info
+        (checking that the next round fits the caches)."""
+        self.info_ev[slot].synchronize()
+        info = self.info_host[slot].clone()
         Tmax_t, Tmax_d = int(info[1]), int(info[2])
         if Tmax_t + self.k + 2 > self.t.cap or Tmax_d + self.k + 2 > self.d.cap:
             if int(info[0]) < self.n_new:
@@ -221,26 +232,81 @@ class SpecDecodeEngine:
         self._Tmax = (Tmax_t, Tmax_d)
         return info
 
+    def _fits_ahead(self) -> bool:
+        """Whether a round may be enqueued before the previous round's info
+        is read: graph replays only (eager rounds size their attention calls
+        by it), and the caches must hold the round after next even if every
+        draft of the round in flight is accepted."""
+        if self.graph is None:
+            return False
+        Tt, Td = self._Tmax
+        grow = 2 * (self.k + 1) + 1
+        return Tt + grow <= self.t.cap and Td + grow <= self.d.cap
+
+    @torch.no_grad()
+    def step(self, uniforms=None) -> torch.Tensor:
+        """One speculative round of every sequence (a graph replay once
+        captured).  uniforms: None (drawn from the engine's generator) or
+        (u_draft, u_acc) supplied by the caller (see _set_uniforms).  Returns
+        info (4,) int64 on the host: min committed count, max target / draft
+        cache length, accepted drafts summed over the batch."""
+        return self._collect(self._launch(uniforms))
+
+    @torch.no_grad()
+    def run_rounds(self, n: int, uniforms=None) -> list:
+        """n rounds back to back, each round enqueued before the previous
+        one's info is read (while the caches allow it), so the GPU does not
+        wait on the host between rounds.  Returns the n infos (see step())."""
+        infos = []
+        if n <= 0:
+            return infos
+        pending = self._launch(None if uniforms is None else uniforms(0))
+        for r in range(1, n + 1):
+            nxt = None
+            if r < n and self._fits_ahead():
+                nxt = self._launch(None if uniforms is None else uniforms(r))
+            infos.append(self._collect(pending))
+            if r < n and nxt is None:
+                nxt = self._launch(None if uniforms is None else uniforms(r))
+            pending = nxt
+        return infos
+
     @torch.no_grad()
     def generate(self, prompts: torch.Tensor, n_new: int, phase_timing: bool = False, uniforms=None):
         """prompts (B, T0) int64 on the device.  Returns (tokens (B, n_new)
         int64 on the device, DecodeStats).  Prefill is timed separately from
         the decode rounds.  uniforms: None, or a callable round_index ->
-        (u_draft, u_acc) giving each round's uniforms (see step())."""
-        B = self.B
+        (u_draft, u_acc) giving each round's uniforms (see step()).
+        A round is enqueued before the previous one's info is read whenever
+        that round certainly is not the last (the slowest sequence still
+        needs more than k + 1 tokens) and the caches allow it; the rounds
+        and their uniforms are the same as with one round at a time."""
+        B, k = self.B, self.k
         st = DecodeStats(prefill_s=self.prefill(prompts, n_new))
         if self.use_graph and self.graph is None:
             self._capture()
         t1 = time.perf_counter()
+        low = 0                                    # min committed count known so far
+        pending = self._launch(None if uniforms is None else uniforms(0))
+        launched = 1
         while True:
             ta = time.perf_counter()
-            info = self.step(None if uniforms is None else uniforms(st.rounds))
+            nxt = None
+            if low + (k + 1) < n_new and self._fits_ahead():
+                nxt = self._launch(None if uniforms is None else uniforms(launched))
+                launched += 1
+            info = self._collect(pending)
             st.rounds += 1
             st.per_round_tokens.append(int(info[3]) + B)
             if phase_timing:
                 st.draft_s += time.perf_counter() - ta
-            if int(info[0]) >= n_new:
-                break
+            low = int(info[0])
+            if low >= n_new:
+                break                              # nxt is None here: low + k + 1 < n_new was false
+            if nxt is None:
+                nxt = self._launch(None if uniforms is None else uniforms(launched))
+                launched += 1
+            pending = nxt
         torch.cuda.synchronize(self.dev)
         st.decode_s = time.perf_counter() - t1
         st.emitted = B * n_new
