@@ -919,7 +919,7 @@ static int tree_attn_f32(const vnx_tree_attn_args* a, void* stream) {
   if (a->tp_batch && (reinterpret_cast<uintptr_t>(a->tp_batch) & 3u)) return VNX_ERR_INVALID_ARG;
   if (!(a->scale > 0.0f) || !__builtin_isfinite(a->scale)) return VNX_ERR_INVALID_ARG;
   if (a->anc_batch_stride < 0) return VNX_ERR_INVALID_ARG;
-  if ((int64_t)B * H * N > (int64_t)INT32_MAX * 2) return VNX_ERR_UNSUPPORTED;
+  if (((int64_t)B * H * N + 3) / 4 >= INT32_MAX) return VNX_ERR_UNSUPPORTED;  // one wave per row, 4 per workgroup
   // 16-byte loads of fp32 rows; 4-element output stores
   if (!strides_ok(a->q_strides[0], a->q_strides[1], a->q_strides[2], 4) ||
       !strides_ok(a->cache_strides[0], a->cache_strides[1], a->cache_strides[2], 4) ||
