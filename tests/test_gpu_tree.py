@@ -395,3 +395,21 @@ def test_fp32_rows_on_a_tree(hip):
     N = par.size
     _run_rows_f32(hip, 3, 4, 2, N, 50, 16, [50, 0, 17], N + 3, True, parent=par, seed=5)
     _run_rows_f32(hip, 2, 2, 1, N, 20, 8, [20, 3], 0, False, parent=par, seed=6)
+
+
+def test_fp32_rows_rejects_bad_arguments(hip):
+    """The fp32-rows path takes heads of 8 / 16 / 32 only, at most 64 nodes
+    with mask words, and no chain (anc None) on the bf16 path."""
+    dev = hip.torch_device
+    f = lambda *s: torch.zeros(s, dtype=torch.float32, device=dev)  # noqa: E731
+    with pytest.raises(ValueError):  # head dim 64 on fp32 rows
+        hip.tree_attention(f(1, 2, 4, 64), None, None, f(1, 1, 4, 64), f(1, 1, 4, 64), None, fp32_rows=True)
+    with pytest.raises(ValueError):  # 65 nodes with mask words
+        hip.tree_attention(f(1, 1, 65, 16), None, None, f(1, 1, 65, 16), f(1, 1, 65, 16), np.ones(65, np.uint64),
+                           fp32_rows=True)
+    with pytest.raises(ValueError):  # a chain without words needs fp32 rows
+        hip.tree_attention(f(1, 1, 4, 64), None, None, f(1, 1, 4, 64), f(1, 1, 4, 64), None)
+    # 65 chain nodes without words are fine
+    out = hip.tree_attention(f(1, 1, 65, 16), None, None, f(1, 1, 65, 16), f(1, 1, 65, 16), None, fp32_rows=True)
+    torch.cuda.synchronize()
+    assert out.shape == (1, 1, 65, 16) and torch.isfinite(out).all()
