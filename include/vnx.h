@@ -376,7 +376,8 @@ int vnx_dequant_w8(const int8_t* wq, int64_t ldw, const float* scale, int64_t N,
  * dimension contiguous and strides {batch, head, row} in elements (multiples
  * of 8, pointers 16-byte aligned).  The tree rows may live inside the cache
  * (k_tree = k_cache + Tp*row stride).  out (B,H,N,d): fp32, bf16 or fp16
- * (round to nearest even), strides multiples of 4.  d in {64, 128}; 1 <= N <= 64.
+ * (round to nearest even), strides multiples of 4.  d in {64, 128}; 1 <= N <= 64
+ * (f32_rows below: fp32 rows, d in {8, 16, 32}, chains of any N).
  * A node that sees no key (Tp == 0 and an empty mask word) gets zeros.
  * The workspace (vnx_tree_attn_workspace bytes, no initialisation) holds the
  * per-split partials when the keys are split over several workgroups.
