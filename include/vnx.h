@@ -68,8 +68,9 @@ const char* vnx_last_hip_error(void);
 /* Phase profiling (a measurement aid with no counterpart in the reference).
  * vnx_profile_begin(max_calls) creates events for up to max_calls entry-point
  * calls; while active, each vnx_spec_accept call records an event before each
- * of its four launches (lse, accept, mass, draw) and one after the last, on
- * its own stream.  vnx_profile_end waits for the recorded events, writes the
+ * of its two launches (the LSE pass; acceptance, masses and draw) and one
+ * after the last, on its own stream (vnx_tree_attn's bf16 path records its
+ * attention and merge launches the same way).  vnx_profile_end waits for the recorded events, writes the
  * summed milliseconds of each phase into phase_ms[0..nphase) and the number of
  * profiled calls into *ncalls, and releases the events.  Not for use while
  * calls run concurrently on several streams. */
