@@ -738,7 +738,7 @@ size_t vnx_spec_accept_workspace(int64_t B, int k, int64_t V) {
   return spec_ws_bytes(B, k, V);
 }
 
-// The four launches for k >= 0 draft positions (k = 0: the draw from p_0
+// The two launches for k >= 0 draft positions (k = 0: the draw from p_0
 // alone, which is sampling from softmax(target / T)).
 static int spec_run(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
                     int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
