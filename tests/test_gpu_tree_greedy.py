@@ -114,7 +114,8 @@ def test_chain_is_reference_prefix_rule_with_bonus(hip):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("V,b", [(5, 1), (17, 4), (1000, 3), (4099, 16), (248320, 4)])
+@pytest.mark.parametrize("V,b", [(5, 1), (17, 4), (1000, 3), (4099, 16), (8193, 8), (248320, 4), (248320, 16),
+                                 (600000, 2)])
 def test_topk_matches_sorted_order(hip, dtype, V, b):
     _say(f"topk V={V} b={b} {dtype}")
     rng = np.random.default_rng(V + b)

@@ -4,7 +4,8 @@
 // Order: value descending, ties to the lower id, NaN above every number (the
 // numpy.argmax order, so b = 1 is argmax); -inf ranks below every number.
 // Two launches, no cross-workgroup
-// signalling: k_topk_chunk streams one chunk of one row per workgroup and
+// signalling: k_topk_filter (rows of up to 64 chunks of 8,192) or
+// k_topk_chunk (longer rows) reduces one chunk of one row per workgroup and
 // writes its best KB (b rounded up to a power of two) to the workspace;
 // k_topk_merge merges a row's chunk lists in one wave.
 #include "rowred.h"
@@ -153,6 +154,90 @@ __global__ __launch_bounds__(kTNT) void k_topk_chunk(TopkParams p) {
   }
 }
 
+// Chunks of kFiltLen elements (32 per thread, all loaded at once): each
+// thread's largest key, then per wave the KB-th largest of its 64 lanes'
+// maxima, t_w -- KB threads of that wave hold an element >= t_w, so t_w is a
+// lower bound of the chunk's KB-th best, and so is t = max_w t_w.  Only
+// elements with key >= t enter the per-thread lists (a few per chunk), so
+// the per-element cost is the key and two compares instead of the insertion
+// network; the lists are then merged as in k_topk_chunk.
+constexpr int kFiltPer = 32;                    // elements per thread
+constexpr int64_t kFiltLen = (int64_t)kTNT * kFiltPer;
+
+template <typename Tin, int KB>
+__global__ __launch_bounds__(kTNT) void k_topk_filter(TopkParams p) {
+  constexpr int VE = Vec<Tin>::N;
+  constexpr int NV = kFiltPer / VE;             // vectors per thread
+  __shared__ uint64_t sk[kTNT / VNX_WAVE];
+  __shared__ uint32_t st[kTNT / VNX_WAVE];
+  const int64_t r = blockIdx.x / p.chunks;
+  const int c = blockIdx.x % p.chunks;
+  const Tin* row = static_cast<const Tin*>(p.x) + r * p.ld;
+  const int64_t c0 = (int64_t)c * p.chunk_len;
+  const int64_t c1 = c0 + p.chunk_len < p.V ? c0 + p.chunk_len : p.V;
+  const int64_t n = c1 - c0;
+  const int tid = threadIdx.x;
+  const int w = tid / VNX_WAVE, l = tid % VNX_WAVE;
+  // vector j of this thread covers offsets (tid + kTNT*j)*VE .. +VE
+  uint32_t key[kFiltPer];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t off = (int64_t)(tid + kTNT * j) * VE;
+    float x[VE];
+    if (off + VE <= n) {
+      Vec<Tin>::load(row + c0 + off, x);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) key[j * VE + e] = vkey(x[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; ++e)
+        key[j * VE + e] = off + e < n ? vkey(Vec<Tin>::load1(row + c0 + off + e)) : 0u;  // 0: no element
+    }
+  }
+  uint32_t tmax = 0u;
+#pragma unroll
+  for (int q = 0; q < kFiltPer; ++q) tmax = key[q] > tmax ? key[q] : tmax;
+  // the wave's KB-th largest lane maximum (lane index breaks ties)
+  uint64_t cur = ((uint64_t)tmax << 32) | (uint32_t)l;
+  uint32_t tw = 0u;
+#pragma unroll
+  for (int q = 0; q < KB; ++q) {
+    const uint64_t m = wave_max_u64(cur);
+    if (cur == m) cur = 0ull;
+    tw = (uint32_t)(m >> 32);
+  }
+  if (l == 0) st[w] = tw;
+  __syncthreads();
+  uint32_t t = st[0];
+#pragma unroll
+  for (int j = 1; j < kTNT / VNX_WAVE; ++j) t = st[j] > t ? st[j] : t;
+  TopList<KB> L;
+  L.init();
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      const uint32_t k = key[j * VE + e];
+      if (k != 0u && k >= t) L.push(k, (uint32_t)((tid + kTNT * j) * VE + e));
+    }
+  KeyList<KB> K;
+#pragma unroll
+  for (int q = 0; q < KB; ++q) K.k[q] = L.i[q] == 0xFFFFFFFFu ? 0ull : full_key(L.k[q], c0 + L.i[q]);
+  uint64_t* out = p.part + ((size_t)r * p.chunks + c) * KB;
+#pragma unroll
+  for (int q = 0; q < KB; ++q) {
+    const uint64_t wm = wave_max_u64(K.k[0]);
+    __syncthreads();
+    if (l == 0) sk[w] = wm;
+    __syncthreads();
+    uint64_t best = sk[0];
+#pragma unroll
+    for (int j = 1; j < kTNT / VNX_WAVE; ++j) best = sk[j] > best ? sk[j] : best;
+    if (K.k[0] == best && best != 0ull) K.pop();
+    if (tid == 0) out[q] = best;
+  }
+}
+
 // One wave per row: lane c holds chunk c's sorted list.
 template <int KB>
 __global__ __launch_bounds__(kTNT) void k_topk_merge(TopkParams p) {
@@ -175,7 +260,10 @@ __global__ __launch_bounds__(kTNT) void k_topk_merge(TopkParams p) {
 
 template <typename Tin, int KB>
 void launch_topk(const TopkParams& p, hipStream_t s) {
-  hipLaunchKernelGGL((k_topk_chunk<Tin, KB>), dim3((unsigned)(p.rows * p.chunks)), dim3(kTNT), 0, s, p);
+  if (p.chunk_len == kFiltLen)
+    hipLaunchKernelGGL((k_topk_filter<Tin, KB>), dim3((unsigned)(p.rows * p.chunks)), dim3(kTNT), 0, s, p);
+  else
+    hipLaunchKernelGGL((k_topk_chunk<Tin, KB>), dim3((unsigned)(p.rows * p.chunks)), dim3(kTNT), 0, s, p);
   hipLaunchKernelGGL(k_topk_merge<KB>, dim3((unsigned)((p.rows + 3) / 4)), dim3(kTNT), 0, s, p);
 }
 
@@ -185,8 +273,15 @@ int kb_of(int b) {
   return kb;
 }
 
+// Rows of at most kTopMaxChunks filter chunks take the filter kernel (one
+// chunk of kFiltLen per workgroup); longer rows the streaming kernel.
 void topk_plan(int64_t rows, int64_t V, int dtype, int* chunks, int64_t* len) {
   const int ve = dtype == VNX_F32 ? 4 : 8;
+  if (V <= kFiltLen * kTopMaxChunks) {
+    *len = kFiltLen;
+    *chunks = (int)((V + kFiltLen - 1) / kFiltLen);
+    return;
+  }
   const int c = pick_chunks(rows, V, ve, kTopMaxChunks, 2048);
   const int64_t l = ((V + c - 1) / c + ve - 1) / ve * ve;
   *len = l;
