@@ -596,6 +596,11 @@ struct SpecPlan {
 // about kMassPerCu workgroups per CU.
 constexpr int64_t kLseWgs = 16384;
 constexpr int64_t kMassPerCu = 4;
+// k = 0 (a plain draw from p_0) streams one row per batch row, not p_n and
+// q_n: half the bytes per workgroup, so half the workgroups (32 rows of
+// 248,320: a 10 us shorter config-5 round; the acceptance at B = 64, k = 8
+// ran its launch B 8 us slower with 2 per CU)
+constexpr int64_t kMassPerCuDraw = 2;
 
 static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype) {
   const int ve = dtype == VNX_F32 ? 4 : 8;
@@ -609,7 +614,7 @@ static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype) {
   pl.chunks = (int)((V + len - 1) / len);
   const int64_t sbl = (int64_t)VNX_WAVE * ve;
   pl.nsb = (V + sbl - 1) / sbl;
-  int64_t c2 = ((int64_t)device_cus() * kMassPerCu + B - 1) / B;
+  int64_t c2 = ((int64_t)device_cus() * (k == 0 ? kMassPerCuDraw : kMassPerCu) + B - 1) / B;
   const int64_t max_c2 = (pl.nsb + kNW - 1) / kNW;  // at least one sub-block per wave
   if (c2 > max_c2) c2 = max_c2;
   if (c2 < 1) c2 = 1;
