@@ -607,8 +607,12 @@ static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype) {
   SpecPlan pl;
   const int64_t rows = B * (2 * k + 1);
   // chunks of at least kNB / 2 vectors per thread: few rows (a decode batch)
-  // get fewer, longer workgroups instead of thousands of one-load ones
-  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccParts / (2 * k + 1)), kLseWgs);
+  // get fewer, longer workgroups instead of thousands of one-load ones.  A
+  // k = 0 draw (one row per batch row) takes about two workgroups per CU:
+  // at 32 rows of 248,320, 16 chunks per row gave a 20 us shorter config-5
+  // round than 60 (and 8 or 4 chunks were slower again)
+  const int64_t wgs = k == 0 ? 2 * (int64_t)device_cus() : kLseWgs;
+  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccParts / (2 * k + 1)), wgs);
   const int64_t len = ((V + c - 1) / c + ve - 1) / ve * ve;
   pl.len = len;
   pl.chunks = (int)((V + len - 1) / len);
