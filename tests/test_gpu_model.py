@@ -134,7 +134,7 @@ def test_bf16_kernel_path_matches_oracle(hip, window, alibi):
     rng = np.random.default_rng(8)
     committed = [list(rng.integers(0, 1000, 70)) for _ in range(B)]
     lens = torch.zeros(B, dtype=torch.int32, device=dev)
-    m.forward(torch.tensor(committed, device=dev), lens, 0)   # prefill: torch path
+    m.forward(torch.tensor(committed, device=dev), lens, 0)   # prefill: the kernel over query chunks
     lens += 70
     worst = 0.0
     for step, adv in enumerate([(1, 7, 3, 5), (7, 2, 1, 4), (3, 3, 7, 1)]):
@@ -149,6 +149,39 @@ def test_bf16_kernel_path_matches_oracle(hip, window, alibi):
             committed[b] += list(new[b][:adv[b]])
         lens += torch.tensor(adv, dtype=torch.int32, device=dev)
     _say(f"bf16 kernel path worst relative err {worst:.2e}")
+
+
+@pytest.mark.parametrize("window,alibi", [(48, True), (1024, False)])
+def test_bf16_long_forwards_run_the_kernel_in_chunks(hip, window, alibi):
+    """bf16 forwards of more rows than one attention call takes (prefill)
+    run vnx_tree_attn over query chunks: a 100-row prefill, then 70 rows on
+    top of 960 cached ones, where the whole call passes 1024 keys, so the
+    ALiBi path is off for every chunk (the reference's rule for the call,
+    not for each chunk); all rows compared with the fp32 oracle."""
+    _say(f"bf16 chunked forwards window={window} alibi={alibi}")
+    cfg = _toy_cfg(window, alibi)
+    W = VM.init_weights(cfg, seed=5)
+    Wn = {k: v.numpy() for k, v in W.items()}
+    dev = hip.torch_device
+    B = 2
+    m = VM.CometSparkGPU(cfg, W, hip, batch=B, capacity=1100, dtype=torch.bfloat16)
+    rng = np.random.default_rng(12)
+    seq = rng.integers(0, 1000, (B, 1030))
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    got = m.logits(m.forward(torch.from_numpy(seq[:, :100]).to(dev), lens, 0)).cpu().numpy()
+    for b in range(B):
+        ref = OM.forward(Wn, cfg, seq[b:b + 1, :100])[0]
+        rel = float(np.max(np.abs(got[b] - ref)) / np.max(np.abs(ref)))
+        assert rel <= 3e-2, (b, rel)
+    lens += 100
+    m.forward(torch.from_numpy(seq[:, 100:960]).to(dev), lens, 100)
+    lens += 860
+    got = m.logits(m.forward(torch.from_numpy(seq[:, 960:]).to(dev), lens, 960)).cpu().numpy()
+    for b in range(B):
+        ref = OM.forward(Wn, cfg, seq[b:b + 1])[0, -70:]
+        rel = float(np.max(np.abs(got[b] - ref)) / np.max(np.abs(ref)))
+        _say(f"  row {b}: relative err {rel:.2e}")
+        assert rel <= 3e-2, (b, rel)
 
 
 @pytest.mark.parametrize("int4", [True, False])

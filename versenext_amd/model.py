@@ -601,7 +601,7 @@ class CometSparkGPU:
         return w
 
     def _tree_call(self, q, kc, vc, cstr, tree_k, tree_v, tstr, anc, B, H, Hkv, Tp, n, d, tp, follows, out,
-                   seg2=None, gates=None, qkv=None):
+                   seg2=None, gates=None, qkv=None, out_sb=None, alibi_max=1024):
         a = _lib.TreeAttnArgs()
         if qkv is not None:
             # queries from the q|k|v rows, RoPE and the cache write in the kernel
@@ -616,12 +616,14 @@ class CometSparkGPU:
         a.anc = anc.data_ptr() if anc is not None else None; a.anc_batch_stride = 0   # None: a chain (fp32 rows)
         a.f32_rows = int(self.f32_rows)
         # output rows in (B, n, H, d) order: the proj input layout
-        a.out = out.data_ptr(); a.out_dtype = _lib.DTYPE_CODES[out.dtype]; a.out_strides[:] = [n * H * d, d, H * d]
+        a.out = out.data_ptr(); a.out_dtype = _lib.DTYPE_CODES[out.dtype]
+        a.out_strides[:] = [n * H * d if out_sb is None else out_sb, d, H * d]
         a.B, a.H, a.Hkv, a.Tp, a.N, a.d = B, H, Hkv, Tp, n, d
         a.scale = 1.0 / math.sqrt(d)
         a.window = self.cfg.window_size
         if self.cfg.use_alibi:
-            a.alibi_slopes = self.slopes.data_ptr(); a.alibi_max_keys = 1024; a.gates = gates.data_ptr()
+            a.alibi_slopes = self.slopes.data_ptr(); a.alibi_max_keys = max(0, int(alibi_max))
+            a.gates = gates.data_ptr()
         a.tp_batch = tp.data_ptr() if tp is not None else None
         a.tree_follows_prefix = 1 if follows else 0
         if seg2 is not None:
@@ -654,6 +656,30 @@ class CometSparkGPU:
         anc = None if self.f32_rows else self._chain_words(n)
         self._tree_call(q, kc, vc, cstr, kc, vc, cstr, anc, B, H, cfg.n_kv_head, Tmax, n, d, lens,
                         True, o, seg2=(Ly.gk, Ly.gv), gates=Ly.gates, qkv=qkv)
+        return o
+
+    def _attn_kernel_chunked(self, q, li, lens, n, Tmax):
+        """bf16 forwards of more rows than one vnx_tree_attn call takes
+        (prefill): the n new rows (already in the cache) in chunks of at
+        most min(64, window) queries, chunk [c0, c1) seeing each row's
+        lens[b] + c0 prefix rows and its own rows under the chain mask.  The
+        ALiBi path keeps the whole call's rule (lens[b] + n <= 1024,
+        tri_sparse_attn.py:600-607): a chunk passes 1024 - (n - c1) as its
+        key limit.  q (B, H, n, d) bf16."""
+        cfg = self.cfg
+        B, H, d = self.B, cfg.n_head, cfg.head_dim
+        kc, vc = self.kc[li], self.vc[li]
+        Ly = self.layers[li]
+        o = torch.empty((B * n, H * d), dtype=self.act_dtype, device=self.dev)
+        cstr = list(kc.stride()[:3])
+        step = min(64, cfg.window_size) if cfg.window_size > 0 else 64
+        for c0 in range(0, n, step):
+            c1 = min(n, c0 + step)
+            m = c1 - c0
+            lens_c = lens + c0 if c0 else lens
+            self._tree_call(q[:, :, c0:c1], kc, vc, cstr, kc, vc, cstr, self._chain_words(m), B, H, cfg.n_kv_head,
+                            Tmax + c0, m, d, lens_c, True, o[c0:], seg2=(Ly.gk, Ly.gv), gates=Ly.gates,
+                            out_sb=n * H * d, alibi_max=1024 - (n - c1))
         return o
 
     def _attn_torch(self, q, li, lens, n, Tmax):
@@ -851,6 +877,8 @@ class CometSparkGPU:
         else:
             x = torch.empty((M, D), dtype=torch.float32, device=self.dev)                # fp32 residual stream
         use_kernel = self.kernel_attention and (self.f32_rows or (n <= 64 and n <= cfg.window_size))
+        # longer bf16 forwards (prefill): the same kernel over query chunks
+        chunked = self.kernel_attention and not use_kernel
         pending = None
         for li, L in enumerate(self.layers):
             # verify-size bf16 forwards: the norms and the residual adds live in
@@ -904,6 +932,8 @@ class CometSparkGPU:
                 return None                                # every layer's new cache rows are written
             if use_kernel:
                 o = self._attn_kernel(q, li, lens, n, Tmax, qkv=attn_qkv)
+            elif chunked:
+                o = self._attn_kernel_chunked(q, li, lens, n, Tmax)
             else:
                 o = self._attn_torch(q, li, lens, n, Tmax).permute(0, 2, 1, 3).reshape(M, H * d)
                 o = o.to(self.act_dtype).contiguous()
