@@ -270,10 +270,11 @@ extern "C" {
 
 int vnx_lm_head(const void* x, int64_t ldx, const void* w, int64_t ldw, int64_t M, int64_t K, int64_t V,
                 void* out, int out_dtype, int64_t ldo, void* stream) {
-  if (!x || !w || !out || M < 0 || K <= 0 || V <= 0) return VNX_ERR_INVALID_ARG;
+  if (M < 0 || K <= 0 || V <= 0) return VNX_ERR_INVALID_ARG;
   if (out_dtype != VNX_F32 && out_dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
   if (ldx < K || ldw < K || ldo < V) return VNX_ERR_INVALID_ARG;
-  if (M == 0) return VNX_OK;
+  if (M == 0) return VNX_OK;  // nothing is read or written: any pointers
+  if (!x || !w || !out) return VNX_ERR_INVALID_ARG;
   if (M > kLhMaxM || K % kLhSlab != 0 || V >= ((int64_t)1 << 31)) return VNX_ERR_UNSUPPORTED;
   // 16-byte loads of X and W rows; 16-byte (fp32) or 8-byte (bf16) stores of
   // 4 consecutive vocab ids.

@@ -99,8 +99,10 @@ __global__ __launch_bounds__(kNT) void k_softmax_write(const Tin* __restrict__ x
 }
 
 static int row_common_check(const void* x, int dtype, int64_t rows, int64_t V, int64_t ld) {
-  if (!x || rows < 0 || V <= 0 || ld < V) return VNX_ERR_INVALID_ARG;
+  if (rows < 0 || V <= 0 || ld < V) return VNX_ERR_INVALID_ARG;
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
+  if (rows == 0) return VNX_OK;  // nothing is read or written: any pointers
+  if (!x) return VNX_ERR_INVALID_ARG;
   const int ve = dtype == VNX_F32 ? 4 : 8;
   if (!aligned16(x) || ld % ve != 0) return VNX_ERR_UNSUPPORTED;
   return VNX_OK;
@@ -176,8 +178,9 @@ int vnx_row_lse(const void* logits, int dtype, int64_t rows, int64_t V, int64_t 
                 int64_t* argmax, void* workspace, size_t workspace_bytes, void* stream) {
   int st = row_common_check(logits, dtype, rows, V, ld);
   if (st) return st;
-  if (!lse || !(temperature > 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
+  if (!(temperature > 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
   if (rows == 0) return VNX_OK;
+  if (!lse) return VNX_ERR_INVALID_ARG;
   if (rows > (int64_t)1 << 24) return VNX_ERR_UNSUPPORTED;
   RowPlan pl = row_plan(rows, V, dtype);
   if (!workspace || workspace_bytes < row_ws(rows, V, dtype, nullptr)) return VNX_ERR_WORKSPACE;
@@ -196,8 +199,8 @@ int vnx_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64
                    int64_t* argmax, void* workspace, size_t workspace_bytes, void* stream) {
   int st = row_common_check(logits, dtype, rows, V, ld);
   if (st) return st;
-  if (!argmax) return VNX_ERR_INVALID_ARG;
   if (rows == 0) return VNX_OK;
+  if (!argmax) return VNX_ERR_INVALID_ARG;
   if (rows > (int64_t)1 << 24) return VNX_ERR_UNSUPPORTED;
   RowPlan pl = row_plan(rows, V, dtype);
   if (!workspace || workspace_bytes < row_ws(rows, V, dtype, nullptr)) return VNX_ERR_WORKSPACE;
@@ -215,9 +218,9 @@ int vnx_softmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t 
                 void* workspace, size_t workspace_bytes, void* stream) {
   int st = row_common_check(logits, dtype, rows, V, ld);
   if (st) return st;
-  if (!out || ldo < V || !(temperature > 0.0f) || !__builtin_isfinite(temperature))
-    return VNX_ERR_INVALID_ARG;
+  if (ldo < V || !(temperature > 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
   if (rows == 0) return VNX_OK;
+  if (!out) return VNX_ERR_INVALID_ARG;
   if (rows > (int64_t)1 << 24) return VNX_ERR_UNSUPPORTED;
   RowPlan pl = row_plan(rows, V, dtype);
   Carve cv(workspace);

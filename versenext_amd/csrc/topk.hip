@@ -310,8 +310,9 @@ int vnx_row_topk(const void* logits, int dtype, int64_t rows, int64_t V, int64_t
                  int64_t* ids, float* vals, int64_t ldo, void* workspace, size_t workspace_bytes,
                  void* stream) {
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
-  if (rows < 0 || V <= 0 || b < 1 || b > kTopMaxB || b > V || !ids || ldo < b) return VNX_ERR_INVALID_ARG;
-  if (rows == 0) return VNX_OK;
+  if (rows < 0 || V <= 0 || b < 1 || b > kTopMaxB || b > V || ldo < b) return VNX_ERR_INVALID_ARG;
+  if (rows == 0) return VNX_OK;  // nothing is read or written: any pointers
+  if (!ids) return VNX_ERR_INVALID_ARG;
   // Ids travel as 32-bit offsets inside 64-bit keys.
   if (rows > (1 << 24) || V >= ((int64_t)1 << 31)) return VNX_ERR_UNSUPPORTED;
   const int ve = dtype == VNX_F32 ? 4 : 8;
