@@ -17,8 +17,11 @@
  *     asynchronous on that stream;
  *   - return value: VNX_OK (0) or a negative vnx_status; no exception or
  *     longjmp crosses the ABI.  Argument checks happen on the host before
- *     anything is launched; an empty batch (no rows) returns VNX_OK after
- *     the size and dtype checks, without reading any pointer;
+ *     anything is launched.  The verification entry points (vnx_row_lse,
+ *     vnx_row_argmax, vnx_softmax, vnx_spec_accept, vnx_sample,
+ *     vnx_sampler_sample, vnx_greedy_verify, vnx_tree_attn, vnx_tree_greedy,
+ *     vnx_row_topk, vnx_lm_head) return VNX_OK for an empty batch (no rows)
+ *     after the size and dtype checks, without reading any pointer;
  *   - dtype codes: VNX_F32 (fp32), VNX_BF16 (bfloat16) for logits;
  *   - token ids are int64, like the reference's int64 token arrays
  *     (packages/verse_nex/verse_nex/speculative.py:161, :202-203);

@@ -286,8 +286,9 @@ int vnx_tree_greedy(const void* target, int dtype, int64_t B, int N, int64_t V, 
                     int32_t* best, int64_t* out_ids, int64_t* pred, void* workspace, size_t workspace_bytes,
                     void* stream) {
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
-  if (B < 0 || N < 1 || N > kMaxNodes || V <= 0 || !parent) return VNX_ERR_INVALID_ARG;
+  if (B < 0 || N < 1 || N > kMaxNodes || V <= 0) return VNX_ERR_INVALID_ARG;
   if (B == 0) return VNX_OK;
+  if (!parent) return VNX_ERR_INVALID_ARG;
   if (B > (1 << 20) || V > ((int64_t)1 << 31)) return VNX_ERR_UNSUPPORTED;
   int st = check_rows(target, dtype, ld, sb, N + 1, V);
   if (st) return st;
