@@ -204,9 +204,15 @@ using namespace vnx;
 
 extern "C" {
 
+// Chunks per target row of the greedy verify: about two workgroups per CU
+// in all (the rows' chunks count into one arrival counter per batch row;
+// B 4 x 7 rows of 248,320: 30 us against 46 us at 64 chunks per row; B 32:
+// 44 us against 46).
+static int64_t gv_wgs() { return 2 * (int64_t)device_cus(); }
+
 size_t vnx_greedy_verify_workspace(int64_t B, int rows_t, int64_t V) {
   if (B <= 0 || rows_t <= 0 || V <= 0) return 256;
-  const int c = pick_chunks(B * rows_t, V, 4, kMaxChunks, 2048);
+  const int c = pick_chunks(B * rows_t, V, 4, kMaxChunks, gv_wgs());
   Carve cv(nullptr);
   cv.take<unsigned>(B);
   cv.take<float>((size_t)B * rows_t * c);
@@ -227,7 +233,7 @@ int vnx_greedy_verify(const void* target, int dtype, int64_t B, int k, int rows_
   if (st) return st;
   if (!draft_ids || !accept_len || !out_ids) return VNX_ERR_INVALID_ARG;
   const int ve = dtype == VNX_F32 ? 4 : 8;
-  int c = pick_chunks(B * rows_t, V, ve, kMaxChunks, 2048);
+  int c = pick_chunks(B * rows_t, V, ve, kMaxChunks, gv_wgs());
   const int64_t len = ((V + c - 1) / c + ve - 1) / ve * ve;
   c = (int)((V + len - 1) / len);
   if (B * rows_t * (int64_t)c >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
