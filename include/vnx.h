@@ -329,6 +329,19 @@ int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const float* norm_w, float e
                         const void* scales, int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
                         const vnx_rope_kv_args* rk, void* stream);
 
+/* vnx_gemv_w4_rope_kv with the first block's input gathered from the token
+ * embedding (CometSparkV05LM.forward, spark/src/base_model.py:170-208:
+ * tok_emb(idx) x scale, then norm1, then the q|k|v projection), replacing
+ * vnx_embed_rmsnorm + vnx_gemv_w4_rope_kv on a quantized draft's first layer:
+ * x_out[b] = emb[tokens[b]] * scale (fp32, row pitch ldx; emb bf16 with row
+ * pitch lde, a multiple of 8; ids clamped to [0, vocab)), written by the
+ * call, and the product's input is RMSNorm(x_out) * norm_w as with norm_w in
+ * vnx_gemv_w4_rope_kv. */
+int vnx_gemv_w4_rope_kv_embed(const int64_t* tokens, const void* emb, int emb_dtype, int64_t lde, int64_t vocab,
+                              float scale, float* x_out, int64_t ldx, const float* norm_w, float eps,
+                              const uint8_t* wq, int64_t ldw, const void* scales, int scale_dtype, int64_t lds,
+                              int64_t B, int64_t N, int64_t K, int group, const vnx_rope_kv_args* rk, void* stream);
+
 /* vnx_gemv_w4 with the residual add fused: res[b*ldr + n] += (x . W^T)[b, n]
  * (fp32; N < 32768), the `x = x + proj(...)` of VerseNexBlock.forward
  * (cometspark.py:236-247) on a quantized projection. */

@@ -212,6 +212,41 @@ def test_cache_only_forward_writes_the_same_cache(hip, int4):
         assert torch.equal(ms[0].vc[li], ms[1].vc[li]), li
 
 
+def test_int4_decode_embedding_fold_matches_separate_norm(hip):
+    """The INT4 decode's first layer with the token embedding gathered inside
+    its q|k|v GEMV (vnx_gemv_w4_rope_kv_embed) against vnx_embed_rmsnorm and
+    the plain GEMV: the two round the normalized input differently (fp16(x *
+    w) with rstd applied to the product, against fp16 of the normalized row),
+    so the hidden states and layer 0's new cache rows agree to fp16 precision
+    carried through the layers (2e-2 of the largest magnitude)."""
+    cfg = VM.ModelConfig(vocab_size=1000, dim=256, n_layer=2, n_head=4, n_kv_head=2,
+                         layer_pattern=("trisparse", "trisparse"), window_size=1024, num_global_tokens=8,
+                         use_alibi=False, use_rope=True)
+    W = VM.init_weights(cfg, seed=37)
+    dev = hip.torch_device
+    B = 8
+    ms = [VM.CometSparkGPU(cfg, W, hip, batch=B, capacity=64, dtype=torch.bfloat16, int4=True) for _ in range(2)]
+    ms[1].embed_fold = False
+    rng = np.random.default_rng(5)
+    prompt = torch.from_numpy(rng.integers(0, 1000, (B, 12))).to(dev)
+    for m in ms:
+        m.forward(prompt, torch.zeros(B, dtype=torch.int32, device=dev), 0)
+    lens = torch.full((B,), 12, dtype=torch.int32, device=dev)
+    hs = []
+    for step in range(3):
+        tok = torch.from_numpy(rng.integers(0, 1000, (B, 1))).to(dev)
+        hs.append([m.forward(tok, lens, 12 + step).float().cpu() for m in ms])
+        lens += 1
+    torch.cuda.synchronize()
+    for a, b in hs:
+        rel = float((a - b).abs().max() / b.abs().max())
+        _say(f"  hidden relative difference {rel:.2e}")
+        assert rel <= 2e-2
+    k0, k1 = ms[0].kc[0][:, :, 12:15].float().cpu(), ms[1].kc[0][:, :, 12:15].float().cpu()
+    assert float((k0 - k1).abs().max() / k1.abs().max()) <= 2e-2
+    assert torch.equal(ms[0].kc[0][:, :, :12], ms[1].kc[0][:, :, :12])  # the prefill takes one path
+
+
 @pytest.mark.parametrize("window,alibi", [(1024, False), (20, True)])
 def test_kernel_and_torch_attention_paths_agree(hip, window, alibi):
     cfg = _toy_cfg(window, alibi)

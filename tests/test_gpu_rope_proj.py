@@ -163,3 +163,81 @@ def test_rope_proj_rejects(hip):
     # rows must be whole sequences of n tokens
     rk.n = 3
     assert L.vnx_gemv_w4_rope_kv(*args(128)) == _lib.VNX_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("B,n,H,Hkv,d,K", [(32, 1, 16, 8, 64, 1024), (3, 1, 2, 1, 128, 128), (40, 1, 3, 1, 16, 256),
+                                           (24, 1, 56, 8, 64, 1024)])
+def test_gemv_w4_rope_kv_embed_equals_two_calls(hip, B, n, H, Hkv, d, K):
+    """vnx_gemv_w4_rope_kv_embed against vnx_embed_rmsnorm followed by the
+    norm form of vnx_gemv_w4_rope_kv (itself checked against the fp64
+    projection above): the residual rows it writes, the q rows and the cache
+    rows must be bit-identical, since both stage fp16(x * w) of the same fp32
+    x = emb[id] * scale and scale by the same rstd.  Token ids outside the
+    table are clamped, as vnx_embed_rmsnorm clamps them."""
+    _say(f"gemv_w4_rope_kv_embed B={B} n={n} H={H} Hkv={Hkv} d={d} K={K}")
+    dev = hip.torch_device
+    heads = H + 2 * Hkv
+    N, M, cap, T, V, scale = heads * d, B * n, 40, 48, 300, 1.7
+    rng = np.random.default_rng(3 * N + K)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    p, s = Q.quantize_int4_g(W, 128)
+    perm = VM.rope_rows(heads, d, 8).numpy()
+    pq = torch.from_numpy(np.ascontiguousarray(p[perm])).to(dev)
+    sq = torch.from_numpy(np.ascontiguousarray(s[perm])).to(dev)
+    emb = torch.from_numpy(rng.normal(0, 1.0, (V, K)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    ids = torch.from_numpy(rng.integers(0, V, M)).to(dev)
+    ids[0], ids[M - 1] = -3, V + 5
+    nwd = torch.from_numpy((rng.random(K) + 0.5).astype(np.float32)).to(dev)
+    L = _lib.lib()
+    outs = []
+    for fused in (True, False):
+        lens, cos, sin, q, kc, vc = _setup(hip, B, n, H, Hkv, d, cap, T, seed=M + d)
+        lens_d, cos_d, sin_d = lens.to(dev), cos.to(dev), sin.to(dev)
+        rk = _args(lens_d, cos_d, sin_d, q, kc, vc, n, H, Hkv, d, 1, cap)
+        x = torch.full((M, K), SENT, dtype=torch.float32, device=dev)
+        if fused:
+            _lib.check(L.vnx_gemv_w4_rope_kv_embed(
+                VP(ids.data_ptr()), VP(emb.data_ptr()), _lib.VNX_BF16, K, V, scale, VP(x.data_ptr()), K,
+                VP(nwd.data_ptr()), 1e-6, VP(pq.data_ptr()), pq.stride(0), VP(sq.data_ptr()), _lib.VNX_F16,
+                sq.stride(0), M, N, K, 128, ctypes.byref(rk), _st()), "gemv_w4_rope_kv_embed")
+        else:
+            y = torch.empty((M, K), dtype=torch.float16, device=dev)
+            _lib.check(L.vnx_embed_rmsnorm(
+                VP(ids.data_ptr()), VP(emb.data_ptr()), _lib.VNX_BF16, K, V, scale, VP(nwd.data_ptr()), 1e-6, M, K,
+                VP(x.data_ptr()), K, VP(y.data_ptr()), _lib.VNX_F16, K, _st()), "embed_rmsnorm")
+            _lib.check(L.vnx_gemv_w4_rope_kv(VP(x.data_ptr()), K, VP(nwd.data_ptr()), 1e-6, VP(pq.data_ptr()),
+                                             pq.stride(0), VP(sq.data_ptr()), _lib.VNX_F16, sq.stride(0), M, N,
+                                             K, 128, ctypes.byref(rk), _st()), "gemv_w4_rope_kv norm")
+        torch.cuda.synchronize()
+        outs.append((x.cpu(), q.cpu(), kc.cpu(), vc.cpu()))
+    xe = emb.cpu().float()[ids.cpu().clamp(0, V - 1)] * scale
+    assert torch.equal(outs[0][0], xe)
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
+
+
+def test_rope_proj_embed_rejects(hip):
+    dev = hip.torch_device
+    x = torch.zeros((4, 128), dtype=torch.float32, device=dev)
+    emb = torch.zeros((8, 128), dtype=torch.bfloat16, device=dev)
+    ids = torch.zeros(4, dtype=torch.int64, device=dev)
+    nw = torch.ones(128, dtype=torch.float32, device=dev)
+    wq = torch.zeros((64, 64), dtype=torch.uint8, device=dev)
+    sc = torch.ones((64, 1), dtype=torch.float16, device=dev)
+    lens = torch.zeros(4, dtype=torch.int32, device=dev)
+    cs = torch.zeros((8, 32), dtype=torch.float32, device=dev)
+    q = torch.zeros(4096, dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    rk = _lib.RopeKvArgs(VP(lens.data_ptr()), 1, 1, 0, 32, VP(cs.data_ptr()), VP(cs.data_ptr()), 8, 1,
+                         VP(q.data_ptr()), VP(q.data_ptr()), VP(q.data_ptr()), 64, 32, 32, 4)
+
+    def call(ids_p=VP(ids.data_ptr()), dt=_lib.VNX_BF16, lde=128, vocab=8, nw_p=VP(nw.data_ptr())):
+        return L.vnx_gemv_w4_rope_kv_embed(ids_p, VP(emb.data_ptr()), dt, lde, vocab, 1.0, VP(x.data_ptr()), 128,
+                                           nw_p, 1e-6, VP(wq.data_ptr()), 64, VP(sc.data_ptr()), _lib.VNX_F16, 1, 4,
+                                           64, 128, 128, ctypes.byref(rk), _st())
+    assert call(ids_p=None) == _lib.VNX_ERR_INVALID_ARG
+    assert call(nw_p=None) == _lib.VNX_ERR_INVALID_ARG
+    assert call(vocab=0) == _lib.VNX_ERR_INVALID_ARG
+    assert call(lde=64) == _lib.VNX_ERR_INVALID_ARG       # a row shorter than K
+    assert call(dt=_lib.VNX_F16) == _lib.VNX_ERR_UNSUPPORTED
+    assert call(lde=132) == _lib.VNX_ERR_UNSUPPORTED      # rows not 16-byte aligned

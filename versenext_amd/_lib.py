@@ -122,6 +122,9 @@ class RopeKvArgs(ctypes.Structure):
 SIGNATURES.update({
     "vnx_gemv_w4_rope_kv": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64,
                                    _int, ctypes.POINTER(RopeKvArgs), _vp]),
+    "vnx_gemv_w4_rope_kv_embed": (_int, [_vp, _vp, _int, _c_i64, _c_i64, _f32, _vp, _c_i64, _vp, _f32, _vp, _c_i64,
+                                         _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int, ctypes.POINTER(RopeKvArgs),
+                                         _vp]),
     "vnx_tree_attn_workspace": (_c_sz, [_int, _int, _int, _int, _int, _int]),
     "vnx_tree_attn_workspace_args": (_c_sz, [ctypes.POINTER(TreeAttnArgs)]),
     "vnx_tree_attn": (_int, [ctypes.POINTER(TreeAttnArgs), _vp, _c_sz, _vp]),

@@ -63,6 +63,14 @@ struct QGemvParams {
   const float* nw;     // NX: RMSNorm weight (K)
   float eps;
   int64_t row_off;     // batch row of x's first row (the launch's 32-row chunks)
+  // NX 2: x rows are the token embedding, xf unused: row b is
+  // emb[ids[b]] * emb_scale (bf16 table, ids clamped to [0, vocab)), and the
+  // workgroups write those fp32 rows to xout (pitch ldx)
+  const int64_t* ids;
+  const uint16_t* emb;
+  int64_t lde, vocab;
+  float emb_scale;
+  float* xout;
   RopeOut ro;
   int64_t ksplit_len;  // K per grid.y split (multiple of kGK; the launches use K)
 };
@@ -301,10 +309,14 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
 // staged operand is fp16(xf * nw), each wave sums the squares of its groups'
 // values per row, and the epilogue scales row b by rstd_b = 1/sqrt(mean
 // xf^2 + eps) (vnnn.py:593-615, the per-row factor on the fp32 sums).
+// NX 2: the same with the rows gathered from the token embedding (the first
+// block's norm of CometSparkV05LM.forward, spark/src/base_model.py:170-208);
+// group g's values of every row go to xout from workgroup g % gridDim.x, so
+// the fp32 residual stream starts without a launch of its own.
 // TP: 16-row tiles per workgroup (2 for grids of more tiles than CUs: each
 // wave's x block is loaded and staged once for both tiles).  GP: groups per
 // pass of a wave (1 where K has at most one group per wave, or TP 2).
-template <int BITS, int NC, int NW, int QE = 0, bool NX = false, int TP = 1, int GP = 2>
+template <int BITS, int NC, int NW, int QE = 0, int NX = 0, int TP = 1, int GP = 2>
 __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   constexpr int WBYTES = BITS == 4 ? 16 : 32;
   constexpr int XR = NC * 16;            // staged batch rows
@@ -354,6 +366,15 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   float ss[NX ? XL : 1];  // NX: this lane's sums of squares, row (i*64 + lane) / 16
 #pragma unroll
   for (int i = 0; i < (NX ? XL : 1); ++i) ss[i] = 0.0f;
+  const uint16_t* erow[NX == 2 ? XL : 1];  // NX 2: embedding row of row (i*64 + lane) / 16
+  if constexpr (NX == 2) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      int64_t tok = p.ids[min((i * 64 + lane) / 16, (int)p.B - 1)];
+      tok = tok < 0 ? 0 : (tok >= p.vocab ? p.vocab - 1 : tok);  // never outside the table
+      erow[i] = p.emb + tok * p.lde;
+    }
+  }
 
   static_assert(GP == 1 || GP == 2, "one or two groups per pass");
   for (int g0 = wave; g0 < ngroups; g0 += GP * NW) {
@@ -381,7 +402,9 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
       for (int i = 0; i < XL; ++i) {
         const int b = (i * 64 + lane) / 16;
-        if constexpr (NX) {
+        if constexpr (NX == 2) {
+          xv[u][i][0] = *reinterpret_cast<const u32x4*>(erow[i] + k0 + m * 8);
+        } else if constexpr (NX) {
           const float* src = p.xf + (int64_t)min(b, (int)p.B - 1) * p.ldx + k0 + m * 8;
           xv[u][i][0] = *reinterpret_cast<const u32x4*>(src);
           xv[u][i][1] = *reinterpret_cast<const u32x4*>(src + 4);
@@ -411,7 +434,25 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
         u32x4 v;
         if constexpr (NX) {
           // fp16(x * w) of 8 columns; their squares into ss (counted once)
-          const f32x4 xa = __builtin_bit_cast(f32x4, xv[u][i][0]), xb = __builtin_bit_cast(f32x4, xv[u][i][1]);
+          f32x4 xa, xb;
+          if constexpr (NX == 2) {
+            // bf16 -> fp32 is exact; one rounding for the scale, as the
+            // residual stream's first value
+            const u32x4 e = xv[u][i][0];
+            const float sc_e = p.emb_scale;
+            xa = f32x4{__builtin_bit_cast(float, e.x << 16) * sc_e, __builtin_bit_cast(float, e.x & 0xFFFF0000u) * sc_e,
+                       __builtin_bit_cast(float, e.y << 16) * sc_e, __builtin_bit_cast(float, e.y & 0xFFFF0000u) * sc_e};
+            xb = f32x4{__builtin_bit_cast(float, e.z << 16) * sc_e, __builtin_bit_cast(float, e.z & 0xFFFF0000u) * sc_e,
+                       __builtin_bit_cast(float, e.w << 16) * sc_e, __builtin_bit_cast(float, e.w & 0xFFFF0000u) * sc_e};
+            if (use && b < p.B && gg[u] % (int)gridDim.x == (int)blockIdx.x) {
+              float* dst = p.xout + (int64_t)b * p.ldx + (int64_t)gg[u] * kGK + m * 8;
+              *reinterpret_cast<f32x4*>(dst) = xa;
+              *reinterpret_cast<f32x4*>(dst + 4) = xb;
+            }
+          } else {
+            xa = __builtin_bit_cast(f32x4, xv[u][i][0]);
+            xb = __builtin_bit_cast(f32x4, xv[u][i][1]);
+          }
           const f32x4 wa = __builtin_bit_cast(f32x4, nwv[u][0]), wb = __builtin_bit_cast(f32x4, nwv[u][1]);
           float t = 0.0f;
 #pragma unroll
@@ -742,6 +783,10 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
     QGemvParams c = p;
     c.x = p.x + b0 * p.ldx;
     if (p.xf) c.xf = p.xf + b0 * p.ldx;
+    if (p.emb) {
+      c.ids = p.ids + b0;
+      c.xout = p.xout + b0 * p.ldx;
+    }
     if (p.y) c.y = p.y + b0 * p.ldy;
     if (p.yh) c.yh = p.yh + b0 * p.ldy;
     c.row_off = b0;
@@ -777,11 +822,11 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
     if (two) VNX_QTILE_W(2, QE, NX); else VNX_QTILE_W(1, QE, NX); \
   } while (0)
       if (c.rope_on) {
-        if (c.xf) VNX_QTILE_Q(2, true); else VNX_QTILE_Q(2, false);
+        if (c.emb) VNX_QTILE_Q(2, 2); else if (c.xf) VNX_QTILE_Q(2, 1); else VNX_QTILE_Q(2, 0);
       } else if (c.yh) {
-        if (c.xf) VNX_QTILE_Q(1, true); else VNX_QTILE_Q(1, false);
+        if (c.xf) VNX_QTILE_Q(1, 1); else VNX_QTILE_Q(1, 0);
       } else if (c.resid) {
-        VNX_QTILE_Q(3, false);
+        VNX_QTILE_Q(3, 0);
       } else if (bits == 4) {
         if (two) { if (wide) VNX_QTILE(4, 2, 8); else VNX_QTILE(4, 2, 4); }
         else { if (wide) VNX_QTILE(4, 1, 8); else VNX_QTILE(4, 1, 4); }
@@ -925,6 +970,29 @@ int vnx_gemv_w4_rope_kv(const void* x, int64_t ldx, const float* norm_w, float e
   if (rs) return rs;
   if (B % rk->n) return VNX_ERR_INVALID_ARG;  // rows are whole sequences of n tokens
   p.x = static_cast<const uint16_t*>(x); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
+  p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.rope_on = 1;
+  p.gpg = group / kGK;
+  const int st = qgemv_check(p, 4);
+  if (st) return st;
+  return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemv_w4_rope_kv_embed(const int64_t* tokens, const void* emb, int emb_dtype, int64_t lde, int64_t vocab,
+                              float scale, float* x_out, int64_t ldx, const float* norm_w, float eps,
+                              const uint8_t* wq, int64_t ldw, const void* scales, int scale_dtype, int64_t lds,
+                              int64_t B, int64_t N, int64_t K, int group, const vnx_rope_kv_args* rk, void* stream) {
+  if (scale_dtype != VNX_F16 && scale_dtype != VNX_F32) return VNX_ERR_UNSUPPORTED;
+  if (!tokens || !emb || !x_out || !norm_w || vocab < 1 || lde < K) return VNX_ERR_INVALID_ARG;
+  if (emb_dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
+  if (lde % 8 || !aligned16(emb)) return VNX_ERR_UNSUPPORTED;  // 16-byte row loads
+  QGemvParams p{};
+  p.xf = x_out; p.nw = norm_w; p.eps = eps;
+  p.ids = tokens; p.emb = static_cast<const uint16_t*>(emb); p.lde = lde; p.vocab = vocab; p.emb_scale = scale;
+  p.xout = x_out;
+  const int rs = rope_out_from(rk, N, &p.ro);
+  if (rs) return rs;
+  if (B % rk->n) return VNX_ERR_INVALID_ARG;  // rows are whole sequences of n tokens
+  p.x = reinterpret_cast<const uint16_t*>(x_out); p.ldx = ldx; p.w = wq; p.ldw = ldw; p.sc = scales; p.lds = lds;
   p.sc_f16 = scale_dtype == VNX_F16; p.B = B; p.N = N; p.K = K; p.G = group; p.rope_on = 1;
   p.gpg = group / kGK;
   const int st = qgemv_check(p, 4);

@@ -402,6 +402,25 @@ class _Linear:
             ctypes.byref(rk), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4_rope_kv")
         return True
 
+    def rope_kv_embed(self, tokens: torch.Tensor, emb: torch.Tensor, scale: float, x: torch.Tensor, rk,
+                      norm_w: torch.Tensor, eps: float) -> bool:
+        """rope_kv of RMSNorm(x) * norm_w where x = emb[tokens] * scale is
+        written by the same call (vnx_gemv_w4_rope_kv_embed: the first
+        layer's input straight from the bf16 token embedding); False (nothing
+        done) when it does not apply."""
+        M = x.shape[0]
+        if (self.wq_rope is None or M > 64 or x.dtype != torch.float32 or emb.dtype != torch.bfloat16
+                or emb.stride(1) != 1 or emb.stride(0) % 8 or emb.data_ptr() % 16 or x.stride(1) != 1):
+            return False
+        P = ctypes.c_void_p
+        _lib.check(self.hip._L.vnx_gemv_w4_rope_kv_embed(
+            P(tokens.data_ptr()), P(emb.data_ptr()), _lib.VNX_BF16, emb.stride(0), emb.shape[0], float(scale),
+            P(x.data_ptr()), x.stride(0), P(norm_w.data_ptr()), float(eps), P(self.wq_rope.data_ptr()),
+            self.wq_rope.stride(0), P(self.sc_rope.data_ptr()), _lib.VNX_F16, self.sc_rope.stride(0), M, self.N,
+            self.K, 128, ctypes.byref(rk), P(torch.cuda.current_stream(x.device).cuda_stream)),
+            "gemv_w4_rope_kv_embed")
+        return True
+
     def gemv_swiglu(self, x: torch.Tensor, norm_w: Optional[torch.Tensor] = None,
                     eps: float = 0.0) -> Optional[torch.Tensor]:
         """silu(gate) * up (M, N/2) fp16 of a fused [gate; up] INT4 weight for
@@ -556,6 +575,9 @@ class CometSparkGPU:
         # dtype of the activations fed to the projections: fp16 for the INT4
         # GEMVs, else the compute dtype
         self.act_dtype = torch.float16 if int4 else dtype
+        # INT4 decode: the first layer's q|k|v GEMV gathers the token embedding
+        # itself (False: vnx_embed_rmsnorm first, the form it is tested against)
+        self.embed_fold = True
 
     @classmethod
     def from_vn(cls, path: str, hip, batch: int, capacity: int, dtype=torch.bfloat16, int4: bool = True,
@@ -901,7 +923,10 @@ class CometSparkGPU:
                                  self.cos.shape[0], int(cfg.use_rope), P(q.data_ptr()), P(kc.data_ptr()),
                                  P(vc.data_ptr()), kc.stride(0), kc.stride(1), kc.stride(2), self.cap)
             done = False                                   # q and the cache rows written
-            if li == 0:
+            if li == 0 and qfused and self.embed_fold and L.wqkv.rope_kv_embed(
+                    tok, self.emb, self.emb_scale, x, rk, L.norm1, cfg.eps):
+                done = True                                # embedding, norm, q|k|v, RoPE, cache rows: one call
+            elif li == 0:
                 h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
                 self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
             elif fused:
