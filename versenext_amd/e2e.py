@@ -82,8 +82,12 @@ class SpecDecodeEngine:
         B, k = self.B, self.k
         self.pbuf = torch.empty((B, k + 1, self.V), dtype=torch.float32, device=dev)
         self.qbuf = torch.empty((B, k, self.V), dtype=torch.float32, device=dev)
-        self.u_draft = torch.zeros((k, B), dtype=torch.float32, device=dev)
-        self.u_acc = torch.zeros((B, k + 1), dtype=torch.float32, device=dev)
+        # both uniform arrays in one buffer (u_acc at a 256-byte boundary), so
+        # a round's fill is one launch
+        off = (k * B + 63) // 64 * 64
+        self.u_all = torch.zeros(off + B * (k + 1), dtype=torch.float32, device=dev)
+        self.u_draft = self.u_all[:k * B].view(k, B)
+        self.u_acc = self.u_all[off:].view(B, k + 1)
         self.xsT = torch.zeros((k, B), dtype=torch.int64, device=dev)   # draft token i of every row: xsT[i]
         self.toks = torch.zeros((B, k + 1), dtype=torch.int64, device=dev)  # [c, x_1 .. x_k] per row
         self.c = torch.zeros(B, dtype=torch.int64, device=dev)
@@ -109,8 +113,7 @@ class SpecDecodeEngine:
     # ---- one round on the static buffers ---------------------------------
     def _fill_uniforms(self):
         if not self.greedy:
-            torch.rand(self.u_draft.shape, generator=self.gen, device=self.dev, out=self.u_draft)
-            torch.rand(self.u_acc.shape, generator=self.gen, device=self.dev, out=self.u_acc)
+            torch.rand(self.u_all.shape, generator=self.gen, device=self.dev, out=self.u_all)
 
     def _round(self, Tmax_t: int, Tmax_d: int):
         B, k = self.B, self.k
