@@ -714,6 +714,18 @@ int vnx_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed,
 int vnx_gemm_bf16_norm(const float* x, int64_t ldx, const float* norm_w, float eps, const void* w_packed,
                        int64_t M, int64_t N, int64_t K, int epilogue, void* y, int64_t ldy, void* stream);
 
+/* vnx_gemm_bf16_norm of the first block, its input gathered from the token
+ * embedding (CometSparkV05LM.forward, spark/src/base_model.py:170-208:
+ * tok_emb(idx) x scale, then norm1, then the q|k|v projection), replacing
+ * vnx_embed_rmsnorm + vnx_gemm_bf16 on the target's first layer: x_out[m] =
+ * emb[tokens[m]] * scale (fp32, row pitch ldx; emb bf16 with row pitch lde, a
+ * multiple of 8; ids clamped to [0, vocab)), written by the call, and y (M, N)
+ * bf16 = RMSNorm(x_out) * norm_w times W as vnx_gemm_bf16_norm (no epilogue). */
+int vnx_gemm_bf16_norm_embed(const int64_t* tokens, const void* emb, int emb_dtype, int64_t lde, int64_t vocab,
+                             float scale, float* x_out, int64_t ldx, const float* norm_w, float eps,
+                             const void* w_packed, int64_t M, int64_t N, int64_t K, void* y, int64_t ldy,
+                             void* stream);
+
 /* vnx_gemm_bf16 (batch 1) with the residual add fused: res[m*ldr + n] +=
  * acc[m, n] (fp32), the `x = x + proj(...)` of VerseNexBlock.forward
  * (cometspark.py:236-247). */

@@ -185,6 +185,69 @@ def test_norm_input(hip, M, N, K, epi):
     _say(f"  worst err / bound = {worst:.2e}")
 
 
+@pytest.mark.parametrize("M,N,K", [(224, 2048, 1024), (37, 96, 192), (257, 40, 64), (7, 3072, 2048)])
+def test_norm_embed_equals_two_calls(hip, M, N, K):
+    """vnx_gemm_bf16_norm_embed against vnx_embed_rmsnorm followed by
+    vnx_gemm_bf16_norm (checked against fp64 above): the residual rows it
+    writes and the product must be bit-identical, since both stage bf16(x * w)
+    of the same fp32 x = emb[id] * scale and scale by the same rstd.  Token
+    ids outside the table are clamped, as vnx_embed_rmsnorm clamps them."""
+    _say(f"gemm norm embed M={M} N={N} K={K}")
+    dev = hip.torch_device
+    g = torch.Generator(device=dev)
+    g.manual_seed(3 * M + N + K)
+    V, scale, eps = 500, 32.0, 1e-6
+    emb = torch.randn((V, K), generator=g, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, V, (M,), generator=g, device=dev)
+    ids[0], ids[M - 1] = -1, V + 3
+    nw = torch.rand((K,), generator=g, device=dev) + 0.5
+    w = (torch.randn((1, N, K), generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wp, _ = _pack(w)
+    L = _lib.lib()
+    st = P(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for fused in (True, False):
+        x = torch.full((M, K), 7.0, dtype=torch.float32, device=dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        if fused:
+            _lib.check(L.vnx_gemm_bf16_norm_embed(P(ids.data_ptr()), P(emb.data_ptr()), _lib.VNX_BF16, K, V, scale,
+                                                  P(x.data_ptr()), K, P(nw.data_ptr()), eps, P(wp.data_ptr()), M, N,
+                                                  K, P(y.data_ptr()), N, st), "gemm_norm_embed")
+        else:
+            h = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+            _lib.check(L.vnx_embed_rmsnorm(P(ids.data_ptr()), P(emb.data_ptr()), _lib.VNX_BF16, K, V, scale,
+                                           P(nw.data_ptr()), eps, M, K, P(x.data_ptr()), K, P(h.data_ptr()),
+                                           _lib.VNX_BF16, K, st), "embed_rmsnorm")
+            _lib.check(L.vnx_gemm_bf16_norm(P(x.data_ptr()), K, P(nw.data_ptr()), eps, P(wp.data_ptr()), M, N, K, 0,
+                                            P(y.data_ptr()), N, st), "gemm_norm")
+        torch.cuda.synchronize()
+        outs.append((x.cpu(), y.cpu()))
+    assert torch.equal(outs[0][0], emb.cpu().float()[ids.cpu().clamp(0, V - 1)] * scale)
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+
+
+def test_norm_embed_rejects(hip):
+    dev = hip.torch_device
+    x = torch.zeros((4, 64), dtype=torch.float32, device=dev)
+    emb = torch.zeros((8, 72), dtype=torch.bfloat16, device=dev)
+    ids = torch.zeros(4, dtype=torch.int64, device=dev)
+    nw = torch.ones(64, dtype=torch.float32, device=dev)
+    wp = torch.zeros(64 * 64, dtype=torch.bfloat16, device=dev)
+    y = torch.zeros((4, 64), dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    st = P(torch.cuda.current_stream().cuda_stream)
+
+    def call(ids_p=P(ids.data_ptr()), dt=_lib.VNX_BF16, lde=72, vocab=8):
+        return L.vnx_gemm_bf16_norm_embed(ids_p, P(emb.data_ptr()), dt, lde, vocab, 1.0, P(x.data_ptr()), 64,
+                                          P(nw.data_ptr()), 1e-6, P(wp.data_ptr()), 4, 64, 64, P(y.data_ptr()), 64, st)
+    assert call(ids_p=None) == _lib.VNX_ERR_INVALID_ARG
+    assert call(vocab=0) == _lib.VNX_ERR_INVALID_ARG
+    assert call(lde=32) == _lib.VNX_ERR_INVALID_ARG       # a row shorter than K
+    assert call(dt=_lib.VNX_F32) == _lib.VNX_ERR_UNSUPPORTED
+    assert call(lde=68) == _lib.VNX_ERR_UNSUPPORTED       # rows not 16-byte aligned
+
+
 @pytest.mark.parametrize("M,N,K", [(224, 1024, 1024), (224, 1024, 2752), (9, 100, 64)])
 def test_residual_epilogue(hip, M, N, K):
     """vnx_gemm_bf16_residual: res += x . W^T in fp32; the GEMM bar plus one

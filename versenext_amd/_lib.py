@@ -151,6 +151,8 @@ SIGNATURES.update({
     "vnx_mod_route_x": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64,
                                _vp, _c_i64, _c_i64, _int, _vp]),
     "vnx_gemm_bf16_norm": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _c_i64, _c_i64, _int, _vp, _c_i64, _vp]),
+    "vnx_gemm_bf16_norm_embed": (_int, [_vp, _vp, _int, _c_i64, _c_i64, _f32, _vp, _c_i64, _vp, _f32, _vp, _c_i64,
+                                        _c_i64, _c_i64, _vp, _c_i64, _vp]),
     "vnx_gemm_bf16_residual": (_int, [_vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp]),
     "vnx_mod_route": (_int, [_vp, _c_i64, _c_i64, _int, _int, _int, _vp, _c_i64, _vp]),
     "vnx_mod_swiglu": (_int, [_vp, _int, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _int, _c_i64, _vp, _int, _c_i64,

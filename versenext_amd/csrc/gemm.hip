@@ -52,6 +52,14 @@ struct VgParams {
   const float* xf;         // NX: the fp32 rows to normalize (x unused), pitch ldx
   const float* nw;         // NX: RMSNorm weight (K)
   float eps;
+  // NX 2: the rows to normalize are the token embedding (xf unused): row m
+  // is emb[ids[m]] * emb_scale (bf16 table, ids clamped to [0, vocab)); the
+  // workgroups of N group c % ng write chunk c of their rows to xout (pitch ldx)
+  const int64_t* ids;
+  const uint16_t* emb;
+  int64_t lde, vocab;
+  float emb_scale;
+  float* xout;
 };
 
 
@@ -80,7 +88,7 @@ __device__ __forceinline__ int xs_off(int r, int c16) { return r * kVgRowB + ((c
 // are staged as bf16, each thread also summing the squares of its row's
 // values, and the epilogue scales row m by rstd_m = 1/sqrt(mean x^2 + eps)
 // (the norm's per-row factor, applied to the fp32 accumulators).
-template <int OT, int EPI, int WN, bool NX = false>
+template <int OT, int EPI, int WN, int NX = 0>
 __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   constexpr int WK = 4 / WN;
   constexpr int SLAB = WK * 32 * kVgRowB;  // staged X bytes per pass (WK chunks)
@@ -109,7 +117,13 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   const int xr = tid >> 3, xc = tid & 7;
   const int xrc = min(m0 + xr, p.M - 1);
   const uint16_t* xrow = p.x + z * p.sxb + (int64_t)xrc * p.ldx + xc * 8;
-  const float* xfrow = NX ? p.xf + (int64_t)xrc * p.ldx + xc * 8 : nullptr;
+  const float* xfrow = NX == 1 ? p.xf + (int64_t)xrc * p.ldx + xc * 8 : nullptr;
+  const uint16_t* erow = nullptr;  // NX 2: this thread's embedding row, column xc*8
+  if constexpr (NX == 2) {
+    int64_t tok = p.ids[xrc];
+    tok = tok < 0 ? 0 : (tok >= p.vocab ? p.vocab - 1 : tok);  // never outside the table
+    erow = p.emb + tok * p.lde + xc * 8;
+  }
   const uint32_t xkeep = m0 + xr < p.M ? 0xFFFFFFFFu : 0u;
   const uint16_t* wt = p.w + z * p.swb + (int64_t)nie * nch * 2048 + lane * 8;
 
@@ -151,8 +165,12 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
     for (int j = 0; j < WK; ++j) {
       const int c = min(ps * WK + j, nch - 1);
       if constexpr (NX) {
-        xs[j][0] = *reinterpret_cast<const u32x4*>(xfrow + c * kVgChunk);
-        xs[j][1] = *reinterpret_cast<const u32x4*>(xfrow + c * kVgChunk + 4);
+        if constexpr (NX == 2) {
+          xs[j][0] = *reinterpret_cast<const u32x4*>(erow + c * kVgChunk);
+        } else {
+          xs[j][0] = *reinterpret_cast<const u32x4*>(xfrow + c * kVgChunk);
+          xs[j][1] = *reinterpret_cast<const u32x4*>(xfrow + c * kVgChunk + 4);
+        }
       } else {
         xs[j][0] = *reinterpret_cast<const u32x4*>(xrow + c * kVgChunk);
       }
@@ -184,7 +202,25 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
           // bf16(x * w) of 8 consecutive columns; their squares into ss
           const bool live = ps * WK + q < nch;  // clamped re-reads are not summed
           const int c = min(ps * WK + q, nch - 1);
-          const f32x4 xa = __builtin_bit_cast(f32x4, xv[j][q][0]), xb = __builtin_bit_cast(f32x4, xv[j][q][1]);
+          f32x4 xa, xb;
+          if constexpr (NX == 2) {
+            // bf16 -> fp32 is exact; one rounding for the scale (the
+            // residual stream's first value)
+            const u32x4 e = xv[j][q][0];
+            const float se = p.emb_scale;
+            xa = f32x4{__builtin_bit_cast(float, e.x << 16) * se, __builtin_bit_cast(float, e.x & 0xFFFF0000u) * se,
+                       __builtin_bit_cast(float, e.y << 16) * se, __builtin_bit_cast(float, e.y & 0xFFFF0000u) * se};
+            xb = f32x4{__builtin_bit_cast(float, e.z << 16) * se, __builtin_bit_cast(float, e.z & 0xFFFF0000u) * se,
+                       __builtin_bit_cast(float, e.w << 16) * se, __builtin_bit_cast(float, e.w & 0xFFFF0000u) * se};
+            if (live && c % p.ng == gi && m0 + xr < p.M) {
+              float* dst = p.xout + (int64_t)(m0 + xr) * p.ldx + c * kVgChunk + xc * 8;
+              *reinterpret_cast<f32x4*>(dst) = xa;
+              *reinterpret_cast<f32x4*>(dst + 4) = xb;
+            }
+          } else {
+            xa = __builtin_bit_cast(f32x4, xv[j][q][0]);
+            xb = __builtin_bit_cast(f32x4, xv[j][q][1]);
+          }
           const f32x4 wa = *reinterpret_cast<const f32x4*>(&nws[c * kVgChunk + xc * 8]);
           const f32x4 wb = *reinterpret_cast<const f32x4*>(&nws[c * kVgChunk + xc * 8 + 4]);
           float t = 0.0f;
@@ -567,20 +603,21 @@ int vg_run(VgParams p, int batch, int epi, int y_dtype, bool nx, hipStream_t s) 
   const dim3 grid((unsigned)wgs, (unsigned)batch);
   auto launch = [&](auto ot, auto ep, auto nxc) {
     constexpr int OT = decltype(ot)::value, EP = decltype(ep)::value;
-    constexpr bool NXC = decltype(nxc)::value;
+    constexpr int NXC = decltype(nxc)::value;
     if (wn == 4) hipLaunchKernelGGL((k_vgemm<OT, EP, 4, NXC>), grid, dim3(256), 0, s, p);
     else if (wn == 2) hipLaunchKernelGGL((k_vgemm<OT, EP, 2, NXC>), grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL((k_vgemm<OT, EP, 1, NXC>), grid, dim3(256), 0, s, p);
   };
   if (epi == 3) {
-    launch(IntC<0>{}, IntC<3>{}, BoolC<false>{});
+    launch(IntC<0>{}, IntC<3>{}, IntC<0>{});
   } else if (nx) {
-    if (epi == VNX_EPI_SWIGLU) launch(IntC<1>{}, IntC<1>{}, BoolC<true>{});
-    else launch(IntC<1>{}, IntC<0>{}, BoolC<true>{});
+    if (p.emb) launch(IntC<1>{}, IntC<0>{}, IntC<2>{});  // embedding rows: no epilogue
+    else if (epi == VNX_EPI_SWIGLU) launch(IntC<1>{}, IntC<1>{}, IntC<1>{});
+    else launch(IntC<1>{}, IntC<0>{}, IntC<1>{});
   } else {
     auto by_epi = [&](auto ot) {
-      if (epi == VNX_EPI_SWIGLU) launch(ot, IntC<1>{}, BoolC<false>{});
-      else launch(ot, IntC<0>{}, BoolC<false>{});
+      if (epi == VNX_EPI_SWIGLU) launch(ot, IntC<1>{}, IntC<0>{});
+      else launch(ot, IntC<0>{}, IntC<0>{});
     };
     if (y_dtype == VNX_F32) by_epi(IntC<0>{});
     else if (y_dtype == VNX_BF16) by_epi(IntC<1>{});
@@ -654,6 +691,30 @@ int vnx_gemm_bf16_norm(const float* x, int64_t ldx, const float* norm_w, float e
   p.ldx = ldx; p.ldy = ldy;
   p.M = (int)M; p.N = (int)N; p.K = (int)K;
   return vg_run(p, 1, epilogue, VNX_BF16, true, static_cast<hipStream_t>(stream));
+}
+
+int vnx_gemm_bf16_norm_embed(const int64_t* tokens, const void* emb, int emb_dtype, int64_t lde, int64_t vocab,
+                             float scale, float* x_out, int64_t ldx, const float* norm_w, float eps,
+                             const void* w_packed, int64_t M, int64_t N, int64_t K, void* y, int64_t ldy,
+                             void* stream) {
+  if (!tokens || !emb || !x_out || !norm_w || !w_packed || !y || M < 0 || N < 0 || K <= 0 || !(eps >= 0.0f))
+    return VNX_ERR_INVALID_ARG;
+  if (vocab < 1 || lde < K || ldx < K || ldy < N) return VNX_ERR_INVALID_ARG;
+  if (emb_dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
+  if (M == 0 || N == 0) return VNX_OK;
+  if (K % kVgChunk || K > kVgNormMaxK || ldx % 4 || lde % 8 || !aligned16(x_out) || !aligned16(emb) ||
+      !aligned16(norm_w) || !aligned16(w_packed))
+    return VNX_ERR_UNSUPPORTED;
+  if (M >= INT32_MAX || N >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  VgParams p{};
+  p.xf = x_out; p.nw = norm_w; p.eps = eps;
+  p.x = reinterpret_cast<const uint16_t*>(x_out);  // not read (NX)
+  p.ids = tokens; p.emb = static_cast<const uint16_t*>(emb); p.lde = lde; p.vocab = vocab; p.emb_scale = scale;
+  p.xout = x_out;
+  p.w = static_cast<const uint16_t*>(w_packed); p.y = y;
+  p.ldx = ldx; p.ldy = ldy;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  return vg_run(p, 1, VNX_EPI_NONE, VNX_BF16, true, static_cast<hipStream_t>(stream));
 }
 
 int vnx_gemm_bf16_residual(const void* x, int64_t ldx, const void* w_packed, int64_t M, int64_t N, int64_t K,

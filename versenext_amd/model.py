@@ -365,6 +365,26 @@ class _Linear:
             ncols, ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemm_bf16_norm")
         return y
 
+    def gemm_norm_embed(self, tokens: torch.Tensor, emb: torch.Tensor, scale: float, x: torch.Tensor,
+                        norm_w: torch.Tensor, eps: float) -> Optional[torch.Tensor]:
+        """gemm_norm of x = emb[tokens] * scale, which the same call writes
+        into x (vnx_gemm_bf16_norm_embed: the first layer's input straight
+        from the bf16 token embedding); None (nothing done) when it does not
+        apply."""
+        M = x.shape[0]
+        if (self.wp is None or M > self.GEMM_MAX_M or x.dtype != torch.float32 or x.stride(1) != 1
+                or self.K > 2048 or emb.dtype != torch.bfloat16 or emb.stride(1) != 1 or emb.stride(0) % 8
+                or emb.data_ptr() % 16):
+            return None
+        y = torch.empty((M, self.N), dtype=torch.bfloat16, device=x.device)
+        P = ctypes.c_void_p
+        _lib.check(self.hip._L.vnx_gemm_bf16_norm_embed(
+            P(tokens.data_ptr()), P(emb.data_ptr()), _lib.VNX_BF16, emb.stride(0), emb.shape[0], float(scale),
+            P(x.data_ptr()), x.stride(0), P(norm_w.data_ptr()), float(eps), P(self.wp.data_ptr()), M, self.N,
+            self.K, P(y.data_ptr()), self.N, P(torch.cuda.current_stream(x.device).cuda_stream)),
+            "gemm_bf16_norm_embed")
+        return y
+
     def gemm_residual(self, x: torch.Tensor, res: torch.Tensor) -> bool:
         """res (M, N) fp32 += x . W^T (vnx_gemm_bf16_residual); False (nothing
         done) when this weight or x does not qualify."""
@@ -575,8 +595,9 @@ class CometSparkGPU:
         # dtype of the activations fed to the projections: fp16 for the INT4
         # GEMVs, else the compute dtype
         self.act_dtype = torch.float16 if int4 else dtype
-        # INT4 decode: the first layer's q|k|v GEMV gathers the token embedding
-        # itself (False: vnx_embed_rmsnorm first, the form it is tested against)
+        # the first layer's q|k|v product gathers the token embedding itself
+        # (INT4 decode and bf16 verify-size forwards; False: vnx_embed_rmsnorm
+        # first, the form it is tested against)
         self.embed_fold = True
 
     @classmethod
@@ -926,6 +947,9 @@ class CometSparkGPU:
             if li == 0 and qfused and self.embed_fold and L.wqkv.rope_kv_embed(
                     tok, self.emb, self.emb_scale, x, rk, L.norm1, cfg.eps):
                 done = True                                # embedding, norm, q|k|v, RoPE, cache rows: one call
+            elif li == 0 and fused and self.embed_fold and (qkv := L.wqkv.gemm_norm_embed(
+                    tok, self.emb, self.emb_scale, x, L.norm1, cfg.eps)) is not None:
+                pass                                       # embedding, norm and q|k|v: one call
             elif li == 0:
                 h = torch.empty((M, D), dtype=self.act_dtype, device=self.dev)
                 self._embed_rms(tok, L.norm1, x, h)        # token embedding folded into the first norm
