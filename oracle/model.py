@@ -178,7 +178,8 @@ def forward(W, cfg, idx, return_hidden=False, last_n=None, head=None):
     the last last_n positions go through the head (the verifier reads k+1
     rows, speculative.py:218-220).  head: the (V, D) head weight when it is
     stored apart from the input embedding (a quantized copy of the tied
-    table), else the tied table itself (cometspark.py:396-398)."""
+    table); else W['head.weight'] for an untied model (cfg.tie_weights
+    False), else the tied table itself (cometspark.py:396-398)."""
     idx = np.asarray(idx, dtype=np.int64)
     if idx.ndim == 1:
         idx = idx[None]
@@ -200,21 +201,77 @@ def forward(W, cfg, idx, return_hidden=False, last_n=None, head=None):
         return x
     if last_n is not None:
         x = x[:, -last_n:]
+    if head is None and not getattr(cfg, "tie_weights", True):
+        head = W["head.weight"]
     return x @ (emb if head is None else head).T
+
+
+def _row_chunks(n_rows: int, rows: int):
+    return [(i, min(n_rows, i + rows)) for i in range(0, n_rows, rows)]
+
+
+def _threads() -> int:
+    import os
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def _parallel_rows(fn, a, out, rows: int = 4096):
+    """out[i:j] = fn(a[i:j]) over row chunks of a 2-D array, on a thread pool
+    (numpy's ufuncs release the GIL); the result is the same as one call."""
+    from concurrent.futures import ThreadPoolExecutor
+    chunks = _row_chunks(a.shape[0], rows)
+    if len(chunks) == 1:
+        out[...] = fn(a)
+        return out
+
+    def one(c):
+        out[c[0]:c[1]] = fn(a[c[0]:c[1]])
+    with ThreadPoolExecutor(max_workers=_threads()) as ex:
+        list(ex.map(one, chunks))
+    return out
+
+
+def _bf16_round_block(a):
+    u = a.view(np.uint32)
+    # finite values and infinities cannot overflow uint32 here (the largest,
+    # 0xFF800000, plus 0x8000 stays below 2^32); NaNs are restored below
+    r = u + np.uint32(0x7FFF)
+    r += (u >> np.uint32(16)) & np.uint32(1)
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
+    nan = np.isnan(a)
+    if nan.any():
+        out = np.where(nan, a, out)
+    return out
 
 
 def bf16_round(a):
     """float32 values rounded to bfloat16 (round to nearest, ties to even),
     returned as float32."""
     a = np.ascontiguousarray(a, dtype=np.float32)
-    u = a.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    out = r.astype(np.uint32).view(np.float32)
-    return np.where(np.isnan(a), a, out).astype(np.float32)
+    if a.ndim < 2:
+        return _bf16_round_block(a.reshape(1, -1)).reshape(a.shape).astype(np.float32)
+    flat = a.reshape(a.shape[0], -1)
+    out = np.empty_like(flat)
+    _parallel_rows(_bf16_round_block, flat, out)
+    return out.reshape(a.shape)
 
 
 _MATRICES = ("attn.wq.weight", "attn.wk.weight", "attn.wv.weight", "attn.proj.weight", "w_gate.weight",
              "w_up.weight", "w_down.weight")
+
+
+def int4_g_stored(w, group: int = 128):
+    """The exact dequantization q * s of the INT4 group quantization of w
+    (oracle.quant.quantize_int4_g then dequantize_int4_g, applied to row
+    chunks on a thread pool: both are row-local)."""
+    from . import quant as OQ
+    w = np.ascontiguousarray(w, dtype=np.float32)
+
+    def rt(c):
+        q, s = OQ.quantize_int4_g(c, group)
+        return OQ.dequantize_int4_g(q, s, c.shape, group)
+    return _parallel_rows(rt, w, np.empty_like(w), rows=2048)
 
 
 def stored_weights(W, int4: bool = False):
@@ -226,14 +283,12 @@ def stored_weights(W, int4: bool = False):
     dequantized INT4 copy of the embedding table (returned second, else
     None).  Norm weights, router weights, global tokens and gate logits stay
     float32."""
-    from . import quant as OQ
     out = {}
     for k, v in W.items():
         v = np.asarray(v, np.float32)
         if k.endswith(_MATRICES):
             if int4 and v.shape[1] % 128 == 0:
-                q, s = OQ.quantize_int4_g(v, 128)
-                out[k] = OQ.dequantize_int4_g(q, s, v.shape, 128)
+                out[k] = int4_g_stored(v, 128)
             else:
                 out[k] = bf16_round(v)
         elif k == "tok_emb.weight":
@@ -242,9 +297,7 @@ def stored_weights(W, int4: bool = False):
             out[k] = v
     head = None
     if int4:
-        emb = np.asarray(W["tok_emb.weight"], np.float32)
-        q, s = OQ.quantize_int4_g(emb, 128)
-        head = OQ.dequantize_int4_g(q, s, emb.shape, 128)
+        head = int4_g_stored(np.asarray(W["tok_emb.weight"], np.float32), 128)
     return out, head
 
 

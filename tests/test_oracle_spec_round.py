@@ -106,3 +106,26 @@ def test_stored_weights_bf16_and_int4(gold):
     assert np.array_equal(OM.bf16_round(np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8], np.float32)),
                           np.array([1.0, 1.0 + 2.0 ** -6], np.float32))
     del rng
+
+
+def test_bf16_round_equals_torch_conversion_in_row_chunks():
+    """bf16_round (row chunks on a thread pool) against torch's CPU
+    float32 -> bfloat16 conversion (round to nearest even) on random values,
+    ties, subnormals, the largest finite values, infinities and NaN, over
+    more rows than one chunk; and the chunked INT4 round trip against one
+    unchunked quantize_int4_g / dequantize_int4_g call."""
+    import torch
+    from oracle import quant as OQ
+    rng = np.random.default_rng(5)
+    a = (rng.standard_normal((9000, 64)) * np.exp(rng.uniform(-30, 30, (9000, 1)))).astype(np.float32)
+    special = np.array([0.0, -0.0, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, np.inf, -np.inf, np.nan,
+                        np.finfo(np.float32).max, -np.finfo(np.float32).max, 1e-40, -1e-40, 2.0 ** -133],
+                       np.float32)
+    a[17, :special.size] = special
+    got = OM.bf16_round(a)
+    ref = torch.from_numpy(a).to(torch.bfloat16).to(torch.float32).numpy()
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all()
+    w = rng.normal(0, 0.02, (5000, 256)).astype(np.float32)
+    q, s = OQ.quantize_int4_g(w, 128)
+    assert np.array_equal(OM.int4_g_stored(w, 128), OQ.dequantize_int4_g(q, s, w.shape, 128))
