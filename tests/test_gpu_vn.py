@@ -143,3 +143,48 @@ def test_from_vn_reads_bf16_weights(hip, tmp_path):
                            int4=True)
     assert torch.equal(m.head.wq, ref.head.wq) and torch.equal(m.layers[1].proj.wq, ref.layers[1].proj.wq)
     assert isinstance(Int4Weight(m.head.wq, m.head.sc), Int4Weight)
+
+
+@pytest.mark.parametrize("int4", [True, False], ids=["int4", "bf16"])
+def test_from_vn_untied_head(hip, tmp_path, int4):
+    """tie_weights false (cometspark.py:396-398): the stored head.weight,
+    not the embedding, is the LM head.  The .vn model equals the in-memory
+    model of the same weights bit for bit, and its logits follow the oracle
+    forward with that head (its INT4 group-128 dequantization for int4)."""
+    from oracle import model as OM
+    cfg = _draft_cfg()
+    cfg.tie_weights = False
+    W = VM.init_weights(cfg, seed=13)
+    assert "head.weight" in W
+    state = {k: v.numpy().astype(np.float32) for k, v in W.items()}
+    conf = dict(_nex_config(cfg), tie_weights=False)
+    path = tmp_path / "untied.vn"
+    write_vn(path, state, conf)
+    dev = hip.torch_device
+    B = 2
+    m = VM.CometSparkGPU.from_vn(str(path), hip, batch=B, capacity=32, dtype=torch.bfloat16, int4=int4,
+                                 chunk_bytes=1 << 20)
+    assert not m.cfg.tie_weights
+    ref = VM.CometSparkGPU(cfg, W, hip, batch=B, capacity=32, dtype=torch.bfloat16, int4=int4)
+    if int4:
+        assert torch.equal(m.head.wq, ref.head.wq) and torch.equal(m.head.sc, ref.head.sc)
+    else:
+        assert torch.equal(m.head_w, ref.head_w) and not torch.equal(m.head_w, m.emb)
+    rng = np.random.default_rng(6)
+    toks = rng.integers(0, cfg.vocab_size, (B, 9))
+    lens = torch.zeros(B, dtype=torch.int32, device=dev)
+    tt = torch.from_numpy(toks).to(dev)
+    la = m.logits(m.forward(tt, lens, 0, out_dtype=m.act_dtype)[:, -2:])
+    lb = ref.logits(ref.forward(tt, lens, 0, out_dtype=ref.act_dtype)[:, -2:])
+    torch.cuda.synchronize()
+    assert torch.equal(la, lb)
+    Wo, _ = OM.stored_weights(state, int4=int4)
+    head = OM.int4_g_stored(state["head.weight"], 128) if int4 else OM.bf16_round(state["head.weight"])
+    want = OM.forward(Wo, cfg, toks, last_n=2, head=head)
+    tied = OM.forward(Wo, cfg, toks, last_n=2)
+    got = la.cpu().numpy()
+    rel = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    rel_tied = float(np.max(np.abs(got - tied)) / np.max(np.abs(tied)))
+    _say(f"untied head ({'int4' if int4 else 'bf16'}): logits rel {rel:.2e} vs the stored head, "
+         f"{rel_tied:.2e} vs the embedding")
+    assert rel <= 3e-2 and rel_tied > 0.3

@@ -114,3 +114,30 @@ def test_config_mapping_both_flavours():
     c5 = VN.config_from_vn(v05, {})
     assert c5.dim == 64 and c5.n_kv_head == 4 and c5.embedding_scale
     assert c5.layer_pattern == ("mod", "trisparse", "trisparse", "trisparse") * 2
+
+
+def test_config_carries_tie_weights_and_temperature_scaling():
+    """tie_weights (cometspark.py:1233, base_config.py:239) and the V05
+    temperature_scaling (base_config.py:266) reach ModelConfig; the NexLM
+    config has no temperature_scaling (1.0)."""
+    from versenext_amd.model import generate_temperature
+    v05 = {"vocab_size": 256, "n_layer": 2, "n_embd": 64, "n_head": 4, "n_kv_head": 2, "layer_pattern": None,
+           "mod_every": 2, "tie_weights": False, "temperature_scaling": 0.7}
+    c = VN.config_from_vn(v05, {})
+    assert not c.tie_weights and c.temperature_scaling == pytest.approx(0.7)
+    assert "head.weight" in __import__("versenext_amd.model", fromlist=["x"]).weight_shapes(c)
+    nex = {"vocab_size": 256, "dim": 64, "n_layer": 1, "n_head": 4, "layer_pattern": ["trisparse"],
+           "temperature_scaling": 0.5}
+    cn = VN.config_from_vn(nex, {})
+    assert cn.tie_weights and cn.temperature_scaling == 1.0
+    # CometSparkV05LM.generate: the default T 1.0 becomes temperature_scaling
+    # (no top_k); CometSparkNexLM.generate: T == 1.0 without top_k is greedy
+    assert generate_temperature(c) == pytest.approx(0.7)
+    assert generate_temperature(c, 0.9) == pytest.approx(0.9)
+    assert generate_temperature(c, 1.0, top_k=50) == 1.0
+    assert generate_temperature(cn) == 0.0 and generate_temperature(cn, 0.8) == pytest.approx(0.8)
+    assert generate_temperature(cn, 0.0) == 1e-8
+    c1 = VN.config_from_vn(dict(v05, temperature_scaling=1.0), {})
+    assert generate_temperature(c1) == 0.0
+    c0 = VN.config_from_vn(dict(v05, temperature_scaling=0.0), {})
+    assert generate_temperature(c0) == 0.0

@@ -72,6 +72,12 @@ class ModelConfig:
     init_std: float = 0.02
     eps: float = 1e-6
     name: str = ""
+    # the LM head shares the embedding table (cometspark.py:396-398); False:
+    # a separate (V, D) 'head.weight'
+    tie_weights: bool = True
+    # CometSparkV05Config.temperature_scaling (spark/src/base_config.py:266),
+    # the default temperature of generate (see generate_temperature)
+    temperature_scaling: float = 1.0
 
     def __post_init__(self):
         self.layer_pattern = tuple(self.layer_pattern)
@@ -99,6 +105,23 @@ class ModelConfig:
         if self.expert_hidden:
             return int(self.expert_hidden)
         return max(int(self.dim * 8 / 3 / 64) * 64, 64)
+
+
+def generate_temperature(cfg: ModelConfig, temperature: float = 1.0, top_k: Optional[int] = None) -> float:
+    """The SpecDecodeEngine temperature (0 = greedy) of the reference's
+    generate(temperature, top_k) on this model: CometSparkV05LM.generate
+    replaces the default temperature 1.0 by config.temperature_scaling when
+    that is positive and not 1.0 and no top_k is given
+    (spark/src/base_model.py:312-319); CometSparkNexLM.generate then decodes
+    greedily when temperature == 1.0 and top_k is None, and otherwise
+    samples from softmax(logits / max(temperature, 1e-8))
+    (cometspark.py:817-818, :895)."""
+    t = float(temperature)
+    if t == 1.0 and top_k is None and cfg.temperature_scaling > 0 and cfg.temperature_scaling != 1.0:
+        t = float(cfg.temperature_scaling)
+    if t == 1.0 and top_k is None:
+        return 0.0
+    return max(t, 1e-8)
 
 
 def v02_pattern(n_layer: int, mod_every: int) -> list:
@@ -172,6 +195,8 @@ def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
                     s[ep + "w_gate.weight"] = (He, D)
                     s[ep + "w_up.weight"] = (He, D)
                     s[ep + "w_down.weight"] = (D, He)
+    if not cfg.tie_weights:
+        s["head.weight"] = (cfg.vocab_size, D)
     return s
 
 
@@ -530,7 +555,21 @@ class CometSparkGPU:
             self.emb = E.to(dtype).contiguous()
         self.emb_scale = math.sqrt(D) if cfg.embedding_scale else 1.0
         self.norm = W["norm.weight"]
-        self.head = _Linear(E, dtype, hip, int4) if int4 else None
+        # the LM head: the embedding table when tied (cometspark.py:396-398),
+        # else the model's own (V, D) head.weight
+        if cfg.tie_weights:
+            Hw = E
+        else:
+            if "head.weight" not in W:
+                raise ValueError("an untied model (tie_weights False) needs 'head.weight'")
+            Hw = W["head.weight"]
+            if tuple(Hw.shape) != (cfg.vocab_size, D):
+                raise ValueError(f"head.weight has shape {tuple(Hw.shape)}, expected {(cfg.vocab_size, D)}")
+            if isinstance(Hw, Int4Weight) and not int4:
+                raise ValueError("an INT4 head needs int4=True")
+        self.head = _Linear(Hw, dtype, hip, int4) if int4 else None
+        # the dense head matrix of the bf16 / fp32 logits path
+        self.head_w = None if int4 else (self.emb if cfg.tie_weights else Hw.to(dtype).contiguous())
         self.layers = []
         for i, kind in enumerate(cfg.layer_pattern):
             p = f"blocks.{i}."
@@ -607,16 +646,19 @@ class CometSparkGPU:
         CometSparkV05LM.save_vn, cometspark.py:1014-1060; loaded by the
         reference through VNFileReader, spark/mate/model/model.py:271-285),
         its weights streamed onto the device: with int4 the projections, the
-        trisparse FFNs and the tied head are quantized chunk by chunk into
+        trisparse FFNs and the LM head are quantized chunk by chunk into
         their INT4 group-128 buffers on the GPU (vnx_quantize_w4_g), never
-        held in full precision.  The untied copy 'head.weight' of a tied
-        model is skipped (the head is the embedding)."""
+        held in full precision.  A tied model's state_dict holds the
+        embedding twice (as 'head.weight' too): that copy is skipped.  With
+        tie_weights false in the config (cometspark.py:396-398) the stored
+        'head.weight' is the LM head."""
         from .vn import VNReader, config_from_vn, int4_matrix, load_vn_weights
         with VNReader(path) as r:
             r.read_meta()
             conf = r.read_config()
+            tied = cfg.tie_weights if cfg is not None else bool(conf.get("tie_weights", True))
             W = load_vn_weights(r, hip, quantize=int4_matrix if int4 else (lambda n, s: False), dense_dtype=dtype,
-                                chunk_bytes=chunk_bytes, skip=lambda n: n == "head.weight")
+                                chunk_bytes=chunk_bytes, skip=lambda n: tied and n == "head.weight")
         if cfg is None:
             cfg = config_from_vn(conf, W, name=f"{path} (.vn)")
         return cls(cfg, W, hip, batch, capacity, dtype, int4)
@@ -1010,9 +1052,10 @@ class CometSparkGPU:
         return out.view(B, n, D)
 
     def logits(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """(B, n, V) fp32 logits of the tied head: vnx_lm_head (bf16, matrix
-        cores) for the verify pass, vnx_gemv_w4 for an INT4 draft, F.linear
-        for an fp32 model."""
+        """(B, n, V) fp32 logits of the LM head (the tied embedding, or
+        head.weight when untied): vnx_lm_head (bf16, matrix cores) for the
+        verify pass, vnx_gemv_w4 for an INT4 draft, F.linear for an fp32
+        model."""
         B, n, D = hidden.shape
         V = self.cfg.vocab_size
         h2 = hidden.reshape(B * n, D)
@@ -1024,9 +1067,9 @@ class CometSparkGPU:
         if self.dtype == torch.bfloat16 and D % 64 == 0 and B * n <= 256:
             if out is None:
                 out = torch.empty((B, n, V), dtype=torch.float32, device=self.dev)
-            self.hip.lm_head(h2.to(torch.bfloat16), self.emb, out=out.view(B * n, V))
+            self.hip.lm_head(h2.to(torch.bfloat16), self.head_w, out=out.view(B * n, V))
             return out
-        y = torch.nn.functional.linear(h2.to(self.dtype), self.emb).float()
+        y = torch.nn.functional.linear(h2.to(self.dtype), self.head_w).float()
         if out is not None:
             out.view(B * n, V).copy_(y)
             return out

@@ -240,11 +240,11 @@ class Int4Weight:
 
 def int4_matrix(name: str, shape) -> bool:
     """The matrices a draft runs as INT4 GEMVs: attention projections, the
-    SwiGLU FFN of 'trisparse' layers and the tied embedding / LM head (MoD
-    experts stay dense), K a multiple of 128."""
+    SwiGLU FFN of 'trisparse' layers, the embedding and an untied LM head
+    (MoD experts stay dense), K a multiple of 128."""
     if len(shape) != 2 or shape[1] % 128:
         return False
-    if name == "tok_emb.weight":
+    if name in ("tok_emb.weight", "head.weight"):
         return True
     if ".parts." in name or ".router" in name:
         return False
@@ -323,8 +323,10 @@ def config_from_vn(conf: dict, weights: Dict[str, object], name: str = ""):
     """ModelConfig from a .vn config.yml: CometSparkNexLM.get_config
     (cometspark.py:1207-1256: dim, no embedding scale) or CometSparkV05Config
     (spark/src/base_config.py:182-260: n_embd, embedding_scale, layer_pattern
-    None -> 'mod' every mod_every layers).  The SwiGLU hidden size comes from
-    the stored w_gate rows when they differ from the default."""
+    None -> 'mod' every mod_every layers; temperature_scaling :266).  Both
+    carry tie_weights (cometspark.py:1233, base_config.py:239).  The SwiGLU
+    hidden size comes from the stored w_gate rows when they differ from the
+    default."""
     from .model import ModelConfig, v02_pattern
     v05 = "n_embd" in conf
     dim = int(conf["n_embd"] if v05 else conf["dim"])
@@ -349,7 +351,9 @@ def config_from_vn(conf: dict, weights: Dict[str, object], name: str = ""):
         rope_theta=float(conf.get("rope_theta", 10000.0)), num_dense_parts=int(conf.get("num_dense_parts", 4)),
         num_experts_per_part=int(conf.get("num_experts_per_part", 4)), top_k=int(conf.get("top_k", 2)),
         expert_hidden=conf.get("expert_hidden"), mlp_hidden=mlp_hidden,
-        embedding_scale=bool(conf.get("embedding_scale", True)) if v05 else False, name=name)
+        embedding_scale=bool(conf.get("embedding_scale", True)) if v05 else False,
+        tie_weights=bool(conf.get("tie_weights", True)),
+        temperature_scaling=float(conf.get("temperature_scaling", 1.0)) if v05 else 1.0, name=name)
 
 
 __all__ = ["VNReader", "TensorStream", "Int4Weight", "int4_matrix", "load_vn_weights", "config_from_vn"]
