@@ -141,3 +141,66 @@ def test_config_carries_tie_weights_and_temperature_scaling():
     assert generate_temperature(c1) == 0.0
     c0 = VN.config_from_vn(dict(v05, temperature_scaling=0.0), {})
     assert generate_temperature(c0) == 0.0
+
+
+GOLDEN = __import__("os").path.join(__import__("os").path.dirname(__import__("os").path.abspath(__file__)), "golden")
+
+
+def _arrays(path, rows_per_chunk=5):
+    """{name: ndarray} of the streamed fp32 tensors."""
+    out = {}
+    for name, (dt, shape, raw) in _read_all(path, rows_per_chunk).items():
+        assert dt == "F32", (name, dt)
+        out[name] = np.frombuffer(raw, np.float32).reshape(shape).copy()
+    return out
+
+
+@pytest.mark.parametrize("fname,fmt", [("cometspark_small_st.vn", "safetensors"),
+                                       ("cometspark_small_npz.vn", "npz")])
+def test_reads_the_reference_written_vn(fname, fmt):
+    """.vn files written by the reference's CometSparkV05LM.save_vn
+    (tests/golden/make_vn_small.py): meta, config and every tensor of the
+    config-1 target equal the state_dict the reference wrote into
+    cometspark_small.npz, and the config maps to small_target()."""
+    import os
+    from versenext_amd import model as VM
+    path = os.path.join(GOLDEN, fname)
+    gold = np.load(os.path.join(GOLDEN, "cometspark_small.npz"))
+    with VN.VNReader(path) as r:
+        meta = r.read_meta()
+        conf = r.read_config()
+        assert r.weight_format == fmt and meta["vn_format_version"] == 2
+    W = _arrays(path, rows_per_chunk=7)
+    want = {k[2:]: gold[k] for k in gold.files if k.startswith("t/")}
+    assert set(W) == set(want)
+    for k, v in want.items():
+        assert W[k].dtype == np.float32 and np.array_equal(W[k], v), k
+    c = VN.config_from_vn(conf, W)
+    ref = VM.small_target()
+    for f in ("vocab_size", "dim", "n_layer", "n_head", "n_kv_head", "layer_pattern", "window_size",
+              "num_global_tokens", "use_alibi", "use_rope", "num_dense_parts", "num_experts_per_part", "top_k",
+              "embedding_scale", "tie_weights", "temperature_scaling", "ffn_hidden", "expert_hidden_eff"):
+        assert getattr(c, f) == getattr(ref, f), f
+
+
+def test_reference_written_untied_vn_matches_its_logits():
+    """The reference's untied one-layer V05 model (tie_weights False,
+    temperature_scaling 0.7): the config maps, and the oracle forward on the
+    stored weights, with the stored head.weight as the head, reproduces the
+    logits the reference computed for the config-1 prompt."""
+    import os
+    from oracle import model as OM
+    from versenext_amd.model import generate_temperature
+    path = os.path.join(GOLDEN, "untied_small.vn")
+    z = np.load(os.path.join(GOLDEN, "vn_small.npz"))
+    with VN.VNReader(path) as r:
+        conf = r.read_config()
+    W = _arrays(path)
+    c = VN.config_from_vn(conf, W)
+    assert not c.tie_weights and c.temperature_scaling == pytest.approx(0.7) and c.embedding_scale
+    assert generate_temperature(c) == pytest.approx(0.7)
+    got = OM.forward(W, c, z["prompt"][None])
+    err = float(np.max(np.abs(got - z["untied_logits"])))
+    assert err <= 1e-5, err
+    tied = OM.forward(W, VN.config_from_vn(dict(conf, tie_weights=True), W), z["prompt"][None])
+    assert float(np.max(np.abs(tied - z["untied_logits"]))) > 1e-2
