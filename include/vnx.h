@@ -173,7 +173,10 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
  *   VNX_SAMPLE_EXACT_K    argpartition(-a, k-1)[:k]: exactly k tokens, NaN
  *                         ranked below every value, ties at the kth value
  *                         taken by lower id (numpy leaves them open); the
- *                         draw runs over the kept ids in id order.
+ *                         draw runs over the kept ids in id order;
+ *   VNX_SAMPLE_UNIFORM_F64 uniforms holds B doubles (else B floats): the
+ *                         float64 value numpy's Generator.random() gives the
+ *                         reference's choice, used without rounding.
  * Optional outputs (NULL to skip): flags (VNX_FLAG_CDF_EDGE / LSE_EDGE), lse
  * = RN32(row LSE), kth (the top-k threshold, -inf if off), p_star / j_star
  * (the last kept token's probability and id, -1 if top_p is off), k_star (the
@@ -183,12 +186,13 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
  * VNX_ERR_INVALID_ARG (the reference's ValueError, sampler.py:54-59). */
 #define VNX_SAMPLE_EXACT_K 1
 #define VNX_SAMPLE_CALIBRATE 2
+#define VNX_SAMPLE_UNIFORM_F64 4
 
 size_t vnx_sampler_workspace(int64_t B, int64_t V, int dtype);
 
 int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float temperature,
                        int64_t top_k, float top_p, int mode, float calib_factor, float calib_eps,
-                       const float* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
+                       const void* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
                        float* p_star, int64_t* j_star, int64_t* k_star, void* workspace, size_t workspace_bytes,
                        void* stream);
 

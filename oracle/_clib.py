@@ -40,7 +40,7 @@ def lib() -> ctypes.CDLL:
         L.vnx_ref_resid_weights.argtypes = [fp, fp, ctypes.c_int64, ctypes.c_float, ctypes.c_float,
                                             ctypes.c_float, ctypes.c_float, ctypes.c_float, fp, fp]
         L.vnx_ref_icdf.restype = ctypes.c_int64
-        L.vnx_ref_icdf.argtypes = [fp, ctypes.c_int64, ctypes.c_float, dp, dp, dp]
+        L.vnx_ref_icdf.argtypes = [fp, ctypes.c_int64, ctypes.c_double, dp, dp, dp]
         _lib = L
     return _lib
 
@@ -83,11 +83,13 @@ def resid_weights(P: np.ndarray, Q, T: float, thr_p: float, thr_q: float, Lp: fl
 
 
 def icdf(w: np.ndarray, u: float):
-    """Returns (index, C_{j-1}, C_j, total) of the inverse-CDF draw."""
+    """Returns (index, C_{j-1}, C_j, total) of the inverse-CDF draw: the
+    first j with C_j > u * total, u taken as given (a float32 uniform
+    converts to double exactly; a float64 one is not rounded)."""
     w = np.ascontiguousarray(w, dtype=np.float32)
     before = ctypes.c_double(0.0)
     after = ctypes.c_double(0.0)
     total = ctypes.c_double(0.0)
-    j = lib().vnx_ref_icdf(_fptr(w), w.shape[0], np.float32(u), ctypes.byref(before),
+    j = lib().vnx_ref_icdf(_fptr(w), w.shape[0], float(u), ctypes.byref(before),
                            ctypes.byref(after), ctypes.byref(total))
     return int(j), before.value, after.value, total.value

@@ -103,13 +103,13 @@ void vnx_ref_resid_weights(const float* P, const float* Q, int64_t V, float T, f
 /* Inverse-CDF draw over weights w (length V): the first j with
  * C_j > u * C_{V-1}, C sequential fp64 partial sums; returns -1 if the total
  * is zero.  before/after receive C_{j-1}, C_j; total the full sum. */
-int64_t vnx_ref_icdf(const float* w, int64_t V, float u, double* before, double* after,
+int64_t vnx_ref_icdf(const float* w, int64_t V, double u, double* before, double* after,
                      double* total) {
   double tot = 0.0;
   for (int64_t j = 0; j < V; ++j) tot += (double)w[j];
   if (total) *total = tot;
   if (!(tot > 0.0)) return -1;
-  const double target = (double)u * tot;
+  const double target = u * tot;
   double run = 0.0;
   int64_t last = -1;
   for (int64_t j = 0; j < V; ++j) {

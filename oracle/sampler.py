@@ -136,7 +136,7 @@ def sample(logits, temperature: float, top_k: int, top_p: float, u: float, exact
         info.update(p_star=p_star, j_star=j_star, cutoff=cutoff)
     j, before, after, total = _clib.icdf(p, u)
     flags = 0
-    t = float(np.float32(u)) * total
+    t = float(u) * total
     if t - before < 1e-12 * total or after - t < 1e-12 * total:
         flags |= FLAG_CDF_EDGE
     return j, flags, info

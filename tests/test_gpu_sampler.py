@@ -120,6 +120,32 @@ def test_sampler_class_reproduces_numpy_choice_stream(hip):
         assert tok == gen.choice(q.size, p=q)
 
 
+def test_sampler_class_stream_3000_draws_full_vocab(hip):
+    """3,000 seeded draws of the Sampler class at V = 248,320 on near-flat
+    rows, where every bucket is about 1/V wide, so rounding the uniform to
+    float32 would move about one draw in 400: the tokens equal numpy's
+    Generator.choice on the canonical probabilities with the same seed, draw
+    for draw (the kernel gets numpy's float64 uniform unrounded)."""
+    Vf = 248320
+    rng = np.random.default_rng(8)
+    rows = rng.normal(0, 0.05, (6, Vf)).astype(np.float32)
+    probs = []
+    for r in rows:
+        _, _, p = OS.probabilities(r, 1.0)
+        probs.append(p.astype(np.float64) / p.astype(np.float64).sum())
+    s = Sampler(temperature=1.0, seed=321)
+    gen = np.random.default_rng(321)
+    dev_rows = [torch.from_numpy(r).to(hip.torch_device) for r in rows]
+    diff = []
+    for i in range(3000):
+        tok = s.sample(dev_rows[i % 6])
+        ref = int(gen.choice(Vf, p=probs[i % 6]))
+        if tok != ref:
+            diff.append((i, tok, ref))
+    _say(f"3000 draws at V={Vf}: {len(diff)} differ from numpy's choice stream")
+    assert not diff, diff[:5]
+
+
 def test_logit_calibration_matches_oracle(hip):
     rng = np.random.default_rng(3)
     x = rng.normal(0.3, 2.5, (6, V)).astype(np.float32)

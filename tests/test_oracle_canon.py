@@ -70,6 +70,19 @@ def test_icdf_is_numpy_choice_rule():
         cw = np.cumsum(w.astype(np.float64))
         assert j == int(np.searchsorted(cw, np.float64(u32) * cw[-1], side="right"))
         assert w[j] > 0
+        # a float64 uniform is used as drawn, not rounded to float32
+        j64 = _clib.icdf(w, u)[0]
+        assert j64 == int(np.searchsorted(cw, u * cw[-1], side="right"))
+
+
+def test_icdf_keeps_the_float64_uniform():
+    """Where float32 rounding of the uniform crosses a bucket edge, the
+    float64 draw follows the unrounded value."""
+    w = np.ones(8, np.float32)
+    u = 0.5 - 2.0 ** -40            # float32(u) == 0.5 exactly: the next bucket
+    assert np.float32(u) == np.float32(0.5)
+    assert _clib.icdf(w, u)[0] == 3
+    assert _clib.icdf(w, np.float32(u))[0] == 4
 
 
 def test_icdf_edges():

@@ -40,6 +40,7 @@ FLAG_BAD_ID = 16
 
 SAMPLE_EXACT_K = 1
 SAMPLE_CALIBRATE = 2
+SAMPLE_UNIFORM_F64 = 4
 
 _c_i64 = ctypes.c_int64
 _c_sz = ctypes.c_size_t

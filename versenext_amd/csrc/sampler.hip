@@ -92,7 +92,8 @@ struct SampParams {
   float cf, ceps;
   int C;
   int64_t clen, nsb;
-  const float* u;
+  const float* u;      // the rows' uniforms (float), or
+  const double* u64;   // ... as doubles (VNX_SAMPLE_UNIFORM_F64; u unused)
   int64_t* out;
   uint8_t* flags;
   float* lse;
@@ -117,6 +118,13 @@ struct SampParams {
   unsigned* nct;              // [B][C] candidates per chunk
   uint32_t* tc;               // [B][C] the chunk's threshold key
 };
+
+// Row b's uniform in double: a float uniform converts exactly, a double one
+// (numpy's Generator.random) is used as drawn.
+__device__ __forceinline__ double samp_u(const SampParams& p, int64_t b) {
+  return p.u64 ? p.u64[b] : (double)p.u[b];
+}
+
 
 // Order-preserving key of a float: larger value, larger key; NaN above all
 // (numpy.partition's order).
@@ -768,7 +776,7 @@ __global__ __launch_bounds__(kSNT) void k_samp_mass(SampParams p) {
     __syncthreads();
   }
   const double total = L.total;
-  const double target = (double)p.u[b] * total;
+  const double target = samp_u(p, b) * total;
   {
     const double T = L.T[tid], end = L.E[tid];
     const double start = tid ? L.E[tid - 1] : 0.0;
@@ -1167,7 +1175,7 @@ __device__ __forceinline__ void single_row(const SampParams& p, int64_t b, float
     __syncthreads();
   }
   const double total = L.total;
-  const double target = (double)p.u[b] * total;
+  const double target = samp_u(p, b) * total;
   {
     const double T = L.u.d.T[tid], end = L.u.d.E[tid];
     const double start = tid ? L.u.d.E[tid - 1] : 0.0;
@@ -1363,7 +1371,7 @@ __device__ __forceinline__ bool cand_wave(const SampParams& p, int64_t b, int n,
   const float w = lane < ncut ? __uint_as_float((uint32_t)d) : 0.0f;
   const double incl = wave_inclusive_scan((double)w);
   const double total = __shfl(incl, VNX_WAVE - 1, VNX_WAVE);
-  const double target = (double)p.u[b] * total;
+  const double target = samp_u(p, b) * total;
   int64_t token = 0;
   if (!(total > 0.0)) {
     fl |= VNX_FLAG_ZERO_RESIDUAL;
@@ -1697,7 +1705,7 @@ __global__ __launch_bounds__(kST) void k_samp_cand(SampParams p) {
   if (tid == 0) L.hit = kCandMax;  // none yet
   __syncthreads();
   const double total = L.total;
-  const double target = (double)p.u[b] * total;
+  const double target = samp_u(p, b) * total;
   if (total > 0.0) {
     // first position whose cumulative sum exceeds the target (the last
     // positive one when rounding leaves none)
@@ -1848,12 +1856,12 @@ size_t vnx_sampler_workspace(int64_t B, int64_t V, int dtype) {
 
 int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int64_t ld, float temperature,
                        int64_t top_k, float top_p, int mode, float calib_factor, float calib_eps,
-                       const float* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
+                       const void* uniforms, int64_t* out_ids, uint8_t* flags, float* lse, float* kth,
                        float* p_star, int64_t* j_star, int64_t* k_star, void* workspace, size_t workspace_bytes,
                        void* stream) {
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
   if (B < 0 || V <= 0 || top_k < 0) return VNX_ERR_INVALID_ARG;
-  if (mode & ~(VNX_SAMPLE_EXACT_K | VNX_SAMPLE_CALIBRATE)) return VNX_ERR_INVALID_ARG;
+  if (mode & ~(VNX_SAMPLE_EXACT_K | VNX_SAMPLE_CALIBRATE | VNX_SAMPLE_UNIFORM_F64)) return VNX_ERR_INVALID_ARG;
   if ((mode & VNX_SAMPLE_CALIBRATE) && (!__builtin_isfinite(calib_factor) || !(calib_eps >= 0.0f)))
     return VNX_ERR_INVALID_ARG;
   if (!(temperature >= 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
@@ -1884,7 +1892,9 @@ int vnx_sampler_sample(const void* logits, int dtype, int64_t B, int64_t V, int6
   // at least one unit: the first token's sum reaches any top_p > 0
   p.p_target = std::max<uint64_t>(1, (uint64_t)floor((double)top_p * 1152921504606846976.0));
   p.C = pl.C; p.clen = pl.clen; p.nsb = pl.nsb;
-  p.u = uniforms; p.out = out_ids; p.flags = flags; p.lse = lse; p.kth = kth; p.p_star = p_star;
+  if (mode & VNX_SAMPLE_UNIFORM_F64) p.u64 = static_cast<const double*>(uniforms);
+  else p.u = static_cast<const float*>(uniforms);
+  p.out = out_ids; p.flags = flags; p.lse = lse; p.kth = kth; p.p_star = p_star;
   p.j_star = j_star; p.k_star = k_star;
   samp_carve(workspace, B, pl, &p);
   hipStream_t s = static_cast<hipStream_t>(stream);

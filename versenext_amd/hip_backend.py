@@ -295,7 +295,8 @@ class HipBackend(DeviceBackend):
         exactly-k top-k (argpartition, ties by lower id); calib_factor (not
         None) first applies its logit calibration with eps calib_eps.  Returns
         ids (B,) int64, or with return_all a dict with ids, flags, lse, kth,
-        p_star, j_star, k_star."""
+        p_star, j_star, k_star.  Float64 uniforms (numpy's Generator.random
+        values) are used as drawn (VNX_SAMPLE_UNIFORM_F64); others as float32."""
         if temperature < 0.0:
             raise ValueError(f"temperature must be >= 0, got {temperature}")
         if top_k < 0:
@@ -306,7 +307,10 @@ class HipBackend(DeviceBackend):
         dev = self._torch_device
         lg = self._rows2d(logits)
         B, V = lg.shape
-        u = _to_tensor(uniforms, dev, torch.float32).reshape(-1).contiguous()
+        u64 = getattr(uniforms, "dtype", None) in (np.float64, torch.float64)
+        if u64:
+            mode |= _lib.SAMPLE_UNIFORM_F64
+        u = _to_tensor(uniforms, dev, torch.float64 if u64 else torch.float32).reshape(-1).contiguous()
         if u.numel() != B:
             raise ValueError(f"uniforms must have {B} entries")
         ids = torch.empty(B, dtype=torch.int64, device=dev)

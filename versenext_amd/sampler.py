@@ -7,7 +7,8 @@ the int token id.  The draw runs on the GPU (vnx_sampler_sample: temperature,
 top-k, softmax, top-p and the inverse-CDF draw in one launch); the one uniform
 it needs per call comes from numpy's default_rng(seed) when a seed is given,
 else from numpy's global legacy stream, as the reference draws its choice
-from either (sampler.py:64, :135-137).
+from either (sampler.py:64, :135-137), and reaches the kernel as the float64
+value numpy's choice would compare against the CDF.
 """
 from __future__ import annotations
 
@@ -49,7 +50,8 @@ class Sampler:
         x = np.asarray(logits, dtype=np.float32).reshape(-1) if not hasattr(logits, "device") else logits
         if getattr(x, "size", None) == 0 or (hasattr(x, "numel") and x.numel() == 0):
             raise ValueError("logits is empty")
-        u = np.array([self._uniform() if self.temperature != 0.0 else 0.0], np.float32)
+        # the float64 uniform numpy's choice compares against the CDF, unrounded
+        u = np.array([self._uniform() if self.temperature != 0.0 else 0.0], np.float64)
         ids = hip.sampler_sample(x.reshape(1, -1), u, self.temperature, self.top_k, self.top_p)
         return int(ids.cpu()[0])
 
@@ -92,7 +94,7 @@ def cometspark_sample(hip, logits, temperature: float, top_k: Optional[int] = No
         u = np.zeros(B, np.float32)
         return hip.sampler_sample(x, u, 0.0, calib_factor=calib_factor)
     if uniforms is None:
-        uniforms = (rng if rng is not None else np.random.default_rng()).random(B).astype(np.float32)
+        uniforms = (rng if rng is not None else np.random.default_rng()).random(B)   # float64, as choice uses it
     return hip.sampler_sample(x, uniforms, max(T, 1e-8), k, 1.0, exact_k=True, calib_factor=calib_factor)
 
 
