@@ -604,7 +604,12 @@ def cpu_baseline_e2e(Wt, Wd, prompt, budget_s: float = 15.0):
     full re-forward of [context, drafts] per round with no KV cache, head read
     at the k+1 verified positions; draft re-forwarded per token; canonical
     acceptance), timed on one sequence of the config-5 workload for about
-    budget_s of host time, BLAS threads limited to the box's CPU share."""
+    budget_s of host time, BLAS threads limited to the box's CPU share.  One
+    sequence, not the batch of 32: the reference's verify_then_commit
+    commits batch row 0 only (speculative.py:262-268), so its decode loop
+    serves one sequence per call, and a 32-row round of this numpy path
+    (one (32, 518)-token target re-forward and six draft re-forwards) takes
+    about a minute of host time, past the bench's bounded CPU sample."""
     import numpy as np
     from threadpoolctl import threadpool_limits
     from oracle import model as OM
@@ -794,7 +799,8 @@ def bench_sampler(args, emit=True):
     the passes after the first mostly from the L2 / MALL; bytes = the row
     read once, 4 V per row.  CPU: the reference's
     numpy Sampler (partition, exp / sum, argsort / cumsum / searchsorted,
-    choice) per row, restated in oracle/sampler.py, 8 rows."""
+    choice) per row, restated in oracle/sampler.py, all 32 rows on the host's
+    cores (up to 16 threads)."""
     import numpy as np
     import torch
     from versenext_amd import get_backend, _lib
@@ -827,17 +833,21 @@ def bench_sampler(args, emit=True):
            "unit": "rows/s", "steps": args.steps, "warmup": args.warmup, "results": rows,
            "config": {"workload": "Sampler.sample, 32 x 248320 fp32 rows, T 0.8", "bytes_per_call": nb}}
     if not args.no_cpu:
-        xs = x[:8].cpu().numpy()
-        us_ = u[:8].cpu().numpy()
+        from concurrent.futures import ThreadPoolExecutor
+        xs = x.cpu().numpy()
+        us_ = u.cpu().numpy()
+        threads = max(1, min(16, os.cpu_count() or 1))
         cpu_rows = []
-        for name, k, p, mode in settings[:3]:
-            t0 = time.perf_counter()
-            for b in range(8):
-                OS.sample(xs[b], 0.8, k, p, us_[b])
-            dt = time.perf_counter() - t0
-            cpu_rows.append({"setting": name, "rows_per_s": round(8 / dt, 2)})
-        out["cpu_baseline"] = dict(cpu_env(1), kind="port", value=cpu_rows[2]["rows_per_s"], unit="rows/s",
-                                   results=cpu_rows, sample="8 of the 32 rows, numpy on one thread")
+        with ThreadPoolExecutor(max_workers=threads) as ex:
+            for name, k, p, mode in settings[:3]:
+                t0 = time.perf_counter()
+                list(ex.map(lambda b: OS.sample(xs[b], 0.8, k, p, us_[b]), range(Bs)))
+                dt = time.perf_counter() - t0
+                cpu_rows.append({"setting": name, "rows_per_s": round(Bs / dt, 2)})
+        out["cpu_baseline"] = dict(cpu_env(threads), kind="port", value=cpu_rows[2]["rows_per_s"], unit="rows/s",
+                                   results=cpu_rows,
+                                   sample=f"all {Bs} rows, one row per task on {threads} threads (numpy releases "
+                                          f"the GIL in its partition, sort, exp and cumsum)")
     if emit:
         print(json.dumps(out), flush=True)
     return out

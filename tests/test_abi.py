@@ -34,6 +34,54 @@ def test_ctypes_signatures_cover_header():
     assert set(_lib.SIGNATURES) == set(header_functions())
 
 
+def header_prototypes():
+    """{name: (return type, [parameter types])} of every function include/vnx.h
+    declares, with qualifiers kept ('const float*', 'int64_t', ...)."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(r"([A-Za-z_][A-Za-z0-9_ \*]*?)\b(vnx_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        types = []
+        for prm in params.split(","):
+            prm = prm.strip()
+            if prm and prm != "void":
+                types.append(re.sub(r"\b[A-Za-z_][A-Za-z0-9_]*$", "", prm).replace(" *", "*").strip())
+        out[name] = (ret.strip(), types)
+    return out
+
+
+def _ctype_of(c: str):
+    """The ctypes type a header type binds to: every data pointer as
+    c_void_p (device or host addresses), const char* as c_char_p."""
+    if c == "const char*":
+        return ctypes.c_char_p
+    if c.endswith("*"):
+        return ctypes.c_void_p
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t, "float": ctypes.c_float,
+            "double": ctypes.c_double, "int32_t": ctypes.c_int32}[c]
+
+
+def test_ctypes_argtypes_match_header_parameter_types():
+    """Every binding's restype and argtypes equal the header prototype's
+    parameter types one by one (a pointer parameter may also bind a ctypes
+    POINTER to the structure the header names)."""
+    protos = header_prototypes()
+    assert set(protos) == set(header_functions())
+    for name, (ret, params) in protos.items():
+        res, args = _lib.SIGNATURES[name]
+        assert len(args) == len(params), (name, len(args), len(params))
+        want_res = None if ret == "void" else _ctype_of(ret)
+        assert res is want_res, (name, "return", ret, res)
+        for i, (c, a) in enumerate(zip(params, args)):
+            want = _ctype_of(c)
+            ok = a is want or (c.endswith("*") and isinstance(a, type) and issubclass(a, ctypes._Pointer))
+            assert ok, (name, i, c, a)
+    # ctypes' own view of the loaded library agrees with the table
+    L = _lib.lib()
+    for name, (res, args) in _lib.SIGNATURES.items():
+        f = getattr(L, name)
+        assert list(f.argtypes) == list(args) and f.restype is res, name
+
+
 def test_status_strings_and_version():
     L = _lib.lib()
     assert L.vnx_version() >= 100

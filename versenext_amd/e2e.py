@@ -104,7 +104,13 @@ class SpecDecodeEngine:
         self.out = None
         self.n_new = 0
         self.graph = None
-        # the last round's acceptance outputs (accept_len, out_ids, flags)
+        # the acceptance outputs (accept_len, out_ids, flags) of the most
+        # recently ENQUEUED round: once captured, these are the graph's static
+        # buffers, which every replay overwrites, so after run_rounds /
+        # generate (a round is enqueued before the previous one's info is
+        # read) they may already hold a later round than the info last
+        # returned; step() enqueues one round and waits for it, so after
+        # step() they are that round's
         self.last = None
         # attention prefix bound used by captured rounds
         self.bound_t = target.cap - (k + 2)

@@ -26,11 +26,20 @@ are written into the cache at lens[b] .. lens[b]+k, and a rejected suffix is
 rolled back by not advancing lens[b].  The rows the verifier reads see the
 same keys either way.
 
-Hot path on the gfx950 kernels of libvnx_hip.so: sliding-window and global
-attention of the new rows over the cache (vnx_tree_attn with per-row prefix
-lengths), the verify-pass LM head (vnx_lm_head), and the INT4 group-128
-draft GEMVs (vnx_gemv_w4).  Prefill, projections and FFN GEMMs run on
-PyTorch-ROCm (hipBLASLt / rocBLAS).
+Kernels of libvnx_hip.so (gfx950) on the decode and verify forwards:
+- attention of the new rows over the cache, all three TriSparse paths
+  (vnx_tree_attn with per-row prefix lengths; RoPE and the cache write of
+  the new rows inside the call for bf16 verify-size forwards);
+- the target's verify-size projections and SwiGLU FFNs on vnx_gemm_bf16
+  (RMSNorm staged into the q|k|v and gate-up products, the residual add in
+  the output and down products' epilogues, the first layer's token
+  embedding gathered by its q|k|v product), the MoD routing
+  (vnx_mod_route_x) and the routed expert products (vnx_expert_gemm_bf16);
+- the INT4 group-128 draft GEMVs (vnx_gemv_w4 and its fused RMSNorm / RoPE /
+  SwiGLU / residual forms) and the verify-pass LM head (vnx_lm_head).
+Prefill-size forwards (more rows than one verify round) run their dense
+products on PyTorch-ROCm (hipBLASLt / rocBLAS); the attention of every
+forward runs on vnx_tree_attn where the head size allows it.
 """
 from __future__ import annotations
 
