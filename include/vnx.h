@@ -311,6 +311,22 @@ int vnx_gemv_w4(const void* x, int64_t ldx, const uint8_t* wq, int64_t ldw, cons
                 int scale_dtype, int64_t lds, int64_t B, int64_t N, int64_t K, int group,
                 float* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
 
+/* vnx_gemv_w4 (group-128 fp16 scales, K = 512 or 1024) on a tiled copy of
+ * the packed weight, for large N (a draft's tied LM head): vnx_pack_w4_tiles
+ * writes it (vnx_w4_tiles_bytes(N, K) bytes, rows padded to a multiple of 16
+ * with zeros): 16-row tile t holds K/128 pieces of 1 KB, piece g holding for
+ * l = 0..63 the 16 bytes W[16t + l % 16][64g + 16(l / 16) .. +16] of the
+ * row-major packing with every nibble in offset form (q + 8 = q ^ 8; a
+ * reordering and an exact recoding, so the product is vnx_gemv_w4's bit for
+ * bit).  scales (N, K/128) fp16 with row pitch lds (a multiple of 8 for
+ * K = 1024, of 4 for K = 512), x and wt 16-byte aligned, ldx % 8 == 0.
+ * Replaces matmul_int4 / QuantizedLinear.forward_fused (quantize.py:277-309,
+ * :506-533) for the tied head of an INT4 draft (cometspark.py:396-398). */
+size_t vnx_w4_tiles_bytes(int64_t N, int64_t K);
+int vnx_pack_w4_tiles(const uint8_t* wq, int64_t ldw, int64_t N, int64_t K, uint8_t* out, void* stream);
+int vnx_gemv_w4_tiles(const void* x, int64_t ldx, const uint8_t* wt, const void* scales, int64_t lds, int64_t B,
+                      int64_t N, int64_t K, float* y, int64_t ldy, void* stream);
+
 /* vnx_gemv_w4 of a fused [gate; up] weight with SwiGLU fused (SwiGLUMLP,
  * packages/verse_torch/verse_torch/vnnn.py:779-807, on QuantizedLinear
  * projections): W (N, K) has its rows interleaved in blocks of 16, the 8 gate

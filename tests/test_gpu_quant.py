@@ -267,3 +267,60 @@ def test_gemv_residual(hip, N, K, B):
     mag = Q.gemv_abs(x16, W)
     err = np.abs(res.cpu().numpy().astype(np.float64) - ref)
     assert np.all(err <= RTOL * mag + 2.0 ** -24 * np.abs(ref) + 1e-30)
+
+
+def _tiles_ref(p, N, K):
+    """vnx_pack_w4_tiles' layout restated from its definition in include/vnx.h:
+    tile t, piece g, lane l = the 16 bytes W[16t + l % 16][64g + 16(l / 16) ..]
+    of the row-major packing, each nibble XOR 8 (offset form); rows past N
+    hold q = 0 (0x88 bytes)."""
+    tiles = (N + 15) // 16
+    full = np.full((tiles * 16, K // 2), 0x00, np.uint8)
+    full[:N] = p
+    a = full.reshape(tiles, 16, K // 128, 4, 16)          # t, m, g, kq, byte
+    a = a.transpose(0, 2, 3, 1, 4)                          # t, g, kq, m, byte -> lane = kq*16 + m
+    return (a.reshape(-1) ^ 0x88).astype(np.uint8)
+
+
+@pytest.mark.parametrize("N,K", [(1000, 512), (40003, 1024), (4096, 1024)])
+def test_pack_w4_tiles_layout(hip, N, K):
+    p, s = _quantized("int4_g128", N, K, 61)
+    got = hip.pack_w4_tiles(torch.from_numpy(p), K).cpu().numpy()
+    assert got.size == hip._L.vnx_w4_tiles_bytes(N, K) == (N + 15) // 16 * 16 * K // 2
+    assert np.array_equal(got, _tiles_ref(p, N, K))
+
+
+@pytest.mark.parametrize("N,K,B", [(4096, 1024, 1), (1000, 512, 3), (33005, 512, 17), (40003, 1024, 32),
+                                   (40003, 1024, 40), (65536, 1024, 16), (248320, 1024, 1), (248320, 1024, 8),
+                                   (248320, 1024, 32)])
+def test_gemv_w4_tiles_equals_row_layout(hip, N, K, B):
+    """vnx_gemv_w4_tiles on the tiled copy equals the fp64 product of the
+    oracle's dequantized weights within the GEMV bar on sampled rows (both
+    ends and a partial last tile included), and, from 32,768 rows (where
+    vnx_gemv_w4 runs its streaming form: the same products summed in the
+    same order), vnx_gemv_w4 on the row layout bit for bit."""
+    p, s = _quantized("int4_g128", N, K, 7)
+    x16 = np.random.default_rng(N + B).normal(0, 1, (B, K)).astype(np.float16)
+    xt = torch.from_numpy(x16)
+    wt = hip.pack_w4_tiles(torch.from_numpy(p), K)
+    y = hip.gemv_w4_tiles(xt, wt, torch.from_numpy(s), N, K).cpu().numpy()
+    assert y.shape == (B, N)
+    if N >= 32768:
+        y_rows = hip.gemv_w4(xt, torch.from_numpy(p), torch.from_numpy(s), 128).cpu().numpy()
+        assert np.array_equal(y.view(np.uint32), y_rows.view(np.uint32))
+    r = np.unique(np.concatenate([np.arange(min(N, 40)), np.arange(max(0, N - 40), N),
+                                  np.random.default_rng(B).choice(N, min(N, 2000), replace=False)]))
+    W = Q.dequantize_int4_g(p[r], s[r], (len(r), K), 128)
+    ref = Q.gemv_ref(x16, W)
+    mag = Q.gemv_abs(x16, W)
+    err = np.abs(y[:, r].astype(np.float64) - ref)
+    worst = float(np.max(err / (mag + 1e-30)))
+    _say(f"  tiles N={N} K={K} B={B}: max err / sum|xw| = {worst:.2e}")
+    assert np.all(err <= RTOL * mag + 1e-30), worst
+
+
+def test_gemv_w4_tiles_rejects_bad_shapes(hip):
+    p, s = _quantized("int4_g128", 64, 256, 3)
+    wt = hip.pack_w4_tiles(torch.from_numpy(p), 256)
+    with pytest.raises(ValueError):   # K must be 512 or 1024
+        hip.gemv_w4_tiles(torch.zeros((1, 256), dtype=torch.float16), wt, torch.from_numpy(s), 64, 256)

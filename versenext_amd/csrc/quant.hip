@@ -655,13 +655,22 @@ __global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_
   const int64_t tiles = (p.N + 15) / 16;
   const int64_t t_lo = (int64_t)blockIdx.x * tiles_per_wg;
   const int64_t t_hi = min(tiles, t_lo + tiles_per_wg);
+  // the workgroup's weight rows as a buffer resource: the ring's loads past
+  // t_hi (issued unconditionally, so the waits count statically) read zeros
+  // without a memory access instead of the next workgroup's rows
+  const int64_t r_lo = t_lo * 16, r_hi = min(p.N, t_hi * 16);
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.w) + r_lo * p.ldw, (short)0, (int)((r_hi - r_lo) * p.ldw), 0x00020000);
   // one tile's loads: the lane's weight row (KG x 16 bytes) and its scales
   auto load = [&](int64_t tile, u32x4 (&wv)[KG], SV& sv) {
     const int64_t t = min(tile, tiles - 1);
-    const int64_t ra = min(t * 16 + m, p.N - 1);
-    const uint8_t* wr = p.w + ra * p.ldw + kq * 16;
+    const int64_t rw = min(t * 16 + m, p.N - 1);
+    const int64_t ra = min(rw, r_hi - 1);             // scale rows stay in the range (a cache hit past it)
+    const int off = (int)(min(t * 16 + m, r_lo + 2 * tiles_per_wg * 16) - r_lo) * (int)p.ldw + kq * 16;
 #pragma unroll
-    for (int g = 0; g < KG; ++g) wv[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + g * 64));
+    for (int g = 0; g < KG; ++g)
+      wv[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, off + g * 64, 0, 2));
+    (void)rw;
     sv = *reinterpret_cast<const SV*>(static_cast<const uint16_t*>(p.sc) + ra * p.lds);
   };
   auto scale = [&](const SV& sv, int g) {
@@ -727,6 +736,192 @@ __global__ __launch_bounds__(kQNT) void k_qgemv_stream(QGemvParams p, int tiles_
       load(ta + 4 * (j + RS), wr[j], sr[j]);
     }
   }
+}
+
+// A operand of one MFMA k-step from one dword of the tiled layout, whose
+// nibbles are in offset form (u = q + 8; nibble i = k i).  Two fp16 values
+// per v_and_or_b32 under the 0x64 exponent bytes (1024 + u for the nibbles
+// at bits 0 and 16, 1024 + 16u for those at bits 4 and 20), then one packed
+// fp16 subtract (u - 8) or fused multiply-add ((1024 + 16u) / 16 - 72 =
+// u - 8), all exact: 9 VALU ops per 8 weights.  Element order k = 0, 4, 1,
+// 5, 2, 6, 3, 7 (stage_perm_w4o stages x the same way).  mlo / mhi / mag are
+// the masks and exponent bytes, held in VGPRs so each pair is one
+// v_and_or_b32 (a VOP3 instruction takes no literal here).
+__device__ __forceinline__ half8 a_w4o(uint32_t u, uint32_t mlo, uint32_t mhi, uint32_t mag) {
+  const uint32_t u8 = u >> 8;
+  const fp16x2 off = {(__fp16)1032.0f, (__fp16)1032.0f};
+  const fp16x2 sixteenth = {(__fp16)0.0625f, (__fp16)0.0625f};
+  const fp16x2 m72 = {(__fp16)-72.0f, (__fp16)-72.0f};
+  const fp16x2 h0 = __builtin_bit_cast(fp16x2, (u & mlo) | mag) - off;
+  const fp16x2 h1 = __builtin_elementwise_fma(__builtin_bit_cast(fp16x2, (u & mhi) | mag), sixteenth, m72);
+  const fp16x2 h2 = __builtin_bit_cast(fp16x2, (u8 & mlo) | mag) - off;
+  const fp16x2 h3 = __builtin_elementwise_fma(__builtin_bit_cast(fp16x2, (u8 & mhi) | mag), sixteenth, m72);
+  return pack_half8(h0, h1, h2, h3);
+}
+
+// x staging order of a_w4o: 8 consecutive fp16 (dwords (h0,h1) .. (h6,h7))
+// as h0, h4, h1, h5, h2, h6, h3, h7.
+__device__ __forceinline__ u32x4 stage_perm_w4o(u32x4 v) {
+  u32x4 o;
+  o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);  // h0, h4
+  o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);  // h1, h5
+  o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);  // h2, h6
+  o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);  // h3, h7
+  return o;
+}
+
+// The same product on the tiled weight layout (vnx_pack_w4_tiles): 16-row
+// tile t holds KG loads of 1 KB, load g of lane l = (kq, m) being the 16
+// bytes W[16t + m][64g + 16kq .. +16] (the lane's slice of row m, group g)
+// with every nibble in offset form (q + 8), so every weight load of a wave
+// reads one contiguous KB and converts with a_w4o.  Each wave takes
+// steps s0, s0 + 4, ... of its workgroup's range (a step = TP adjacent
+// tiles, whose MFMAs share each x fragment read from LDS) through a ring of
+// RS steps; the ring's first loads are issued before x is staged, and no
+// load reaches past the workgroup's range (a streaming read measured 6.2-6.5
+// TB/s this way, against 4.7 with 64-byte row pieces and the ring's
+// overshoot into the next workgroup's tiles).
+template <int NC, int KG, int TP, int RS, int NW, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void k_qgemv_tiles(QGemvParams p, int steps_per_wg) {
+  static_assert(KG == 4 || KG == 8, "K of 512 or 1024");
+  using SV = std::conditional_t<KG == 8, u32x4, uint2>;  // one row's KG fp16 scales
+  constexpr int XS = KG * kGK + kXPad;                    // LDS row pitch of x (fp16)
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs_dyn[];
+  uint16_t* xs = xs_dyn;
+  const int tid = threadIdx.x;
+  const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
+  const int m = lane % 16, kq = lane / 16;
+  const int64_t tiles = (p.N + 15) / 16;
+  const int64_t steps = (tiles + TP - 1) / TP;
+  const int64_t s_lo = (int64_t)blockIdx.x * steps_per_wg;
+  const int64_t s_hi = min(steps, s_lo + steps_per_wg);
+  // the workgroup's tiles as a buffer resource: every load below is issued
+  // (so the waits count statically), and one past the range reads zeros
+  // without a memory access
+  constexpr int64_t kTileB = KG * 1024;
+  const int64_t range_b = max((int64_t)0, s_hi - s_lo) * TP * kTileB;
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.w) + s_lo * TP * kTileB, (short)0, (int)range_b, 0x00020000);
+  const int64_t last_row = min(p.N, (s_hi * TP) * 16) - 1;  // the range's last real weight row
+  uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, mag = 0x64006400u;
+  asm volatile("" : "+v"(mlo), "+v"(mhi), "+v"(mag));  // in VGPRs (see a_w4o)
+  auto load = [&](int64_t st, u32x4 (&wv)[TP][KG], SV (&sv)[TP]) {
+#pragma unroll
+    for (int tp = 0; tp < TP; ++tp) {
+      const int64_t rel = min(st - s_lo, (int64_t)steps_per_wg + 2 * NW * RS) * TP + tp;  // tiles from the range start
+      const int off = (int)(rel * kTileB) + lane * 16;
+#pragma unroll
+      for (int g = 0; g < KG; ++g)
+        wv[tp][g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, off + g * 1024, 0, 2));
+      const int64_t ra = min((s_lo * TP + rel) * 16 + m, last_row);
+      sv[tp] = *reinterpret_cast<const SV*>(static_cast<const uint16_t*>(p.sc) + ra * p.lds);
+    }
+  };
+  auto scale = [&](const SV& sv, int g) {
+    uint32_t wd;
+    if constexpr (KG == 8) {
+      const int e = g / 2;
+      wd = e == 0 ? sv.x : e == 1 ? sv.y : e == 2 ? sv.z : sv.w;
+    } else {
+      wd = (g / 2) == 0 ? sv.x : sv.y;
+    }
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(wd >> (16 * (g % 2))));
+  };
+  auto compute_store = [&](int64_t st, const u32x4 (&wv)[TP][KG], const SV (&sv)[TP]) {
+    f32x4 yacc[TP][NC];
+#pragma unroll
+    for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) yacc[tp][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < KG; ++g) {
+      f32x4 acc[TP][NC];
+#pragma unroll
+      for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[tp][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        half8 bw[TP];
+#pragma unroll
+        for (int tp = 0; tp < TP; ++tp) {
+          const u32x4 v = wv[tp][g];
+          bw[tp] = a_w4o(s4 == 0 ? v.x : s4 == 1 ? v.y : s4 == 2 ? v.z : v.w, mlo, mhi, mag);
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const half8 ax = *reinterpret_cast<const half8*>(&xs[(c * 16 + m) * XS + g * kGK + kq * 32 + s4 * 8]);
+#pragma unroll
+          for (int tp = 0; tp < TP; ++tp)
+            acc[tp][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ax, bw[tp], acc[tp][c], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int tp = 0; tp < TP; ++tp) {
+        const float sg = scale(sv[tp], g);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) yacc[tp][c][j] = __builtin_fmaf(sg, acc[tp][c][j], yacc[tp][c][j]);
+      }
+      // one group's conversions live at a time (keeps the register count,
+      // and so two waves per SIMD)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int tp = 0; tp < TP; ++tp) {
+      const int64_t tile = st * TP + tp;
+      const int64_t n = tile * 16 + m;
+      if (tile >= tiles || n >= p.N) continue;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t b = c * 16 + 4 * kq + j;
+          if (b < p.B) p.y[b * p.ldy + n] = yacc[tp][c][j];
+        }
+    }
+  };
+  u32x4 wr[RS][TP][KG];
+  SV sr[RS][TP];
+  const int64_t s0 = s_lo + wave;
+#pragma unroll
+  for (int j = 0; j < RS; ++j) load(s0 + NW * j, wr[j], sr[j]);
+  // x (up to NC*16 batch rows) into LDS, in the A operand's k order; rows
+  // past B are zeros
+  for (int idx = tid; idx < NC * 16 * KG * 16; idx += NW * 64) {
+    const int b = idx / (KG * 16), c8 = idx % (KG * 16);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (b < p.B) v = *reinterpret_cast<const u32x4*>(p.x + b * p.ldx + c8 * 8);
+    *reinterpret_cast<u32x4*>(&xs[b * XS + c8 * 8]) = stage_perm_w4o(v);
+  }
+  __syncthreads();
+  for (int64_t sa = s0; sa < s_hi; sa += NW * RS) {
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+      const int64_t st = sa + NW * j;
+      if (st < s_hi) compute_store(st, wr[j], sr[j]);  // uniform per wave
+      load(st + NW * RS, wr[j], sr[j]);
+    }
+  }
+}
+
+// The tiled layout from the row-major packing: one thread per 16-byte piece
+// of the output, every nibble flipped to offset form (q ^ 8 = q + 8 in 0..15);
+// rows past N (the last tile's padding) hold q = 0.
+__global__ void k_pack_w4_tiles(const uint8_t* __restrict__ wq, int64_t ldw, int64_t N, int kg, int64_t pieces,
+                                uint8_t* __restrict__ out) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= pieces) return;
+  const int l = (int)(q % 64);
+  const int64_t tg = q / 64;  // tile * kg + g
+  const int g = (int)(tg % kg);
+  const int64_t t = tg / kg;
+  const int64_t row = t * 16 + (l % 16);
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (row < N) v = *reinterpret_cast<const u32x4*>(wq + row * ldw + g * 64 + (l / 16) * 16);
+  const uint32_t f = 0x88888888u;
+  *reinterpret_cast<u32x4*>(out + q * 16) = u32x4{v.x ^ f, v.y ^ f, v.z ^ f, v.w ^ f};
 }
 
 // Dequantization (bit-exact reference for the kernels' weights):
@@ -847,6 +1042,9 @@ static int qgemv_launch(QGemvParams p, int bits, hipStream_t s) {
       const int64_t wgs_target = 2 * device_cus();
       int64_t tpw = (tiles + wgs_target - 1) / wgs_target;
       tpw = (tpw + 7) / 8 * 8;
+      // a workgroup's row range (and the ring's overshoot) stays inside the
+      // 32-bit buffer offsets
+      tpw = min(tpw, ((int64_t)1 << 30) / (3 * 16 * c.ldw) / 8 * 8);
       const dim3 grid((unsigned)((tiles + tpw - 1) / tpw));
       const int nc = two ? 2 : 1;
       const size_t lds = (size_t)nc * 16 * (c.K + kXPad) * 2;
@@ -1011,6 +1209,66 @@ int vnx_gemv_w4_residual(const void* x, int64_t ldx, const uint8_t* wq, int64_t 
   const int st = qgemv_check(p, 4);
   if (st) return st;
   return qgemv_launch(p, 4, static_cast<hipStream_t>(stream));
+}
+
+size_t vnx_w4_tiles_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % kGK) return 0;
+  return (size_t)((N + 15) / 16) * 16 * (size_t)(K / 2);
+}
+
+int vnx_pack_w4_tiles(const uint8_t* wq, int64_t ldw, int64_t N, int64_t K, uint8_t* out, void* stream) {
+  if (!wq || !out || N <= 0 || K <= 0 || ldw < K / 2) return VNX_ERR_INVALID_ARG;
+  if (K % kGK) return VNX_ERR_UNSUPPORTED;
+  if (!aligned16(wq) || ldw % 16 || !aligned16(out)) return VNX_ERR_UNSUPPORTED;
+  const int kg = (int)(K / kGK);
+  const int64_t pieces = (N + 15) / 16 * kg * 64;
+  hipLaunchKernelGGL(k_pack_w4_tiles, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), wq, ldw, N, kg, pieces, out);
+  VNX_LAUNCH_CHECK();
+  return VNX_OK;
+}
+
+int vnx_gemv_w4_tiles(const void* x, int64_t ldx, const uint8_t* wt, const void* scales, int64_t lds, int64_t B,
+                      int64_t N, int64_t K, float* y, int64_t ldy, void* stream) {
+  if (!x || !wt || !scales || !y || B < 0 || N <= 0 || K <= 0) return VNX_ERR_INVALID_ARG;
+  if (K != 512 && K != 1024) return VNX_ERR_UNSUPPORTED;
+  if (ldx < K || ldy < N || lds < K / kGK) return VNX_ERR_INVALID_ARG;
+  // 16-byte loads of x and of the tiles; 8- or 16-byte loads of a row's scales
+  if (!aligned16(x) || ldx % 8 || !aligned16(wt) || !aligned16(scales) || lds % (K == 1024 ? 8 : 4))
+    return VNX_ERR_UNSUPPORTED;
+  if (B == 0) return VNX_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t tiles = (N + 15) / 16;
+  for (int64_t b0 = 0; b0 < B; b0 += 32) {
+    QGemvParams c{};
+    c.x = static_cast<const uint16_t*>(x) + b0 * ldx; c.ldx = ldx; c.w = wt; c.sc = scales; c.lds = lds;
+    c.sc_f16 = 1; c.B = min((int64_t)32, B - b0); c.N = N; c.K = K; c.G = kGK; c.gpg = 1;
+    c.y = y + b0 * ldy; c.ldy = ldy; c.row_off = b0;
+    const bool two = c.B > 16;
+    // one tile per step; up to 16 batch rows: 4-wave workgroups, about 4
+    // per CU over the launch; beyond: 8-wave workgroups (one staged copy of
+    // the 2 x 16 rows of x for twice the waves), about 2 per CU
+    constexpr int TP = 1;
+    const int64_t steps = (tiles + TP - 1) / TP;
+    const int64_t wgs_target = (two ? 2 : 4) * device_cus();
+    // a workgroup's range stays well inside the 32-bit buffer offsets
+    const int64_t spw_max = ((int64_t)1 << 30) / (TP * (K / kGK) * 1024);
+    const int64_t spw = min(spw_max, max((int64_t)4, (steps + wgs_target - 1) / wgs_target));
+    const dim3 grid((unsigned)((steps + spw - 1) / spw));
+    const size_t lds_bytes = (size_t)(two ? 2 : 1) * 16 * (K + kXPad) * 2;
+#define VNX_QTILES(NC, KG, RS, NW, OCC) \
+  hipLaunchKernelGGL((k_qgemv_tiles<NC, KG, TP, RS, NW, OCC>), grid, dim3(NW * 64), lds_bytes, s, c, (int)spw)
+    // (measured on the 248,320 x 1024 head, three weight copies: one column
+    // block with a 2-step ring at 4 waves per SIMD, B = 1 26.9 us; two blocks
+    // with 8-wave workgroups and no ring (128 VGPRs, 4 waves per SIMD) 37.1
+    // us, against 39.5 us for 4-wave workgroups with the ring at 2 waves per
+    // SIMD and 67 us where the ring at 4 waves per SIMD spilled)
+    if (K == 512) { if (two) VNX_QTILES(2, 4, 1, 8, 4); else VNX_QTILES(1, 4, 2, 4, 4); }
+    else { if (two) VNX_QTILES(2, 8, 1, 8, 4); else VNX_QTILES(1, 8, 2, 4, 4); }
+#undef VNX_QTILES
+    VNX_LAUNCH_CHECK();
+  }
+  return VNX_OK;
 }
 
 int vnx_gemv_w8(const void* x, int64_t ldx, const int8_t* wq, int64_t ldw, const float* scale,

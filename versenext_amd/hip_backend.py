@@ -389,6 +389,31 @@ class HipBackend(DeviceBackend):
                                        ctypes.c_void_p(self._stream().cuda_stream)), "gemv_w4")
         return y.reshape(*lead, N)
 
+    def pack_w4_tiles(self, wq, K: int) -> torch.Tensor:
+        """The tiled copy (vnx_pack_w4_tiles: 16-row tiles of 1 KB pieces,
+        nibbles in offset form) of packed int4 wq (N, K/2); returns a uint8
+        tensor of vnx_w4_tiles_bytes(N, K) bytes."""
+        dev = self._torch_device
+        w = self._rows16(_to_tensor(wq, dev, torch.uint8))
+        N = w.shape[0]
+        out = torch.empty(self._L.vnx_w4_tiles_bytes(N, K), dtype=torch.uint8, device=dev)
+        _lib.check(self._L.vnx_pack_w4_tiles(_ptr(w), w.stride(0), N, K, _ptr(out),
+                                             ctypes.c_void_p(self._stream().cuda_stream)), "pack_w4_tiles")
+        return out
+
+    def gemv_w4_tiles(self, x, wt, scales, N: int, K: int) -> torch.Tensor:
+        """y = x @ (q * s)^T from the tiled copy wt (pack_w4_tiles) and fp16
+        group-128 scales (N, K/128); returns (..., N) fp32 (vnx_gemv_w4_tiles)."""
+        dev = self._torch_device
+        sc = _to_tensor(scales, dev, torch.float16).reshape(N, -1).contiguous()
+        lead = _to_tensor(x, dev).shape[:-1]
+        x2 = self._acts(x, K)
+        B = x2.shape[0]
+        y = torch.empty((B, N), dtype=torch.float32, device=dev)
+        _lib.check(self._L.vnx_gemv_w4_tiles(_ptr(x2), K, _ptr(wt), _ptr(sc), sc.stride(0), B, N, K, _ptr(y), N,
+                                             ctypes.c_void_p(self._stream().cuda_stream)), "gemv_w4_tiles")
+        return y.reshape(*lead, N)
+
     def gemv_w8(self, x, wq, scale) -> torch.Tensor:
         """y = x @ (q * s)^T for int8 wq (N, K) and per-row fp32 scale (N,)."""
         dev = self._torch_device

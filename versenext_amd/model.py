@@ -315,6 +315,7 @@ class _Linear:
     def __init__(self, w, dtype, hip, int4: bool, swiglu: bool = False, rope_head_dim: int = 0):
         self.N, self.K = w.shape
         self.wq_rope = None
+        self.wt = None
         self.dtype = dtype
         self.hip = hip
         pre = isinstance(w, Int4Weight)  # already quantized (streamed from a .vn file)
@@ -344,6 +345,16 @@ class _Linear:
             L = hip._L
             self._ws = torch.zeros(max(256, L.vnx_gemv_workspace(64, self.N, self.K)), dtype=torch.uint8,
                                    device=hip.torch_device)
+            # large N (a tied LM head): a tiled copy for vnx_gemv_w4_tiles
+            # (1 KB per wave load, nibbles in offset form)
+            self.wt = None
+            if self.N >= self.TILES_MIN_N and self.K in (512, 1024) and self.sc.dtype == torch.float16:
+                self.wt = torch.empty(L.vnx_w4_tiles_bytes(self.N, self.K), dtype=torch.uint8,
+                                      device=hip.torch_device)
+                _lib.check(L.vnx_pack_w4_tiles(ctypes.c_void_p(self.wq.data_ptr()), self.wq.stride(0), self.N,
+                                               self.K, ctypes.c_void_p(self.wt.data_ptr()),
+                                               ctypes.c_void_p(torch.cuda.current_stream(hip.torch_device)
+                                                               .cuda_stream)), "pack_w4_tiles")
         else:
             self.wd = w.to(dtype).contiguous()
             # verify-size products (M <= GEMM_MAX_M) run vnx_gemm_bf16 on a
@@ -365,6 +376,8 @@ class _Linear:
 
 
     GEMM_MAX_M = 256
+    # rows from which an INT4 weight also keeps the tiled copy (the LM head)
+    TILES_MIN_N = 32768
 
     def gemm(self, x: torch.Tensor, epilogue: int = 0, out_dtype=None) -> Optional[torch.Tensor]:
         """vnx_gemm_bf16 of the packed weight for x (M <= GEMM_MAX_M, bf16
@@ -516,6 +529,13 @@ class _Linear:
             x16 = x.to(torch.float16).contiguous()
             y = out if out is not None else torch.empty((M, self.N), dtype=torch.float32, device=x.device)
             L = self.hip._L
+            if self.wt is not None:
+                _lib.check(L.vnx_gemv_w4_tiles(
+                    ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wt.data_ptr()),
+                    ctypes.c_void_p(self.sc.data_ptr()), self.sc.stride(0), M, self.N, self.K,
+                    ctypes.c_void_p(y.data_ptr()), y.stride(0),
+                    ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4_tiles")
+                return y
             _lib.check(L.vnx_gemv_w4(
                 ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq.data_ptr()), self.wq.stride(0),
                 ctypes.c_void_p(self.sc.data_ptr()), _lib.VNX_F16, self.sc.stride(0), M, self.N, self.K, 128,
