@@ -241,17 +241,19 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
         }
         *reinterpret_cast<u32x4*>(buf + q * 32 * kVgRowB + xs_off(xr, xc)) = v & xkeep;
       }
-      const u32x4 wq[4] = {wv[j][0], wv[j][1], wv[j][2], wv[j][3]};
       __syncthreads();  // pass ps's X is staged; the other buffer was read before it
-      load_pass(ps + PD, xv[j], wv[j]);  // past the end: clamped re-reads, never used
       if (ps * WK + wk < nch) {  // uniform per wave
         const char* xb = buf + wk * 32 * kVgRowB;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(r, h * 4 + s));
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wq[s]), acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j][s]), acc, 0, 0, 0);
         }
       }
+      // the slot's next pass, issued after its W operands are consumed: the
+      // ring's registers then carry over the loop's back edge in place (a copy
+      // of them would make the compiler wait for every load in flight there)
+      load_pass(ps + PD, xv[j], wv[j]);  // past the end: clamped re-reads, never used
     }
   }
 
