@@ -173,7 +173,8 @@ def cpu_gemv(packed, qtype, x_list, reps_head: int = 3, reps: int = 5):
 def bench_gemv(args, emit=True):
     """weight-only INT4 (group 128, fp16 scales) and INT8
     (per-channel) GEMV, weights N(0, 0.02), fp16 activations N(0, 1), B in
-    {1, 8, 32}.  bytes per launch = weight + scales + 2*B*K (fp16 x) + 4*B*N
+    {1, 8, 32}; the INT4 tied head (N >= 32,768) through vnx_gemv_w4_tiles on
+    its tiled copy, the layout the draft model keeps for its head.  bytes per launch = weight + scales + 2*B*K (fp16 x) + 4*B*N
     (fp32 y).  Time: the C entry point is called `steps` times back to back on
     preallocated buffers, between two HIP events on its stream, so the small
     FFN layers are timed on the GPU rather than on the Python launch path.
@@ -198,6 +199,9 @@ def bench_gemv(args, emit=True):
         del w
         for qtype in ("int4_g128", "int8"):
             wq, sc = packed[qtype]
+            wt = None
+            if qtype == "int4_g128" and N >= 32768 and K in (512, 1024):
+                wt = hip.pack_w4_tiles(wq, K)   # vnx_gemv_w4_tiles' layout (the tied head's copy)
             xs = []
             for B in (1, 8, 32):
                 x = (torch.randn((B, K), generator=g, device=dev)).to(torch.float16)
@@ -211,6 +215,10 @@ def bench_gemv(args, emit=True):
                     call, argv = L.vnx_gemv_w8, (P(x.data_ptr()), K, P(wq.data_ptr()), wq.stride(0),
                                                  P(sc.data_ptr()), B, N, K, P(y.data_ptr()), N,
                                                  P(ws.data_ptr()), ws.numel(), st)
+                elif wt is not None:
+                    # the tied head as the draft runs it: the tiled copy
+                    call, argv = L.vnx_gemv_w4_tiles, (P(x.data_ptr()), K, P(wt.data_ptr()), P(sc.data_ptr()),
+                                                       sc.stride(0), B, N, K, P(y.data_ptr()), N, st)
                 else:
                     call, argv = L.vnx_gemv_w4, (P(x.data_ptr()), K, P(wq.data_ptr()), wq.stride(0),
                                                  P(sc.data_ptr()), _lib.VNX_F16, sc.stride(0), B, N, K, 128,
@@ -219,6 +227,7 @@ def bench_gemv(args, emit=True):
                 nbytes = VQ.weight_bytes(qtype, N, K) + 2 * B * K + 4 * B * N
                 gbs = nbytes / (us * 1e-6) / 1e9
                 rows.append({"shape": name, "N": N, "K": K, "qtype": qtype, "B": B, "us": round(us, 2),
+                             "entry": call.__name__,
                              "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                              "TFLOP/s": round(2 * B * N * K / (us * 1e-6) / 1e12, 2)})
             if not args.no_cpu:
@@ -238,7 +247,8 @@ def bench_gemv(args, emit=True):
            "steps": args.steps, "warmup": args.warmup, "higher_is_better": True, "dtype": "int4/int8 x fp16",
            "data": "synthetic", "config": {"workload": "BASELINE config 4: weight-only dequant-GEMV"},
            "roofline": {"bound": "hbm", "achieved": best["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": best["frac"], "traffic": None, "kernel": "k_qgemv_stream<*, 8, 2> (tied head)"},
+                        "frac": best["frac"], "traffic": None,
+                        "kernel": "k_qgemv_tiles (vnx_gemv_w4_tiles, tied head)"},
            "results": rows}
     if cpu_rows:
         out["cpu_baseline"] = dict(cpu_env(CPU_THREADS), kind="port", results=cpu_rows,

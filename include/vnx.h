@@ -149,6 +149,23 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype,
                     float* lse_t, float* lse_d,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* vnx_spec_accept for a caller whose draws already computed the draft rows'
+ * log-sum-exps (the k draws of a speculative round, vnx_sample with its lse
+ * and flags outputs, at the same temperature and without top-k): lse_d_in
+ * [i * ld_in + b] is RN32 of the LSE of draft row i of batch row b, and
+ * flags_d_in (same layout, may be NULL) their flags, whose VNX_FLAG_LSE_EDGE
+ * bit carries over to the positions those rows decide.  The first launch
+ * then streams only the k + 1 target rows per batch row (and reads the draft
+ * rows at the draft ids), so the draft logits are not read twice in a round;
+ * the decisions equal vnx_spec_accept's given the same draft LSEs.  No
+ * per-row thresholds.  Workspace: vnx_spec_accept_workspace(B, k, V). */
+int vnx_spec_accept_draft_lse(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
+                              int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
+                              const int64_t* draft_ids, const float* uniforms, float temperature,
+                              const float* lse_d_in, const uint8_t* flags_d_in, int64_t ld_in,
+                              int32_t* accept_len, int64_t* out_ids, uint8_t* flags, float* lse_t, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* Sampler.sample, one call per batch of rows: out_ids[b] = the token the
  * reference's Sampler draws from logits row b with temperature, top_k, top_p
  * and the uniform uniforms[b] in place of its RNG

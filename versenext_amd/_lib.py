@@ -64,6 +64,8 @@ SIGNATURES = {
     "vnx_spec_accept_workspace": (_c_sz, [_c_i64, _int, _c_i64]),
     "vnx_spec_accept": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "vnx_spec_accept_draft_lse": (_int, [_vp, _vp, _int, _c_i64, _int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _vp, _vp, _f32, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "vnx_sampler_workspace": (_c_sz, [_c_i64, _c_i64, _int]),
     "vnx_sampler_sample": (_int, [_vp, _int, _c_i64, _c_i64, _c_i64, _f32, _c_i64, _f32, _int, _f32, _f32,
                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),

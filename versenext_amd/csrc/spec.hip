@@ -78,6 +78,15 @@ struct SpecParams {
   double* sbm;     // [B][nsb] sub-block draw masses
   unsigned* cnt;   // [B] arrival counters of launch B
   float* gath;     // [B][2k] scaled target / draft logits at the draft ids
+  // Draft rows' LSEs supplied by the caller (the draws that produced the
+  // draft ids computed them): lse_din[i * ld_din + b] = RN32(LSE of q_i / T),
+  // fl_din the draws' flags (VNX_FLAG_LSE_EDGE used).  Then launch A streams
+  // only the k + 1 target rows (rows_a = k + 1, else 2k + 1) and gathers
+  // the draft logits at the draft ids beside the target's.
+  const float* lse_din;
+  const uint8_t* fl_din;
+  int64_t ld_din;
+  int rows_a;
 };
 
 // Distance test of an fp64 LSE to the rounding midpoints around its fp32 value.
@@ -114,7 +123,7 @@ __device__ __forceinline__ float row_thr(const SpecParams& p, int64_t b, int ri)
 template <typename Tin, int SM, bool THR>
 __device__ __forceinline__ void lse_work(const SpecParams& p, int64_t r, int c, ReduceLds& lds) {
   const int k = p.k;
-  const int R = 2 * k + 1;
+  const int R = p.rows_a;
   const int64_t b = r / R;
   const int ri = (int)(r - b * R);
   const int64_t c0 = (int64_t)c * p.chunk_len;
@@ -124,9 +133,14 @@ __device__ __forceinline__ void lse_work(const SpecParams& p, int64_t r, int c, 
   if (ri != k) {
     const int pos = ri < k ? ri : ri - k - 1;
     const int64_t x = p.ids[b * k + pos];
-    if (x >= c0 && x < c1 && threadIdx.x == 0)
+    if (x >= c0 && x < c1 && threadIdx.x == 0) {
       p.gath[b * 2 * k + (ri < k ? pos : k + pos)] =
           scaled_at<Tin, SM, THR>(row_ptr<Tin>(p, b, ri), x, p.sc, row_thr<THR>(p, b, ri));
+      // draft rows not streamed here: their value at the id with the target's
+      if (p.lse_din && ri < k)
+        p.gath[b * 2 * k + k + pos] =
+            scaled_at<Tin, SM, THR>(row_ptr<Tin>(p, b, k + 1 + ri), x, p.sc, row_thr<THR>(p, b, k + 1 + ri));
+    }
   }
   const ChunkResult cr = reduce_chunk<Tin, SM, THR, true, false, kNT, kNB>(row_ptr<Tin>(p, b, ri), c0, c1,
                                                                            p.sc, row_thr<THR>(p, b, ri), lds);
@@ -141,7 +155,7 @@ __device__ __forceinline__ void lse_work(const SpecParams& p, int64_t r, int c, 
 // tests.  Every workgroup of b's mass chunks runs it and gets the same job
 // (fixed lane order, no atomics); with `write`, the workgroup also stores
 // accept_len, out_ids (accepted prefix, -1 after), flags and the LSEs.
-// pm_l / ps_l: LDS room for the row's (2k+1)*chunks partials.
+// pm_l / ps_l: LDS room for the row's rows_a * chunks partials.
 // ---------------------------------------------------------------------------
 struct AcceptLds {
   float Ls[2 * kMaxK + 1];
@@ -174,7 +188,8 @@ __device__ __forceinline__ Job accept_row(const SpecParams& p, int64_t b, bool w
   // lane's partials rescaled to it and summed in lane order, then a
   // butterfly sum across the segment.
   const int C = p.chunks;
-  const int total = R * C;  // <= kAccParts (host check)
+  const int RA = p.rows_a;   // rows with partials (the draft rows come from lse_din otherwise)
+  const int total = RA * C;  // <= kAccParts (host check)
   const int64_t pbase = b * (int64_t)total;
   for (int i = tid; i < total; i += kNT) {
     pm_l[i] = p.part_m[pbase + i];
@@ -183,7 +198,14 @@ __device__ __forceinline__ Job accept_row(const SpecParams& p, int64_t b, bool w
   __syncthreads();
   constexpr int SEG = 16;
   const int sl = tid % SEG;
-  for (int r = tid / SEG; r < R; r += kNT / SEG) {
+  if (RA < R && tid < k) {
+    // the draft rows' LSEs as the draws computed them, with their edge flags
+    const float Ld = p.lse_din[tid * p.ld_din + b];
+    L.Ls[k + 1 + tid] = Ld;
+    L.Ledge[k + 1 + tid] = (p.fl_din && (p.fl_din[tid * p.ld_din + b] & VNX_FLAG_LSE_EDGE)) ? 1 : 0;
+    if (write && p.lse_d) p.lse_d[b * k + tid] = Ld;
+  }
+  for (int r = tid / SEG; r < RA; r += kNT / SEG) {
     const int base = r * C;
     float M = kNegInf;
     for (int c = sl; c < C; c += SEG) M = fmaxf(M, pm_l[base + c]);
@@ -551,7 +573,7 @@ __global__ __launch_bounds__(kNT) void k_spec_lse(SpecParams p) {
   const int64_t zc = (int64_t)blockIdx.x * kNT + threadIdx.x;
   if (zc < p.B) p.cnt[zc] = 0u;
   const int64_t w = blockIdx.x;
-  if (w < p.B * (2 * p.k + 1) * p.chunks) lse_work<Tin, SM, THR>(p, w / p.chunks, (int)(w % p.chunks), lds);
+  if (w < p.B * p.rows_a * p.chunks) lse_work<Tin, SM, THR>(p, w / p.chunks, (int)(w % p.chunks), lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -571,7 +593,7 @@ __global__ __launch_bounds__(kNT) void k_spec_mass_draw(SpecParams p) {
   extern __shared__ double dyn[];
   const int c = blockIdx.x % p.chunks2;
   const int64_t b = blockIdx.x / p.chunks2;
-  const int total = (2 * p.k + 1) * p.chunks;
+  const int total = p.rows_a * p.chunks;  // the partials' LDS, sized by the host for rows_a rows
   const Job jb = accept_row<Tin, SM, THR>(p, b, c == 0, lds.acc, reinterpret_cast<float*>(dyn + total), dyn);
   const DrawRows d = draw_rows<THR>(p, b, jb);
   const Tin* P = static_cast<const Tin*>(p.tgt) + d.poff;
@@ -602,17 +624,18 @@ constexpr int64_t kMassPerCu = 4;
 // ran its launch B 8 us slower with 2 per CU)
 constexpr int64_t kMassPerCuDraw = 2;
 
-static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype) {
+static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype, int rows_a = -1) {
   const int ve = dtype == VNX_F32 ? 4 : 8;
   SpecPlan pl;
-  const int64_t rows = B * (2 * k + 1);
+  if (rows_a < 0) rows_a = 2 * k + 1;
+  const int64_t rows = B * rows_a;
   // chunks of at least kNB / 2 vectors per thread: few rows (a decode batch)
   // get fewer, longer workgroups instead of thousands of one-load ones.  A
   // k = 0 draw (one row per batch row) takes about two workgroups per CU:
   // at 32 rows of 248,320, 16 chunks per row gave a 20 us shorter config-5
   // round than 60 (and 8 or 4 chunks were slower again)
   const int64_t wgs = k == 0 ? 2 * (int64_t)device_cus() : kLseWgs;
-  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccParts / (2 * k + 1)), wgs);
+  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccParts / rows_a), wgs);
   const int64_t len = ((V + c - 1) / c + ve - 1) / ve * ve;
   pl.len = len;
   pl.chunks = (int)((V + len - 1) / len);
@@ -641,11 +664,13 @@ static size_t spec_carve(void* ws, int64_t B, int k, const SpecPlan& pl, SpecPar
   return cv.bytes();
 }
 
-// Workspace bound over both dtypes.
+// Workspace bound over both dtypes, with and without caller-supplied draft
+// LSEs (whose plan may cut the rows into more chunks).
 static size_t spec_ws_bytes(int64_t B, int k, int64_t V) {
-  const size_t a = spec_carve(nullptr, B, k, spec_plan(B, k, V, VNX_F32), nullptr);
-  const size_t b = spec_carve(nullptr, B, k, spec_plan(B, k, V, VNX_BF16), nullptr);
-  return a > b ? a : b;
+  size_t m = 0;
+  for (int dt : {VNX_F32, VNX_BF16})
+    for (int ra : {2 * k + 1, k + 1}) m = std::max(m, spec_carve(nullptr, B, k, spec_plan(B, k, V, dt, ra), nullptr));
+  return m;
 }
 
 // Commit of one speculative round for every sequence (one workgroup, one
@@ -754,7 +779,8 @@ static int spec_run(const void* target, const void* draft, int dtype, int64_t B,
                     const int64_t* draft_ids, const float* uniforms,
                     float temperature, const float* thr_t, const float* thr_d, int32_t* accept_len,
                     int64_t* out_ids, uint8_t* flags, float* lse_t, float* lse_d, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    size_t workspace_bytes, void* stream, const float* lse_din = nullptr,
+                    const uint8_t* fl_din = nullptr, int64_t ld_din = 0) {
   if (dtype != VNX_F32 && dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
   if (B < 0 || k < 0 || k > kMaxK || V <= 0) return VNX_ERR_INVALID_ARG;
   if (!(temperature > 0.0f) || !__builtin_isfinite(temperature)) return VNX_ERR_INVALID_ARG;
@@ -768,10 +794,12 @@ static int spec_run(const void* target, const void* draft, int dtype, int64_t B,
     if (!draft_ids) return VNX_ERR_INVALID_ARG;
   }
   if (!uniforms || !accept_len || !out_ids) return VNX_ERR_INVALID_ARG;
-  const SpecPlan pl = spec_plan(B, k, V, dtype);
-  if (B * (2 * k + 1) * (int64_t)pl.chunks >= INT32_MAX || B * (int64_t)pl.chunks2 >= INT32_MAX ||
-      pl.nsb > kDrawLds || (2 * k + 1) * pl.chunks > kAccParts)
+  const int rows_a = lse_din ? k + 1 : 2 * k + 1;
+  const SpecPlan pl = spec_plan(B, k, V, dtype, rows_a);
+  if (B * rows_a * (int64_t)pl.chunks >= INT32_MAX || B * (int64_t)pl.chunks2 >= INT32_MAX ||
+      pl.nsb > kDrawLds || rows_a * pl.chunks > kAccParts)
     return VNX_ERR_UNSUPPORTED;
+  // (the partials are carved for 2k + 1 rows of this plan's chunks: enough)
   if (!workspace || workspace_bytes < spec_carve(nullptr, B, k, pl, nullptr)) return VNX_ERR_WORKSPACE;
   SpecParams p{};
   p.tgt = target; p.dft = draft; p.B = B; p.k = k; p.V = V;
@@ -780,11 +808,12 @@ static int spec_run(const void* target, const void* draft, int dtype, int64_t B,
   const int sm = make_scale(temperature, &p.sc);
   p.thr_t = thr_t; p.thr_d = thr_d; p.ids = draft_ids; p.u = uniforms;
   p.accept_len = accept_len; p.out_ids = out_ids; p.flags = flags; p.lse_t = lse_t; p.lse_d = lse_d;
+  p.lse_din = lse_din; p.fl_din = fl_din; p.ld_din = ld_din; p.rows_a = rows_a;
   spec_carve(workspace, B, k, pl, &p);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t na = B * (2 * k + 1) * pl.chunks;
+  const int64_t na = B * rows_a * pl.chunks;
   const dim3 ga((unsigned)std::max<int64_t>(na, (B + kNT - 1) / kNT)), gb((unsigned)(B * pl.chunks2));
-  const size_t lds_b = std::max((size_t)pl.nsb * sizeof(double), (size_t)(2 * k + 1) * pl.chunks * 12);
+  const size_t lds_b = std::max((size_t)pl.nsb * sizeof(double), (size_t)rows_a * pl.chunks * 12);
   hipEvent_t* ev = profile_slot(2);
   auto mark = [&](int j) -> int {
     if (ev) VNX_HIP_CHECK(hipEventRecord(ev[j], s));
@@ -814,6 +843,18 @@ int vnx_spec_accept(const void* target, const void* draft, int dtype, int64_t B,
   if (k < 1) return VNX_ERR_INVALID_ARG;
   return spec_run(target, draft, dtype, B, k, V, ld_t, sb_t, ld_d, sb_d, draft_ids, uniforms, temperature,
                   thr_t, thr_d, accept_len, out_ids, flags, lse_t, lse_d, workspace, workspace_bytes, stream);
+}
+
+int vnx_spec_accept_draft_lse(const void* target, const void* draft, int dtype, int64_t B, int k, int64_t V,
+                              int64_t ld_t, int64_t sb_t, int64_t ld_d, int64_t sb_d,
+                              const int64_t* draft_ids, const float* uniforms, float temperature,
+                              const float* lse_d_in, const uint8_t* flags_d_in, int64_t ld_in,
+                              int32_t* accept_len, int64_t* out_ids, uint8_t* flags, float* lse_t, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (k < 1 || !lse_d_in || ld_in < B) return VNX_ERR_INVALID_ARG;
+  return spec_run(target, draft, dtype, B, k, V, ld_t, sb_t, ld_d, sb_d, draft_ids, uniforms, temperature,
+                  nullptr, nullptr, accept_len, out_ids, flags, lse_t, nullptr, workspace, workspace_bytes, stream,
+                  lse_d_in, flags_d_in, ld_in);
 }
 
 size_t vnx_spec_accept_noalloc_max_bytes(void) { return kSpecScratchBytes; }

@@ -10,8 +10,9 @@ Per round (all sequences of the batch at once):
    softmax(q_i / T) (argmax when greedy);
 2. verify: the target runs [c, x_1 .. x_k] at positions lens_t[b] + i and
    the matrix-core LM head writes p (B, k+1, V) fp32;
-3. accept: vnx_spec_accept (Leviathan et al. 2023, Alg. 1 with host uniforms)
-   or, greedy, vnx_greedy_verify with the bonus row: n_b accepted tokens and
+3. accept: vnx_spec_accept_draft_lse (Leviathan et al. 2023, Alg. 1 with
+   host uniforms; the draft rows' LSEs come from the draws of step 1) or,
+   greedy, vnx_greedy_verify with the bonus row: n_b accepted tokens and
    one drawn / bonus token per sequence;
 4. commit: lens_t, lens_d += n_b + 1 (the rejected suffix of both caches is
    rolled back by not advancing), the drawn token becomes c.
@@ -89,6 +90,10 @@ class SpecDecodeEngine:
         self.u_draft = self.u_all[:k * B].view(k, B)
         self.u_acc = self.u_all[off:].view(B, k + 1)
         self.xsT = torch.zeros((k, B), dtype=torch.int64, device=dev)   # draft token i of every row: xsT[i]
+        # the draws' row LSEs of q_i / T and their flags, which the acceptance
+        # takes instead of streaming the k draft rows again
+        self.lse_dr = torch.zeros((k, B), dtype=torch.float32, device=dev)
+        self.fl_dr = torch.zeros((k, B), dtype=torch.uint8, device=dev)
         self.toks = torch.zeros((B, k + 1), dtype=torch.int64, device=dev)  # [c, x_1 .. x_k] per row
         self.c = torch.zeros(B, dtype=torch.int64, device=dev)
         self.lens_t = torch.zeros(B, dtype=torch.int32, device=dev)
@@ -136,7 +141,8 @@ class SpecDecodeEngine:
             if self.greedy:
                 self.xsT[i].copy_(self.hip.argmax(self.qbuf[:, i]).view(B))
             else:
-                self.hip.sample(self.qbuf[:, i], self.u_draft[i], temperature=self.T, out=self.xsT[i])
+                self.hip.sample(self.qbuf[:, i], self.u_draft[i], temperature=self.T, out=self.xsT[i],
+                                lse_out=self.lse_dr[i], flags_out=self.fl_dr[i])
             tok = self.xsT[i]
         torch.cat([self.c.view(B, 1), self.xsT.t()], dim=1, out=self.toks)
         xs = self.toks[:, 1:]
@@ -146,7 +152,8 @@ class SpecDecodeEngine:
             _, _, alen, ids = self.hip.greedy_verify(self.pbuf, xs, rows_t=k + 1)
             self.last = dict(accept_len=alen, out_ids=ids, flags=None)
         else:
-            res = self.hip.spec_accept(self.pbuf, self.qbuf, xs, self.u_acc, temperature=self.T)
+            res = self.hip.spec_accept(self.pbuf, self.qbuf, xs, self.u_acc, temperature=self.T,
+                                       lse_d_in=self.lse_dr, flags_d_in=self.fl_dr)
             alen, ids = res["accept_len"], res["out_ids"]
             self.last = res
         # commit (one launch, no data-dependent shapes, so the round can be

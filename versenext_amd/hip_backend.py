@@ -226,9 +226,12 @@ class HipBackend(DeviceBackend):
         return am.reshape(lead)
 
     def spec_accept(self, target, draft, draft_ids, uniforms, temperature: float = 1.0,
-                    thr_t=None, thr_d=None):
+                    thr_t=None, thr_d=None, lse_d_in=None, flags_d_in=None):
         """Stochastic acceptance (see vnx_spec_accept in include/vnx.h).
         target (B,k+1,V), draft (B,k,V) fp32/bf16; draft_ids (B,k); uniforms (B,k+1).
+        lse_d_in (k, B) fp32 with flags_d_in (k, B) uint8: the draft rows'
+        LSEs and flags as the draws produced them (vnx_spec_accept_draft_lse:
+        the draft rows are then read only at the draft ids; no thresholds).
         Returns dict of device tensors: accept_len (B,) int32, out_ids (B,k+1)
         int64, flags (B,k+1) uint8, lse_t (B,k+1) f32, lse_d (B,k) f32."""
         dev = self._torch_device
@@ -254,6 +257,24 @@ class HipBackend(DeviceBackend):
         lse_t = torch.empty((B, k + 1), dtype=torch.float32, device=dev)
         lse_d = torch.empty((B, k), dtype=torch.float32, device=dev)
         ws = self._workspace(self._L.vnx_spec_accept_workspace(B, k, V))
+        if lse_d_in is not None:
+            if tt is not None or td is not None:
+                raise ValueError("draft LSEs from the draws exclude per-row thresholds")
+            ld = _to_tensor(lse_d_in, dev, torch.float32)
+            if tuple(ld.shape) != (k, B) or ld.stride(1) != 1:
+                raise ValueError(f"lse_d_in must be (k, B) = ({k}, {B}) with unit column stride")
+            fd = None
+            if flags_d_in is not None:
+                fd = _to_tensor(flags_d_in, dev, torch.uint8)
+                if tuple(fd.shape) != (k, B) or fd.stride(1) != 1 or fd.stride(0) != ld.stride(0):
+                    raise ValueError("flags_d_in must match lse_d_in's layout")
+            _lib.check(self._L.vnx_spec_accept_draft_lse(
+                _ptr(tg), _ptr(df), _LOGIT_DTYPES[tg.dtype], B, k, V,
+                tg.stride(1), tg.stride(0), df.stride(1), df.stride(0),
+                _ptr(ids), _ptr(u), float(temperature), _ptr(ld), _ptr(fd), ld.stride(0),
+                _ptr(alen), _ptr(out), _ptr(flags), _ptr(lse_t),
+                _ptr(ws), ws.numel(), ctypes.c_void_p(self._stream().cuda_stream)), "spec_accept_draft_lse")
+            return dict(accept_len=alen, out_ids=out, flags=flags, lse_t=lse_t, lse_d=ld.t())
         _lib.check(self._L.vnx_spec_accept(
             _ptr(tg), _ptr(df), _LOGIT_DTYPES[tg.dtype], B, k, V,
             tg.stride(1), tg.stride(0), df.stride(1), df.stride(0),
@@ -263,11 +284,13 @@ class HipBackend(DeviceBackend):
         return dict(accept_len=alen, out_ids=out, flags=flags, lse_t=lse_t, lse_d=lse_d)
 
     def sample(self, logits, uniforms, temperature: float = 1.0, thresholds=None, out=None,
-               return_all: bool = False):
+               return_all: bool = False, lse_out=None, flags_out=None):
         """Inverse-CDF draw per row from softmax(logits / T) with the given
         uniforms (vnx_sample).  logits (B, V) (strided rows allowed);
         returns ids (B,) int64 (written into `out` when given), or with
-        return_all a dict with ids, flags and the fp32 row LSEs."""
+        return_all a dict with ids, flags and the fp32 row LSEs.  lse_out /
+        flags_out: (B,) contiguous tensors the row LSEs and flags are written
+        into (for vnx_spec_accept_draft_lse)."""
         dev = self._torch_device
         lg = self._rows2d(logits)
         B, V = lg.shape
@@ -276,8 +299,13 @@ class HipBackend(DeviceBackend):
             raise ValueError(f"uniforms must have {B} entries")
         thr = None if thresholds is None else _to_tensor(thresholds, dev, torch.float32).contiguous()
         ids = out if out is not None else torch.empty(B, dtype=torch.int64, device=dev)
-        flags = torch.empty(B, dtype=torch.uint8, device=dev) if return_all else None
-        lse = torch.empty(B, dtype=torch.float32, device=dev) if return_all else None
+        flags = flags_out if flags_out is not None else (
+            torch.empty(B, dtype=torch.uint8, device=dev) if return_all else None)
+        lse = lse_out if lse_out is not None else (
+            torch.empty(B, dtype=torch.float32, device=dev) if return_all else None)
+        for t_, dt_ in ((flags, torch.uint8), (lse, torch.float32)):
+            if t_ is not None and (t_.dtype != dt_ or t_.numel() != B or not t_.is_contiguous()):
+                raise ValueError("lse_out / flags_out must be contiguous (B,) float32 / uint8 tensors")
         ws = self._workspace(self._L.vnx_sample_workspace(B, V))
         _lib.check(self._L.vnx_sample(
             _ptr(lg), _LOGIT_DTYPES[lg.dtype], B, V, lg.stride(0), _ptr(u), float(temperature), _ptr(thr),
