@@ -21,9 +21,16 @@
 //      crosses the kernel boundary.
 // (Measured and dropped: the acceptance inside launch A by arrival counting
 // -- the counter round trip of 17K short workgroups slowed the streaming by
-// half; and a pipeline of row parts whose accept / mass / draw run beside
+// half; a pipeline of row parts whose accept / mass / draw run beside
 // the next part's streaming -- launch B is latency-bound, so a tail part
-// costs nearly as much as the whole.)
+// costs nearly as much as the whole; and one launch whose mass workgroups
+// follow the lse workgroups of a later row in the grid and poll for their
+// row's partials (posted as self-validating words, no atomics) -- at
+// B = 64, k = 8 it took 205-217 us per call in a graph against 205 us for
+// the two launches, because the mass workgroups hold CU slots while the
+// rows stream and the merged kernel runs one wave per SIMD fewer.  The mass
+// pass is VALU-bound: about 57 instructions per element of max(0, p - q),
+// two canonical exps among them.)
 // Probabilities that feed decisions use vnx_exp_canon(a - L32), a = RN(l/T),
 // L32 = RN32(row LSE), so the CPU checker reproduces them bit for bit.
 #include <algorithm>
