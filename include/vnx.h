@@ -344,6 +344,14 @@ int vnx_pack_w4_tiles(const uint8_t* wq, int64_t ldw, int64_t N, int64_t K, uint
 int vnx_gemv_w4_tiles(const void* x, int64_t ldx, const uint8_t* wt, const void* scales, int64_t lds, int64_t B,
                       int64_t N, int64_t K, float* y, int64_t ldy, void* stream);
 
+/* vnx_gemv_w4_tiles with the output dtype chosen: y_dtype VNX_F32 (the
+ * vnx_gemv_w4_tiles call) or VNX_BF16 (each fp32 sum rounded to nearest even
+ * once), for a draft head whose logits are kept in the model's bf16, as the
+ * reference's head Linear returns them in the module dtype
+ * (spark/src/base_model.py:207, :271). */
+int vnx_gemv_w4_tiles_out(const void* x, int64_t ldx, const uint8_t* wt, const void* scales, int64_t lds, int64_t B,
+                          int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
+
 /* vnx_gemv_w4 of a fused [gate; up] weight with SwiGLU fused (SwiGLUMLP,
  * packages/verse_torch/verse_torch/vnnn.py:779-807, on QuantizedLinear
  * projections): W (N, K) has its rows interleaved in blocks of 16, the 8 gate

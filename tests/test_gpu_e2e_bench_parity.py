@@ -104,8 +104,8 @@ def test_bench_workload_rounds_match_oracle(hip, bench_models, which):
         eng.step((ud, ua))
         torch.cuda.synchronize()
         c1 = eng.count.cpu().numpy()
-        p = eng.pbuf.cpu().numpy()
-        q = eng.qbuf.cpu().numpy()
+        p = eng.pbuf.float().cpu().numpy()   # (bf16 logits upcast exactly)
+        q = eng.qbuf.float().cpu().numpy()
         xs = eng.toks[:, 1:].cpu().numpy()
         alen = eng.last["accept_len"].cpu().numpy()
         oids = eng.last["out_ids"].cpu().numpy()

@@ -319,6 +319,21 @@ def test_gemv_w4_tiles_equals_row_layout(hip, N, K, B):
     assert np.all(err <= RTOL * mag + 1e-30), worst
 
 
+@pytest.mark.parametrize("N,K,B", [(1000, 512, 3), (40003, 1024, 32), (248320, 1024, 32)])
+def test_gemv_w4_tiles_bf16_out_is_rounded_fp32(hip, N, K, B):
+    """vnx_gemv_w4_tiles_out with bf16 output writes the fp32 output of the
+    same product rounded to nearest even, bit for bit (torch's fp32 -> bf16
+    cast rounds the same way)."""
+    p, s = _quantized("int4_g128", N, K, 11)
+    x16 = np.random.default_rng(N + 3 * B).normal(0, 1, (B, K)).astype(np.float16)
+    xt = torch.from_numpy(x16)
+    wt = hip.pack_w4_tiles(torch.from_numpy(p), K)
+    y32 = hip.gemv_w4_tiles(xt, wt, torch.from_numpy(s), N, K)
+    y16 = hip.gemv_w4_tiles(xt, wt, torch.from_numpy(s), N, K, out_dtype=torch.bfloat16)
+    assert y16.dtype == torch.bfloat16 and tuple(y16.shape) == (B, N)
+    assert torch.equal(y16.cpu().view(torch.int16), y32.to(torch.bfloat16).cpu().view(torch.int16))
+
+
 def test_gemv_w4_tiles_rejects_bad_shapes(hip):
     p, s = _quantized("int4_g128", 64, 256, 3)
     wt = hip.pack_w4_tiles(torch.from_numpy(p), 256)

@@ -80,6 +80,7 @@ SIGNATURES = {
     "vnx_w4_tiles_bytes": (_c_sz, [_c_i64, _c_i64]),
     "vnx_pack_w4_tiles": (_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
     "vnx_gemv_w4_tiles": (_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _vp]),
+    "vnx_gemv_w4_tiles_out": (_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _int, _c_i64, _vp]),
     "vnx_gemv_w4_swiglu": (_int, [_vp, _c_i64, _vp, _f32, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64,
                                   _int, _vp, _c_i64, _vp]),
     "vnx_gemv_w4_residual": (_int, [_vp, _c_i64, _vp, _c_i64, _vp, _int, _c_i64, _c_i64, _c_i64, _c_i64, _int,

@@ -56,6 +56,7 @@ struct QGemvParams {
   int gpg;             // 128-column groups per scale: G / 128
   float* y;            // (B, N), row pitch ldy
   int64_t ldy;
+  uint16_t* yb;        // k_qgemv_tiles with OB: bf16 bits (B, N), row pitch ldy (then y is unused)
   uint16_t* yh;        // SwiGLU output: fp16 bits (B, N/2), row pitch ldy (then y is unused)
   int rope_on;         // RoPE + cache store epilogue (ro; y and yh unused)
   int resid;           // residual epilogue: y += the product (fp32)
@@ -781,7 +782,7 @@ __device__ __forceinline__ u32x4 stage_perm_w4o(u32x4 v) {
 // load reaches past the workgroup's range (a streaming read measured 6.2-6.5
 // TB/s this way, against 4.7 with 64-byte row pieces and the ring's
 // overshoot into the next workgroup's tiles).
-template <int NC, int KG, int TP, int RS, int NW, int OCC>
+template <int NC, int KG, int TP, int RS, int NW, int OCC, bool OB = false>
 __global__ __launch_bounds__(NW * 64, OCC) void k_qgemv_tiles(QGemvParams p, int steps_per_wg) {
   static_assert(KG == 4 || KG == 8, "K of 512 or 1024");
   using SV = std::conditional_t<KG == 8, u32x4, uint2>;  // one row's KG fp16 scales
@@ -878,7 +879,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void k_qgemv_tiles(QGemvParams p, int
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t b = c * 16 + 4 * kq + j;
-          if (b < p.B) p.y[b * p.ldy + n] = yacc[tp][c][j];
+          if (b < p.B) {
+            if constexpr (OB) p.yb[b * p.ldy + n] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(yacc[tp][c][j]));
+            else p.y[b * p.ldy + n] = yacc[tp][c][j];
+          }
         }
     }
   };
@@ -1230,7 +1234,14 @@ int vnx_pack_w4_tiles(const uint8_t* wq, int64_t ldw, int64_t N, int64_t K, uint
 
 int vnx_gemv_w4_tiles(const void* x, int64_t ldx, const uint8_t* wt, const void* scales, int64_t lds, int64_t B,
                       int64_t N, int64_t K, float* y, int64_t ldy, void* stream) {
+  return vnx_gemv_w4_tiles_out(x, ldx, wt, scales, lds, B, N, K, y, VNX_F32, ldy, stream);
+}
+
+int vnx_gemv_w4_tiles_out(const void* x, int64_t ldx, const uint8_t* wt, const void* scales, int64_t lds, int64_t B,
+                          int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream) {
   if (!x || !wt || !scales || !y || B < 0 || N <= 0 || K <= 0) return VNX_ERR_INVALID_ARG;
+  if (y_dtype != VNX_F32 && y_dtype != VNX_BF16) return VNX_ERR_UNSUPPORTED;
+  const bool ob = y_dtype == VNX_BF16;
   if (K != 512 && K != 1024) return VNX_ERR_UNSUPPORTED;
   if (ldx < K || ldy < N || lds < K / kGK) return VNX_ERR_INVALID_ARG;
   // 16-byte loads of x and of the tiles; 8- or 16-byte loads of a row's scales
@@ -1243,7 +1254,9 @@ int vnx_gemv_w4_tiles(const void* x, int64_t ldx, const uint8_t* wt, const void*
     QGemvParams c{};
     c.x = static_cast<const uint16_t*>(x) + b0 * ldx; c.ldx = ldx; c.w = wt; c.sc = scales; c.lds = lds;
     c.sc_f16 = 1; c.B = min((int64_t)32, B - b0); c.N = N; c.K = K; c.G = kGK; c.gpg = 1;
-    c.y = y + b0 * ldy; c.ldy = ldy; c.row_off = b0;
+    if (ob) c.yb = static_cast<uint16_t*>(y) + b0 * ldy;
+    else c.y = static_cast<float*>(y) + b0 * ldy;
+    c.ldy = ldy; c.row_off = b0;
     const bool two = c.B > 16;
     // one tile per step; up to 16 batch rows: 4-wave workgroups, about 4
     // per CU over the launch; beyond: 8-wave workgroups (one staged copy of
@@ -1257,7 +1270,11 @@ int vnx_gemv_w4_tiles(const void* x, int64_t ldx, const uint8_t* wt, const void*
     const dim3 grid((unsigned)((steps + spw - 1) / spw));
     const size_t lds_bytes = (size_t)(two ? 2 : 1) * 16 * (K + kXPad) * 2;
 #define VNX_QTILES(NC, KG, RS, NW, OCC) \
-  hipLaunchKernelGGL((k_qgemv_tiles<NC, KG, TP, RS, NW, OCC>), grid, dim3(NW * 64), lds_bytes, s, c, (int)spw)
+  do { \
+    if (ob) hipLaunchKernelGGL((k_qgemv_tiles<NC, KG, TP, RS, NW, OCC, true>), grid, dim3(NW * 64), lds_bytes, s, c, \
+                               (int)spw); \
+    else hipLaunchKernelGGL((k_qgemv_tiles<NC, KG, TP, RS, NW, OCC>), grid, dim3(NW * 64), lds_bytes, s, c, (int)spw); \
+  } while (0)
     // (measured on the 248,320 x 1024 head, three weight copies: one column
     // block with a 2-step ring at 4 waves per SIMD, B = 1 26.9 us; two blocks
     // with 8-wave workgroups and no ring (128 VGPRs, 4 waves per SIMD) 37.1

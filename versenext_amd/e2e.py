@@ -62,7 +62,7 @@ class SpecDecodeEngine:
     its own lens[b] prefix rows)."""
 
     def __init__(self, target: CometSparkGPU, draft: CometSparkGPU, hip, k: int, temperature: float,
-                 seed: int = 31, use_graph: bool = False):
+                 seed: int = 31, use_graph: bool = False, logits_dtype: Optional[torch.dtype] = None):
         if target.B != draft.B:
             raise ValueError("target and draft caches must have the same batch")
         if target.cfg.vocab_size != draft.cfg.vocab_size:
@@ -81,8 +81,19 @@ class SpecDecodeEngine:
         self.gen = torch.Generator(device=dev)
         self.gen.manual_seed(int(seed))
         B, k = self.B, self.k
-        self.pbuf = torch.empty((B, k + 1, self.V), dtype=torch.float32, device=dev)
-        self.qbuf = torch.empty((B, k, self.V), dtype=torch.float32, device=dev)
+        # Logits of a sampled round stay in a bf16 target's dtype (the
+        # reference's head Linear returns them in the module dtype,
+        # spark/src/base_model.py:207): half the bytes for the heads to write
+        # and the draws and the acceptance to read.  Greedy rounds, fp32
+        # models and heads without a bf16 output keep fp32.
+        if logits_dtype is None:
+            logits_dtype = (torch.bfloat16 if not self.greedy and target.dtype == torch.bfloat16
+                            and target.head_writes_bf16() and draft.head_writes_bf16() else torch.float32)
+        if logits_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("logits_dtype must be torch.float32 or torch.bfloat16")
+        self.logits_dtype = logits_dtype
+        self.pbuf = torch.empty((B, k + 1, self.V), dtype=logits_dtype, device=dev)
+        self.qbuf = torch.empty((B, k, self.V), dtype=logits_dtype, device=dev)
         # both uniform arrays in one buffer (u_acc at a 256-byte boundary), so
         # a round's fill is one launch
         off = (k * B + 63) // 64 * 64

@@ -429,17 +429,21 @@ class HipBackend(DeviceBackend):
                                              ctypes.c_void_p(self._stream().cuda_stream)), "pack_w4_tiles")
         return out
 
-    def gemv_w4_tiles(self, x, wt, scales, N: int, K: int) -> torch.Tensor:
+    def gemv_w4_tiles(self, x, wt, scales, N: int, K: int, out_dtype=torch.float32) -> torch.Tensor:
         """y = x @ (q * s)^T from the tiled copy wt (pack_w4_tiles) and fp16
-        group-128 scales (N, K/128); returns (..., N) fp32 (vnx_gemv_w4_tiles)."""
+        group-128 scales (N, K/128); returns (..., N) fp32 (vnx_gemv_w4_tiles)
+        or bf16 (vnx_gemv_w4_tiles_out: the fp32 sums rounded once)."""
         dev = self._torch_device
+        if out_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("out_dtype must be torch.float32 or torch.bfloat16")
         sc = _to_tensor(scales, dev, torch.float16).reshape(N, -1).contiguous()
         lead = _to_tensor(x, dev).shape[:-1]
         x2 = self._acts(x, K)
         B = x2.shape[0]
-        y = torch.empty((B, N), dtype=torch.float32, device=dev)
-        _lib.check(self._L.vnx_gemv_w4_tiles(_ptr(x2), K, _ptr(wt), _ptr(sc), sc.stride(0), B, N, K, _ptr(y), N,
-                                             ctypes.c_void_p(self._stream().cuda_stream)), "gemv_w4_tiles")
+        y = torch.empty((B, N), dtype=out_dtype, device=dev)
+        _lib.check(self._L.vnx_gemv_w4_tiles_out(_ptr(x2), K, _ptr(wt), _ptr(sc), sc.stride(0), B, N, K, _ptr(y),
+                                                 _LOGIT_DTYPES[out_dtype], N,
+                                                 ctypes.c_void_p(self._stream().cuda_stream)), "gemv_w4_tiles")
         return y.reshape(*lead, N)
 
     def gemv_w8(self, x, wq, scale) -> torch.Tensor:

@@ -522,20 +522,24 @@ class _Linear:
 
     def __call__(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x (M, K); returns (M, N) in the compute dtype (dense) or fp32
-        (INT4 GEMV, written into `out` when given: an (M, N) fp32 view with
-        unit column stride)."""
+        (INT4 GEMV, written into `out` when given: an (M, N) view with unit
+        column stride, fp32, or bf16 for the tiled large-N product)."""
         M = x.shape[0]
         if self.int4 and M <= 64:
             x16 = x.to(torch.float16).contiguous()
             y = out if out is not None else torch.empty((M, self.N), dtype=torch.float32, device=x.device)
             L = self.hip._L
             if self.wt is not None:
-                _lib.check(L.vnx_gemv_w4_tiles(
+                if y.dtype not in (torch.float32, torch.bfloat16):
+                    raise ValueError("the INT4 head writes fp32 or bf16 logits")
+                _lib.check(L.vnx_gemv_w4_tiles_out(
                     ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wt.data_ptr()),
                     ctypes.c_void_p(self.sc.data_ptr()), self.sc.stride(0), M, self.N, self.K,
-                    ctypes.c_void_p(y.data_ptr()), y.stride(0),
-                    ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4_tiles")
+                    ctypes.c_void_p(y.data_ptr()), _lib.VNX_BF16 if y.dtype == torch.bfloat16 else _lib.VNX_F32,
+                    y.stride(0), ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)), "gemv_w4_tiles")
                 return y
+            if y.dtype != torch.float32:
+                raise ValueError("the INT4 GEMV writes fp32")
             _lib.check(L.vnx_gemv_w4(
                 ctypes.c_void_p(x16.data_ptr()), self.K, ctypes.c_void_p(self.wq.data_ptr()), self.wq.stride(0),
                 ctypes.c_void_p(self.sc.data_ptr()), _lib.VNX_F16, self.sc.stride(0), M, self.N, self.K, 128,
@@ -1080,11 +1084,19 @@ class CometSparkGPU:
         self._rms(x, pending, self.norm, out)
         return out.view(B, n, D)
 
+    def head_writes_bf16(self) -> bool:
+        """Whether logits(out=<bf16 tensor>) is written by the head itself:
+        the bf16 LM head (vnx_lm_head), or an INT4 head on its tiled copy
+        (vnx_gemv_w4_tiles_out)."""
+        if self.head is not None:
+            return self.head.wt is not None if self.head.int4 else self.dtype == torch.bfloat16
+        return self.dtype == torch.bfloat16
+
     def logits(self, hidden: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """(B, n, V) fp32 logits of the LM head (the tied embedding, or
-        head.weight when untied): vnx_lm_head (bf16, matrix cores) for the
-        verify pass, vnx_gemv_w4 for an INT4 draft, F.linear for an fp32
-        model."""
+        """(B, n, V) logits of the LM head (the tied embedding, or
+        head.weight when untied), fp32 or in out's dtype (bf16 where
+        head_writes_bf16()): vnx_lm_head (bf16, matrix cores) for the verify
+        pass, vnx_gemv_w4 for an INT4 draft, F.linear for an fp32 model."""
         B, n, D = hidden.shape
         V = self.cfg.vocab_size
         h2 = hidden.reshape(B * n, D)
