@@ -360,12 +360,34 @@ struct XgParams {
   int M, N, K, E;
   int nt, ng;
   int xcd_group;           // the workgroups of one expert on one XCD
+  int vec_out;             // rows of y 16-byte aligned (and N % 32 == 0 without SwiGLU): tiles leave through LDS
 };
+
+// Eight consecutive outputs of type OT from fp32 (16 bytes for bf16 / fp16,
+// 32 for fp32).
+template <int OT>
+__device__ __forceinline__ void vg_store8(char* y, int64_t off, const float (&v)[8]) {
+  if constexpr (OT == 0) {
+    float* d = reinterpret_cast<float*>(y) + off;
+    *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  } else if constexpr (OT == 1) {
+    __bf16 t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = static_cast<__bf16>(v[e]);
+    *reinterpret_cast<u32x4*>(reinterpret_cast<__bf16*>(y) + off) = __builtin_bit_cast(u32x4, t);
+  } else {
+    _Float16 t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = static_cast<_Float16>(v[e]);
+    *reinterpret_cast<u32x4*>(reinterpret_cast<_Float16*>(y) + off) = __builtin_bit_cast(u32x4, t);
+  }
+}
 
 constexpr int kXgRows = 128;  // rows per pass
 
 template <int OT, int EPI, int WN, bool ROUTE>
-__global__ __launch_bounds__(256) void k_xgemm(XgParams p) {
+__global__ __launch_bounds__(256, 2) void k_xgemm(XgParams p) {
   constexpr int WK = 4 / WN;
   constexpr int SLAB = WK * kXgRows * kVgRowB;       // staged X bytes per step
   constexpr int RED = (WK - 1) * WN * 4 * 64 * 64;   // K-split partial tiles
@@ -499,14 +521,40 @@ __global__ __launch_bounds__(256) void k_xgemm(XgParams p) {
         load_x(st + PDX, xv[j % PDX]);  // past the end: clamped re-reads, never used
         if (st * WK + wk < nch) {  // uniform per wave
           const char* xb = buf + wk * kXgRows * kVgRowB;
+          if constexpr (EPI == 1) {
+            // all four row tiles (rows past the count are zero and not stored);
+            // the A operands of k-step s + 1 are read while step s multiplies
+            u32x4 a[2][4];
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
+            for (int i = 0; i < 4; ++i) a[0][i] = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              // all four row tiles (rows past the count are zero and not stored)
-              const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s));
-              acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
+            for (int s = 0; s < 4; ++s) {
+              if (s < 3) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                  a[(s + 1) & 1][i] = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s + 1));
+              }
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a[s & 1][i]), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int s = 0; s < 3; ++s) {
+              __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+              __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+          } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                // all four row tiles (rows past the count are zero and not stored)
+                const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s));
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
+              }
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
         load_w(st + PDW, wv[j % PDW]);
@@ -528,7 +576,60 @@ __global__ __launch_bounds__(256) void k_xgemm(XgParams p) {
           for (int i = 0; i < 4; ++i)
             if (i < live) acc[i] += red[(((k - 1) * WN + wn) * 4 + i) * 64 + lane];
     }
-    if (wk == 0 && ni < p.nt) {
+    if (wk == 0 && ni < p.nt && p.vec_out) {
+      // Each 32 x 32 tile leaves through this wave's LDS tile (the X
+      // buffers and the reduction tiles are dead): lane (r, h) writes
+      // D[8ii + 4h + e][r], then lane l reads row l/2's columns
+      // 16 (l % 2) .. +16 and stores them as 16- or 32-byte pieces, so a row
+      // tile is one or two store instructions instead of 16 of 2-4 bytes.
+      constexpr int TP = 36;  // row pitch (floats): conflict-free writes, 16-byte aligned rows
+      static_assert(RED + WN * 32 * TP * 4 <= SM, "the transpose tiles fit the dead staging LDS");
+      float* tr = reinterpret_cast<float*>(smem + RED) + wn * 32 * TP;
+      const int tr_row = lane >> 1, tr_half = lane & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (i >= live) continue;
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tr[(8 * ii + 4 * h + e) * TP + r] = acc[i][4 * ii + e];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int j = m0 + i * 32 + tr_row;
+        const float* row = tr + tr_row * TP;
+        if constexpr (EPI == 0) {
+          // columns 16*half .. +16 of the tile
+          float v0[8], v1[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { v0[e] = row[16 * tr_half + e]; v1[e] = row[16 * tr_half + 8 + e]; }
+          if (j < cnt) {
+            const int64_t o = (int64_t)j * p.ldy + ni * 32 + 16 * tr_half;
+            vg_store8<OT>(ybase, o, v0);
+            vg_store8<OT>(ybase, o + 8, v1);
+          }
+        } else {
+          // hidden units ni*16 + 8*half .. +8: gates in columns 0-15, ups in 16-31
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float g = row[8 * tr_half + e], u = row[16 + 8 * tr_half + e];
+            v[e] = g / (1.0f + __expf(-g)) * u;
+          }
+          if (j < cnt) {
+            if (p.comb) {
+              const float cw = cwl[j - m0];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[e] *= cw;
+            }
+            vg_store8<OT>(ybase, (int64_t)j * p.ldy + ni * 16 + 8 * tr_half, v);
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    } else if (wk == 0 && ni < p.nt) {
       // lane holds D[row 8ii + 4h + e][col r] of row tile i in acc[i][4ii + e]
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -759,6 +860,7 @@ int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_
   p.ldx = ldx; p.sxb = sxb; p.swb = swb; p.ldy = ldy; p.syb = syb; p.ldc = ldc;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.E = experts;
   p.nt = (int)((N + 31) / 32);
+  p.vec_out = aligned16(y) && ldy % 8 == 0 && syb % 8 == 0 && (epilogue == VNX_EPI_SWIGLU || N % 32 == 0);
   // 4 N tiles per workgroup unless that leaves the CUs short of workgroups;
   // then 2 N tiles and K split over 2 waves each
   const int64_t cus = device_cus();
