@@ -49,6 +49,7 @@ struct VgParams {
   int64_t ldx, sxb, swb, ldy, syb, ldc;
   int M, N, K;             // N = rows of W
   int mt, nt, ng;          // 32-row tiles of M and N; N groups of WN tiles
+  int vec_out;             // N % 32 == 0, rows of y 16-byte aligned: tiles leave through LDS
   const float* xf;         // NX: the fp32 rows to normalize (x unused), pitch ldx
   const float* nw;         // NX: RMSNorm weight (K)
   float eps;
@@ -75,6 +76,27 @@ __device__ __forceinline__ void vg_store(char* y, int64_t off, float v) {
   }
 }
 
+// Eight consecutive outputs of type OT from fp32 (16 bytes for bf16 / fp16,
+// 32 for fp32).
+template <int OT>
+__device__ __forceinline__ void vg_store8(char* y, int64_t off, const float (&v)[8]) {
+  if constexpr (OT == 0) {
+    float* d = reinterpret_cast<float*>(y) + off;
+    *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  } else if constexpr (OT == 1) {
+    __bf16 t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = static_cast<__bf16>(v[e]);
+    *reinterpret_cast<u32x4*>(reinterpret_cast<__bf16*>(y) + off) = __builtin_bit_cast(u32x4, t);
+  } else {
+    _Float16 t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = static_cast<_Float16>(v[e]);
+    *reinterpret_cast<u32x4*>(reinterpret_cast<_Float16*>(y) + off) = __builtin_bit_cast(u32x4, t);
+  }
+}
+
 __device__ __forceinline__ bf16x8 as_b8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // LDS byte offset of 16-byte column c16 (0..7) of staged row r (0..31).
@@ -93,7 +115,12 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   constexpr int WK = 4 / WN;
   constexpr int SLAB = WK * 32 * kVgRowB;  // staged X bytes per pass (WK chunks)
   constexpr int RED = 3 * 64 * 64;         // K-split partial tiles
-  __shared__ __attribute__((aligned(16))) char smem[2 * SLAB > RED ? 2 * SLAB : RED];
+  constexpr int TP = 36;                   // row pitch (floats) of the output transpose tiles
+  constexpr int TR = WK > 1 ? RED : 0;     // their offset: past the partial tiles, else over the dead X buffers
+  constexpr int TRB = TR + WN * 32 * TP * 4;
+  constexpr int SMB = 2 * SLAB > TRB ? 2 * SLAB : TRB;
+  static_assert(SMB >= RED, "the partial tiles fit");
+  __shared__ __attribute__((aligned(16))) char smem[SMB];
   __shared__ float rsd[NX ? 32 : 1];
   __shared__ __attribute__((aligned(16))) float nws[NX ? kVgNormMaxK : 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -131,15 +158,28 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
   // EPI 3: the residual values this lane adds to load now, under the K loop
-  // (lane holds rows 8i + 4h + e of column ni*32 + r; only split 0 stores)
+  // (only split 0 stores).  vec_out: row m0 + lane/2, columns
+  // ni*32 + 16 (lane % 2) .. +16, the layout of the transposed tile; else
+  // rows 8i + 4h + e of column ni*32 + r, the accumulator layout.
   float old[EPI == 3 ? 16 : 1];
   if constexpr (EPI == 3) {
     if (wk == 0) {
-      const float* yf = reinterpret_cast<const float*>(p.y) + (int64_t)z * p.syb + min(ni * 32 + r, p.N - 1);
+      if (p.vec_out) {
+        const float* yf = reinterpret_cast<const float*>(p.y) + (int64_t)z * p.syb +
+                          (int64_t)min(m0 + (lane >> 1), p.M - 1) * p.ldy + nie * 32 + 16 * (lane & 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(yf + 4 * q);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) old[4 * i + e] = yf[(int64_t)min(m0 + 8 * i + 4 * h + e, p.M - 1) * p.ldy];
+          for (int e = 0; e < 4; ++e) old[4 * q + e] = v[e];
+        }
+      } else {
+        const float* yf = reinterpret_cast<const float*>(p.y) + (int64_t)z * p.syb + min(ni * 32 + r, p.N - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) old[4 * i + e] = yf[(int64_t)min(m0 + 8 * i + 4 * h + e, p.M - 1) * p.ldy];
+      }
     }
   }
   float ss = 0.0f;  // NX: sum of squares of this thread's values of row xr
@@ -257,6 +297,9 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
     }
   }
 
+  if constexpr (WK == 1 && !NX) {
+    if (p.vec_out) __syncthreads();  // the X buffers are dead before the transpose tiles reuse them
+  }
   if constexpr (NX) {
     // row xr's sum of squares over its 8 threads (consecutive lanes)
     ss += __shfl_xor(ss, 1);
@@ -285,6 +328,51 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
       for (int e = 0; e < 4; ++e) acc[4 * i + e] *= rsd[8 * i + 4 * h + e];
   }
   char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
+  if (p.vec_out) {
+    // The tile leaves through this wave's LDS tile: lane (r, h) writes
+    // D[8i + 4h + e][r], then lane l holds row l/2's columns 16 (l % 2) .. +16
+    // and stores them as 16- or 32-byte pieces: one or two store
+    // instructions per tile instead of 16 of 2-4 bytes.
+    float* tr = reinterpret_cast<float*>(smem + TR) + wn * 32 * TP;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tr[(8 * i + 4 * h + e) * TP + r] = acc[4 * i + e];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int hf = lane & 1, m = m0 + (lane >> 1);
+    const float* row = tr + (lane >> 1) * TP;
+    if (m >= p.M) return;
+    if constexpr (EPI == 3) {
+      float* yf = reinterpret_cast<float*>(ybase) + (int64_t)m * p.ldy + ni * 32 + 16 * hf;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(row + 16 * hf + 4 * q);
+        *reinterpret_cast<f32x4*>(yf + 4 * q) =
+            f32x4{old[4 * q] + v[0], old[4 * q + 1] + v[1], old[4 * q + 2] + v[2], old[4 * q + 3] + v[3]};
+      }
+    } else if constexpr (EPI == 0) {
+      float v0[8], v1[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { v0[e] = row[16 * hf + e]; v1[e] = row[16 * hf + 8 + e]; }
+      const int64_t o = (int64_t)m * p.ldy + ni * 32 + 16 * hf;
+      vg_store8<OT>(ybase, o, v0);
+      vg_store8<OT>(ybase, o + 8, v1);
+    } else {
+      // hidden units ni*16 + 8 (lane % 2) .. +8: gates in columns 0-15, ups in 16-31
+      const float cw = p.comb ? p.comb[(int64_t)m * p.ldc + z] : 1.0f;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float g = row[8 * hf + e], u = row[16 + 8 * hf + e];
+        v[e] = g / (1.0f + __expf(-g)) * u;
+        if (p.comb) v[e] *= cw;
+      }
+      vg_store8<OT>(ybase, (int64_t)m * p.ldy + ni * 16 + 8 * hf, v);
+    }
+    return;
+  }
   if constexpr (EPI == 3) {
     // the residual values were loaded before the K loop (rows past M re-read
     // row M-1 and are not stored)
@@ -362,27 +450,6 @@ struct XgParams {
   int xcd_group;           // the workgroups of one expert on one XCD
   int vec_out;             // rows of y 16-byte aligned (and N % 32 == 0 without SwiGLU): tiles leave through LDS
 };
-
-// Eight consecutive outputs of type OT from fp32 (16 bytes for bf16 / fp16,
-// 32 for fp32).
-template <int OT>
-__device__ __forceinline__ void vg_store8(char* y, int64_t off, const float (&v)[8]) {
-  if constexpr (OT == 0) {
-    float* d = reinterpret_cast<float*>(y) + off;
-    *reinterpret_cast<f32x4*>(d) = f32x4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(d + 4) = f32x4{v[4], v[5], v[6], v[7]};
-  } else if constexpr (OT == 1) {
-    __bf16 t[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = static_cast<__bf16>(v[e]);
-    *reinterpret_cast<u32x4*>(reinterpret_cast<__bf16*>(y) + off) = __builtin_bit_cast(u32x4, t);
-  } else {
-    _Float16 t[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) t[e] = static_cast<_Float16>(v[e]);
-    *reinterpret_cast<u32x4*>(reinterpret_cast<_Float16*>(y) + off) = __builtin_bit_cast(u32x4, t);
-  }
-}
 
 constexpr int kXgRows = 128;  // rows per pass
 
@@ -694,6 +761,7 @@ __global__ __launch_bounds__(256) void k_vpack(const uint16_t* w, int64_t ldw, i
 int vg_run(VgParams p, int batch, int epi, int y_dtype, bool nx, hipStream_t s) {
   p.mt = (int)((p.M + 31) / 32);
   p.nt = (int)((p.N + 31) / 32);
+  p.vec_out = aligned16(p.y) && p.ldy % 8 == 0 && p.syb % 8 == 0 && p.N % 32 == 0;
   // N tiles per workgroup: the most that still keep about three quarters of
   // the CUs busy (fewer tiles per workgroup split K over its waves instead)
   const int64_t cus = device_cus();
