@@ -454,7 +454,7 @@ struct XgParams {
 constexpr int kXgRows = 128;  // rows per pass
 
 template <int OT, int EPI, int WN, bool ROUTE>
-__global__ __launch_bounds__(256, 2) void k_xgemm(XgParams p) {
+__global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
   constexpr int WK = 4 / WN;
   constexpr int SLAB = WK * kXgRows * kVgRowB;       // staged X bytes per step
   constexpr int RED = (WK - 1) * WN * 4 * 64 * 64;   // K-split partial tiles
@@ -521,15 +521,15 @@ __global__ __launch_bounds__(256, 2) void k_xgemm(XgParams p) {
   // than one pass adds workgroups, not time to its workgroups' critical path
   for (int m0 = blockIdx.y * kXgRows; m0 < cnt; m0 += gridDim.y * kXgRows) {
     const int live = min(4, (cnt - m0 + 31) / 32);  // row tiles of this pass
+    // rows past the count re-read row cnt - 1: their outputs are computed
+    // from finite values and never stored (MFMA rows are independent)
     const uint16_t* xrow[4];
-    uint32_t keep[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int j = m0 + xr + 32 * q;
       const int jc = min(j, cnt - 1);
       if constexpr (ROUTE) xrow[q] = p.x + (int64_t)rl[jc] * p.ldx + xc * 8;
       else xrow[q] = p.x + z * p.sxb + (int64_t)jc * p.ldx + xc * 8;
-      keep[q] = j < cnt ? 0xFFFFFFFFu : 0u;
     }
     if (EPI == 1 && tid < kXgRows) {
       // read before the epilogue: the K loop's barriers order it
@@ -549,10 +549,14 @@ __global__ __launch_bounds__(256, 2) void k_xgemm(XgParams p) {
     // the barrier; a W slot is reloaded only after this step's MFMAs have
     // read it (no register rotation, so nothing in flight has to be waited
     // for at the loop edge).
-    // Both shapes keep two workgroups per CU (<= 256 registers a lane), so
-    // the workgroups of a second row pass run beside the first ones rather
-    // than after them; one workgroup per CU with deeper rings measured slower.
-    constexpr int PDW = WN == 4 ? 3 : 4, PDX = WN == 4 ? 3 : 2;
+    // The gate-up shape (WN 4) keeps three workgroups per CU (<= 168
+    // registers a lane, hence the shallow rings): at the MoD shapes its 16 x
+    // 42 workgroups then all run at once, where two per CU left a second
+    // wave of 160 (43.9 against 49.5 us).  The down shape (K split over two
+    // waves) keeps two per CU, so the workgroups of a second row pass run
+    // beside the first ones; one workgroup per CU with deeper rings measured
+    // slower.
+    constexpr int PDW = WN == 4 ? 2 : 4, PDX = WN == 4 ? 1 : 2;
     constexpr int UN = PDW > PDX ? PDW : PDX;  // loop unroll: a multiple of both
     static_assert(UN % PDW == 0 && UN % PDX == 0, "ring depths must divide the unroll");
     u32x4 xv[PDX][WK][4], wv[PDW][4];
@@ -583,45 +587,19 @@ __global__ __launch_bounds__(256, 2) void k_xgemm(XgParams p) {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             *reinterpret_cast<u32x4*>(buf + c * kXgRows * kVgRowB + xs_off(xr + 32 * q, xc)) =
-                xv[j % PDX][c][q] & keep[q];
+                xv[j % PDX][c][q];
         __syncthreads();  // step st's X is staged; the other buffer was read before it
         load_x(st + PDX, xv[j % PDX]);  // past the end: clamped re-reads, never used
         if (st * WK + wk < nch) {  // uniform per wave
           const char* xb = buf + wk * kXgRows * kVgRowB;
-          if constexpr (EPI == 1) {
-            // all four row tiles (rows past the count are zero and not stored);
-            // the A operands of k-step s + 1 are read while step s multiplies
-            u32x4 a[2][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[0][i] = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4));
+          for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              if (s < 3) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                  a[(s + 1) & 1][i] = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s + 1));
-              }
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a[s & 1][i]), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+              // all four row tiles (rows past the count are not stored)
+              const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s));
+              acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-            for (int s = 0; s < 3; ++s) {
-              __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-              __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-          } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                // all four row tiles (rows past the count are zero and not stored)
-                const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s));
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
-              }
-          }
         }
         __builtin_amdgcn_sched_barrier(0);
         load_w(st + PDW, wv[j % PDW]);
