@@ -423,12 +423,13 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
 // Routed MoD expert products (vnx_expert_gemm_bf16).  Expert z multiplies only
 // the rows routed to it (about top_k / E of them), and every expert's weight
 // should stream from HBM once, so a workgroup owns WN adjacent 32-row tiles
-// of W_z and a pass of up to 128 of the expert's rows (four MFMA row tiles
-// per wave, the W operand reused across them from registers): at the usual
-// <= 128 rows per expert one workgroup covers them all, and the workgroups of
-// further passes (grid.y) exit at once.  Its 4 waves are WN (N tiles) x WK
-// (K splits), as in k_vgemm.  X (128 rows x WK chunks per step) is staged
-// through LDS like k_vgemm's, the rows gathered through the row list.
+// of W_z and a pass of up to 128 (gate-up) or 160 (down) of the expert's
+// rows (four or five MFMA row tiles per wave, the W operand reused across
+// them from registers): when one pass covers an expert's rows, the
+// workgroups of further passes (grid.y) exit at once.  Its 4 waves are WN
+// (N tiles) x WK (K splits), as in k_vgemm.  X (a pass's rows x WK chunks
+// per step) is staged through LDS like k_vgemm's, the rows gathered through
+// the row list.
 //
 // ROUTE: the row list of expert z is { m : comb[m*ldc + z] != 0 }, ascending;
 // each workgroup builds it in LDS from comb (M <= 256: one ballot per wave),
@@ -451,17 +452,21 @@ struct XgParams {
   int vec_out;             // rows of y 16-byte aligned (and N % 32 == 0 without SwiGLU): tiles leave through LDS
 };
 
-constexpr int kXgRows = 128;  // rows per pass
+// MFMA row tiles of 32 per pass: 4 for the gate-up shape (WN 4), 5 for the
+// down shape (a pass of 160 rows)
+constexpr int xg_row_tiles(int wn) { return wn == 4 ? 4 : 5; }
 
 template <int OT, int EPI, int WN, bool ROUTE>
 __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
   constexpr int WK = 4 / WN;
-  constexpr int SLAB = WK * kXgRows * kVgRowB;       // staged X bytes per step
-  constexpr int RED = (WK - 1) * WN * 4 * 64 * 64;   // K-split partial tiles
+  constexpr int RT = xg_row_tiles(WN);
+  constexpr int ROWS = 32 * RT;                       // rows per pass
+  constexpr int SLAB = WK * ROWS * kVgRowB;           // staged X bytes per step
+  constexpr int RED = (WK - 1) * WN * RT * 64 * 64;   // K-split partial tiles
   constexpr int SM = 2 * SLAB > RED ? 2 * SLAB : RED;
   __shared__ __attribute__((aligned(16))) char smem[SM];
   __shared__ int rl[256];
-  __shared__ float cwl[kXgRows];  // SwiGLU weights of the pass's rows
+  __shared__ float cwl[ROWS];  // SwiGLU weights of the pass's rows
   __shared__ unsigned long long wmask[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WN, wk = wave / WN;
@@ -517,28 +522,28 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
   const uint16_t* wt = p.w + z * p.swb + (int64_t)nie * nch * 2048 + lane * 8;
   char* ybase = static_cast<char*>(p.y) + (int64_t)z * p.syb * (OT == 0 ? 4 : 2);
 
-  // passes of 128 rows are dealt over grid.y, so an expert with more rows
+  // passes of ROWS rows are dealt over grid.y, so an expert with more rows
   // than one pass adds workgroups, not time to its workgroups' critical path
-  for (int m0 = blockIdx.y * kXgRows; m0 < cnt; m0 += gridDim.y * kXgRows) {
-    const int live = min(4, (cnt - m0 + 31) / 32);  // row tiles of this pass
+  for (int m0 = blockIdx.y * ROWS; m0 < cnt; m0 += gridDim.y * ROWS) {
+    const int live = min(RT, (cnt - m0 + 31) / 32);  // row tiles of this pass
     // rows past the count re-read row cnt - 1: their outputs are computed
     // from finite values and never stored (MFMA rows are independent)
-    const uint16_t* xrow[4];
+    const uint16_t* xrow[RT];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < RT; ++q) {
       const int j = m0 + xr + 32 * q;
       const int jc = min(j, cnt - 1);
       if constexpr (ROUTE) xrow[q] = p.x + (int64_t)rl[jc] * p.ldx + xc * 8;
       else xrow[q] = p.x + z * p.sxb + (int64_t)jc * p.ldx + xc * 8;
     }
-    if (EPI == 1 && tid < kXgRows) {
+    if (EPI == 1 && tid < ROWS) {
       // read before the epilogue: the K loop's barriers order it
       const int j = m0 + tid;
       cwl[tid] = p.comb && j < cnt ? p.comb[(int64_t)(ROUTE ? rl[j] : j) * p.ldc + z] : 1.0f;
     }
-    f32x16 acc[4];
+    f32x16 acc[RT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
 
@@ -553,19 +558,21 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
     // registers a lane, hence the shallow rings): at the MoD shapes its 16 x
     // 42 workgroups then all run at once, where two per CU left a second
     // wave of 160 (43.9 against 49.5 us).  The down shape (K split over two
-    // waves) keeps two per CU, so the workgroups of a second row pass run
-    // beside the first ones; one workgroup per CU with deeper rings measured
-    // slower.
-    constexpr int PDW = WN == 4 ? 2 : 4, PDX = WN == 4 ? 1 : 2;
+    // waves) keeps two per CU with passes of 160 rows: the routed counts of
+    // the config-5 target reach 140-154 rows for 2-4 of the 16 experts, and a
+    // second pass re-reads such an expert's weights (30.9 against 38.9 us at
+    // those counts, 30.7 against 27.3 when every expert has <= 128 rows);
+    // one workgroup per CU with deeper rings measured slower.
+    constexpr int PDW = WN == 4 ? 2 : 3, PDX = 1;
     constexpr int UN = PDW > PDX ? PDW : PDX;  // loop unroll: a multiple of both
     static_assert(UN % PDW == 0 && UN % PDX == 0, "ring depths must divide the unroll");
-    u32x4 xv[PDX][WK][4], wv[PDW][4];
-    auto load_x = [&](int st, u32x4 (&xs)[WK][4]) {
+    u32x4 xv[PDX][WK][RT], wv[PDW][4];
+    auto load_x = [&](int st, u32x4 (&xs)[WK][RT]) {
 #pragma unroll
       for (int j = 0; j < WK; ++j) {
         const int c = min(st * WK + j, nch - 1);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xs[j][q] = *reinterpret_cast<const u32x4*>(xrow[q] + c * kVgChunk);
+        for (int q = 0; q < RT; ++q) xs[j][q] = *reinterpret_cast<const u32x4*>(xrow[q] + c * kVgChunk);
       }
     };
     auto load_w = [&](int st, u32x4 (&ws)[4]) {
@@ -585,18 +592,17 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
 #pragma unroll
         for (int c = 0; c < WK; ++c)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<u32x4*>(buf + c * kXgRows * kVgRowB + xs_off(xr + 32 * q, xc)) =
-                xv[j % PDX][c][q];
+          for (int q = 0; q < RT; ++q)
+            *reinterpret_cast<u32x4*>(buf + c * ROWS * kVgRowB + xs_off(xr + 32 * q, xc)) = xv[j % PDX][c][q];
         __syncthreads();  // step st's X is staged; the other buffer was read before it
         load_x(st + PDX, xv[j % PDX]);  // past the end: clamped re-reads, never used
         if (st * WK + wk < nch) {  // uniform per wave
-          const char* xb = buf + wk * kXgRows * kVgRowB;
+          const char* xb = buf + wk * ROWS * kVgRowB;
 #pragma unroll
           for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              // all four row tiles (rows past the count are not stored)
+            for (int i = 0; i < RT; ++i) {
+              // every row tile (rows past the count are not stored)
               const u32x4 a = *reinterpret_cast<const u32x4*>(xb + xs_off(i * 32 + r, h * 4 + s));
               acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(wv[j % PDW][s]), acc[i], 0, 0, 0);
             }
@@ -611,15 +617,15 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
       f32x16* red = reinterpret_cast<f32x16*>(smem);
       if (wk > 0)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (i < live) red[(((wk - 1) * WN + wn) * 4 + i) * 64 + lane] = acc[i];
+        for (int i = 0; i < RT; ++i)
+          if (i < live) red[(((wk - 1) * WN + wn) * RT + i) * 64 + lane] = acc[i];
       __syncthreads();
       if (wk == 0)
 #pragma unroll
         for (int k = 1; k < WK; ++k)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (i < live) acc[i] += red[(((k - 1) * WN + wn) * 4 + i) * 64 + lane];
+          for (int i = 0; i < RT; ++i)
+            if (i < live) acc[i] += red[(((k - 1) * WN + wn) * RT + i) * 64 + lane];
     }
     if (wk == 0 && ni < p.nt && p.vec_out) {
       // Each 32 x 32 tile leaves through this wave's LDS tile (the X
@@ -632,7 +638,7 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
       float* tr = reinterpret_cast<float*>(smem + RED) + wn * 32 * TP;
       const int tr_row = lane >> 1, tr_half = lane & 1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < RT; ++i) {
         if (i >= live) continue;
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
@@ -677,7 +683,7 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
     } else if (wk == 0 && ni < p.nt) {
       // lane holds D[row 8ii + 4h + e][col r] of row tile i in acc[i][4ii + e]
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < RT; ++i) {
         if (i >= live) continue;
         if constexpr (EPI == 0) {
           const int n = ni * 32 + r;
@@ -916,7 +922,7 @@ int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_
   // expert's workgroups on one XCD; the routed gate-up keeps them spread
   p.xcd_group = (experts % 8 == 0 && route == 0) ? 1 : 0;
   const int64_t wgs = (int64_t)experts * p.ng;
-  const int64_t passes = (M + kXgRows - 1) / kXgRows;
+  const int64_t passes = (M + 32 * xg_row_tiles(wn) - 1) / (32 * xg_row_tiles(wn));
   if (wgs >= INT32_MAX || passes > 65535) return VNX_ERR_UNSUPPORTED;
   const dim3 grid((unsigned)wgs, (unsigned)passes);
   hipStream_t s = static_cast<hipStream_t>(stream);
