@@ -791,8 +791,9 @@ int vnx_gemm_bf16_residual(const void* x, int64_t ldx, const void* w_packed, int
  * route == 0: X_z[j] = x[z*sxb + j*ldx], n_z = counts[z] (counts NULL: M),
  *   rows / slots unused.
  * W_z packed by vnx_pack_bf16 at w_packed + z*swb elements; K multiple of
- * 64.  Each element's summation order depends on the shapes only, not on
- * the row lists (deterministic). */
+ * 64; M * ldx * 2 < 2^31 (VNX_ERR_UNSUPPORTED otherwise).  Each element's
+ * summation order depends on the shapes only, not on the row lists
+ * (deterministic). */
 int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_packed, int64_t swb, int64_t M,
                          int64_t N, int64_t K, int experts, int epilogue, const float* comb, int64_t ldc, int route,
                          int32_t* rows, int32_t* counts, int32_t* slots, void* y, int y_dtype, int64_t ldy,

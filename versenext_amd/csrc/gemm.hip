@@ -528,13 +528,17 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
     const int live = min(RT, (cnt - m0 + 31) / 32);  // row tiles of this pass
     // rows past the count re-read row cnt - 1: their outputs are computed
     // from finite values and never stored (MFMA rows are independent)
-    const uint16_t* xrow[RT];
+    // X through a buffer resource over the expert's M rows: 32-bit byte
+    // offsets per row (the host bounds M * ldx), the chunk offset a scalar
+    const uint16_t* xbase = ROUTE ? p.x : p.x + z * p.sxb;
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(xbase), (short)0, (int)((int64_t)p.M * p.ldx * 2), 0x00020000);
+    uint32_t xoff[RT];
 #pragma unroll
     for (int q = 0; q < RT; ++q) {
       const int j = m0 + xr + 32 * q;
       const int jc = min(j, cnt - 1);
-      if constexpr (ROUTE) xrow[q] = p.x + (int64_t)rl[jc] * p.ldx + xc * 8;
-      else xrow[q] = p.x + z * p.sxb + (int64_t)jc * p.ldx + xc * 8;
+      xoff[q] = (uint32_t)(((ROUTE ? rl[jc] : jc) * (int)p.ldx + xc * 8) * 2);
     }
     if (EPI == 1 && tid < ROWS) {
       // read before the epilogue: the K loop's barriers order it
@@ -572,7 +576,8 @@ __global__ __launch_bounds__(256, WN == 4 ? 3 : 2) void k_xgemm(XgParams p) {
       for (int j = 0; j < WK; ++j) {
         const int c = min(st * WK + j, nch - 1);
 #pragma unroll
-        for (int q = 0; q < RT; ++q) xs[j][q] = *reinterpret_cast<const u32x4*>(xrow[q] + c * kVgChunk);
+        for (int q = 0; q < RT; ++q)
+          xs[j][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[q], c * kVgChunk * 2, 0));
       }
     };
     auto load_w = [&](int st, u32x4 (&ws)[4]) {
@@ -906,6 +911,7 @@ int vnx_expert_gemm_bf16(const void* x, int64_t ldx, int64_t sxb, const void* w_
   if (K % kVgChunk || ldx % 8 || sxb % 8 || swb % 8 || !aligned16(x) || !aligned16(w_packed))
     return VNX_ERR_UNSUPPORTED;
   if (M >= INT32_MAX || N >= INT32_MAX || K >= INT32_MAX) return VNX_ERR_UNSUPPORTED;
+  if (ldx >= INT32_MAX || M * ldx * 2 >= INT32_MAX) return VNX_ERR_UNSUPPORTED;  // 32-bit buffer offsets of x
   XgParams p{};
   p.x = static_cast<const uint16_t*>(x); p.w = static_cast<const uint16_t*>(w_packed); p.y = y; p.comb = comb;
   p.rows = rows; p.counts = counts; p.slots = slots;
