@@ -149,9 +149,10 @@ constexpr bool ta_variant_ok(int D, int QT, int NW, bool PF) {
 
 // One workgroup of NW waves per (b, kv head, query group, key split).  PF:
 // issue the loads of a wave's next key step before the current step's math
-// (more registers; for grids of at most one workgroup per CU).
+// (more registers: with d = 64 they fit two 4-wave workgroups per CU, <= 256
+// a lane, so grids of up to two workgroups per CU keep every wave resident).
 template <int D, int QT, int OT, int NW, bool PF, bool EXT>
-__global__ __launch_bounds__(NW * 64) void k_tree_attn(TreeAttnParams p) {
+__global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(TreeAttnParams p) {
   constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
   constexpr int DT = D / 16;          // 16-wide dimension tiles of O
   constexpr int R = TaSmem<D, QT, NW>::R;
@@ -604,9 +605,12 @@ static size_t ta_ws_bytes(const TaPlan& pl, int B, int H, int N, int d) {
 
 // Waves per workgroup (5: 4 with prefetch).  A grid of at most one workgroup
 // per CU gets 8 waves (16 when 8 does not fit the query tile), so each wave
-// walks few key steps and more loads are in flight per CU; larger grids keep
-// 4 waves.  force (the args' force_waves: 4, 5, 8, 16) overrides the choice
-// where the shape fits.  EXT launches (window / ALiBi) have 4 or 8 waves.
+// walks few key steps and more loads are in flight per CU; up to two per CU,
+// 8 waves where the query tile fits them, else (d = 64) 4 waves with the
+// next key step's loads in flight (config 3: 38.5-41.1 against 41.6-42.0 us
+// for 4 waves without, on two boxes); larger grids keep 4 waves.  force (the args'
+// force_waves: 4, 5, 8, 16) overrides the choice where the shape fits.  EXT
+// launches (window / ALiBi) have 4 or 8 waves.
 static int ta_waves(int D, int QT, int64_t nwg, int force, bool ext) {
   auto ok = [&](int nw) {
     if (ext && nw != 4 && nw != 8) return false;
@@ -620,7 +624,10 @@ static int ta_waves(int D, int QT, int64_t nwg, int force, bool ext) {
     if (ok(16)) return 16;
     return 5;
   }
-  if (nwg <= 2 * cus && ok(8)) return 8;
+  if (nwg <= 2 * cus) {
+    if (ok(8)) return 8;
+    if (D == 64 && ok(5)) return 5;
+  }
   return 4;
 }
 
