@@ -522,7 +522,8 @@ typedef struct vnx_tree_attn_args {
   const float* alibi_slopes;
   int alibi_max_keys;
   /* Tuning: force_splits >= 1 fixes the key splits, force_waves (4, 5 = 4
-   * with prefetch, 8, 16) the workgroup shape where the query tile fits;
+   * with prefetch, 8, 9 = 8 with prefetch, 16) the workgroup shape where the
+   * query tile fits;
    * 0: the launch plan's choice.  (Size the workspace with
    * vnx_tree_attn_workspace_args when forcing splits.) */
   int force_splits;

@@ -140,11 +140,11 @@ def test_splits_cover_one_and_many(hip):
     _run(hip, 1, 1, 1, 40, 8192, 64, seed=6)
 
 
-@pytest.mark.parametrize("waves", ["4", "5", "8", "16"])
+@pytest.mark.parametrize("waves", ["4", "5", "8", "9", "16"])
 @pytest.mark.parametrize("B,H,Hkv,N,Tp,d", [(8, 16, 8, 1, 640, 64), (8, 16, 8, 7, 301, 64),
                                             (2, 16, 16, 40, 700, 64), (2, 4, 2, 20, 300, 128)])
 def test_workgroup_shapes(hip, waves, B, H, Hkv, N, Tp, d):
-    """Every workgroup shape (4 waves, 4 with prefetch, 8, 16; a shape that
+    """Every workgroup shape (4 waves, 4 with prefetch, 8, 8 with prefetch, 16; a shape that
     does not fit the query tile falls back to the default) on decode-like
     (N 1, 7) and verify-like (N 40) calls."""
     par = T.chain(N) if N < 40 else None

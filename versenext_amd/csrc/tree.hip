@@ -94,8 +94,12 @@ struct TreeAttnParams {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// 16 bytes from device memory, always as a global (not flat) load: flat
+// loads also count against the LDS counter, which serialises the waits of a
+// key loop that mixes them with LDS traffic.
 __device__ __forceinline__ u32x4 ldg16(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+  typedef const __attribute__((address_space(1))) u32x4* gptr;
+  return *(gptr)(p);
 }
 
 // exp2 on the transcendental unit (v_exp_f32); exp2(-inf) = 0.
@@ -139,30 +143,38 @@ struct TaSmem {
 };
 
 // The (D, QT, NW, PF) variants that fit: at most 64 KB of LDS, the VGPRs of
-// NW waves per CU (16 waves: 128 each), and the prefetch copy only at 4 waves.
-constexpr bool ta_variant_ok(int D, int QT, int NW, bool PF) {
-  if (PF && NW != 4) return false;
+// NW waves per CU (16 waves: 128 each), and prefetch rings only at 4 waves
+// (PF 2 for d = 64 and 128, and at 8 waves for d = 64; the deeper rings, one
+// workgroup per CU, d = 64).
+constexpr bool ta_variant_ok(int D, int QT, int NW, int PF) {
+  if (PF && NW != 4 && NW != 8) return false;
+  if (PF > 2 && (D != 64 || NW != 4)) return false;
+  if (PF && NW == 8) return D == 64 && QT <= 4;  // merge area up to 135 KB of the 160 KB LDS
   if (D == 64) return NW == 4 ? QT <= 4 : NW == 8 ? QT <= 2 : NW == 16 ? QT == 1 : false;
   if (D == 128) return NW == 4 ? QT <= 2 : NW == 8 ? QT == 1 : false;
   return false;
 }
 
-// One workgroup of NW waves per (b, kv head, query group, key split).  PF:
-// issue the loads of a wave's next key step before the current step's math
-// (more registers: with d = 64 they fit two 4-wave workgroups per CU, <= 256
-// a lane, so grids of up to two workgroups per CU keep every wave resident).
-template <int D, int QT, int OT, int NW, bool PF, bool EXT>
-__global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(TreeAttnParams p) {
+// One workgroup of NW waves per (b, kv head, query group, key split).  PF > 0:
+// a ring of PF register sets, the loads of a wave's next PF - 1 key steps in
+// flight during a step's math.  PF 2 with d = 64 fits two 4-wave workgroups
+// per CU (<= 256 registers a lane), so grids of up to two workgroups per CU
+// keep every wave resident; deeper rings take one workgroup per CU (up to
+// 512 registers a lane, VGPRs and AGPRs) and keep more bytes in flight.
+template <int D, int QT, int OT, int NW, int PF, bool EXT>
+__global__ __launch_bounds__(NW * 64, (PF == 2 && D == 64 && NW == 4) ? 2 : 1) void k_tree_attn(TreeAttnParams p) {
   constexpr int KS = D / 32;          // MFMA k-steps over the head dimension
   constexpr int DT = D / 16;          // 16-wide dimension tiles of O
   constexpr int R = TaSmem<D, QT, NW>::R;
   constexpr int LPR = D / 8;          // lanes per 16-byte-chunked row
   constexpr int VLD = D / 16;         // 16-byte V loads per lane per 32-key step
+  static_assert(PF == 0 || (PF >= 2 && PF <= 6), "prefetch ring of 2-6 register sets");
   __shared__ __align__(16) char smem[TaSmem<D, QT, NW>::bytes];
   uint16_t* s_q = reinterpret_cast<uint16_t*>(smem);
   uint16_t* s_v = reinterpret_cast<uint16_t*>(smem + TaSmem<D, QT, NW>::q_bytes);
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, col = lane & 15,
+            grp = lane >> 4;
   int bid = blockIdx.x;
   const int s = bid % p.S;
   bid /= p.S;
@@ -176,7 +188,7 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
   if (p.qkv) {
     // qkv mode.  Element pairs (j, j + D/2) of a head rotate together: item
     // (r, c) takes 8-dim chunk c < LPR/2 and its partner chunk c + LPR/2.
-    const int tpb = min(max(p.tp_batch[b], 0), p.Tp);
+    const int tpb = __builtin_amdgcn_readfirstlane(min(max(p.tp_batch[b], 0), p.Tp));
     auto rot8 = [&](const uint16_t* src, int64_t pos, int c, u32x4& lo, u32x4& hi) {
       const u32x4 a = ldg16(src + c * 8), z = ldg16(src + D / 2 + c * 8);
       if (!p.rope) { lo = a; hi = z; return; }
@@ -267,6 +279,9 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
   // ALiBi): segment 1's keys again.
   int Tp = p.Tp;
   if (p.tp_batch) Tp = min(max(p.tp_batch[b], 0), p.Tp);
+  // One value per workgroup, read by a vector load: made wave-uniform, so the
+  // key bounds and step tests below are scalar.
+  Tp = __builtin_amdgcn_readfirstlane(Tp);
   // The segment this wave walks: split 0 gives its last W2 waves the second
   // segment and, with ALiBi, the W3 before them the third (wave-uniform, so
   // the selects below are scalar).
@@ -336,34 +351,61 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
   // One step's loads: K fragments (A rows = keys base + kt*16 + col, k = dims
   // ks*32 + grp*8 .. +8) and V rows, coalesced (load v covers keys
   // v*(64/LPR) + lane/LPR, chunk lane%LPR).
+  // Lane offsets of a step whose keys are all cache rows (the usual step):
+  // then every load is a uniform row pointer plus one of these.
+  const bool small_stride = csr <= (1 << 24);
+  int koff[2], voff[VLD];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) koff[kt] = (kt * 16 + col) * (int)csr + grp * 8;
+#pragma unroll
+  for (int v = 0; v < VLD; ++v) voff[v] = (v * (64 / LPR) + lane / LPR) * (int)csr + (lane % LPR) * 8;
+  // The two paths choose row addresses only; the loads after them are the
+  // same instructions whichever path ran, so the wait counts stay exact.
   auto load_step = [&](int base, u32x4 (&kf)[2][KS], u32x4 (&vv)[VLD]) {
+    const uint16_t* kr[2];
+    const uint16_t* vr[VLD];
+    if (base + 32 <= Tpe && small_stride) {
+      const uint16_t* kb = kc + cbase + base * csr;
+      const uint16_t* vb = vc + cbase + base * csr;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const uint16_t* r = krow(base + kt * 16 + col, kc, p.kt);
+      for (int kt = 0; kt < 2; ++kt) kr[kt] = kb + koff[kt];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = ldg16(r + ks * 32 + grp * 8);
-    }
-#pragma unroll
-    for (int v = 0; v < VLD; ++v) {
-      const int key = base + v * (64 / LPR) + lane / LPR;
-      vv[v] = ldg16(krow(key, vc, p.vt) + (lane % LPR) * 8);
-      if (key >= k_hi) vv[v] = u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  u32x4 kf[2][KS], vv[VLD], kfn[2][KS], vvn[VLD];
-  if (PF && wi < nsteps) load_step(k_lo + wi * 32, kf, vv);
-  for (int st = wi; st < nsteps; st += nws) {
-    const int base = k_lo + st * 32;
-    const bool more = PF && st + nws < nsteps;
-    if constexpr (PF) {
-      if (more) load_step(base + nws * 32, kfn, vvn);
+      for (int v = 0; v < VLD; ++v) vr[v] = vb + voff[v];
     } else {
-      load_step(base, kf, vv);
-    }
-    wave_lds_sync();  // previous step's V^T reads are done
 #pragma unroll
-    for (int v = 0; v < VLD; ++v)
-      *reinterpret_cast<u32x4*>(vt_w + (v * (64 / LPR) + lane / LPR) * R + (lane % LPR) * 8) = vv[v];
+      for (int kt = 0; kt < 2; ++kt) kr[kt] = krow(base + kt * 16 + col, kc, p.kt) + grp * 8;
+#pragma unroll
+      for (int v = 0; v < VLD; ++v) vr[v] = krow(base + v * (64 / LPR) + lane / LPR, vc, p.vt) + (lane % LPR) * 8;
+    }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = ldg16(kr[kt] + ks * 32);
+#pragma unroll
+    for (int v = 0; v < VLD; ++v) vv[v] = ldg16(vr[v]);
+  };
+
+  // One step's math on its loaded K fragments and V rows.
+  auto step = [&](const int base, const u32x4 (&kf)[2][KS], const u32x4 (&vv)[VLD]) {
+    // masks: the step reaches tree keys or the end, or keys below a window
+    const bool edge = base + 32 > Tpe || (EXT && base < wlim);
+    wave_lds_sync();  // previous step's V^T reads are done
+    // V rows of keys past the split enter the tile as zeros (only a step that
+    // reaches the end has any).  The select sits here, where the store waits
+    // for the loads anyway: right after a prefetch it would wait for the next
+    // step's loads at once.
+    if (base + 32 > k_hi) {
+#pragma unroll
+      for (int v = 0; v < VLD; ++v) {
+        const int key = base + v * (64 / LPR) + lane / LPR;
+        *reinterpret_cast<u32x4*>(vt_w + (v * (64 / LPR) + lane / LPR) * R + (lane % LPR) * 8) =
+            key < k_hi ? vv[v] : u32x4{0u, 0u, 0u, 0u};
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < VLD; ++v)
+        *reinterpret_cast<u32x4*>(vt_w + (v * (64 / LPR) + lane / LPR) * R + (lane % LPR) * 8) = vv[v];
+    }
     wave_lds_sync();
     // V^T A-operands: lane holds V[key kappa(grp, e)][dim dt*16 + col],
     // kappa = (e < 4 ? 0 : 16) + grp*4 + (e & 3): the keys whose scores this
@@ -376,8 +418,6 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
       for (int e = 0; e < 8; ++e) e8[e] = vt_w[((e < 4 ? 0 : 16) + grp * 4 + (e & 3)) * R + dt * 16 + col];
       va[dt] = __builtin_bit_cast(bf16x8, e8);
     }
-    // masks: the step reaches tree keys or the end, or keys below a window
-    const bool edge = base + 32 > Tpe || (EXT && base < wlim);
     int kpos[EXT ? 8 : 1];
     if constexpr (EXT) {
       if (seg3) {
@@ -400,22 +440,29 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
         sa[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[0][ks]), qf, sa[0], 0, 0, 0);
         sa[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[1][ks]), qf, sa[1], 0, 0, 0);
       }
+      // Raw scores q.k: the scale c (> 0) enters with the max (the max of the
+      // scaled scores is c times the raw max, rounding being monotone) and in
+      // each exponent's fma.  ALiBi rows are scaled and biased here.
       float x[8];
+      float cs = p.c;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = sa[e >> 2][e & 3] * p.c;
+      for (int e = 0; e < 8; ++e) x[e] = sa[e >> 2][e & 3];
       if constexpr (EXT) {
         if (seg3) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = __builtin_fmaf(cb[qt], (float)(qpos[qt] - kpos[e]), x[e]);
+          for (int e = 0; e < 8; ++e) x[e] = __builtin_fmaf(cb[qt], (float)(qpos[qt] - kpos[e]), x[e] * p.c);
+          cs = 1.0f;
         }
       }
       if (edge) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int key = base + (e < 4 ? 0 : 16) + grp * 4 + (e & 3);
-          bool vis = key < k_hi;
-          if (key >= Tpe) vis = vis && ((anc[qt] >> (key - Tpe)) & 1ull);
-          else if (EXT) vis = vis && key >= kmin[qt];
+          // selects, not branches: tree keys by their ancestor bit, prefix
+          // keys by the window
+          const bool tree_vis = (anc[qt] >> ((unsigned)(key - Tpe) & 63u)) & 1ull;
+          const bool pre_vis = EXT ? key >= kmin[qt] : true;
+          const bool vis = key < k_hi && (key >= Tpe ? tree_vis : pre_vis);
           x[e] = vis ? x[e] : kNegInf;
         }
       }
@@ -424,17 +471,22 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
       for (int e = 1; e < 8; ++e) mx = __builtin_fmaxf(mx, x[e]);
       mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16));
       mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+      mx *= cs;
       const float mn = __builtin_fmaxf(m[qt], mx);
       const float ms = mn == kNegInf ? 0.0f : mn;
-      const float alpha = ex2(m[qt] - ms);
-      m[qt] = mn;
-      l[qt] *= alpha;
+      // (l, O) are rescaled only when some lane's finite running max moved:
+      // otherwise alpha is exactly 1 (or they are still zero).
+      if (__builtin_amdgcn_ballot_w64(mn != m[qt] && m[qt] != kNegInf)) {
+        const float alpha = ex2(m[qt] - ms);
+        l[qt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) o[qt][dt] *= alpha;
+      }
+      m[qt] = mn;
       __bf16 ph[8], pl[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float pe = ex2(x[e] - ms);
+        const float pe = ex2(__builtin_fmaf(x[e], cs, -ms));
         l[qt] += pe;
         ph[e] = static_cast<__bf16>(pe);
         pl[e] = static_cast<__bf16>(pe - static_cast<float>(ph[e]));
@@ -446,13 +498,54 @@ __global__ __launch_bounds__(NW * 64, (PF && D == 64) ? 2 : 1) void k_tree_attn(
         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], bl, o[qt][dt], 0, 0, 0);
       }
     }
-    if (more) {
+  };
+
+  // The ancestor words (and the prologue's other loads) land before the walk,
+  // so no mask test inside it waits on the vector-memory counter, which would
+  // also wait for a prefetched step.
+  __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (PF >= 2) {
+    // PF register sets in turn: a step's math runs while the next PF - 1
+    // steps' loads are in flight.  The loads are unconditional (past the last
+    // step they fetch the last step's rows again, an L2 hit) and nothing is
+    // copied between the sets, so each step waits only for its own loads.
+    u32x4 kS[PF][2][KS], vS[PF][VLD];
+    int st = wi;
+    if (st < nsteps) {
+      const int last = nsteps - 1;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) kf[kt][ks] = kfn[kt][ks];
-#pragma unroll
-      for (int v = 0; v < VLD; ++v) vv[v] = vvn[v];
+      for (int r = 0; r < PF - 1; ++r) load_step(k_lo + min(st + r * nws, last) * 32, kS[r], vS[r]);
+      // step st from set `cur`, then the loads of step st + (PF - 1) * nws into
+      // set `nxt` (the one the previous step consumed); true once done
+      auto stage = [&](const u32x4 (&kc)[2][KS], const u32x4 (&vc)[VLD], u32x4 (&kn)[2][KS],
+                       u32x4 (&vn)[VLD]) -> bool {
+        load_step(k_lo + min(st + (PF - 1) * nws, last) * 32, kn, vn);
+        step(k_lo + st * 32, kc, vc);
+        st += nws;
+        return st >= nsteps;
+      };
+      for (;;) {
+        if (stage(kS[0], vS[0], kS[PF - 1], vS[PF - 1])) break;
+        if (stage(kS[1], vS[1], kS[0], vS[0])) break;
+        if constexpr (PF > 2) {
+          if (stage(kS[2 % PF], vS[2 % PF], kS[1], vS[1])) break;
+        }
+        if constexpr (PF > 3) {
+          if (stage(kS[3 % PF], vS[3 % PF], kS[2 % PF], vS[2 % PF])) break;
+        }
+        if constexpr (PF > 4) {
+          if (stage(kS[4 % PF], vS[4 % PF], kS[3 % PF], vS[3 % PF])) break;
+        }
+        if constexpr (PF > 5) {
+          if (stage(kS[5 % PF], vS[5 % PF], kS[4 % PF], vS[4 % PF])) break;
+        }
+      }
+    }
+  } else {
+    for (int st = wi; st < nsteps; st += nws) {
+      u32x4 kf[2][KS], vv[VLD];
+      load_step(k_lo + st * 32, kf, vv);
+      step(k_lo + st * 32, kf, vv);
     }
   }
 
@@ -577,12 +670,13 @@ static TaPlan ta_plan(int B, int H, int Hkv, int N, int Tp, int d, int force_spl
   const int KT = (window > 0 && Tp > window - 1 ? window - 1 : Tp) + N;
   const int steps = (KT + 31) / 32;
   const int64_t base = (int64_t)B * Hkv * pl.G;
-  const int64_t target = (int64_t)device_cus() * 4;
-  int S = (int)((target + base - 1) / base);
-  // A split must carry enough keys to pay for the merge launch: at least 24
-  // 32-key steps each (the config-3 sweep: 2 splits of 33 steps beat 4 of
-  // 17; a verify step over ~800 keys runs best unsplit).
-  const int sby_work = steps / 24 > 1 ? steps / 24 : 1;
+  // Key splits only to give every CU a workgroup: a grid that already has
+  // one per CU runs unsplit (config 3, 256 workgroups of 66 key steps: 32.7
+  // us unsplit against 35-36 us in two splits plus the merge launch), and a
+  // split carries at least 8 key steps.
+  const int64_t cus = device_cus();
+  int S = base >= cus ? 1 : (int)((cus + base - 1) / base);
+  const int sby_work = steps / 8 > 1 ? steps / 8 : 1;
   S = S < sby_work ? S : sby_work;
   const int smax = (steps + 3) / 4;  // at least one 32-key step per wave
   if (force_splits > 0) S = force_splits;
@@ -603,24 +697,37 @@ static size_t ta_ws_bytes(const TaPlan& pl, int B, int H, int N, int d) {
   return c.bytes();
 }
 
-// Waves per workgroup (5: 4 with prefetch).  A grid of at most one workgroup
-// per CU gets 8 waves (16 when 8 does not fit the query tile), so each wave
-// walks few key steps and more loads are in flight per CU; up to two per CU,
-// 8 waves where the query tile fits them, else (d = 64) 4 waves with the
-// next key step's loads in flight (config 3: 38.5-41.1 against 41.6-42.0 us
-// for 4 waves without, on two boxes); larger grids keep 4 waves.  force (the args'
-// force_waves: 4, 5, 8, 16) overrides the choice where the shape fits.  EXT
-// launches (window / ALiBi) have 4 or 8 waves.
+// Workgroup shapes (the args' force_waves codes): 4, 8, 16 waves; 5 = 4
+// waves and 9 = 8 waves with the next key step's loads in flight (a ring of
+// two register sets).
+struct TaShape {
+  int nw, pf;
+};
+static TaShape ta_shape(int code) {
+  if (code == 5) return {4, 2};
+  if (code == 9) return {8, 2};
+  return {code, 0};
+}
+
+// The shape of a launch.  A grid of at most one workgroup per CU gets 8 waves
+// (8 with prefetch when the query tile is 3 or 4, 16 when neither fits), so
+// each wave walks few key steps and more loads are in flight per CU; up to
+// two per CU, 8 waves where the query tile fits them, else (d = 64) 4 waves
+// with prefetch; larger grids keep 4 waves.  force (the args' force_waves)
+// overrides the choice where the shape fits.  EXT launches (window / ALiBi)
+// have 4 or 8 waves.
 static int ta_waves(int D, int QT, int64_t nwg, int force, bool ext) {
-  auto ok = [&](int nw) {
-    if (ext && nw != 4 && nw != 8) return false;
-    return nw == 5 ? ta_variant_ok(D, QT, 4, true) : ta_variant_ok(D, QT, nw, false);
+  auto ok = [&](int code) {
+    const TaShape sh = ta_shape(code);
+    if (ext && (sh.pf || (sh.nw != 4 && sh.nw != 8))) return false;
+    return ta_variant_ok(D, QT, sh.nw, sh.pf);
   };
   if (force && ok(force)) return force;
   if (ext) return ok(8) && nwg <= 2 * device_cus() ? 8 : 4;
   const int64_t cus = device_cus();
   if (nwg <= cus) {
     if (ok(8)) return 8;  // (measured at least as fast as 16 at decode shapes, with twice the registers)
+    if (ok(9)) return 9;
     if (ok(16)) return 16;
     return 5;
   }
@@ -631,7 +738,7 @@ static int ta_waves(int D, int QT, int64_t nwg, int force, bool ext) {
   return 4;
 }
 
-template <int D, int OT, int NW, bool PF, bool EXT>
+template <int D, int OT, int NW, int PF, bool EXT>
 static void ta_launch_qt(const TreeAttnParams& p, int QT, dim3 grid, hipStream_t st) {
   const dim3 block(NW * 64);
   switch (QT) {
@@ -659,7 +766,7 @@ static int ta_launch_d(TreeAttnParams p, int QT, bool ext, int force_waves, hipS
   const int64_t nwg = (int64_t)p.B * p.Hkv * p.G * p.S;
   const dim3 grid((unsigned)nwg);
   const int nw = ta_waves(D, QT, nwg, force_waves, ext);
-  const int waves = nw == 5 ? 4 : nw;
+  const int waves = ta_shape(nw).nw;
   if (p.T2 > 0) {
     // split 0's share of waves for the second segment: a quarter, at most
     // one per 32-row step of it
@@ -674,14 +781,15 @@ static int ta_launch_d(TreeAttnParams p, int QT, bool ext, int force_waves, hipS
   }
   if (ev) VNX_HIP_CHECK(hipEventRecord(ev[0], st));
   if (ext) {
-    if (nw == 8) ta_launch_qt<D, OT, 8, false, true>(p, QT, grid, st);
-    else ta_launch_qt<D, OT, 4, false, true>(p, QT, grid, st);
+    if (nw == 8) ta_launch_qt<D, OT, 8, 0, true>(p, QT, grid, st);
+    else ta_launch_qt<D, OT, 4, 0, true>(p, QT, grid, st);
   } else {
     switch (nw) {
-      case 16: ta_launch_qt<D, OT, 16, false, false>(p, QT, grid, st); break;
-      case 8: ta_launch_qt<D, OT, 8, false, false>(p, QT, grid, st); break;
-      case 5: ta_launch_qt<D, OT, 4, true, false>(p, QT, grid, st); break;
-      default: ta_launch_qt<D, OT, 4, false, false>(p, QT, grid, st); break;
+      case 16: ta_launch_qt<D, OT, 16, 0, false>(p, QT, grid, st); break;
+      case 8: ta_launch_qt<D, OT, 8, 0, false>(p, QT, grid, st); break;
+      case 5: ta_launch_qt<D, OT, 4, 2, false>(p, QT, grid, st); break;
+      case 9: ta_launch_qt<D, OT, 8, 2, false>(p, QT, grid, st); break;
+      default: ta_launch_qt<D, OT, 4, 0, false>(p, QT, grid, st); break;
     }
   }
   VNX_LAUNCH_CHECK();
