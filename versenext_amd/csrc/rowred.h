@@ -133,22 +133,25 @@ __device__ __forceinline__ ChunkResult reduce_chunk(const Tin* __restrict__ row,
     });
   }
   if (nfull < nvec) {
-    float x[NB * VE];
-    int nvalid = 0;
+    // The last, partial batch: every load first (all in flight), then each
+    // loaded vector consumed on its own, so a short batch costs its vectors'
+    // work only (no -inf padding through the scaling and the exps).
+    u32x4 raw[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int64_t vi = nfull + tid + (int64_t)NT * j;
+      raw[j] = u32x4{0u, 0u, 0u, 0u};
+      if (vi < nvec) raw[j] = Vec<Tin>::load_raw(base + vi * VE);
+    }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int64_t vi = nfull + tid + (int64_t)NT * j;
       if (vi < nvec) {
-        Vec<Tin>::load(base + vi * VE, &x[j * VE]);
-        nvalid += VE;
-      } else {
-#pragma unroll
-        for (int e = 0; e < VE; ++e) x[j * VE + e] = kNegInf;
+        float x[VE];
+        Vec<Tin>::cvt_raw(raw[j], x);
+        consume<SM, THR, LSE, ARGMAX>(x, VE, st, sc, thr, [&](int q) { return c0 + vi * VE + q; });
       }
     }
-    consume<SM, THR, LSE, ARGMAX>(x, nvalid, st, sc, thr, [&](int q) {
-      return c0 + (nfull + tid + (int64_t)NT * (q / VE)) * VE + (q % VE);
-    });
   }
   // Tail: fewer than VE elements after the last full vector.
   const int64_t tail0 = nvec * VE;

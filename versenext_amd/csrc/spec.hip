@@ -641,8 +641,11 @@ static SpecPlan spec_plan(int64_t B, int k, int64_t V, int dtype, int rows_a = -
   // k = 0 draw (one row per batch row) takes about two workgroups per CU:
   // at 32 rows of 248,320, 16 chunks per row gave a 20 us shorter config-5
   // round than 60 (and 8 or 4 chunks were slower again)
+  // An acceptance (k > 0) takes chunks of at least one full batch (kNB
+  // vectors per thread): at B = 32, k = 6 in bf16, 30 chunks of 4 vectors per
+  // thread ran the 224-row LSE launch in 51 us, mostly per-workgroup cost.
   const int64_t wgs = k == 0 ? 2 * (int64_t)device_cus() : kLseWgs;
-  int c = pick_chunks(rows, V, ve * (kNB / 2), std::min(kMaxChunks, kAccParts / rows_a), wgs);
+  int c = pick_chunks(rows, V, ve * (k == 0 ? kNB / 2 : kNB), std::min(kMaxChunks, kAccParts / rows_a), wgs);
   const int64_t len = ((V + c - 1) / c + ve - 1) / ve * ve;
   pl.len = len;
   pl.chunks = (int)((V + len - 1) / len);

@@ -232,6 +232,15 @@ template <> struct Vec<float> {
     out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
   }
   __device__ __forceinline__ static float load1(const float* p) { return *p; }
+  // The 16 bytes alone, converted later (a load under a per-lane condition
+  // then carries no conversion that would wait for it inside the condition).
+  __device__ __forceinline__ static u32x4 load_raw(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  }
+  __device__ __forceinline__ static void cvt_raw(const u32x4& v, float* out) {
+    out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
+    out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
+  }
 };
 template <> struct Vec<__hip_bfloat16> {
   static constexpr int N = 8;
@@ -247,6 +256,17 @@ template <> struct Vec<__hip_bfloat16> {
   }
   __device__ __forceinline__ static float load1(const __hip_bfloat16* p) {
     return __uint_as_float((uint32_t)(*reinterpret_cast<const uint16_t*>(p)) << 16);
+  }
+  __device__ __forceinline__ static u32x4 load_raw(const __hip_bfloat16* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  }
+  __device__ __forceinline__ static void cvt_raw(const u32x4& v, float* out) {
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[2 * j] = __uint_as_float(w[j] << 16);
+      out[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+    }
   }
 };
 
