@@ -363,6 +363,10 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
 #pragma unroll
   for (int r = 0; r < RM; ++r) acc[r] = 0.0f;
   float ss = 0.0f;  // nw: sum of squares of the raw row
+  // A row of at most 256 * VW columns (one block per thread) stays in
+  // registers for the experts' bf16 copies below.
+  const bool one_block = D <= 256 * VW;
+  float x1[VW], w1[VW];
   // thread tid takes columns tid*VW .. +VW of every 256*VW block
   for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
     // every row's load issued unconditionally (rows past R re-read row R-1
@@ -381,6 +385,8 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
       else w[0] = nw[c];
 #pragma unroll
       for (int e = 0; e < VW; ++e) {
+        x1[e] = x[e];
+        w1[e] = w[e];
         ss = __builtin_fmaf(x[e], x[e], ss);
         x[e] *= w[e];
       }
@@ -425,12 +431,18 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
     lg[tid] = nw ? v * rstd : v;
   }
   __syncthreads();
-  if (wave == 0) route_wave(lane < R ? lg[lane] : 0.0f, P, E, topk, comb + m * ldc);
   if (nw && xo) {
     // the experts' bf16 input rows: bf16(x * rstd * w), as RMSNorm rounds them
+    // (stored before wave 0 routes, so the stores drain under the routing)
     for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
       float x[VW], w[VW];
-      if constexpr (VW == 4) {
+      if (one_block) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          x[e] = x1[e];
+          w[e] = w1[e];
+        }
+      } else if constexpr (VW == 4) {
         ld4(h + m * ldh + c, x);
         ld4(nw + c, w);
       } else {
@@ -446,6 +458,7 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
       }
     }
   }
+  if (wave == 0) route_wave(lane < R ? lg[lane] : 0.0f, P, E, topk, comb + m * ldc);
 }
 
 // Expert activations of all PE experts for every row, scaled by the routing

@@ -76,6 +76,20 @@ struct QGemvParams {
   int64_t ksplit_len;  // K per grid.y split (multiple of kGK; the launches use K)
 };
 
+// The same with the format fixed at compile time: no branch between a scale
+// load and its conversion, so the conversion waits at the scale's use, not
+// at the load (a converting branch right after the load waits for every load
+// issued before it, weights and x included).
+template <bool SF16>
+__device__ __forceinline__ float load_scale_t(const QGemvParams& p, int64_t row, unsigned g) {
+  if constexpr (SF16) {
+    const uint16_t h = static_cast<const uint16_t*>(p.sc)[row * p.lds + g];
+    return (float)__builtin_bit_cast(_Float16, h);
+  } else {
+    return static_cast<const float*>(p.sc)[row * p.lds + g];
+  }
+}
+
 __device__ __forceinline__ float load_scale(const QGemvParams& p, int64_t row, unsigned g) {
   if (p.sc_f16) {
     const uint16_t h = static_cast<const uint16_t*>(p.sc)[row * p.lds + g];
@@ -317,18 +331,17 @@ __global__ __launch_bounds__(kQNT) void k_qgemv(QGemvParams p) {
 // TP: 16-row tiles per workgroup (2 for grids of more tiles than CUs: each
 // wave's x block is loaded and staged once for both tiles).  GP: groups per
 // pass of a wave (1 where K has at most one group per wave, or TP 2).
-template <int BITS, int NC, int NW, int QE = 0, int NX = 0, int TP = 1, int GP = 2>
-__global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
+template <int BITS, int NC, int NW, int QE, int NX, int TP, int GP, bool SF16>
+__device__ __forceinline__ void qgemv_tile_body(const QGemvParams& p, char* smem, float* ssp_flat) {
   constexpr int WBYTES = BITS == 4 ? 16 : 32;
   constexpr int XR = NC * 16;            // staged batch rows
   constexpr int XP = kGK + kXPad;        // LDS row pitch (fp16)
   constexpr int XL = XR * (kGK / 8) / 64;  // 16-byte x loads per lane per group
   // the per-wave x tiles, reused for the partial tiles after the K loop
   constexpr size_t kXBytes = size_t(NW) * XR * XP * 2, kRBytes = size_t(NW) * TP * NC * 64 * 16;
-  __shared__ __attribute__((aligned(16))) char smem[kXBytes > kRBytes ? kXBytes : kRBytes];
   auto xs_all = reinterpret_cast<uint16_t(*)[XR * XP]>(smem);
   auto red = reinterpret_cast<f32x4(*)[TP][NC][64]>(smem);
-  __shared__ float ssp[NX ? NW : 1][NX ? XR : 1];  // NX: per-wave sums of squares per row
+  auto ssp = reinterpret_cast<float(*)[NX ? XR : 1]>(ssp_flat);  // NX: per-wave sums of squares per row
   const int tid = threadIdx.x;
   const int wave = tid / VNX_WAVE, lane = tid % VNX_WAVE;
   const int m = lane % 16, kq = lane / 16;
@@ -422,7 +435,7 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
 #pragma unroll
         for (int t = 0; t < TP; ++t)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) sc[u][t][j] = load_scale(p, min((tile0 + t) * 16 + 4 * kq + j, p.N - 1), col);
+          for (int j = 0; j < 4; ++j) sc[u][t][j] = load_scale_t<SF16>(p, min((tile0 + t) * 16 + 4 * kq + j, p.N - 1), col);
       }
     }
 #pragma unroll
@@ -540,7 +553,7 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
   if (n0 >= p.N) return;
   if constexpr (BITS == 8) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] *= load_scale(p, min(n0 + j, p.N - 1), 0);
+    for (int j = 0; j < 4; ++j) v[j] *= load_scale_t<SF16>(p, min(n0 + j, p.N - 1), 0);
   }
   if constexpr (NX) {
     float t = 0.0f;
@@ -626,6 +639,18 @@ __global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
     for (int j = 0; j < 4; ++j)
       if (n0 + j < p.N) dst[j] = v[j];
   }
+}
+
+// The kernel: the scale format picks one of two bodies once, at entry.
+template <int BITS, int NC, int NW, int QE = 0, int NX = 0, int TP = 1, int GP = 2>
+__global__ __launch_bounds__(NW * 64) void k_qgemv_tile(QGemvParams p) {
+  constexpr int XR = NC * 16;
+  constexpr int XP = kGK + kXPad;
+  constexpr size_t kXBytes = size_t(NW) * XR * XP * 2, kRBytes = size_t(NW) * TP * NC * 64 * 16;
+  __shared__ __attribute__((aligned(16))) char smem[kXBytes > kRBytes ? kXBytes : kRBytes];
+  __shared__ float ssp[NX ? NW : 1][NX ? XR : 1];
+  if (p.sc_f16) qgemv_tile_body<BITS, NC, NW, QE, NX, TP, GP, true>(p, smem, &ssp[0][0]);
+  else qgemv_tile_body<BITS, NC, NW, QE, NX, TP, GP, false>(p, smem, &ssp[0][0]);
 }
 
 // Large N, W4 with group-128 fp16 scales (the tied LM head of a draft):
