@@ -109,18 +109,31 @@ __global__ __launch_bounds__(kRnThreads) void k_rmsnorm(const float* x, int64_t 
   __shared__ float red[kRnThreads / VNX_WAVE];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
-  float v[kRnPer], wv[kRnPer];
+  float v[kRnPer], wv[kRnPer], rv[kRnPer];
   float ss = 0.0f;
-  // every load (x, residual, weight) issued before the reduction
+  // Every load (x, residual, weight) is issued before any value is used, with
+  // no per-lane condition between them (columns past D re-read column D - 1
+  // and count as 0 below): a use or a select beside a conditional load would
+  // wait there for every load in flight.  nb (wave-uniform) bounds the blocks.
+  const int nb = (int)min((int64_t)kRnPer, (D + kRnThreads - 1) / kRnThreads);
 #pragma unroll
   for (int j = 0; j < kRnPer; ++j) {
-    const int c = tid + j * kRnThreads;
-    float a = 0.0f;
-    wv[j] = 0.0f;
-    if (c < D) {
-      a = x[row * ldx + c];
-      if (r) a += Elt<TR>::ld(r + row * ldr + c);
+    if (j < nb) {
+      const int64_t c = min((int64_t)(tid + j * kRnThreads), D - 1);
+      v[j] = x[row * ldx + c];
       wv[j] = w[c];
+      if (r) rv[j] = Elt<TR>::ld(r + row * ldr + c);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRnPer; ++j) {
+    const bool in = j < nb && tid + j * kRnThreads < D;
+    float a = 0.0f;
+    if (j < nb) {
+      a = v[j];
+      if (r) a += rv[j];
+      a = in ? a : 0.0f;
+      wv[j] = in ? wv[j] : 0.0f;
     }
     v[j] = a;
     ss = __builtin_fmaf(a, a, ss);
@@ -536,6 +549,12 @@ __global__ __launch_bounds__(256) void k_sum_expert_rows(const TY* y, int64_t ld
   float acc[VW];
 #pragma unroll
   for (int e = 0; e < VW; ++e) acc[e] = 0.0f;
+  // the residual values (accumulate) load first, under the expert loads
+  float o[VW];
+  if (accumulate) {
+    if constexpr (VW == 4) ld4(out + m * ldo + c, o);
+    else o[0] = out[m * ldo + c];
+  }
   for (int z0 = 0; z0 < E; z0 += ZB) {
     // every load of the batch issued before any is used: unrouted experts
     // read row 0 and add +0.0, as their zero rows do in the dense sum
@@ -556,14 +575,8 @@ __global__ __launch_bounds__(256) void k_sum_expert_rows(const TY* y, int64_t ld
       for (int e = 0; e < VW; ++e) acc[e] += sl[q] >= 0 ? v[q][e] : 0.0f;
   }
   if (accumulate) {  // out += the expert sum (the block's residual add)
-    if constexpr (VW == 4) {
-      float o[4];
-      ld4(out + m * ldo + c, o);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = o[e] + acc[e];
-    } else {
-      acc[0] = out[m * ldo + c] + acc[0];
-    }
+    for (int e = 0; e < VW; ++e) acc[e] = o[e] + acc[e];
   }
   if constexpr (VW == 4) st4(out + m * ldo + c, acc);
   else out[m * ldo + c] = acc[0];

@@ -350,6 +350,30 @@ __device__ __forceinline__ void lane_vec(const Tin* row, int64_t sbi, int64_t V,
   }
 }
 
+// The same vector as raw bits (elements past V carry -inf bits), converted
+// later: a conversion beside the load would wait for it there, and with it for
+// every load issued before it.
+template <typename Tin>
+__device__ __forceinline__ u32x4 lane_raw(const Tin* row, int64_t sbi, int64_t V) {
+  constexpr int VE = Vec<Tin>::N;
+  const int64_t e = (sbi * VNX_WAVE + (threadIdx.x % VNX_WAVE)) * VE;
+  if (e + VE <= V) return Vec<Tin>::load_raw(row + e);
+  uint32_t w[4];
+  if constexpr (VE == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = e + i < V ? __float_as_uint(Vec<Tin>::load1(row + e + i)) : 0xFF800000u;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = e + 2 * i < V ? (__float_as_uint(Vec<Tin>::load1(row + e + 2 * i)) >> 16) : 0xFF80u;
+      const uint32_t hi = e + 2 * i + 1 < V ? (__float_as_uint(Vec<Tin>::load1(row + e + 2 * i + 1)) >> 16) : 0xFF80u;
+      w[i] = lo | (hi << 16);
+    }
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
 // Draw mass of this lane's vector of sub-block sbi (sequential fp64 sum in
 // element order), and its weights.
 template <typename Tin, int SM, bool THR>
@@ -381,23 +405,28 @@ __device__ __forceinline__ void mass_chunk(const SpecParams& p, int64_t b, int c
   const int64_t s0 = (int64_t)c * spc;
   const int64_t s1 = min(s0 + spc, p.nsb);
   for (int64_t sb = s0 + wave; sb < s1; sb += (int64_t)kNW * kNB2) {
-    float xp[kNB2][VE], xq[kNB2][VE];
+    // every load of the batch in flight first (raw bits), then the weights
+    u32x4 rp[kNB2], rq[kNB2];
 #pragma unroll
     for (int j = 0; j < kNB2; ++j) {
       const int64_t sbi = sb + (int64_t)kNW * j;
+      rp[j] = rq[j] = u32x4{0u, 0u, 0u, 0u};
       if (sbi < s1) {
-        lane_vec<Tin>(P, sbi, p.V, xp[j]);
-        if constexpr (WSEL == W_RESID) lane_vec<Tin>(Q, sbi, p.V, xq[j]);
+        rp[j] = lane_raw<Tin>(P, sbi, p.V);
+        if constexpr (WSEL == W_RESID) rq[j] = lane_raw<Tin>(Q, sbi, p.V);
       }
     }
 #pragma unroll
     for (int j = 0; j < kNB2; ++j) {
       const int64_t sbi = sb + (int64_t)kNW * j;
       if (sbi < s1) {
+        float xp[VE], xq[VE];
+        Vec<Tin>::cvt_raw(rp[j], xp);
+        if constexpr (WSEL == W_RESID) Vec<Tin>::cvt_raw(rq[j], xq);
         double m = 0.0;
 #pragma unroll
         for (int i = 0; i < VE; ++i)
-          m += (double)draw_weight<SM, THR>(xp[j][i], WSEL == W_RESID ? xq[j][i] : 0.0f, WSEL, p.sc, d.thr_p,
+          m += (double)draw_weight<SM, THR>(xp[i], WSEL == W_RESID ? xq[i] : 0.0f, WSEL, p.sc, d.thr_p,
                                             d.thr_q, jb.Lp, jb.Lq);
         m = wave_sum(m);
         if (threadIdx.x % VNX_WAVE == 0) st_agent(&p.sbm[b * p.nsb + sbi], m);
@@ -453,7 +482,21 @@ __device__ __forceinline__ void draw_work(const SpecParams& p, int64_t b, const 
     if (tid == kNT - 1) L.total = incl;
     __syncthreads();
   };
-  for (int64_t i = tid; i < p.nsb; i += kNT) sh_m[i] = ld_agent(&sbm[i]);
+  {
+    // every load in flight first (at most kDrawLds / kNT per thread), then
+    // the LDS stores
+    double v[kDrawLds / kNT];
+#pragma unroll
+    for (int j = 0; j < kDrawLds / kNT; ++j) {
+      const int64_t i = tid + (int64_t)j * kNT;
+      v[j] = i < p.nsb ? ld_agent(&sbm[i]) : 0.0;
+    }
+#pragma unroll
+    for (int j = 0; j < kDrawLds / kNT; ++j) {
+      const int64_t i = tid + (int64_t)j * kNT;
+      if (i < p.nsb) sh_m[i] = v[j];
+    }
+  }
   scan_totals();
   if (!(L.total > 0.0) && wsel == W_RESID) {
     // max(0, p_n - q_n) has no mass (p_n == q_n after rounding): draw from
