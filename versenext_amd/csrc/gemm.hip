@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   __shared__ __attribute__((aligned(16))) char smem[SMB];
   __shared__ float rsd[NX ? 32 : 1];
   __shared__ __attribute__((aligned(16))) float nws[NX ? kVgNormMaxK : 4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave % WN, wk = wave / WN;
   const int z = blockIdx.y;
   const int t = blockIdx.x;
@@ -161,24 +161,22 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
   // (only split 0 stores).  vec_out: row m0 + lane/2, columns
   // ni*32 + 16 (lane % 2) .. +16, the layout of the transposed tile; else
   // rows 8i + 4h + e of column ni*32 + r, the accumulator layout.
-  float old[EPI == 3 ? 16 : 1];
+  // The loads land in their final registers (a copy beside them would wait
+  // for them at once), under a wave-uniform branch.
+  f32x4 old[EPI == 3 ? 4 : 1];
   if constexpr (EPI == 3) {
     if (wk == 0) {
       if (p.vec_out) {
         const float* yf = reinterpret_cast<const float*>(p.y) + (int64_t)z * p.syb +
                           (int64_t)min(m0 + (lane >> 1), p.M - 1) * p.ldy + nie * 32 + 16 * (lane & 1);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(yf + 4 * q);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) old[4 * q + e] = v[e];
-        }
+        for (int q = 0; q < 4; ++q) old[q] = *reinterpret_cast<const f32x4*>(yf + 4 * q);
       } else {
         const float* yf = reinterpret_cast<const float*>(p.y) + (int64_t)z * p.syb + min(ni * 32 + r, p.N - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) old[4 * i + e] = yf[(int64_t)min(m0 + 8 * i + 4 * h + e, p.M - 1) * p.ldy];
+          for (int e = 0; e < 4; ++e) old[i][e] = yf[(int64_t)min(m0 + 8 * i + 4 * h + e, p.M - 1) * p.ldy];
       }
     }
   }
@@ -350,7 +348,7 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
       for (int q = 0; q < 4; ++q) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(row + 16 * hf + 4 * q);
         *reinterpret_cast<f32x4*>(yf + 4 * q) =
-            f32x4{old[4 * q] + v[0], old[4 * q + 1] + v[1], old[4 * q + 2] + v[2], old[4 * q + 3] + v[3]};
+            f32x4{old[q][0] + v[0], old[q][1] + v[1], old[q][2] + v[2], old[q][3] + v[3]};
       }
     } else if constexpr (EPI == 0) {
       float v0[8], v1[8];
@@ -384,7 +382,7 @@ __global__ __launch_bounds__(256) void k_vgemm(VgParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 8 * i + 4 * h + e;
-        if (m < p.M) yf[(int64_t)m * p.ldy + n] = old[4 * i + e] + acc[4 * i + e];
+        if (m < p.M) yf[(int64_t)m * p.ldy + n] = old[i][e] + acc[4 * i + e];
       }
     return;
   }

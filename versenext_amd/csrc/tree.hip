@@ -213,38 +213,49 @@ __global__ __launch_bounds__(NW * 64, (PF == 2 && D == 64 && NW == 4) ? 2 : 1) v
       lo = __builtin_bit_cast(u32x4, lo8);
       hi = __builtin_bit_cast(u32x4, hi8);
     };
-    // this head's tree rows: rotated keys and values into the cache
-    for (int idx = tid; idx < p.N * LPR; idx += NW * 64) {
-      const int i = idx / LPR, c = idx - i * LPR;
-      const int64_t pos = (int64_t)tpb + i;
-      if (pos >= p.cap) continue;
-      const uint16_t* row = p.qkv + (int64_t)(b * p.N + i) * p.qkv_ld;
-      uint16_t* kd = const_cast<uint16_t*>(p.kt) + b * p.t_sb + kvh * p.t_sh + pos * p.t_sr;
-      uint16_t* vd = const_cast<uint16_t*>(p.vt) + b * p.t_sb + kvh * p.t_sh + pos * p.t_sr;
-      if (c < LPR / 2) {
-        u32x4 lo, hi;
-        rot8(row + (int64_t)(p.H + kvh) * D, pos, c, lo, hi);
-        *reinterpret_cast<u32x4*>(kd + c * 8) = lo;
-        *reinterpret_cast<u32x4*>(kd + D / 2 + c * 8) = hi;
-      } else {
-        const int cv = c - LPR / 2;  // two value chunks per item
-        const uint16_t* vs = row + (int64_t)(p.H + p.Hkv + kvh) * D;
-        *reinterpret_cast<u32x4*>(vd + cv * 8) = ldg16(vs + cv * 8);
-        *reinterpret_cast<u32x4*>(vd + D / 2 + cv * 8) = ldg16(vs + D / 2 + cv * 8);
+    // Three kinds of items, each starting on a wave boundary so their load ->
+    // math -> store chains run in different waves side by side: the tree
+    // rows' rotated keys (item (i, c): chunk c < LPR/2 of row i and its
+    // partner), the group's rotated queries into LDS (rows past nrows are
+    // zero), and the tree rows' values (two chunks per item), copied.
+    const int nk = p.N * (LPR / 2), nq = QT * 16 * (LPR / 2);
+    const int oq = (nk + 63) / 64 * 64, ov = oq + (nq + 63) / 64 * 64;
+    for (int slot = tid; slot < ov + nk; slot += NW * 64) {
+      if (slot < nk) {
+        const int i = slot / (LPR / 2), c = slot - i * (LPR / 2);
+        const int64_t pos = (int64_t)tpb + i;
+        if (pos < p.cap) {
+          const uint16_t* row = p.qkv + (int64_t)(b * p.N + i) * p.qkv_ld;
+          uint16_t* kd = const_cast<uint16_t*>(p.kt) + b * p.t_sb + kvh * p.t_sh + pos * p.t_sr;
+          u32x4 lo, hi;
+          rot8(row + (int64_t)(p.H + kvh) * D, pos, c, lo, hi);
+          *reinterpret_cast<u32x4*>(kd + c * 8) = lo;
+          *reinterpret_cast<u32x4*>(kd + D / 2 + c * 8) = hi;
+        }
+      } else if (slot >= oq && slot < oq + nq) {
+        const int idx = slot - oq;
+        const int r = idx / (LPR / 2), c = idx - r * (LPR / 2);
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+        if (r < nrows) {
+          const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
+          const int h = kvh * p.n_rep + rep;
+          const int64_t pos = min((int64_t)tpb + node, p.cap - 1);
+          rot8(p.qkv + (int64_t)(b * p.N + node) * p.qkv_ld + (int64_t)h * D, pos, c, lo, hi);
+        }
+        *reinterpret_cast<u32x4*>(s_q + r * R + c * 8) = lo;
+        *reinterpret_cast<u32x4*>(s_q + r * R + D / 2 + c * 8) = hi;
+      } else if (slot >= ov) {
+        const int j = slot - ov;
+        const int i = j / (LPR / 2), cv = j - i * (LPR / 2);
+        const int64_t pos = (int64_t)tpb + i;
+        if (pos < p.cap) {
+          const uint16_t* vs = p.qkv + (int64_t)(b * p.N + i) * p.qkv_ld + (int64_t)(p.H + p.Hkv + kvh) * D;
+          uint16_t* vd = const_cast<uint16_t*>(p.vt) + b * p.t_sb + kvh * p.t_sh + pos * p.t_sr;
+          const u32x4 v0 = ldg16(vs + cv * 8), v1 = ldg16(vs + D / 2 + cv * 8);
+          *reinterpret_cast<u32x4*>(vd + cv * 8) = v0;
+          *reinterpret_cast<u32x4*>(vd + D / 2 + cv * 8) = v1;
+        }
       }
-    }
-    // Q rows of this group -> LDS, rotated (rows past nrows are zero)
-    for (int idx = tid; idx < QT * 16 * (LPR / 2); idx += NW * 64) {
-      const int r = idx / (LPR / 2), c = idx - r * (LPR / 2);
-      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-      if (r < nrows) {
-        const int rr = row0 + r, rep = rr / p.N, node = rr - rep * p.N;
-        const int h = kvh * p.n_rep + rep;
-        const int64_t pos = min((int64_t)tpb + node, p.cap - 1);
-        rot8(p.qkv + (int64_t)(b * p.N + node) * p.qkv_ld + (int64_t)h * D, pos, c, lo, hi);
-      }
-      *reinterpret_cast<u32x4*>(s_q + r * R + c * 8) = lo;
-      *reinterpret_cast<u32x4*>(s_q + r * R + D / 2 + c * 8) = hi;
     }
     __builtin_amdgcn_s_waitcnt(0);  // the cache rows are written before any wave reads them
   } else {
