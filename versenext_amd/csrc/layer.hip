@@ -384,18 +384,28 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
   for (int64_t c = (int64_t)tid * VW; c < D; c += 256 * VW) {
     // every row's load issued unconditionally (rows past R re-read row R-1
     // and are not accumulated): no branches between the loads
-    float x[VW];
+    // every load of the block first (row, norm weight, router rows), the
+    // math after them: a use beside a load would wait there for all loads
+    float x[VW], w[VW];
     if constexpr (VW == 4) {
       ld4(h + m * ldh + c, x);
     } else {
       x[0] = h[m * ldh + c];
     }
     if (nw) {
-      // RMSNorm input: the products use x * w; the per-row factor is applied
-      // to the reduced logits
-      float w[VW];
       if constexpr (VW == 4) ld4(nw + c, w);
       else w[0] = nw[c];
+    }
+    float wv[RM][VW];
+#pragma unroll
+    for (int r = 0; r < RM; ++r) {
+      const float* wrow = wr + (int64_t)(r < R ? r : R - 1) * ldw + c;
+      if constexpr (VW == 4) ld4(wrow, wv[r]);
+      else wv[r][0] = wrow[0];
+    }
+    if (nw) {
+      // RMSNorm input: the products use x * w; the per-row factor is applied
+      // to the reduced logits
 #pragma unroll
       for (int e = 0; e < VW; ++e) {
         x1[e] = x[e];
@@ -409,13 +419,6 @@ __global__ __launch_bounds__(256) void k_mod_route_x(const float* h, int64_t ldh
         if constexpr (VW == 4) st4(dst + q * sxo, x);
         else Elt<__hip_bfloat16>::st(dst + q * sxo, x[0]);
       }
-    }
-    float wv[RM][VW];
-#pragma unroll
-    for (int r = 0; r < RM; ++r) {
-      const float* wrow = wr + (int64_t)(r < R ? r : R - 1) * ldw + c;
-      if constexpr (VW == 4) ld4(wrow, wv[r]);
-      else wv[r][0] = wrow[0];
     }
 #pragma unroll
     for (int r = 0; r < RM; ++r)
