@@ -179,13 +179,27 @@ __global__ __launch_bounds__(kTNT) void k_topk_filter(TopkParams p) {
   const int tid = threadIdx.x;
   const int w = tid / VNX_WAVE, l = tid % VNX_WAVE;
   // vector j of this thread covers offsets (tid + kTNT*j)*VE .. +VE
+  // Every full vector's load first (raw bits), the keys after: a conversion
+  // beside its load would wait there for every load in flight.
+  // The loads carry no condition (vectors past the chunk re-read its last full
+  // vector; their keys come from the element loads below), so no select or
+  // copy sits beside them.
   uint32_t key[kFiltPer];
+  u32x4 raw[NV];
+  if (n >= VE) {  // uniform
+    const int64_t last = (n / VE - 1) * VE;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t off = (int64_t)(tid + kTNT * j) * VE;
+      raw[j] = Vec<Tin>::load_raw(row + c0 + (off + VE <= n ? off : last));
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int64_t off = (int64_t)(tid + kTNT * j) * VE;
-    float x[VE];
     if (off + VE <= n) {
-      Vec<Tin>::load(row + c0 + off, x);
+      float x[VE];
+      Vec<Tin>::cvt_raw(raw[j], x);
 #pragma unroll
       for (int e = 0; e < VE; ++e) key[j * VE + e] = vkey(x[e]);
     } else {
