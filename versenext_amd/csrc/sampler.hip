@@ -158,19 +158,27 @@ __device__ __forceinline__ void for_range(const Tin* row, int64_t j0, int64_t j1
   constexpr int VE = Vec<Tin>::N;
   const int64_t nv = (j1 - j0) / VE;
   const int tid = threadIdx.x;
+  // The range's full vectors through a buffer resource: every load is issued
+  // (one past the range reads zeros without a memory access, and is not
+  // consumed), so no condition or select sits beside a load and the waits
+  // count statically; raw bits are converted in the second loop.
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<Tin*>(row + j0), (short)0, (int)(nv * VE * (int64_t)sizeof(Tin)), 0x00020000);
   for (int64_t v0 = 0; v0 < nv; v0 += (int64_t)NT * kSNB) {
-    float x[kSNB][VE];
+    u32x4 raw[kSNB];
 #pragma unroll
     for (int q = 0; q < kSNB; ++q) {
       const int64_t v = v0 + tid + (int64_t)NT * q;
-      if (v < nv) Vec<Tin>::load(row + j0 + v * VE, x[q]);
+      raw[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(v * 16), 0, 2));
     }
 #pragma unroll
     for (int q = 0; q < kSNB; ++q) {
       const int64_t v = v0 + tid + (int64_t)NT * q;
       if (v < nv) {
+        float x[VE];
+        Vec<Tin>::cvt_raw(raw[q], x);
 #pragma unroll
-        for (int e = 0; e < VE; ++e) f(j0 + v * VE + e, x[q][e]);
+        for (int e = 0; e < VE; ++e) f(j0 + v * VE + e, x[e]);
       }
     }
   }
