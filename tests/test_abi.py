@@ -34,6 +34,16 @@ def test_ctypes_signatures_cover_header():
     assert set(_lib.SIGNATURES) == set(header_functions())
 
 
+def test_integration_guide_names_every_header_function():
+    """The integration guide (INTEGRATION.md at the repository root) names
+    every function the header declares, so a maintainer wiring the reference
+    finds each entry point's role there."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    named = set(re.findall(r"\b(vnx_[a-z0-9_]+)\b", text))
+    missing = [f for f in header_functions() if f not in named]
+    assert not missing, f"not named in INTEGRATION.md: {missing}"
+
+
 def header_prototypes():
     """{name: (return type, [parameter types])} of every function include/vnx.h
     declares, with qualifiers kept ('const float*', 'int64_t', ...)."""
